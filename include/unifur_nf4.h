@@ -1,0 +1,162 @@
+/*
+ * unifur_nf4.h -- C ABI of the MI355X-native NF4 quantized-linear library
+ * (libunifur_nf4.so, hand-written gfx950 HIP kernels).
+ *
+ * It replaces the NF4 path of unifur (crate `diffusionblocks`): the codec in
+ * src/quantize.rs and the NF4-resident linear layers in src/qwennet.rs.  Each
+ * entry point names the reference item it stands in for (file:line).  The
+ * reference has no FFI for this path today (it is in-process Rust); these are
+ * the symbols its FFI crate would bind -- see INTEGRATION.md.
+ *
+ * Conventions (all entry points):
+ *   - Data buffers are DEVICE pointers owned by the caller; `stream` is a
+ *     hipStream_t (NULL = the default stream).  Every call is stream-ordered:
+ *     it only enqueues work and returns; results are ready when the stream
+ *     has reached the call.
+ *   - Return value: UNIFUR_NF4_OK (0) or a negative status; the message of the
+ *     last failure on the calling thread is unifur_nf4_last_error().
+ *   - The library holds no global mutable state except an optional internal
+ *     workspace cache (used only when a call passes workspace == NULL),
+ *     guarded by a mutex and keyed by (device, stream).
+ *   - Layout of a quantized tensor of `len` values (src/quantize.rs:221-257):
+ *     ceil(len/64) blocks of 64 consecutive values; `packed` holds
+ *     ceil(len/2) bytes, value 2i in the low nibble of byte i; scales are one
+ *     f32 absmax per block, or with double quantization one u8 code per block
+ *     and one f32 scale of scales.
+ *   - A linear weight is the reference's [d_in, d_out] row-major matrix
+ *     (y = x W, src/qwennet.rs:2196-2211), so its 64-value blocks run along
+ *     d_out.
+ */
+#ifndef UNIFUR_NF4_H
+#define UNIFUR_NF4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* BLOCK_SIZE (src/quantize.rs:36-37). */
+#define UNIFUR_NF4_BLOCK_SIZE 64
+
+enum {
+  UNIFUR_NF4_OK = 0,
+  UNIFUR_NF4_ERR_INVALID = -1,     /* bad argument (null pointer, shape, dtype) */
+  UNIFUR_NF4_ERR_HIP = -2,         /* a HIP runtime call or launch failed */
+  UNIFUR_NF4_ERR_WORKSPACE = -3,   /* workspace smaller than required */
+};
+
+/* Element types of activations and outputs. */
+enum { UNIFUR_NF4_F32 = 0, UNIFUR_NF4_BF16 = 1 };
+
+/* PackedScales (src/quantize.rs:221-233). */
+enum { UNIFUR_NF4_SCALES_F32 = 0, UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED = 1 };
+
+typedef struct unifur_nf4_scales {
+  int32_t kind;                 /* UNIFUR_NF4_SCALES_* */
+  const float *absmax;          /* F32: one f32 per block */
+  const uint8_t *dq_codes;      /* DOUBLE_QUANTIZED: one u8 per block */
+  const float *scale_of_scales; /* DOUBLE_QUANTIZED: one f32 (device pointer) */
+} unifur_nf4_scales;
+
+/* The packed weight an Nf4Linear holds (src/qwennet.rs:161-178). */
+typedef struct unifur_nf4_weight {
+  const uint8_t *packed;
+  unifur_nf4_scales scales;
+  uint64_t d_in;
+  uint64_t d_out;
+} unifur_nf4_weight;
+
+/* LoraAdapter factors (src/quantize.rs:556-565): a [d_in, rank] and
+ * b [rank, d_out], f32 row-major; forward adds (x a) b * scaling. */
+typedef struct unifur_nf4_lora {
+  const float *a;
+  const float *b;
+  uint32_t rank;
+  float scaling;
+} unifur_nf4_lora;
+
+/* Message of the calling thread's last failure ("" if none). */
+const char *unifur_nf4_last_error(void);
+
+/* ---- host-only accounting ------------------------------------------------ */
+
+/* NF4_LEVELS (src/quantize.rs:49-66), copied into out[16]. */
+int unifur_nf4_levels(float out[16]);
+
+/* Nf4Tensor::num_blocks / PackedNf4Tensor::num_blocks (src/quantize.rs:165-167, :325-327). */
+uint64_t unifur_nf4_num_blocks(uint64_t len);
+
+/* Bytes of the packed code array, ceil(len/2) (src/quantize.rs:250-251). */
+uint64_t unifur_nf4_packed_bytes(uint64_t len);
+
+/* PackedNf4Tensor::estimated_resident_bytes (src/quantize.rs:391-399); equal to
+ * resident_bytes() of a tensor of that length (src/quantize.rs:370-376). */
+uint64_t unifur_nf4_estimated_resident_bytes(uint64_t len, int double_quantized);
+
+/* PackedNf4Tensor::bits_per_value (src/quantize.rs:382-388). */
+double unifur_nf4_bits_per_value(uint64_t len, int double_quantized);
+
+/* Nf4Tensor::bits_per_value (src/quantize.rs:190-200), the simulated form. */
+double unifur_nf4_simulated_bits_per_value(uint64_t len, int double_quantized);
+
+/* ---- codec (bit-exact to the reference) ------------------------------------ */
+
+/* PackedNf4Tensor::quantize (src/quantize.rs:262-279), which takes its codes
+ * from Nf4Tensor::quantize (src/quantize.rs:99-124): per block absmax, codes
+ * of v/absmax by the nearest-level scan (src/quantize.rs:208-219), packed.
+ * values[len] -> packed[ceil(len/2)], absmax[ceil(len/64)]. */
+int unifur_nf4_quantize(const float *values, uint64_t len, uint8_t *packed, float *absmax, void *stream);
+
+/* PackedNf4Tensor::with_double_quantization (src/quantize.rs:284-309), same
+ * formula as Nf4Tensor::with_double_quantization (src/quantize.rs:129-149):
+ * absmax[num_blocks] -> dq_codes[num_blocks], *scale_of_scales (device). */
+int unifur_nf4_double_quantize(const float *absmax, uint64_t num_blocks, uint8_t *dq_codes,
+                               float *scale_of_scales, void *stream);
+
+/* PackedNf4Tensor::dequantize (src/quantize.rs:355-366), bit-identical to
+ * Nf4Tensor::dequantize (src/quantize.rs:178-185): out[len] =
+ * NF4_LEVELS[code] * block scale, as f32 (bit-exact) or bf16 (that f32
+ * rounded to nearest even). */
+int unifur_nf4_dequantize(const uint8_t *packed, const unifur_nf4_scales *scales, uint64_t len, void *out,
+                          int out_dtype, void *stream);
+
+/* ---- linear layers ----------------------------------------------------------- */
+
+/* Device workspace bytes unifur_nf4_linear_forward needs for these
+ * arguments.  A caller-provided workspace must be zero-filled before its
+ * first use; every call leaves it ready for the next one. */
+uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
+                                          uint32_t lora_rank);
+
+/* Nf4Linear::forward (src/qwennet.rs:238-241): y = x deq(W) (+ bias), and with
+ * lora != NULL QloraLinear::forward (src/qwennet.rs:325-345): base(x) +
+ * (x a) b * scaling.  x [rows, d_in] (f32 or bf16), y [rows, d_out]
+ * (f32 or bf16), bias [d_out] f32 or NULL.  workspace == NULL selects the
+ * internal workspace cache. */
+int unifur_nf4_linear_forward(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,
+                              const float *bias, const unifur_nf4_lora *lora, void *y, int y_dtype,
+                              void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* QloraLinear::forward (src/qwennet.rs:325-345); identical to
+ * unifur_nf4_linear_forward with a non-NULL lora. */
+int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,
+                             const unifur_nf4_lora *lora, void *y, int y_dtype, void *workspace,
+                             uint64_t workspace_bytes, void *stream);
+
+/* Workspace bytes of unifur_nf4_swiglu_forward (same contract as above). */
+uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype);
+
+/* QwenMlp::forward (src/qwennet.rs:816-819): y = down(silu(gate x) * up x),
+ * silu(z) = z * sigmoid(z) (src/tensor_ext.rs:87-90).  gate and up are
+ * [hidden, intermediate], down is [intermediate, hidden]; x [rows, hidden],
+ * y [rows, hidden]. */
+int unifur_nf4_swiglu_forward(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *gate,
+                              const unifur_nf4_weight *up, const unifur_nf4_weight *down, void *y, int y_dtype,
+                              void *workspace, uint64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* UNIFUR_NF4_H */

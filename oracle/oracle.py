@@ -1,0 +1,235 @@
+"""Python face of the CPU oracle (test infrastructure only).
+
+Loads ``oracle/libnf4_oracle.so`` (the C restatement of unifur's
+``src/quantize.rs`` NF4 codec, built by ``oracle/Makefile``) and adds the
+float64 reference products the GEMV/GEMM/MLP parity tests compare against.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module, as the checker or the timed CPU
+baseline.  The product (``unifur_amd``) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libnf4_oracle.so")
+_lib = None
+
+BLOCK = 64
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+
+
+def build() -> str:
+    """Compile the C restatement with its own Makefile (gcc, no GPU)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.nf4o_levels.argtypes = [_f32p]
+        L.nf4o_nearest_level_code.argtypes = [ctypes.c_float]
+        L.nf4o_nearest_level_code.restype = ctypes.c_uint8
+        for name in ("nf4o_quantize_sim", "nf4o_quantize_packed"):
+            getattr(L, name).argtypes = [_f32p, ctypes.c_size_t, _u8p, _f32p]
+        L.nf4o_double_quantize.argtypes = [_f32p, ctypes.c_size_t, _u8p, _f32p]
+        L.nf4o_dq_scale.argtypes = [ctypes.c_uint8, ctypes.c_float]
+        L.nf4o_dq_scale.restype = ctypes.c_float
+        for name in ("nf4o_dequantize_sim", "nf4o_dequantize_packed"):
+            getattr(L, name).argtypes = [_u8p, ctypes.c_size_t, _f32p, _u8p, ctypes.c_float, _f32p]
+        L.nf4o_estimated_resident_bytes.argtypes = [ctypes.c_size_t, ctypes.c_int]
+        L.nf4o_estimated_resident_bytes.restype = ctypes.c_size_t
+        for name in ("nf4o_bits_per_value_sim", "nf4o_bits_per_value_packed"):
+            getattr(L, name).argtypes = [ctypes.c_size_t, ctypes.c_int]
+            getattr(L, name).restype = ctypes.c_double
+        L.nf4o_transpose.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, _f32p]
+        L.nf4o_silu.argtypes = [ctypes.c_float]
+        L.nf4o_silu.restype = ctypes.c_float
+        L.nf4o_silu_vec.argtypes = [_f32p, ctypes.c_size_t, _f32p]
+        L.nf4o_linear_f32.argtypes = [_f32p, ctypes.c_size_t, _f32p, ctypes.c_size_t,
+                                      ctypes.c_size_t, _f32p, _f32p, ctypes.c_int]
+        L.nf4o_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_double, ctypes.c_size_t, _f32p]
+        L.nf4o_round_bf16.argtypes = [_f32p, ctypes.c_size_t, _f32p]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, t):
+    return a.ctypes.data_as(t)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def num_blocks(n: int) -> int:
+    return (n + BLOCK - 1) // BLOCK
+
+
+# --------------------------------------------------------------- codec ----
+
+def levels() -> np.ndarray:
+    out = np.empty(16, np.float32)
+    lib().nf4o_levels(_p(out, _f32p))
+    return out
+
+
+def nearest_level_code(v: float) -> int:
+    return int(lib().nf4o_nearest_level_code(ctypes.c_float(v)))
+
+
+def quantize_sim(values) -> tuple[np.ndarray, np.ndarray]:
+    """Nf4Tensor::quantize -> (codes u8[n], absmax f32[nb])."""
+    v = _f32(values).ravel()
+    codes = np.empty(v.size, np.uint8)
+    absmax = np.empty(num_blocks(v.size), np.float32)
+    lib().nf4o_quantize_sim(_p(v, _f32p), v.size, _p(codes, _u8p), _p(absmax, _f32p))
+    return codes, absmax
+
+
+def quantize_packed(values) -> tuple[np.ndarray, np.ndarray]:
+    """PackedNf4Tensor::quantize -> (packed u8[ceil(n/2)], absmax f32[nb])."""
+    v = _f32(values).ravel()
+    packed = np.empty((v.size + 1) // 2, np.uint8)
+    absmax = np.empty(num_blocks(v.size), np.float32)
+    lib().nf4o_quantize_packed(_p(v, _f32p), v.size, _p(packed, _u8p), _p(absmax, _f32p))
+    return packed, absmax
+
+
+def double_quantize(absmax) -> tuple[np.ndarray, np.float32]:
+    """with_double_quantization -> (q u8[nb], scale_of_scales f32)."""
+    a = _f32(absmax).ravel()
+    q = np.empty(a.size, np.uint8)
+    sos = np.zeros(1, np.float32)
+    lib().nf4o_double_quantize(_p(a, _f32p), a.size, _p(q, _u8p), _p(sos, _f32p))
+    return q, sos[0]
+
+
+def dq_scale(q: int, sos: float) -> np.float32:
+    return np.float32(lib().nf4o_dq_scale(ctypes.c_uint8(q), ctypes.c_float(sos)))
+
+
+def _dequant(fn, codes, n, absmax, dq_codes, sos):
+    out = np.empty(n, np.float32)
+    a = _f32(absmax if absmax is not None else np.zeros(num_blocks(n), np.float32))
+    dq = None if dq_codes is None else np.ascontiguousarray(dq_codes, np.uint8)
+    fn(_p(codes, _u8p), n, _p(a, _f32p), None if dq is None else _p(dq, _u8p),
+       ctypes.c_float(0.0 if sos is None else float(sos)), _p(out, _f32p))
+    return out
+
+
+def dequantize_sim(codes, absmax=None, dq_codes=None, sos=None) -> np.ndarray:
+    c = np.ascontiguousarray(codes, np.uint8)
+    return _dequant(lib().nf4o_dequantize_sim, c, c.size, absmax, dq_codes, sos)
+
+
+def dequantize_packed(packed, n, absmax=None, dq_codes=None, sos=None) -> np.ndarray:
+    p = np.ascontiguousarray(packed, np.uint8)
+    return _dequant(lib().nf4o_dequantize_packed, p, n, absmax, dq_codes, sos)
+
+
+def estimated_resident_bytes(n: int, dq: bool) -> int:
+    return int(lib().nf4o_estimated_resident_bytes(n, int(dq)))
+
+
+def bits_per_value_sim(n: int, dq: bool) -> float:
+    return float(lib().nf4o_bits_per_value_sim(n, int(dq)))
+
+
+def bits_per_value_packed(n: int, dq: bool) -> float:
+    return float(lib().nf4o_bits_per_value_packed(n, int(dq)))
+
+
+def transpose(data, rows: int, cols: int) -> np.ndarray:
+    d = _f32(data).ravel()
+    out = np.empty(rows * cols, np.float32)
+    lib().nf4o_transpose(_p(d, _f32p), rows, cols, _p(out, _f32p))
+    return out
+
+
+def silu(x) -> np.ndarray:
+    v = _f32(x)
+    out = np.empty_like(v)
+    lib().nf4o_silu_vec(_p(v, _f32p), v.size, _p(out, _f32p))
+    return out
+
+
+def linear_f32(x, w, d_in: int, d_out: int, bias=None, threads: int = 0) -> np.ndarray:
+    """Restated burn linear in f32 (the timed CPU baseline's matmul)."""
+    xv = _f32(x).reshape(-1, d_in)
+    wv = _f32(w).reshape(d_in, d_out)
+    b = None if bias is None else _f32(bias)
+    y = np.empty((xv.shape[0], d_out), np.float32)
+    lib().nf4o_linear_f32(_p(xv, _f32p), xv.shape[0], _p(wv, _f32p), d_in, d_out,
+                          None if b is None else _p(b, _f32p), _p(y, _f32p), int(threads))
+    return y
+
+
+def fill_normal(seed: int, sigma: float, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().nf4o_fill_normal(ctypes.c_uint64(seed), float(sigma), n, _p(out, _f32p))
+    return out
+
+
+def round_bf16(x) -> np.ndarray:
+    v = _f32(x)
+    out = np.empty_like(v)
+    lib().nf4o_round_bf16(_p(v, _f32p), v.size, _p(out, _f32p))
+    return out
+
+
+# ------------------------------------------------- float64 references ----
+
+def linear_ref_f64(x, w_deq, bias=None) -> np.ndarray:
+    """y = x @ W (+ b) in float64 on exactly the inputs the GPU sees."""
+    y = np.asarray(x, np.float64) @ np.asarray(w_deq, np.float64)
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    return y
+
+
+def lora_ref_f64(x, a, b, scaling) -> np.ndarray:
+    """LoraAdapter::forward (src/quantize.rs:619-624): (x @ A) @ B * scaling."""
+    x64 = np.asarray(x, np.float64)
+    return (x64 @ np.asarray(a, np.float64)) @ np.asarray(b, np.float64) * float(scaling)
+
+
+def silu_f64(z):
+    z = np.asarray(z, np.float64)
+    return z / (1.0 + np.exp(-z))
+
+
+def swiglu_ref_f64(x, wg, wu, wd) -> np.ndarray:
+    """QwenMlp::forward (src/qwennet.rs:816-819): down(silu(gate x) * up x)."""
+    x64 = np.asarray(x, np.float64)
+    h = silu_f64(x64 @ np.asarray(wg, np.float64)) * (x64 @ np.asarray(wu, np.float64))
+    return h @ np.asarray(wd, np.float64)
+
+
+def normwise_error(y, ref, x, w_abs_bound) -> float:
+    """max_n |y_n - r_n| / max(sum_k |x_k| |W_kn|, tiny), per output row.
+
+    ``w_abs_bound`` is |x| @ |W| (float64), the scale of the accumulated
+    terms; elementwise relative error is unbounded near zero outputs."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.maximum(np.asarray(w_abs_bound, np.float64), 1e-30)
+    return float(np.max(np.abs(y - ref) / den))
+
+
+def max_rel_error(y, ref) -> float:
+    """BASELINE-literal max|y - r| / max|r|."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-30))

@@ -1,0 +1,77 @@
+"""The C ABI library on a CPU-only host: it loads, exports every symbol that
+include/unifur_nf4.h declares, and its host-only accounting agrees with the
+oracle.  No kernel is launched here."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "unifur_nf4.h")
+
+
+def declared_symbols() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(unifur_nf4_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from unifur_amd import _lib
+    return _lib.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from unifur_amd import _lib
+    syms = declared_symbols()
+    assert len(syms) >= 15
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in unifur_nf4.h but not exported"
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
+
+
+def test_levels_match_oracle(lib, oracle):
+    out = (ctypes.c_float * 16)()
+    assert lib.unifur_nf4_levels(out) == 0
+    assert np.array_equal(np.array(out, np.float32).view(np.uint32), oracle.levels().view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 63, 64, 65, 69, 127, 128, 640, 1000, 4096 * 11008])
+def test_accounting_matches_oracle(lib, oracle, n):
+    assert lib.unifur_nf4_num_blocks(n) == (n + 63) // 64
+    assert lib.unifur_nf4_packed_bytes(n) == (n + 1) // 2
+    for dq in (0, 1):
+        assert lib.unifur_nf4_estimated_resident_bytes(n, dq) == oracle.estimated_resident_bytes(n, dq)
+        assert lib.unifur_nf4_bits_per_value(n, dq) == oracle.bits_per_value_packed(n, dq)
+        assert lib.unifur_nf4_simulated_bits_per_value(n, dq) == oracle.bits_per_value_sim(n, dq)
+
+
+def test_invalid_arguments_fail_before_any_device_work(lib):
+    from unifur_amd import _lib
+    st = lib.unifur_nf4_quantize(None, 10, None, None, None)
+    assert st == _lib.ERR_INVALID and b"NULL" in lib.unifur_nf4_last_error()
+    s = _lib.Scales(7, None, None, None)
+    assert lib.unifur_nf4_dequantize(None, ctypes.byref(s), 10, None, 0, None) == _lib.ERR_INVALID
+    assert b"scales kind" in lib.unifur_nf4_last_error()
+    w = _lib.Weight(None, _lib.Scales(0, None, None, None), 4, 4)
+    assert lib.unifur_nf4_linear_forward(None, 0, 1, ctypes.byref(w), None, None, None, 0, None, 0,
+                                         None) == _lib.ERR_INVALID
+    assert lib.unifur_nf4_linear_forward(None, 5, 1, ctypes.byref(w), None, None, None, 0, None, 0,
+                                         None) == _lib.ERR_INVALID
+    assert lib.unifur_nf4_qlora_forward(None, 0, 1, ctypes.byref(w), None, None, 0, None, 0,
+                                        None) == _lib.ERR_INVALID
+
+
+def test_workspace_sizes_are_consistent(lib):
+    # GEMV path: counters + split-K partials; generic path: an f32 weight copy
+    small = lib.unifur_nf4_linear_workspace_size(1, 4096, 11008, 0, 0)
+    assert 0 < small < 4096 * 11008 * 4
+    generic = lib.unifur_nf4_linear_workspace_size(1, 100, 70, 0, 0)
+    assert generic >= 100 * 70 * 4
+    assert lib.unifur_nf4_linear_workspace_size(0, 10, 10, 0, 0) == 0
+    assert lib.unifur_nf4_swiglu_workspace_size(1, 4096, 11008, 1) >= 11008 * 4

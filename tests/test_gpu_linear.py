@@ -1,0 +1,150 @@
+"""GPU parity of the NF4 linear path (GEMV, generic GEMM, QLoRA, SwiGLU).
+
+The reference value is the float64 product of the same inputs with the
+oracle's dequantized weight (bit-identical to the reference's dequantized
+f32 weight).  Tolerances, from BASELINE.json's north star:
+  * f32 activations / f32 output: normwise error <= 1e-5 and
+    max|y - r| / max|r| <= 1e-5;
+  * bf16 activations or bf16 output: both <= 1e-2.
+Normwise error is max_n |y_n - r_n| / sum_k |x_k| |W_kn| (elementwise
+relative error is unbounded near zero outputs).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from unifur_amd import quantize as Q
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16 = 1e-2
+
+
+def make_linear(oracle, d_in, d_out, seed, device, dq=True, sigma=0.02):
+    """Nf4Linear from seeded [d_in, d_out] values; returns (layer, W_deq f32)."""
+    v = oracle.fill_normal(seed, sigma, d_in * d_out)
+    packed, absmax = oracle.quantize_packed(v)
+    if dq:
+        q, sos = oracle.double_quantize(absmax)
+        wdeq = oracle.dequantize_packed(packed, v.size, None, q, sos)
+    else:
+        wdeq = oracle.dequantize_packed(packed, v.size, absmax)
+    p = Q.PackedNf4Tensor.quantize(torch.from_numpy(v).to(device))
+    if dq:
+        p = p.with_double_quantization()
+    assert np.array_equal(p.codes.cpu().numpy(), packed)
+    return Q.Nf4Linear.from_packed(p, d_in, d_out), wdeq.reshape(d_in, d_out)
+
+
+def check(y, ref, x, wdeq, tol, tag):
+    y = y.float().cpu().numpy().reshape(ref.shape)
+    bound = np.abs(np.asarray(x, np.float64)) @ np.abs(np.asarray(wdeq, np.float64))
+    from oracle import oracle as O
+    nw = O.normwise_error(y, ref, x, bound)
+    lit = O.max_rel_error(y, ref)
+    print(f"{tag}: normwise {nw:.3e} literal {lit:.3e}", flush=True)
+    assert nw <= tol and lit <= tol, f"{tag}: normwise {nw:.3e}, literal {lit:.3e} > {tol}"
+
+
+def acts(oracle, rows, d_in, seed, dtype, device):
+    x = oracle.fill_normal(seed, 1.0, rows * d_in).reshape(rows, d_in)
+    if dtype == torch.bfloat16:
+        x = oracle.round_bf16(x).reshape(rows, d_in)
+    return x, torch.from_numpy(x).to(device).to(dtype)
+
+
+def test_orientation_known_answer(device, oracle):
+    # src/qwennet.rs:2196-2211: W [[1,2,3],[4,5,6]] as [in=2, out=3], x = [1, -1]
+    v = np.arange(1, 7, dtype=np.float32)
+    lin = Q.Nf4Linear.from_values(torch.from_numpy(v).to(device), 2, 3)
+    w = lin.dequantized_weight().cpu().numpy().astype(np.float64)
+    y = lin.forward(torch.tensor([[1.0, -1.0]], device=device)).cpu().numpy()
+    assert np.allclose(y, [w[0] - w[1]], rtol=0, atol=1e-6)
+    # the dequantized weight keeps each row's largest value exact (absmax endpoint)
+    assert w[1, 2] == pytest.approx(6.0, abs=6 * 2 / 255)
+
+
+@pytest.mark.parametrize("dq", [True, False])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_gemv_config2_4096_to_11008(device, oracle, dq, x_dtype):
+    # x[1, 4096] ~ N(0,1), W logical 11008x4096 stored [4096, 11008]
+    lin, wdeq = make_linear(oracle, 4096, 11008, 0x4E463457 + 1, device, dq=dq)
+    x, xt = acts(oracle, 1, 4096, 0x58 + 1, x_dtype, device)
+    ref = oracle.linear_ref_f64(x, wdeq)
+    y = lin.forward(xt, out_dtype=torch.float32)
+    tol = TOL_F32 if x_dtype == torch.float32 else TOL_BF16
+    check(y, ref, x, wdeq, tol, f"gemv dq={dq} x={x_dtype}")
+    yb = lin.forward(xt, out_dtype=torch.bfloat16)
+    check(yb, ref, x, wdeq, TOL_BF16, f"gemv bf16-out dq={dq}")
+    # deterministic: the split-K reduction runs in a fixed order
+    assert torch.equal(lin.forward(xt, out_dtype=torch.float32), y)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4])
+@pytest.mark.parametrize("shape", [(896, 4864), (4864, 896), (896, 128), (256, 64), (4096, 4096)])
+def test_gemv_rows_and_shapes(device, oracle, rows, shape):
+    d_in, d_out = shape
+    lin, wdeq = make_linear(oracle, d_in, d_out, 11 + d_in + d_out, device)
+    x, xt = acts(oracle, rows, d_in, 5 + rows, torch.float32, device)
+    check(lin.forward(xt), oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_F32, f"gemv rows={rows} {shape}")
+
+
+def test_gemv_bias_and_qlora(device, oracle):
+    d_in, d_out, r = 4096, 4096, 16
+    lin, wdeq = make_linear(oracle, d_in, d_out, 21, device, dq=True)
+    bias = oracle.fill_normal(22, 0.1, d_out)
+    lin.bias = torch.from_numpy(bias).to(device)
+    x, xt = acts(oracle, 2, d_in, 23, torch.float32, device)
+    ref = oracle.linear_ref_f64(x, wdeq, bias)
+    check(lin.forward(xt), ref, x, wdeq, TOL_F32, "gemv bias")
+    a = oracle.fill_normal(0x41, 0.01, d_in * r).reshape(d_in, r)
+    b = oracle.fill_normal(0x42, 0.01, r * d_out).reshape(r, d_out)
+    ad = Q.LoraAdapter.from_parts(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device), 2.0)
+    ql = Q.QloraLinear(lin, ad)
+    ref_l = ref + oracle.lora_ref_f64(x, a, b, 2.0)
+    check(ql.forward(xt), ref_l, x, wdeq, TOL_F32, "gemv qlora")
+    # a fresh adapter (B = 0) is an exact no-op (src/quantize.rs:1059-1081)
+    fresh = Q.LoraAdapter.new(Q.LoraConfig.new(d_in, d_out, r), device=device)
+    assert torch.equal(Q.QloraLinear(lin, fresh).forward(xt), lin.forward(xt))
+
+
+@pytest.mark.parametrize("shape,rows,dt", [((8, 6), 4, torch.float32), ((100, 70), 1, torch.float32),
+                                          ((96, 130), 5, torch.bfloat16), ((256, 512), 9, torch.float32),
+                                          ((4096, 4096), 16, torch.float32)])
+def test_generic_path_dequantize_then_matmul(device, oracle, shape, rows, dt):
+    # d_out not a multiple of 64, or f32 activations with more than 4 rows:
+    # the reference's own dequantize + f32 matmul sequence.
+    d_in, d_out = shape
+    lin, wdeq = make_linear(oracle, d_in, d_out, 31 + d_in, device, dq=True, sigma=1.0)
+    x, xt = acts(oracle, rows, d_in, 33, dt, device)
+    tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+    check(lin.forward(xt, out_dtype=torch.float32), oracle.linear_ref_f64(x, wdeq), x, wdeq, tol,
+          f"generic {shape} rows={rows}")
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 7])
+def test_swiglu_small(device, oracle, rows):
+    hidden, inter = 256, 512
+    g, wg = make_linear(oracle, hidden, inter, 41, device)
+    u, wu = make_linear(oracle, hidden, inter, 42, device)
+    d, wd = make_linear(oracle, inter, hidden, 43, device)
+    mlp = Q.QwenMlp(g, u, d)
+    x, xt = acts(oracle, rows, hidden, 44, torch.float32, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    check(mlp.forward(xt), ref, h, wd, TOL_F32, f"swiglu rows={rows}")
+
+
+def test_swiglu_config4_t1(device, oracle):
+    # BASELINE config 4 at T = 1: hidden 4096, intermediate 11008, bf16 x
+    g, wg = make_linear(oracle, 4096, 11008, 0x4E463457 + 4, device)
+    u, wu = make_linear(oracle, 4096, 11008, 0x4E463457 + 5, device)
+    d, wd = make_linear(oracle, 11008, 4096, 0x4E463457 + 6, device)
+    x, xt = acts(oracle, 1, 4096, 0x58 + 4, torch.bfloat16, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    y = Q.QwenMlp(g, u, d).forward(xt, out_dtype=torch.float32)
+    check(y, ref, h, wd, TOL_BF16, "swiglu config4 T=1")

@@ -1,0 +1,283 @@
+// nf4_codec.hip -- blockwise absmax NF4 quantize / double-quantize / dequantize.
+//
+// Bit-exact restatement of src/quantize.rs:99-124 (quantize), :129-149 and
+// :284-309 (double quantization), :169-185 and :329-366 (dequantize) as
+// gfx950 kernels.  Every f32 operation that the reference performs is
+// performed here with the same operands in the same order (IEEE RN, no
+// contraction), so codes, bytes, absmax, DQ codes and dequantized f32 values
+// equal the reference's.
+#include "nf4_codec.hpp"
+
+#pragma clang fp contract(off)
+
+namespace unifur {
+namespace {
+
+// Exact decision thresholds of nearest_level_code (src/quantize.rs:208-219):
+// for u in [-1, 1], scan(u) == #{t : u >= T[t]}.  Each T[t] is the smallest
+// f32 at which the strict-< scan over f32 distances first returns code t+1;
+// nine of them sit one ulp away from the f32 midpoint of adjacent levels.
+__constant__ uint32_t kThresholdBits[15] = {
+    0xbf591cd8u, 0xbf1c5270u, 0xbeeb847fu, 0xbeadea76u, 0xbe703cecu,
+    0xbe0d38bbu, 0xbd3a7870u, 0x3d22fb00u, 0x3df64863u, 0x3e5067e1u,
+    0x3e9582d5u, 0x3ec753fau, 0x3f006d04u, 0x3f248db0u, 0x3f5c89dau};
+
+// Bucket table over floor(16 u) in [-16, 16]: no two thresholds are closer
+// than 1/16, so bucket j holds at most one threshold.  Entry j stores
+// {count of thresholds <= j/16, the threshold inside the bucket or 2.0f}.
+struct BucketEntry {
+  float t_in;
+  uint32_t base;
+};
+
+__device__ __forceinline__ void build_bucket_table(BucketEntry* tab) {
+  for (int j = threadIdx.x; j < 33; j += blockDim.x) {
+    float lo = (float)(j - 16) * 0.0625f;
+    float hi = lo + 0.0625f;
+    uint32_t base = 0;
+    float t_in = 2.0f;
+    for (int t = 0; t < 15; ++t) {
+      float T = __uint_as_float(kThresholdBits[t]);
+      if (T <= lo) base++;
+      else if (T < hi) t_in = T;
+    }
+    tab[j] = BucketEntry{t_in, base};
+  }
+}
+
+// scan(u) for u = v / absmax in [-1, 1] or NaN.  u * 16 is exact (power of
+// two).  fmaxf/fminf are IEEE maxNum/minNum, so a NaN u clamps to bucket 0,
+// whose base is 0 and whose compare is false: NaN -> code 0, as the scan.
+__device__ __forceinline__ uint32_t code_of(float u, const BucketEntry* tab) {
+  float s = fminf(fmaxf(__builtin_floorf(u * 16.0f), -16.0f), 16.0f);
+  BucketEntry e = tab[(int)s + 16];
+  return e.base + (u >= e.t_in ? 1u : 0u);
+}
+
+// ---------------------------------------------------------------- quantize --
+// One wave covers 16 blocks (1024 values, 4 KiB) per step.  Load instruction
+// q of lane l reads float4 #(q*64 + l) of the wave's span, so every load is a
+// contiguous 1 KiB across the wave and block (q*4 + l/16) lives in the 16
+// consecutive lanes of one instruction: absmax is a 16-lane max reduction.
+constexpr int kQuantWaves = 4;  // waves per workgroup
+constexpr int kQuantThreads = kQuantWaves * 64;
+
+__device__ __forceinline__ float max16(float v) {
+  // NaN never reaches here (inputs pass through fabs + fmax with 0 start),
+  // so the order of the butterfly does not matter.
+  v = fmaxf(v, __shfl_xor(v, 1, 16));
+  v = fmaxf(v, __shfl_xor(v, 2, 16));
+  v = fmaxf(v, __shfl_xor(v, 4, 16));
+  v = fmaxf(v, __shfl_xor(v, 8, 16));
+  return v;
+}
+
+__global__ __launch_bounds__(kQuantThreads) void quantize_full_kernel(
+    const float* __restrict__ values, uint8_t* __restrict__ packed, float* __restrict__ absmax,
+    size_t n_full_spans) {
+  __shared__ BucketEntry tab[33];
+  build_bucket_table(tab);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const size_t wave = (size_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  const size_t nwaves = (size_t)gridDim.x * kQuantWaves;
+  for (size_t span = wave; span < n_full_spans; span += nwaves) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(values) + span * 256;
+    f32x4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = __builtin_nontemporal_load(src + q * 64 + lane);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // absmax = fold(0, max(acc, |v|)) (src/quantize.rs:103); fmaxf is
+      // IEEE maxNum, so NaN inputs are ignored exactly as Rust's f32::max.
+      float m = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v[q].x)), fmaxf(fabsf(v[q].y), fabsf(v[q].z))),
+                      fabsf(v[q].w));
+      m = max16(m);
+      uint32_t nib = 0;
+      if (m == 0.0f) {
+        nib = 0x7777u;  // all-zero block -> scan(0) = 7 (src/quantize.rs:108-110)
+      } else {
+        nib = code_of(v[q].x / m, tab) | (code_of(v[q].y / m, tab) << 4) |
+              (code_of(v[q].z / m, tab) << 8) | (code_of(v[q].w / m, tab) << 12);
+      }
+      const size_t f4 = span * 256 + q * 64 + lane;  // float4 index == u16 index of packed
+      reinterpret_cast<uint16_t*>(packed)[f4] = (uint16_t)nib;
+      if ((lane & 15) == 0) absmax[f4 / 16] = m;
+    }
+  }
+}
+
+// Tail (fewer than 1024 values): one thread per block, scalar, any n.
+__global__ void quantize_tail_kernel(const float* __restrict__ values, uint8_t* __restrict__ packed,
+                                     float* __restrict__ absmax, size_t first_block, size_t n) {
+  __shared__ BucketEntry tab[33];
+  build_bucket_table(tab);
+  __syncthreads();
+  size_t b = first_block + (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t start = b * kBlock;
+  if (start >= n) return;
+  size_t end = start + kBlock < n ? start + kBlock : n;
+  float m = 0.0f;
+  for (size_t i = start; i < end; ++i) m = fmaxf(m, fabsf(values[i]));
+  for (size_t i = start; i < end; i += 2) {
+    uint32_t lo = m == 0.0f ? 7u : code_of(values[i] / m, tab);
+    uint32_t hi = 0;
+    if (i + 1 < end) hi = m == 0.0f ? 7u : code_of(values[i + 1] / m, tab);
+    packed[i / 2] = (uint8_t)(lo | (hi << 4));
+  }
+  absmax[b] = m;
+}
+
+// ------------------------------------------------------- double quantize --
+// Pass 1: max over the f32 absmax values.  All are >= 0 and never NaN (they
+// come out of a NaN-ignoring max from 0), so their bit patterns order like
+// the values and an integer atomic max is exact.  Pass 2 encodes.
+__global__ void dq_max_kernel(const float* __restrict__ absmax, size_t nb, uint32_t* __restrict__ max_bits) {
+  float m = 0.0f;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nb; i += (size_t)gridDim.x * blockDim.x)
+    m = fmaxf(m, absmax[i]);
+  m = fmaxf(m, __shfl_xor(m, 1));
+  m = fmaxf(m, __shfl_xor(m, 2));
+  m = fmaxf(m, __shfl_xor(m, 4));
+  m = fmaxf(m, __shfl_xor(m, 8));
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+  if ((threadIdx.x & 63) == 0) atomicMax(max_bits, __float_as_uint(m));
+}
+
+__global__ void dq_encode_kernel(const float* __restrict__ absmax, size_t nb, const uint32_t* __restrict__ max_bits,
+                                 uint8_t* __restrict__ q) {
+  const float M = __uint_as_float(*max_bits);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nb; i += (size_t)gridDim.x * blockDim.x) {
+    uint8_t c = 0;
+    if (M != 0.0f) {
+      // (s / max_scale * 255.0).round().clamp(0.0, 255.0) as u8
+      float r = roundf((absmax[i] / M) * 255.0f);  // half away from zero
+      c = (r == r) ? (uint8_t)fminf(fmaxf(r, 0.0f), 255.0f) : (uint8_t)0;
+    }
+    q[i] = c;
+  }
+}
+
+// -------------------------------------------------------------- dequantize --
+// LUT in LDS: byte b -> {level[b & 15], level[b >> 4]}.  The DQ scale is
+// ((float)q / 255.0f) * sos, evaluated per block exactly as the reference.
+__device__ __forceinline__ void build_byte_lut(f32x2* lut) {
+  for (int b = threadIdx.x; b < 256; b += blockDim.x) lut[b] = f32x2{level(b & 15), level(b >> 4)};
+}
+
+__device__ __forceinline__ float block_scale(const ScalesArg& s, size_t blk) {
+  if (s.kind == kScalesF32) return s.absmax[blk];
+  return ((float)s.dq_codes[blk] / 255.0f) * (*s.scale_of_scales);
+}
+
+// Each thread expands 8 codes (4 bytes, one u32) per step; one block of 64
+// values is 8 threads.  Lanes read consecutive u32 (256 B per wave load).
+template <bool kBf16Out>
+__global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* __restrict__ packed, ScalesArg scales,
+                                                         size_t n8, void* __restrict__ out) {
+  __shared__ f32x2 lut[256];
+  build_byte_lut(lut);
+  __syncthreads();
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(packed);
+  for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < n8; g += (size_t)gridDim.x * blockDim.x) {
+    uint32_t w = __builtin_nontemporal_load(src + g);
+    float s = block_scale(scales, g / 8);
+    f32x2 p0 = lut[w & 0xff], p1 = lut[(w >> 8) & 0xff], p2 = lut[(w >> 16) & 0xff], p3 = lut[w >> 24];
+    // out = NF4_LEVELS[c] * scale: one f32 multiply, as src/quantize.rs:362
+    float o0 = p0.x * s, o1 = p0.y * s, o2 = p1.x * s, o3 = p1.y * s;
+    float o4 = p2.x * s, o5 = p2.y * s, o6 = p3.x * s, o7 = p3.y * s;
+    if constexpr (kBf16Out) {
+      u32x4 r = {pack_bf16x2(o0, o1), pack_bf16x2(o2, o3), pack_bf16x2(o4, o5), pack_bf16x2(o6, o7)};
+      __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(out) + g);
+    } else {
+      f32x4* d = reinterpret_cast<f32x4*>(out) + 2 * g;
+      __builtin_nontemporal_store(f32x4{o0, o1, o2, o3}, d);
+      __builtin_nontemporal_store(f32x4{o4, o5, o6, o7}, d + 1);
+    }
+  }
+}
+
+// Tail: values [first, n), one thread per value.
+template <bool kBf16Out>
+__global__ void dequantize_tail_kernel(const uint8_t* __restrict__ packed, ScalesArg scales, size_t first, size_t n,
+                                       void* __restrict__ out) {
+  size_t i = first + (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint8_t byte = packed[i / 2];
+  uint32_t c = (i & 1) ? (byte >> 4) : (byte & 15);
+  float o = level(c) * block_scale(scales, i / kBlock);
+  if constexpr (kBf16Out) {
+    reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)(pack_bf16x2(o, 0.0f) & 0xffffu);
+  } else {
+    reinterpret_cast<float*>(out)[i] = o;
+  }
+}
+
+int grid_for(size_t work_items, int threads, int max_blocks) {
+  size_t g = (work_items + threads - 1) / threads;
+  if (g > (size_t)max_blocks) g = max_blocks;
+  return g < 1 ? 1 : (int)g;
+}
+
+}  // namespace
+
+hipError_t launch_quantize(const float* values, size_t n, uint8_t* packed, float* absmax, bool aligned,
+                           hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  // full 16-block spans take the vector kernel (needs 16-byte aligned values
+  // and 2-byte aligned codes); the rest, or everything if misaligned, the
+  // scalar one.
+  const size_t spans = aligned ? n / 1024 : 0;
+  if (spans) {
+    int grid = grid_for(spans, kQuantWaves, 8192);
+    quantize_full_kernel<<<grid, kQuantThreads, 0, stream>>>(values, packed, absmax, spans);
+  }
+  const size_t first_block = spans * 16;
+  const size_t nb = (n + kBlock - 1) / kBlock;
+  if (first_block < nb) {
+    size_t tail_blocks = nb - first_block;
+    quantize_tail_kernel<<<(unsigned)((tail_blocks + 63) / 64), 64, 0, stream>>>(values, packed, absmax,
+                                                                              first_block, n);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_double_quantize(const float* absmax, size_t nb, uint8_t* q, float* scale_of_scales,
+                                  hipStream_t stream) {
+  // The scale of scales is the max itself, so its own storage is the
+  // accumulator of the integer atomic max (non-negative f32 bits order as u32).
+  uint32_t* max_bits = reinterpret_cast<uint32_t*>(scale_of_scales);
+  hipError_t e = hipMemsetAsync(max_bits, 0, sizeof(uint32_t), stream);
+  if (e != hipSuccess) return e;
+  if (nb == 0) return hipSuccess;
+  dq_max_kernel<<<grid_for(nb, 256, 1024), 256, 0, stream>>>(absmax, nb, max_bits);
+  dq_encode_kernel<<<grid_for(nb, 256, 4096), 256, 0, stream>>>(absmax, nb, max_bits, q);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, size_t n, void* out, bool bf16_out,
+                             bool aligned, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  // groups of 8 values take the vector kernel (4-byte aligned codes, 16-byte
+  // aligned output); the remainder, or everything if misaligned, the scalar one.
+  const size_t n8 = aligned ? n / 8 : 0;
+  if (n8) {
+    int grid = grid_for(n8, 256, 16384);
+    if (bf16_out)
+      dequantize_kernel<true><<<grid, 256, 0, stream>>>(packed, scales, n8, out);
+    else
+      dequantize_kernel<false><<<grid, 256, 0, stream>>>(packed, scales, n8, out);
+  }
+  const size_t first = n8 * 8;
+  if (first < n) {
+    unsigned g = (unsigned)((n - first + 63) / 64);
+    if (bf16_out)
+      dequantize_tail_kernel<true><<<g, 64, 0, stream>>>(packed, scales, first, n, out);
+    else
+      dequantize_tail_kernel<false><<<g, 64, 0, stream>>>(packed, scales, first, n, out);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace unifur

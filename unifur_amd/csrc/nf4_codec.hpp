@@ -1,0 +1,25 @@
+// nf4_codec.hpp -- internal launcher declarations shared by the C-ABI layer.
+#pragma once
+
+#include "nf4_common.hpp"
+
+namespace unifur {
+
+enum : int { kScalesF32 = 0, kScalesDQ = 1 };
+
+// Per-block scales as the kernels receive them (device pointers).
+struct ScalesArg {
+  int kind;                      // kScalesF32 or kScalesDQ
+  const float* absmax;           // kScalesF32: one f32 per block
+  const uint8_t* dq_codes;       // kScalesDQ: one u8 per block
+  const float* scale_of_scales;  // kScalesDQ: one f32 (device)
+};
+
+hipError_t launch_quantize(const float* values, size_t n, uint8_t* packed, float* absmax, bool aligned,
+                           hipStream_t stream);
+hipError_t launch_double_quantize(const float* absmax, size_t nb, uint8_t* q, float* scale_of_scales,
+                                  hipStream_t stream);
+hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, size_t n, void* out, bool bf16_out,
+                             bool aligned, hipStream_t stream);
+
+}  // namespace unifur

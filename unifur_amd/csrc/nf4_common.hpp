@@ -1,0 +1,54 @@
+// nf4_common.hpp -- shared device-side definitions for the NF4 kernels.
+//
+// Layout facts every kernel relies on (they are the reference's, see
+// src/quantize.rs:36-66 and :240-247):
+//   * a tensor of n values is cut into ceil(n/64) blocks of 64 consecutive
+//     values (the last block may be short);
+//   * codes are packed two per byte, value 2i in the low nibble of byte i;
+//   * a block's scale is its f32 absmax, or with double quantization
+//     ((float)q / 255.0f) * scale_of_scales.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace unifur {
+
+constexpr int kBlock = 64;
+
+// NF4_LEVELS (src/quantize.rs:49-66) as the f32 bit patterns the decimal
+// literals round to; identical to the reference's table bit for bit.
+__host__ __device__ constexpr uint32_t level_bits(int c) {
+  constexpr uint32_t bits[16] = {
+      0xbf800000u, 0xbf3239b1u, 0xbf066b30u, 0xbeca32a0u, 0xbe91a24du, 0xbe3d353fu,
+      0xbdba7871u, 0x00000000u, 0x3da2faffu, 0x3e24cae3u, 0x3e7c04ddu, 0x3ead033au,
+      0x3ee1a4b8u, 0x3f1007abu, 0x3f3913b3u, 0x3f800000u};
+  return bits[c];
+}
+
+__device__ __forceinline__ float level(int c) { return __uint_as_float(level_bits(c)); }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// Two f32 -> packed bf16x2, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  bf16x2 r = __builtin_convertvector(v, bf16x2);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+// v_perm_b32: result byte i = byte sel[i] of the 8-byte value {a:b}
+// (bytes 0-3 come from b, 4-7 from a, selector 0x0c yields 0x00).
+__device__ __forceinline__ uint32_t perm_b32(uint32_t a, uint32_t b, uint32_t sel) {
+  return __builtin_amdgcn_perm(a, b, sel);
+}
+
+}  // namespace unifur

@@ -1,0 +1,47 @@
+// nf4_gemv.hpp -- internal interface of the decode GEMV (few input rows).
+#pragma once
+
+#include "nf4_codec.hpp"
+
+namespace unifur {
+
+constexpr int kMaxGemvWeights = 3;
+
+// One NF4 weight [d_in, d_out] of a (possibly batched) GEMV launch.
+struct GemvWeight {
+  const uint8_t* packed;  // ceil(d_in * d_out / 2) bytes
+  ScalesArg scales;
+  int d_out;
+  void* y;  // [rows, d_out] f32 or bf16
+  int y_bf16;
+  const float* bias;     // [d_out] or null
+  const float* lora_xa;  // [rows, lora_rank] = x A, or null
+  const float* lora_b;   // [lora_rank, d_out]
+  int lora_rank;
+  float lora_scaling;
+  unsigned* counters;  // workspace: one zeroed u32 per 256-column tile
+  float* partials;     // workspace: splits * rows * d_out floats (split-K)
+};
+
+struct GemvPlan {
+  bool pair;  // gate/up SwiGLU pair: weights[0], weights[1] share x and d_out
+  int rows_per_thread;
+  int rows_per_wg;
+  int splits;
+  int tiles;
+  int counter_count[kMaxGemvWeights];
+  size_t partial_count[kMaxGemvWeights];
+};
+
+constexpr int kGemvMaxRows = 4;      // activation rows handled by the GEMV path
+constexpr int kGemvPairMaxRows = 2;  // ... and by its SwiGLU gate/up pair mode
+
+// Plan a launch over nweights weights sharing x [rows, d_in]; with pair, the
+// two weights are gate and up of a SwiGLU block and weights[0].y receives
+// silu(gate x) * (up x).
+GemvPlan plan_gemv(int rows, int d_in, const int* d_out, int nweights, bool pair);
+
+hipError_t launch_gemv(const GemvPlan& p, const void* x, bool x_bf16, int rows, int d_in, const GemvWeight* weights,
+                       int nweights, hipStream_t stream);
+
+}  // namespace unifur

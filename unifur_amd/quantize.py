@@ -1,0 +1,384 @@
+"""Host-side mirror of unifur's NF4 API over the MI355X library.
+
+Names, argument meaning and error behaviour follow the reference's Rust
+types so that code written against them reads the same:
+
+=====================================  ==========================================
+this module                            reference (s-b-repo/unifur)
+=====================================  ==========================================
+``BLOCK_SIZE``, ``nf4_levels()``       ``BLOCK_SIZE``, ``NF4_LEVELS`` (src/quantize.rs:37, :49-66)
+``PackedNf4Tensor``                    ``PackedNf4Tensor`` (src/quantize.rs:249-400)
+``Nf4Tensor``                          ``Nf4Tensor`` (src/quantize.rs:79-201)
+``quantize_dequantize_tensor``         ``quantize_dequantize_tensor`` (src/quantize.rs:404-416)
+``LoraConfig``, ``LoraAdapter``        ``LoraConfig``, ``LoraAdapter`` (src/quantize.rs:513-635)
+``Nf4Linear``                          ``Nf4Linear`` (src/qwennet.rs:161-242)
+``QloraLinear``                        ``QloraLinear`` (src/qwennet.rs:311-345)
+``QwenMlp``                            ``QwenMlp`` (src/qwennet.rs:786-820)
+=====================================  ==========================================
+
+Device memory and streams come from PyTorch (tensors on ``cuda``); every
+computation is a call into ``libunifur_nf4.so``.  There is no CPU or torch
+fallback: without the built library, or without a GPU, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+
+BLOCK_SIZE = L.BLOCK_SIZE
+
+
+def nf4_levels() -> list[float]:
+    """NF4_LEVELS as the library holds them (src/quantize.rs:49-66)."""
+    out = (ctypes.c_float * 16)()
+    L.check(L.lib().unifur_nf4_levels(out))
+    return list(out)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return L.F32
+    if dtype == torch.bfloat16:
+        return L.BF16
+    raise ValueError(f"unsupported dtype {dtype}; the NF4 path takes float32 or bfloat16")
+
+
+def _require_cuda(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA (HIP) device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+class PackedNf4Tensor:
+    """Packed NF4 storage: two codes per byte, low nibble first, per-block
+    f32 absmax or double-quantized u8 scales (src/quantize.rs:235-257)."""
+
+    def __init__(self, codes: torch.Tensor, length: int, absmax: Optional[torch.Tensor] = None,
+                 dq_codes: Optional[torch.Tensor] = None, scale_of_scales: Optional[torch.Tensor] = None):
+        self.codes = codes
+        self._len = int(length)
+        self.absmax = absmax
+        self.dq_codes = dq_codes
+        self.scale_of_scales = scale_of_scales  # 1-element f32 device tensor
+
+    # -- construction -------------------------------------------------------------
+    @staticmethod
+    def quantize(values: torch.Tensor) -> "PackedNf4Tensor":
+        """PackedNf4Tensor::quantize (src/quantize.rs:262-279) on a flat f32 view."""
+        _require_cuda(values, "values")
+        if values.dtype != torch.float32:
+            raise ValueError("quantize takes float32 values, as the reference's &[f32]")
+        n = values.numel()
+        nb = (n + BLOCK_SIZE - 1) // BLOCK_SIZE
+        codes = torch.empty((n + 1) // 2, dtype=torch.uint8, device=values.device)
+        absmax = torch.empty(nb, dtype=torch.float32, device=values.device)
+        L.check(L.lib().unifur_nf4_quantize(values.data_ptr(), n, codes.data_ptr(), absmax.data_ptr(), _stream()))
+        return PackedNf4Tensor(codes, n, absmax=absmax)
+
+    def with_double_quantization(self) -> "PackedNf4Tensor":
+        """src/quantize.rs:284-309; idempotent."""
+        if self.is_double_quantized():
+            return self
+        nb = self.num_blocks()
+        dq = torch.empty(nb, dtype=torch.uint8, device=self.codes.device)
+        sos = torch.empty(1, dtype=torch.float32, device=self.codes.device)
+        L.check(L.lib().unifur_nf4_double_quantize(self.absmax.data_ptr(), nb, dq.data_ptr(), sos.data_ptr(),
+                                                   _stream()))
+        return PackedNf4Tensor(self.codes, self._len, dq_codes=dq, scale_of_scales=sos)
+
+    # -- accessors -------------------------------------------------------------------
+    def is_double_quantized(self) -> bool:
+        return self.dq_codes is not None
+
+    def __len__(self) -> int:
+        return self._len
+
+    def len(self) -> int:
+        return self._len
+
+    def is_empty(self) -> bool:
+        return self._len == 0
+
+    def num_blocks(self) -> int:
+        return int(L.lib().unifur_nf4_num_blocks(self._len))
+
+    def scales_struct(self) -> L.Scales:
+        if self.is_double_quantized():
+            return L.Scales(L.SCALES_DOUBLE_QUANTIZED, None, self.dq_codes.data_ptr(),
+                            self.scale_of_scales.data_ptr())
+        return L.Scales(L.SCALES_F32, self.absmax.data_ptr(), None, None)
+
+    def dequantize(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """src/quantize.rs:355-366: f32 bit-identical to the reference, or bf16
+        (that f32 rounded to nearest even)."""
+        out = torch.empty(self._len, dtype=dtype, device=self.codes.device)
+        s = self.scales_struct()
+        L.check(L.lib().unifur_nf4_dequantize(self.codes.data_ptr(), ctypes.byref(s), self._len, out.data_ptr(),
+                                              _dtype_code(dtype), _stream()))
+        return out
+
+    def resident_bytes(self) -> int:
+        """src/quantize.rs:370-376."""
+        return PackedNf4Tensor.estimated_resident_bytes(self._len, self.is_double_quantized())
+
+    def bits_per_value(self) -> float:
+        """src/quantize.rs:382-388."""
+        return float(L.lib().unifur_nf4_bits_per_value(self._len, int(self.is_double_quantized())))
+
+    @staticmethod
+    def estimated_resident_bytes(length: int, double_quantized: bool) -> int:
+        """src/quantize.rs:391-399."""
+        return int(L.lib().unifur_nf4_estimated_resident_bytes(length, int(double_quantized)))
+
+
+class Nf4Tensor:
+    """The reference's simulated form (one code per byte, src/quantize.rs:79-201).
+
+    It is numerically identical to the packed form (src/quantize.rs:240-247),
+    so it is held packed on the device; only its accounting differs."""
+
+    def __init__(self, packed: PackedNf4Tensor):
+        self._packed = packed
+
+    @staticmethod
+    def quantize(values: torch.Tensor) -> "Nf4Tensor":
+        return Nf4Tensor(PackedNf4Tensor.quantize(values))
+
+    def with_double_quantization(self) -> "Nf4Tensor":
+        return Nf4Tensor(self._packed.with_double_quantization())
+
+    def is_double_quantized(self) -> bool:
+        return self._packed.is_double_quantized()
+
+    def len(self) -> int:
+        return len(self._packed)
+
+    def __len__(self) -> int:
+        return len(self._packed)
+
+    def is_empty(self) -> bool:
+        return self._packed.is_empty()
+
+    def num_blocks(self) -> int:
+        return self._packed.num_blocks()
+
+    def dequantize(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        return self._packed.dequantize(dtype)
+
+    def bits_per_value(self) -> float:
+        """src/quantize.rs:190-200: quotes a 4-bit payload it does not pack."""
+        return float(L.lib().unifur_nf4_simulated_bits_per_value(len(self._packed),
+                                                                 int(self.is_double_quantized())))
+
+    def packed(self) -> PackedNf4Tensor:
+        return self._packed
+
+
+def quantize_dequantize_tensor(tensor: torch.Tensor, double_quantization: bool) -> torch.Tensor:
+    """src/quantize.rs:404-416: the NF4 round trip of a rank-2 tensor, on its
+    flat row-major buffer."""
+    if tensor.dim() != 2:
+        raise ValueError("quantize_dequantize_tensor takes a rank-2 tensor")
+    q = PackedNf4Tensor.quantize(tensor.contiguous().view(-1))
+    if double_quantization:
+        q = q.with_double_quantization()
+    return q.dequantize().view(tensor.shape)
+
+
+# ---------------------------------------------------------------------- LoRA --
+
+@dataclass
+class LoraConfig:
+    """src/quantize.rs:513-548."""
+    in_features: int
+    out_features: int
+    rank: int
+    alpha: float
+
+    @staticmethod
+    def new(in_features: int, out_features: int, rank: int) -> "LoraConfig":
+        r = max(rank, 1)
+        return LoraConfig(in_features, out_features, r, float(r))
+
+    def with_alpha(self, alpha: float) -> "LoraConfig":
+        return LoraConfig(self.in_features, self.out_features, self.rank, float(alpha))
+
+    def scaling(self) -> float:
+        return self.alpha / max(self.rank, 1)
+
+    def num_parameters(self) -> int:
+        return self.rank * (self.in_features + self.out_features)
+
+
+class LoraAdapter:
+    """src/quantize.rs:550-635: a [in, rank], b [rank, out] (f32), scaling."""
+
+    def __init__(self, a: torch.Tensor, b: torch.Tensor, scaling: float):
+        _require_cuda(a, "lora a")
+        _require_cuda(b, "lora b")
+        if a.dtype != torch.float32 or b.dtype != torch.float32:
+            raise ValueError("LoRA factors are float32, as the reference's")
+        if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[0]:
+            raise ValueError(f"LoRA factor shapes {tuple(a.shape)} and {tuple(b.shape)} do not chain")
+        self.a = a
+        self.b = b
+        self._scaling = float(scaling)
+
+    @staticmethod
+    def new(config: LoraConfig, device="cuda", generator: Optional[torch.Generator] = None) -> "LoraAdapter":
+        """A ~ N(0, 1/rank), B = 0: an exact no-op until trained."""
+        std = 1.0 / math.sqrt(max(config.rank, 1))
+        a = torch.randn(config.in_features, config.rank, generator=generator, dtype=torch.float32) * std
+        b = torch.zeros(config.rank, config.out_features, dtype=torch.float32)
+        return LoraAdapter(a.to(device), b.to(device), config.scaling())
+
+    @staticmethod
+    def from_parts(a: torch.Tensor, b: torch.Tensor, scaling: float) -> "LoraAdapter":
+        return LoraAdapter(a.contiguous(), b.contiguous(), scaling)
+
+    def in_features(self) -> int:
+        return self.a.shape[0]
+
+    def out_features(self) -> int:
+        return self.b.shape[1]
+
+    def rank(self) -> int:
+        return self.a.shape[1]
+
+    def scaling(self) -> float:
+        return self._scaling
+
+    def struct(self) -> L.Lora:
+        return L.Lora(self.a.data_ptr(), self.b.data_ptr(), self.rank(), self._scaling)
+
+
+# ------------------------------------------------------------------- linears --
+
+def _weight_struct(packed: PackedNf4Tensor, d_in: int, d_out: int) -> L.Weight:
+    return L.Weight(packed.codes.data_ptr(), packed.scales_struct(), d_in, d_out)
+
+
+class Nf4Linear:
+    """A frozen NF4-resident linear with weight [d_input, d_output]
+    (src/qwennet.rs:161-242); forward never materialises the weight."""
+
+    def __init__(self, packed: PackedNf4Tensor, d_input: int, d_output: int, bias: Optional[torch.Tensor] = None):
+        if len(packed) != d_input * d_output:
+            raise ValueError(f"packed weight holds {len(packed)} values, [{d_input}, {d_output}] needs "
+                             f"{d_input * d_output}")
+        if bias is not None:
+            _require_cuda(bias, "bias")
+            if bias.dtype != torch.float32 or bias.numel() != d_output:
+                raise ValueError("bias must be float32 [d_output]")
+        self._packed = packed
+        self._d_in = int(d_input)
+        self._d_out = int(d_output)
+        self.bias = bias
+
+    @staticmethod
+    def from_packed(packed: PackedNf4Tensor, d_input: int, d_output: int,
+                    bias: Optional[torch.Tensor] = None) -> "Nf4Linear":
+        return Nf4Linear(packed, d_input, d_output, bias)
+
+    @staticmethod
+    def from_values(values: torch.Tensor, d_input: int, d_output: int) -> "Nf4Linear":
+        """src/qwennet.rs:198-205: quantize [d_input, d_output] row-major values,
+        always with double quantization."""
+        return Nf4Linear(PackedNf4Tensor.quantize(values.contiguous().view(-1)).with_double_quantization(),
+                         d_input, d_output)
+
+    def d_input(self) -> int:
+        return self._d_in
+
+    def d_output(self) -> int:
+        return self._d_out
+
+    def resident_bytes(self) -> int:
+        return self._packed.resident_bytes()
+
+    def packed(self) -> PackedNf4Tensor:
+        return self._packed
+
+    def dequantized_weight(self) -> torch.Tensor:
+        """src/qwennet.rs:230-236."""
+        return self._packed.dequantize().view(self._d_in, self._d_out)
+
+    def weight_struct(self) -> L.Weight:
+        return _weight_struct(self._packed, self._d_in, self._d_out)
+
+    def _forward(self, x: torch.Tensor, lora: Optional[LoraAdapter], out_dtype: Optional[torch.dtype]):
+        _require_cuda(x, "x")
+        if x.shape[-1] != self._d_in:
+            raise ValueError(f"x has last dim {x.shape[-1]}, the layer takes {self._d_in}")
+        rows = x.numel() // self._d_in
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(*x.shape[:-1], self._d_out, dtype=out_dtype, device=x.device)
+        w = self.weight_struct()
+        lo = lora.struct() if lora is not None else None
+        L.check(L.lib().unifur_nf4_linear_forward(
+            x.data_ptr(), _dtype_code(x.dtype), rows, ctypes.byref(w),
+            self.bias.data_ptr() if self.bias is not None else None,
+            ctypes.byref(lo) if lo is not None else None,
+            y.data_ptr(), _dtype_code(out_dtype), None, 0, _stream()))
+        return y
+
+    def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """src/qwennet.rs:238-241: y = x W (+ bias) over the last dim of x."""
+        return self._forward(x, None, out_dtype)
+
+    __call__ = forward
+
+
+class QloraLinear:
+    """Frozen packed NF4 base plus a LoRA adapter (src/qwennet.rs:311-345):
+    forward(x) = base(x) + (x a) b * scaling, fused into one launch chain."""
+
+    def __init__(self, base: Nf4Linear, adapter: LoraAdapter):
+        if adapter.in_features() != base.d_input() or adapter.out_features() != base.d_output():
+            raise ValueError("adapter shape does not match the base layer")
+        self.base = base
+        self.adapter = adapter
+
+    def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        return self.base._forward(x, self.adapter, out_dtype)
+
+    __call__ = forward
+
+
+class QwenMlp:
+    """down(silu(gate(x)) * up(x)) with three bias-free NF4 linears
+    (src/qwennet.rs:786-820)."""
+
+    def __init__(self, gate_proj: Nf4Linear, up_proj: Nf4Linear, down_proj: Nf4Linear):
+        hidden, inter = gate_proj.d_input(), gate_proj.d_output()
+        if (up_proj.d_input(), up_proj.d_output()) != (hidden, inter) or \
+                (down_proj.d_input(), down_proj.d_output()) != (inter, hidden):
+            raise ValueError("gate/up must be [hidden, intermediate] and down [intermediate, hidden]")
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+
+    def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        _require_cuda(x, "x")
+        hidden = self.gate_proj.d_input()
+        if x.shape[-1] != hidden:
+            raise ValueError(f"x has last dim {x.shape[-1]}, the block takes {hidden}")
+        rows = x.numel() // hidden
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(*x.shape[:-1], hidden, dtype=out_dtype, device=x.device)
+        g, u, d = (self.gate_proj.weight_struct(), self.up_proj.weight_struct(), self.down_proj.weight_struct())
+        L.check(L.lib().unifur_nf4_swiglu_forward(
+            x.data_ptr(), _dtype_code(x.dtype), rows, ctypes.byref(g), ctypes.byref(u), ctypes.byref(d),
+            y.data_ptr(), _dtype_code(out_dtype), None, 0, _stream()))
+        return y
+
+    __call__ = forward
