@@ -74,4 +74,6 @@ def test_workspace_sizes_are_consistent(lib):
     generic = lib.unifur_nf4_linear_workspace_size(1, 100, 70, 0, 0)
     assert generic >= 100 * 70 * 4
     assert lib.unifur_nf4_linear_workspace_size(0, 10, 10, 0, 0) == 0
+    # every non-empty plan starts with the 64 KiB counter region
+    assert lib.unifur_nf4_linear_workspace_size(1, 64, 64, 0, 0) >= 65536
     assert lib.unifur_nf4_swiglu_workspace_size(1, 4096, 11008, 1) >= 11008 * 4

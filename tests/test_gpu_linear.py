@@ -148,3 +148,27 @@ def test_swiglu_config4_t1(device, oracle):
     h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
     y = Q.QwenMlp(g, u, d).forward(xt, out_dtype=torch.float32)
     check(y, ref, h, wd, TOL_BF16, "swiglu config4 T=1")
+
+
+def test_workspace_shared_by_generic_then_gemv_calls(device, oracle):
+    # A generic-path call writes an f32 weight copy into the workspace; the
+    # GEMV's split-K arrival counters live in a region nothing else touches,
+    # so a later GEMV on the same workspace is still correct.
+    from unifur_amd import _lib as L
+    import ctypes
+    small, wsmall = make_linear(oracle, 64, 70, 51, device, sigma=1.0)    # generic (70 % 64 != 0)
+    big, wbig = make_linear(oracle, 4096, 4096, 52, device)               # GEMV, split-K
+    need = max(L.lib().unifur_nf4_linear_workspace_size(1, 64, 70, 0, 0),
+               L.lib().unifur_nf4_linear_workspace_size(1, 4096, 4096, 0, 0))
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    xs, xst = acts(oracle, 1, 64, 53, torch.float32, device)
+    xb, xbt = acts(oracle, 1, 4096, 54, torch.float32, device)
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        for lin, xt, x, wd in ((small, xst, xs, wsmall), (big, xbt, xb, wbig)):
+            y = torch.empty(1, lin.d_output(), device=device)
+            w = lin.weight_struct()
+            L.check(L.lib().unifur_nf4_linear_forward(xt.data_ptr(), L.F32, 1, ctypes.byref(w), None, None,
+                                                      y.data_ptr(), L.F32, ws.data_ptr(), need, stream))
+            check(y, oracle.linear_ref_f64(x, wd), x, wd, TOL_F32, f"shared ws {lin.d_output()}")
+    assert int(ws[:65536].count_nonzero()) == 0, "counter region must be left zeroed"

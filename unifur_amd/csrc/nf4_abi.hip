@@ -125,9 +125,16 @@ int resolve_workspace(void* user, uint64_t user_bytes, size_t need, hipStream_t 
   return internal_workspace(need, stream, out);
 }
 
+// Every workspace starts with a fixed region of split-K arrival counters.
+// Only the GEMV's last-arrival logic writes it and it always leaves it zero,
+// so it stays valid across calls of any shape and path; every other region
+// (partials, dequantized weights, intermediates) is scratch carved after it.
+constexpr size_t kCounterRegion = 64 << 10;
+constexpr int kMaxCounters = (int)(kCounterRegion / sizeof(unsigned));
+
 // Carves consecutive 256-byte-aligned regions out of one workspace.
 struct Carver {
-  size_t off = 0;
+  size_t off = kCounterRegion;
   size_t take(size_t bytes) {
     size_t o = off;
     off += align_up(bytes);
@@ -139,10 +146,11 @@ struct Carver {
 
 enum class LinearPath { kGemv, kGeneric };
 
-// The fused GEMV needs whole 64-blocks per weight row (d_out % 64 == 0) and
-// 16-byte aligned code rows; every other shape takes the generic path.
-bool gemv_layout_ok(uint64_t d_out, const void* packed) {
-  return d_out % 64 == 0 && (reinterpret_cast<uintptr_t>(packed) & 15u) == 0;
+// The fused GEMV needs whole 64-blocks per weight row (d_out % 64 == 0),
+// 16-byte aligned code rows and a weight that 32-bit buffer offsets reach
+// (under 2 GiB of codes, 4 G values); every other shape takes the generic path.
+bool gemv_layout_ok(uint64_t d_in, uint64_t d_out, const void* packed) {
+  return d_out % 64 == 0 && (reinterpret_cast<uintptr_t>(packed) & 15u) == 0 && d_in * d_out / 2 < (1ull << 31);
 }
 
 struct LinearLayout {
@@ -154,12 +162,13 @@ struct LinearLayout {
 LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t lora_rank, const void* packed) {
   LinearLayout L{};
   Carver c;
-  const bool gemv = rows <= (uint64_t)kGemvMaxRows && gemv_layout_ok(d_out, packed);
+  const bool gemv = rows <= (uint64_t)kGemvMaxRows && gemv_layout_ok(d_in, d_out, packed) &&
+                    ceil_div_u64(d_out, 256) <= (uint64_t)kMaxCounters;
   if (gemv) {
     L.path = LinearPath::kGemv;
     const int n = (int)d_out;
     L.gemv = plan_gemv((int)rows, (int)d_in, &n, 1, false);
-    L.counters = c.take((size_t)L.gemv.counter_count[0] * sizeof(unsigned));
+    L.counters = 0;
     L.partials = c.take(L.gemv.partial_count[0] * sizeof(float));
   } else {
     L.path = LinearPath::kGeneric;
@@ -238,15 +247,16 @@ struct MlpLayout {
 MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const void* pg, const void* pu, const void* pd) {
   MlpLayout L{};
   Carver c;
-  const bool layout = gemv_layout_ok(inter, pg) && gemv_layout_ok(inter, pu) && gemv_layout_ok(hidden, pd);
+  const bool layout = gemv_layout_ok(hidden, inter, pg) && gemv_layout_ok(hidden, inter, pu) &&
+                      gemv_layout_ok(inter, hidden, pd) &&
+                      ceil_div_u64(std::max(inter, hidden), 256) <= (uint64_t)kMaxCounters;
   if (layout && rows <= (uint64_t)kGemvMaxRows) {
     L.path = rows <= (uint64_t)kGemvPairMaxRows ? MlpPath::kPairGemv : MlpPath::kGemv;
     const int gi[2] = {(int)inter, (int)inter};
     const int hd = (int)hidden;
     L.up_plan = plan_gemv((int)rows, (int)hidden, gi, 2, L.path == MlpPath::kPairGemv);
     L.down_plan = plan_gemv((int)rows, (int)inter, &hd, 1, false);
-    const size_t ncount = std::max(L.up_plan.counter_count[0], L.down_plan.counter_count[0]);
-    L.counters = c.take(ncount * sizeof(unsigned));
+    L.counters = 0;
     L.partials0 = c.take(std::max(L.up_plan.partial_count[0], L.down_plan.partial_count[0]) * sizeof(float));
     L.partials1 = c.take(L.up_plan.partial_count[1] * sizeof(float));
     L.h = c.take((size_t)rows * inter * sizeof(float));
@@ -395,8 +405,8 @@ int unifur_nf4_double_quantize(const float* absmax, uint64_t num_blocks, uint8_t
 int unifur_nf4_dequantize(const uint8_t* packed, const unifur_nf4_scales* scales, uint64_t len, void* out,
                           int out_dtype, void* stream) {
   UNIFUR_ARG(valid_dtype(out_dtype), "out_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  if (len == 0) return UNIFUR_NF4_OK;  // an empty tensor holds no scales to validate
   if (int r = check_scales(scales)) return r;
-  if (len == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(packed && out, "packed or out is NULL");
   const bool aligned = (reinterpret_cast<uintptr_t>(packed) & 3u) == 0 &&
                        (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
