@@ -1,0 +1,127 @@
+"""GPU parity of the MFMA prefill GEMM (bf16 activations, more than four
+rows): NF4 weight dequantized into LDS as bf16, f32 accumulation, fused bias
+and scaled LoRA epilogue.
+
+The reference value is the float64 product of the same (bf16-valued) inputs
+with the oracle's dequantized weight, which is bit-identical to the
+reference's dequantized f32 weight (src/quantize.rs:355-366).  The bf16
+tolerance of BASELINE.json's north star applies: normwise error and
+max|y - r| / max|r| both <= 1e-2.  Rounding the dequantized weight to bf16
+bounds the normwise error by 2^-9 plus accumulation error, so a dropped term,
+a wrong scale or a transposed tile fails it by orders of magnitude.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from unifur_amd import _lib as L
+from unifur_amd import quantize as Q
+
+from test_gpu_linear import TOL_BF16, acts, check, make_linear
+
+pytestmark = pytest.mark.gpu
+
+
+def lora_parts(oracle, d_in, d_out, r, seed, device, scaling=2.0):
+    a = oracle.fill_normal(seed, 0.02, d_in * r).reshape(d_in, r)
+    b = oracle.fill_normal(seed + 1, 0.02, r * d_out).reshape(r, d_out)
+    ad = Q.LoraAdapter.from_parts(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device), scaling)
+    return a, b, ad
+
+
+def test_config3_prefill_qlora(device, oracle):
+    # X bf16 [2048, 4096], W NF4 4096 -> 4096 with double
+    # quantization, LoRA r = 16, scale 2, bf16 output.
+    M, K, N, r = 2048, 4096, 4096, 16
+    lin, wdeq = make_linear(oracle, K, N, 0x4E463457 + 3, device, dq=True)
+    x, xt = acts(oracle, M, K, 0x58 + 3, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 0x41 + 3, device)
+    ql = Q.QloraLinear(lin, ad)
+    ref = oracle.linear_ref_f64(x, wdeq) + oracle.lora_ref_f64(x, a, b, 2.0)
+    y = ql.forward(xt, out_dtype=torch.bfloat16)
+    assert y.dtype == torch.bfloat16 and y.shape == (M, N)
+    check(y, ref, x, wdeq, TOL_BF16, "mfma config3 qlora bf16-out")
+    yf = ql.forward(xt, out_dtype=torch.float32)
+    check(yf, ref, x, wdeq, TOL_BF16, "mfma config3 qlora f32-out")
+    # deterministic: no atomics, fixed accumulation order
+    assert torch.equal(ql.forward(xt, out_dtype=torch.float32), yf)
+
+
+@pytest.mark.parametrize("M", [5, 64, 127, 128, 129, 300])
+@pytest.mark.parametrize("dq", [True, False])
+def test_ragged_rows_and_scale_kinds(device, oracle, M, dq):
+    K, N = 512, 384
+    lin, wdeq = make_linear(oracle, K, N, 100 + M, device, dq=dq)
+    x, xt = acts(oracle, M, K, 200 + M, torch.bfloat16, device)
+    ref = oracle.linear_ref_f64(x, wdeq)
+    check(lin.forward(xt, out_dtype=torch.float32), ref, x, wdeq, TOL_BF16, f"mfma M={M} dq={dq}")
+
+
+@pytest.mark.parametrize("shape", [(896, 4864), (4864, 896), (896, 128), (64, 128), (11008, 4096)])
+def test_qwen_and_edge_shapes(device, oracle, shape):
+    K, N = shape
+    M = 32
+    lin, wdeq = make_linear(oracle, K, N, 300 + K + N, device)
+    x, xt = acts(oracle, M, K, 301, torch.bfloat16, device)
+    check(lin.forward(xt, out_dtype=torch.bfloat16), oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_BF16,
+          f"mfma {shape}")
+
+
+@pytest.mark.parametrize("r", [1, 8, 16, 40, 64])
+def test_bias_and_lora_ranks(device, oracle, r):
+    M, K, N = 200, 1024, 512
+    lin, wdeq = make_linear(oracle, K, N, 400 + r, device)
+    bias = oracle.fill_normal(401, 0.1, N)
+    lin.bias = torch.from_numpy(bias).to(device)
+    x, xt = acts(oracle, M, K, 402, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 403 + r, device, scaling=16.0 / r)
+    ref = oracle.linear_ref_f64(x, wdeq, bias) + oracle.lora_ref_f64(x, a, b, 16.0 / r)
+    check(Q.QloraLinear(lin, ad).forward(xt, out_dtype=torch.float32), ref, x, wdeq, TOL_BF16,
+          f"mfma bias+lora r={r}")
+    # a fresh adapter (B = 0) adds exactly nothing (src/quantize.rs:1059-1081)
+    fresh = Q.LoraAdapter.new(Q.LoraConfig.new(K, N, r), device=device)
+    assert torch.equal(Q.QloraLinear(lin, fresh).forward(xt), lin.forward(xt))
+
+
+def test_misaligned_activations_take_the_generic_path(device, oracle):
+    # X not 16-byte aligned: the generic dequantize + f32 matmul serves it,
+    # with the same result to the bf16 tolerance.
+    M, K, N = 16, 256, 128
+    lin, wdeq = make_linear(oracle, K, N, 500, device)
+    x, _ = acts(oracle, M, K, 501, torch.bfloat16, device)
+    buf = torch.zeros(M * K + 1, dtype=torch.bfloat16, device=device)
+    buf[1:] = torch.from_numpy(x.reshape(-1)).to(torch.bfloat16)
+    xv = buf[1:].view(M, K)
+    assert xv.data_ptr() % 16 != 0
+    y = torch.empty(M, N, device=device)
+    w = lin.weight_struct()
+    stream = torch.cuda.current_stream().cuda_stream
+    L.check(L.lib().unifur_nf4_linear_forward(xv.data_ptr(), L.BF16, M, ctypes.byref(w), None, None, y.data_ptr(),
+                                              L.F32, None, 0, stream))
+    check(y, oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_BF16, "misaligned x")
+    aligned = lin.forward(torch.from_numpy(x).to(device).to(torch.bfloat16), out_dtype=torch.float32)
+    check(aligned, oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_BF16, "aligned x")
+
+
+def test_workspace_for_mfma_lora_is_small(device, oracle):
+    # the MFMA path needs only the LoRA xa buffer beyond the counter region
+    need = L.lib().unifur_nf4_linear_workspace_size(2048, 4096, 4096, L.BF16, 16)
+    assert need <= 65536 + 2048 * 16 * 4 + 256
+    M, K, N, r = 256, 512, 256, 16
+    lin, wdeq = make_linear(oracle, K, N, 600, device)
+    x, xt = acts(oracle, M, K, 601, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 602, device)
+    need = L.lib().unifur_nf4_linear_workspace_size(M, K, N, L.BF16, r)
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    y = torch.empty(M, N, device=device)
+    w, lo = lin.weight_struct(), ad.struct()
+    stream = torch.cuda.current_stream().cuda_stream
+    L.check(L.lib().unifur_nf4_qlora_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w), ctypes.byref(lo),
+                                             y.data_ptr(), L.F32, ws.data_ptr(), need, stream))
+    ref = oracle.linear_ref_f64(x, wdeq) + oracle.lora_ref_f64(x, a, b, 2.0)
+    check(y, ref, x, wdeq, TOL_BF16, "mfma user workspace")
+    assert int(ws[:65536].count_nonzero()) == 0

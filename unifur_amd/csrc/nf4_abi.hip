@@ -14,6 +14,7 @@
 
 #include "../../include/unifur_nf4.h"
 #include "nf4_codec.hpp"
+#include "nf4_gemm.hpp"
 #include "nf4_generic.hpp"
 #include "nf4_gemv.hpp"
 
@@ -144,7 +145,7 @@ struct Carver {
 
 // ------------------------------------------------------------- linear plans --
 
-enum class LinearPath { kGemv, kGeneric };
+enum class LinearPath { kGemv, kMfma, kGeneric };
 
 // The fused GEMV needs whole 64-blocks per weight row (d_out % 64 == 0),
 // 16-byte aligned code rows and a weight that 32-bit buffer offsets reach
@@ -159,22 +160,31 @@ struct LinearLayout {
   size_t counters, partials, xa, wf32, total;
 };
 
-LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t lora_rank, const void* packed) {
+// Decode-sized batches (<= 4 rows) take the fused GEMV; larger bf16 batches
+// the MFMA GEMM; everything else the generic dequantize + f32 matmul.
+LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t lora_rank, const void* packed,
+                         int x_dtype, const void* x) {
   LinearLayout L{};
   Carver c;
   const bool gemv = rows <= (uint64_t)kGemvMaxRows && gemv_layout_ok(d_in, d_out, packed) &&
                     ceil_div_u64(d_out, 256) <= (uint64_t)kMaxCounters;
+  const bool mfma = !gemv && x_dtype == UNIFUR_NF4_BF16 && gemv_layout_ok(d_in, d_out, packed) &&
+                    rows <= 0x7fffffffu && d_in <= 0x7fffffffu && d_out <= 0x7fffffffu &&
+                    gemm_supported((int)rows, (int)d_in, (int)d_out, x);
   if (gemv) {
     L.path = LinearPath::kGemv;
     const int n = (int)d_out;
     L.gemv = plan_gemv((int)rows, (int)d_in, &n, 1, false);
     L.counters = 0;
     L.partials = c.take(L.gemv.partial_count[0] * sizeof(float));
+  } else if (mfma) {
+    L.path = LinearPath::kMfma;
   } else {
     L.path = LinearPath::kGeneric;
     L.wf32 = c.take((size_t)d_in * d_out * sizeof(float));
   }
-  L.xa = c.take((size_t)rows * lora_rank * sizeof(float));
+  const uint64_t xa_cols = L.path == LinearPath::kMfma && lora_rank ? (uint64_t)lora_pad((int)lora_rank) : lora_rank;
+  L.xa = c.take((size_t)rows * xa_cols * sizeof(float));
   L.total = c.off;
   return L;
 }
@@ -197,11 +207,21 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     UNIFUR_ARG(lora->a != nullptr && lora->b != nullptr, "lora factors are NULL");
     UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
   }
-  const LinearLayout L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed);
+  const LinearLayout L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x);
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool xbf = x_dtype == UNIFUR_NF4_BF16;
   float* xa = nullptr;
+  if (L.path == LinearPath::kMfma) {
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    if (lora) {
+      xa = at<float>(ws, L.xa);
+      UNIFUR_HIP(launch_lora_xa_bf16(xb, lora->a, (int)rows, (int)w->d_in, (int)rank, lora->scaling, xa, stream));
+    }
+    UNIFUR_HIP(launch_gemm(xb, w->packed, to_scales(w->scales), (int)rows, (int)w->d_in, (int)w->d_out, bias, xa,
+                           lora ? lora->b : nullptr, (int)rank, y, y_dtype == UNIFUR_NF4_BF16, stream));
+    return UNIFUR_NF4_OK;
+  }
   if (lora) {
     xa = at<float>(ws, L.xa);
     UNIFUR_HIP(launch_lora_xa(x, xbf, lora->a, (int)rows, (int)w->d_in, (int)rank, xa, stream));
@@ -417,10 +437,12 @@ int unifur_nf4_dequantize(const uint8_t* packed, const unifur_nf4_scales* scales
 
 uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
                                           uint32_t lora_rank) {
-  (void)x_dtype;
   if (rows == 0 || d_in == 0 || d_out == 0) return 0;
-  // sized for 16-byte-aligned packed codes, as hipMalloc returns them
-  return plan_linear(rows, d_in, d_out, lora_rank, reinterpret_cast<const void*>(uintptr_t{256})).total;
+  // sized for 16-byte-aligned buffers, as hipMalloc returns them; a call
+  // with misaligned buffers may take the generic path, which needs more and
+  // reports UNIFUR_NF4_ERR_WORKSPACE with the size when given less
+  const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
+  return plan_linear(rows, d_in, d_out, lora_rank, aligned, x_dtype, aligned).total;
 }
 
 int unifur_nf4_linear_forward(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w,
