@@ -157,7 +157,7 @@ bool gemv_layout_ok(uint64_t d_in, uint64_t d_out, const void* packed) {
 struct LinearLayout {
   LinearPath path;
   GemvPlan gemv;
-  size_t counters, partials, xa, wf32, total;
+  size_t counters, partials, xa, xa_part, wf32, total;
 };
 
 // Decode-sized batches (<= 4 rows) take the fused GEMV; larger bf16 batches
@@ -185,6 +185,8 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
   }
   const uint64_t xa_cols = L.path == LinearPath::kMfma && lora_rank ? (uint64_t)lora_pad((int)lora_rank) : lora_rank;
   L.xa = c.take((size_t)rows * xa_cols * sizeof(float));
+  if (L.path == LinearPath::kMfma && lora_rank)
+    L.xa_part = c.take(lora_xa_partial_floats((int)rows, (int)d_in, (int)lora_rank) * sizeof(float));
   L.total = c.off;
   return L;
 }
@@ -216,7 +218,8 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     const uint16_t* xb = static_cast<const uint16_t*>(x);
     if (lora) {
       xa = at<float>(ws, L.xa);
-      UNIFUR_HIP(launch_lora_xa_bf16(xb, lora->a, (int)rows, (int)w->d_in, (int)rank, lora->scaling, xa, stream));
+      UNIFUR_HIP(launch_lora_xa_bf16(xb, lora->a, (int)rows, (int)w->d_in, (int)rank, lora->scaling,
+                                     at<float>(ws, L.xa_part), xa, stream));
     }
     UNIFUR_HIP(launch_gemm(xb, w->packed, to_scales(w->scales), (int)rows, (int)w->d_in, (int)w->d_out, bias, xa,
                            lora ? lora->b : nullptr, (int)rank, y, y_dtype == UNIFUR_NF4_BF16, stream));

@@ -8,31 +8,36 @@
 // NF4_LEVELS[c] * scale is the reference's f32 value (src/quantize.rs:362),
 // rounded to bf16 for the MFMA; products accumulate in f32.
 //
-// Tiling.  A 256-thread workgroup (4 waves, 2 x 2) computes a 128 x 128
-// output tile; each wave owns 64 x 64 (2 x 2 MFMA 32x32x16 tiles, f32
-// accumulators).  K advances in steps of 64 through double-buffered LDS:
-// while the MFMAs consume step k, the global loads of step k + 1 (X rows and
-// NF4 codes + scales) are in flight; afterwards the X tile is written to LDS
-// and the codes are expanded (byte LUT -> level pair, x block scale, -> bf16)
-// into the B tile, stored [n][k] so that each MFMA operand fetch is one
-// 16-byte ds_read.  Both tiles use a 16-byte-chunk XOR swizzle,
-// chunk ^ ((row % 8) ^ (row / 8 % 8)), which makes the operand reads (8
-// consecutive rows, one chunk) and the tile writes conflict-free.
+// Tiling.  A 512-thread workgroup computes a 256 x 128 output tile, K in
+// steps of 64.  It is warp-specialised: four MFMA waves (one per SIMD) each
+// own 64 rows x 128 columns (2 x 4 MFMA 32x32x16 tiles, f32 accumulators)
+// and only read LDS and issue MFMAs; four producer waves (one per SIMD
+// beside an MFMA wave) copy X into LDS with coalesced buffer_load ... lds
+// copies (three stages, two steps ahead) and expand the NF4 codes (byte LUT
+// -> level pair, x block scale, -> bf16) into a double-buffered W tile
+// stored [n][k], so that every MFMA operand fetch is one 16-byte ds_read.
+// Their VALU / LDS / memory work overlaps the MFMAs on the same SIMD; one
+// workgroup barrier per step hands the buffers over.  Both tiles use a
+// 16-byte-chunk XOR swizzle, chunk ^ ((row % 8) ^ (row / 8 % 8)), which
+// makes the operand reads (8 consecutive rows, one chunk) conflict-free.
 #include "nf4_gemm.hpp"
 
+#include <algorithm>
 #include <atomic>
 
 namespace unifur {
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kGemmThreads = 256;
-constexpr int kTileBytes = kBM * kBK * 2;               // one bf16 tile (A or B): 16 KiB
-constexpr int kLdsA = 0;                                // 2 buffers
-constexpr int kLdsB = 2 * kTileBytes;                   // 2 buffers
-constexpr int kLdsLut = 4 * kTileBytes;                 // byte LUT, 256 x f32x2
-constexpr int kLdsDq = kLdsLut + 256 * 8;               // DQ scale LUT, 256 x f32
-constexpr size_t kGemmSmem = kLdsDq + 256 * 4;          // 67 KiB: two workgroups per CU
+constexpr int kBM = 256, kBN = 128, kBK = 64;
+constexpr int kGemmThreads = 512;  // 4 MFMA waves + 4 producer waves
+constexpr int kBTileBytes = kBN * kBK * 2;       // dequantized bf16 W tile: 16 KiB
+constexpr int kATileBytes = kBM * kBK * 2;       // X tile: 32 KiB (8 KiB per wave)
+constexpr int kAStages = 3;
+constexpr int kLdsA = 0;                         // kAStages buffers
+constexpr int kLdsB = kAStages * kATileBytes;    // 2 buffers
+constexpr int kLdsLut = kLdsB + 2 * kBTileBytes; // byte LUT, 256 x f32x2
+constexpr int kLdsDq = kLdsLut + 256 * 8;        // DQ scale LUT, 256 x f32
+constexpr size_t kGemmSmem = kLdsDq + 256 * 4;   // 131 KiB: one workgroup per CU
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -61,56 +66,56 @@ __device__ __forceinline__ uint32_t lds_addr(int base, int row, int chunk) {
   return (uint32_t)(base + row * (kBK * 2) + swz(row, chunk) * 16);
 }
 
-// Global-memory operands of one K step, held in registers between the loads
-// and the LDS writes.
-template <bool DQ>
-struct StepLoads {
-  u32x4 a[4];        // X: rows t/8 + 32 p, 16-byte chunk t % 8
-  uint32_t code[4];  // W: rows 4 (t / 16) + i, bytes of columns 8 (t % 16) .. + 7
+// X tile of one K step, copied by each wave for its own 64 rows straight
+// from global memory into its LDS region (buffer_load ... lds): 8 coalesced
+// 1 KiB copies of 8 rows x 128 bytes.  Lane l of copy p writes LDS slot l,
+// i.e. row 8 p + l / 8, physical chunk l % 8, so it fetches the logical chunk
+// that the swizzle puts there.  Rows past M read as zero (buffer bound).
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void load_a(__amdgpu_buffer_rsrc_t xr, int K, int row0, int k0, int abase, int lane) {
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int r = 8 * p + (lane >> 3);
+    const int c = swz(r, lane & 7);  // swz is an involution on the chunk index
+    const uint32_t off = ((uint32_t)(row0 + r) * (uint32_t)K + (uint32_t)(k0 + 8 * c)) * 2u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(size_t)(abase + p * 1024), 16, off, 0, 0, 0);
+  }
+}
+
+// NF4 codes and block scales of one K step: thread t covers rows 4 (t / 16)
+// .. + 3 and columns 8 (t % 16) .. + 7 of the 64 x 128 W tile.
+struct BStep {
+  uint32_t code[4];
   uint32_t scale[4];
 };
 
 template <bool DQ>
-__device__ __forceinline__ void load_step(StepLoads<DQ>& L, const GemmArgs& g, int m0, int n0, int k0, int tid) {
-  // X tile: 128 rows x 64 k; rows past M read as zero (buffer bound).
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(g.x), (short)0, (int)((uint32_t)g.M * (uint32_t)g.K * 2u), 0x00020000);
-  const int ar = tid >> 3, ach = tid & 7;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const uint32_t off = ((uint32_t)(m0 + ar + 32 * p) * (uint32_t)g.K + (uint32_t)(k0 + ach * 8)) * 2u;
-    L.a[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
-  }
-  // W codes: 64 rows x 128 columns = 64 bytes per row.
+__device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int k0, int tid) {
   const int c = tid & 15, g4 = tid >> 4;
   const uint32_t row_bytes = (uint32_t)g.N / 2;
   const uint32_t bpr = (uint32_t)g.N / kBlock;
   const uint8_t* cp = g.packed + (size_t)(k0 + 4 * g4) * row_bytes + (n0 + 8 * c) / 2;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) L.code[i] = *reinterpret_cast<const uint32_t*>(cp + (size_t)i * row_bytes);
+  for (int i = 0; i < 4; ++i) B.code[i] = *reinterpret_cast<const uint32_t*>(cp + (size_t)i * row_bytes);
   const size_t blk = (size_t)(k0 + 4 * g4) * bpr + (n0 + 8 * c) / kBlock;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if constexpr (DQ)
-      L.scale[i] = g.scales.dq_codes[blk + (size_t)i * bpr];
+      B.scale[i] = g.scales.dq_codes[blk + (size_t)i * bpr];
     else
-      L.scale[i] = __float_as_uint(g.scales.absmax[blk + (size_t)i * bpr]);
+      B.scale[i] = __float_as_uint(g.scales.absmax[blk + (size_t)i * bpr]);
   }
 }
 
-// X registers -> LDS A tile; codes -> dequantized bf16 B tile [n][k].
+// Codes -> dequantized bf16 W tile [n][k] in LDS buffer buf.
 template <bool DQ>
-__device__ __forceinline__ void store_step(const StepLoads<DQ>& L, unsigned char* smem, int buf, int tid) {
-  const int ar = tid >> 3, ach = tid & 7;
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-    *reinterpret_cast<lds_u32x4*>((size_t)lds_addr(kLdsA + buf * kTileBytes, ar + 32 * p, ach)) = L.a[p];
-
+__device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int tid) {
   const int c = tid & 15, g4 = tid >> 4;
   const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq);
   float s[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) s[i] = DQ ? dq_lut[L.scale[i] & 0xffu] : __uint_as_float(L.scale[i]);
+  for (int i = 0; i < 4; ++i) s[i] = DQ ? dq_lut[B.scale[i] & 0xffu] : __uint_as_float(B.scale[i]);
   // v[i][j]: row k0 + 4 g4 + i, column n0 + 8 c + j; value level[code] * scale
   // (one f32 multiply, as the reference's dequantize), then bf16.
   float v[4][8];
@@ -118,18 +123,18 @@ __device__ __forceinline__ void store_step(const StepLoads<DQ>& L, unsigned char
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const uint32_t byte = (L.code[i] >> (8 * b)) & 0xffu;
+      const uint32_t byte = (B.code[i] >> (8 * b)) & 0xffu;
       const f32x2 lv = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + byte * 8));
       v[i][2 * b] = lv.x * s[i];
       v[i][2 * b + 1] = lv.y * s[i];
     }
   }
-  // column n0 + 8c + j gets k = 4 g4 .. 4 g4 + 3: half (g4 & 1) of chunk g4 / 2
+  // column 8c + j gets k = 4 g4 .. 4 g4 + 3: half (g4 & 1) of chunk g4 / 2
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int n = 8 * c + j;
     const u32x2 w = {pack_bf16x2(v[0][j], v[1][j]), pack_bf16x2(v[2][j], v[3][j])};
-    const uint32_t addr = lds_addr(kLdsB + buf * kTileBytes, n, g4 >> 1) + (uint32_t)(g4 & 1) * 8u;
+    const uint32_t addr = lds_addr(kLdsB + buf * kBTileBytes, n, g4 >> 1) + (uint32_t)(g4 & 1) * 8u;
     *reinterpret_cast<lds_u32x2*>((size_t)addr) = w;
   }
 }
@@ -138,24 +143,71 @@ __device__ __forceinline__ bf16x8 read_frag(int base, int row, int chunk) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<lds_u32x4*>((size_t)lds_addr(base, row, chunk)));
 }
 
+// One K step: the wave's 64 x 128 tile as 2 x 4 32x32x16 MFMA tiles over
+// four k16 slices, A fragments from the wave's LDS region at abase and B
+// fragments from the W tile at bbase.  The k order inside a step is permuted
+// the same way for both operands: lane l's slice kk is chunk 4 (l / 32) + kk.
+// The fragments of slice kk + 1 are read while slice kk's MFMAs run.
+struct Frags {
+  bf16x8 a[2], b[4];
+};
+
+__device__ __forceinline__ void read_frags(Frags& F, int abase, int bbase, int kk, int lane) {
+  const int ch = 4 * (lane >> 5) + kk;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) F.a[i] = read_frag(abase, 32 * i + (lane & 31), ch);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) F.b[j] = read_frag(bbase, 32 * j + (lane & 31), ch);
+}
+
+__device__ __forceinline__ void mma_frags(f32x16 (&acc)[2][4], const Frags& F) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
+}
+
+__device__ __forceinline__ void mma_step(f32x16 (&acc)[2][4], int abase, int bbase, int lane) {
+  Frags F0, F1;
+  read_frags(F0, abase, bbase, 0, lane);
+  read_frags(F1, abase, bbase, 1, lane);
+  mma_frags(acc, F0);
+  read_frags(F0, abase, bbase, 2, lane);
+  mma_frags(acc, F1);
+  read_frags(F1, abase, bbase, 3, lane);
+  mma_frags(acc, F0);
+  mma_frags(acc, F1);
+}
+
+// vmcnt(n): wait until at most n vector-memory loads of this wave are in
+// flight (they complete in issue order).
+#define UNIFUR_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+// Workgroup tile 256 x 128, warp-specialised: waves 0-3 ("MFMA waves") own
+// rows 64 w .. + 63 and all 128 columns and only read LDS and issue MFMAs;
+// waves 4-7 ("producer waves", one per SIMD beside an MFMA wave) copy the X
+// tiles into LDS and dequantize the W tiles, one step ahead, so that their
+// VALU / LDS / memory work overlaps the MFMAs on the same SIMD.  One
+// workgroup barrier per K step hands the buffers over.
 template <bool DQ, bool YBF16, bool LORA>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;  // wave's 64 x 64 quadrant
+  const bool producer = wave >= 4;
+  const int w4 = wave & 3;   // MFMA wave index, or the MFMA wave a producer copies X for
+  const int pt = tid & 255;  // producer thread index
 
-  // XCD-aware tile order: workgroup b runs on XCD b % 8; each XCD gets a
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; each XCD takes a
   // contiguous run of tiles in row-major (m, n) order, so the workgroups
-  // sharing an X row band sit on the same XCD and share its L2.
+  // sharing an X row band share that XCD's L2.
   const int nb = gridDim.x;
   const int b = blockIdx.x;
-  const int per_xcd = nb / 8;
-  const int t = (nb % 8 == 0) ? (b % 8) * per_xcd + b / 8 : b;
+  const int t = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
   const int m0 = (t / g.tiles_n) * kBM, n0 = (t % g.tiles_n) * kBN;
+  const int row0 = m0 + 64 * w4;
 
-  // LUTs: byte -> {level[lo], level[hi]}; DQ code -> scale.
-  {
+  if (tid < 256) {
     float* lut = reinterpret_cast<float*>(smem + kLdsLut);
     lut[2 * tid] = level(tid & 15);
     lut[2 * tid + 1] = level(tid >> 4);
@@ -163,79 +215,109 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
       reinterpret_cast<float*>(smem + kLdsDq)[tid] = ((float)tid / 255.0f) * (*g.scales.scale_of_scales);
   }
 
-  f32x16 acc[2][2];
+  // rows past M read as zero (buffer bound)
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(g.x), (short)0, (int)((uint32_t)g.M * (uint32_t)g.K * 2u), 0x00020000);
+  const int nk = g.K / kBK;
+  const int awave = kLdsA + w4 * (kATileBytes / 4);
+
+  // Both roles pass the same number of workgroup barriers: 2 before the
+  // loop and one per K step.
+  if (producer) {
+    // Loads per step, in issue order: 8 X copies, then 4 code + 4 scale
+    // loads.  Load indices are clamped to the last step (a harmless
+    // in-bounds reload into a free stage) so that every step issues the same
+    // loads and the vmcnt arithmetic holds.
+    BStep B0, B1;
+    load_a(xr, g.K, row0, 0, awave, lane);
+    load_b<DQ>(B0, g, n0, 0, pt);
+    load_a(xr, g.K, row0, min(1, nk - 1) * kBK, awave + kATileBytes, lane);
+    load_b<DQ>(B1, g, n0, min(1, nk - 1) * kBK, pt);
+    __syncthreads();  // LUTs visible
+    store_b<DQ>(B0, smem, 0, pt);
+    UNIFUR_WAIT_VMCNT(16);  // X of step 0 landed (step 1's 16 loads may be in flight)
+    __syncthreads();
+    int sa = 0;  // X stage of step kt
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      int s2 = sa >= 1 ? sa - 1 : sa + 2;  // (kt + 2) % 3
+      load_a(xr, g.K, row0, min(kt + 2, nk - 1) * kBK, awave + s2 * kATileBytes, lane);
+      load_b<DQ>(B0, g, n0, min(kt + 2, nk - 1) * kBK, pt);
+      store_b<DQ>(B1, smem, 1, pt);
+      UNIFUR_WAIT_VMCNT(16);
+      __syncthreads();
+      sa = sa == 2 ? 0 : sa + 1;
+      s2 = sa >= 1 ? sa - 1 : sa + 2;
+      load_a(xr, g.K, row0, min(kt + 3, nk - 1) * kBK, awave + s2 * kATileBytes, lane);
+      load_b<DQ>(B1, g, n0, min(kt + 3, nk - 1) * kBK, pt);
+      store_b<DQ>(B0, smem, 0, pt);
+      UNIFUR_WAIT_VMCNT(16);
+      __syncthreads();
+      sa = sa == 2 ? 0 : sa + 1;
+    }
+    UNIFUR_WAIT_VMCNT(0);  // drain the clamped reloads before the wave exits
+    return;
+  }
+
+  f32x16 acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  const int nk = g.K / kBK;
-  StepLoads<DQ> L;
-  load_step<DQ>(L, g, m0, n0, 0, tid);
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
   __syncthreads();  // LUTs visible
-  store_step<DQ>(L, smem, 0, tid);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load_step<DQ>(L, g, m0, n0, (kt + 1) * kBK, tid);
-    const int abase = kLdsA + cur * kTileBytes, bbase = kLdsB + cur * kTileBytes;
-#pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int ch = kk * 2 + (lane >> 5);
-      bf16x8 af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = read_frag(abase, wr * 64 + i * 32 + (lane & 31), ch);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = read_frag(bbase, wc * 64 + j * 32 + (lane & 31), ch);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) store_step<DQ>(L, smem, cur ^ 1, tid);
+  __syncthreads();  // step 0 ready
+  int sa = 0;
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    mma_step(acc, awave + sa * kATileBytes, kLdsB, lane);
     __syncthreads();
+    sa = sa == 2 ? 0 : sa + 1;
+    mma_step(acc, awave + sa * kATileBytes, kLdsB + kBTileBytes, lane);
+    __syncthreads();
+    sa = sa == 2 ? 0 : sa + 1;
   }
+  if (kt < nk) mma_step(acc, awave + sa * kATileBytes, kLdsB, lane);  // odd step count: last W in buffer 0
 
   if constexpr (LORA) {
     // acc += xa[rows, r] . B[r, cols], xa already scaled: one 32x32x16 MFMA
     // per tile and 16 adapter columns (columns past lora_rank contribute zero).
     const int kr = (lane >> 5) * 8;
     for (int r0 = 0; r0 < g.lora_rank; r0 += 16) {
+      bf16x8 bfr[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 32 * j + (lane & 31);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int r = r0 + kr + q;
+          bfr[j][q] = r < g.lora_rank ? (__bf16)g.lora_b[(size_t)r * g.N + n] : (__bf16)0.0f;
+        }
+      }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int m = m0 + wr * 64 + i * 32 + (lane & 31);
+        const int m = row0 + 32 * i + (lane & 31);
         bf16x8 af;
 #pragma unroll
         for (int q = 0; q < 8; ++q)
           af[q] = m < g.M ? (__bf16)g.lora_xa[(size_t)m * g.lora_pad + r0 + kr + q] : (__bf16)0.0f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int n = n0 + wc * 64 + j * 32 + (lane & 31);
-          bf16x8 bfr;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const int r = r0 + kr + q;
-            bfr[q] = r < g.lora_rank ? (__bf16)g.lora_b[(size_t)r * g.N + n] : (__bf16)0.0f;
-          }
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr, acc[i][j], 0, 0, 0);
-        }
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr[j], acc[i][j], 0, 0, 0);
       }
     }
   }
 
   // Epilogue: acc[i][j][4 a + e] = C[row 8 a + 4 (lane / 32) + e][col lane % 32].
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + 32 * j + (lane & 31);
+    const float bias = g.bias ? g.bias[n] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wc * 64 + j * 32 + (lane & 31);
-      const float bias = g.bias ? g.bias[n] : 0.0f;
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
       for (int a4 = 0; a4 < 4; ++a4) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int m = m0 + wr * 64 + i * 32 + 8 * a4 + 4 * (lane >> 5) + e;
+          const int m = row0 + 32 * i + 8 * a4 + 4 * (lane >> 5) + e;
           if (m >= g.M) continue;
           const float yv = acc[i][j][4 * a4 + e] + bias;
           const size_t idx = (size_t)m * g.N + n;
@@ -271,42 +353,59 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
 // xa[m][j] = scaling * sum_k x[m][k] a[k][j], the first factor of
 // LoraAdapter::forward (src/quantize.rs:619-624) with the scaling folded in,
 // laid out [M, pad] (pad = rank rounded up to 16, zero past the rank) for the
-// fused epilogue.  A workgroup covers 16 rows and 16 adapter columns; its
-// four waves take interleaved 32-wide K slices (X rows as the A operand of a
-// 16x16x32 MFMA, a as the B operand) and are summed in LDS.
-constexpr int kXaWaves = 4;
+// fused epilogue.  Two launches: partial products over 256-wide K slices
+// (one workgroup per 64 rows x 16 adapter columns x slice; the slice of a is
+// staged in LDS as bf16 and is the B operand of 16x16x32 MFMAs whose A
+// operand is read straight from X, all eight loads of a wave issued before
+// its MFMAs), then a fixed-order sum over the slices.
+constexpr int kXaK = 256;
+constexpr int kXaRowsPerWg = 64;
+constexpr int kXaColStride = kXaK + 8;  // bf16 elements: 16-byte pad per column row
 
-__global__ __launch_bounds__(64 * kXaWaves) void lora_xa_mfma_kernel(const uint16_t* __restrict__ x,
-                                                                    const float* __restrict__ a, int M, int K,
-                                                                    int rank, int pad, float scaling,
-                                                                    float* __restrict__ xa) {
-  __shared__ float part[kXaWaves][16][16];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int m0 = blockIdx.x * 16, c0 = blockIdx.y * 16;
-  const int row = m0 + (lane & 15);
-  const int col = c0 + (lane & 15);
-  f32x4 acc = {};
-#pragma unroll 4
-  for (int k = w * 32; k < K; k += 32 * kXaWaves) {
-    const int kb = k + (lane >> 4) * 8;
-    bf16x8 af, bf;
-    if (row < M)
-      af = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(x + (size_t)row * K + kb));
-    else
-      af = bf16x8{};
+__global__ __launch_bounds__(256) void lora_xa_partial_kernel(const uint16_t* __restrict__ x,
+                                                              const float* __restrict__ a, int M, int K, int rank,
+                                                              int pad, float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) __bf16 as[16 * kXaColStride];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int m0 = blockIdx.x * kXaRowsPerWg, s = blockIdx.y, c0 = blockIdx.z * 16;
+  const int k0 = s * kXaK;
+  const int kl = min(kXaK, K - k0);  // a multiple of 32
+  for (int i = tid; i < kXaK * 16; i += 256) {  // zero past the slice end and the rank
+    const int k = i >> 4, c = i & 15;
+    const float v = (k < kl && c0 + c < rank) ? a[(size_t)(k0 + k) * rank + c0 + c] : 0.0f;
+    as[c * kXaColStride + k] = (__bf16)v;
+  }
+  __syncthreads();
+  const int row = m0 + 16 * w + (lane & 15);
+  const uint16_t* xr = x + (size_t)row * K + k0 + (lane >> 4) * 8;
+  const __bf16* ar = as + (lane & 15) * kXaColStride + (lane >> 4) * 8;
+  bf16x8 xv[kXaK / 32];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) bf[q] = col < rank ? (__bf16)a[(size_t)(kb + q) * rank + col] : (__bf16)0.0f;
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf, acc, 0, 0, 0);
+  for (int q = 0; q < kXaK / 32; ++q)
+    xv[q] = (row < M && 32 * q < kl) ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xr + 32 * q))
+                                     : bf16x8{};
+  f32x4 acc = {};
+#pragma unroll
+  for (int q = 0; q < kXaK / 32; ++q) {
+    const bf16x8 bf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ar + 32 * q));
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[q], bf, acc, 0, 0, 0);
   }
   // acc[e] = C[row 4 (lane / 16) + e][col lane % 16]
 #pragma unroll
-  for (int e = 0; e < 4; ++e) part[w][4 * (lane >> 4) + e][lane & 15] = acc[e];
-  __syncthreads();
-  const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
-  float s = 0.0f;
-#pragma unroll
-  for (int q = 0; q < kXaWaves; ++q) s += part[q][r][c];
-  if (m0 + r < M) xa[(size_t)(m0 + r) * pad + c0 + c] = c0 + c < rank ? s * scaling : 0.0f;
+  for (int e = 0; e < 4; ++e) {
+    const int m = m0 + 16 * w + 4 * (lane >> 4) + e;
+    if (m < M) part[((size_t)s * M + m) * pad + c0 + (lane & 15)] = acc[e];
+  }
+}
+
+__global__ void lora_xa_reduce_kernel(const float* __restrict__ part, int slices, int M, int rank, int pad,
+                                      float scaling, float* __restrict__ xa) {
+  const size_t n = (size_t)M * pad;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    float v = 0.0f;
+    for (int s = 0; s < slices; ++s) v += part[(size_t)s * n + i];
+    xa[i] = (int)(i % pad) < rank ? v * scaling : 0.0f;
+  }
 }
 
 }  // namespace
@@ -319,11 +418,21 @@ bool gemm_supported(int M, int K, int N, const void* x) {
 
 int lora_pad(int rank) { return (rank + 15) / 16 * 16; }
 
-hipError_t launch_lora_xa_bf16(const uint16_t* x, const float* a, int M, int K, int rank, float scaling, float* xa,
-                               hipStream_t stream) {
+size_t lora_xa_partial_floats(int M, int K, int rank) {
+  return (size_t)((K + kXaK - 1) / kXaK) * (size_t)M * (size_t)lora_pad(rank);
+}
+
+hipError_t launch_lora_xa_bf16(const uint16_t* x, const float* a, int M, int K, int rank, float scaling, float* part,
+                               float* xa, hipStream_t stream) {
   if (rank < 1 || rank > 64 || K % 32 != 0) return hipErrorInvalidValue;
-  const dim3 grid((M + 15) / 16, lora_pad(rank) / 16);
-  lora_xa_mfma_kernel<<<grid, 64 * kXaWaves, 0, stream>>>(x, a, M, K, rank, lora_pad(rank), scaling, xa);
+  const int pad = lora_pad(rank), slices = (K + kXaK - 1) / kXaK;
+  const dim3 grid((M + kXaRowsPerWg - 1) / kXaRowsPerWg, slices, pad / 16);
+  lora_xa_partial_kernel<<<grid, 256, 0, stream>>>(x, a, M, K, rank, pad, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t n = (size_t)M * pad;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 2048);
+  lora_xa_reduce_kernel<<<blocks, 256, 0, stream>>>(part, slices, M, rank, pad, scaling, xa);
   return hipGetLastError();
 }
 
