@@ -25,7 +25,9 @@
  *     and one f32 scale of scales.
  *   - A linear weight is the reference's [d_in, d_out] row-major matrix
  *     (y = x W, src/qwennet.rs:2196-2211), so its 64-value blocks run along
- *     d_out.
+ *     d_out.  On the device it may also be held in the column-striped
+ *     layout (UNIFUR_NF4_LAYOUT_STRIPED), a byte permutation of the same
+ *     codes and scales that the decode kernels stream contiguously.
  */
 #ifndef UNIFUR_NF4_H
 #define UNIFUR_NF4_H
@@ -60,12 +62,22 @@ typedef struct unifur_nf4_scales {
   const float *scale_of_scales; /* DOUBLE_QUANTIZED: one f32 (device pointer) */
 } unifur_nf4_scales;
 
+/* Device layouts of a linear weight's codes and scales (d_in = K, d_out = N):
+ *   ROW_MAJOR  the reference's: packed[ceil(K*N/2)] in value order, scales
+ *              one per 64-value block in value order (src/quantize.rs:240-257);
+ *   STRIPED    N % 64 == 0: 16-column stripe s of all K rows contiguous,
+ *              packed[(s*K + k)*8 + j] = row-major packed[k*N/2 + s*8 + j], and
+ *              scales block-major, scale[b*K + k] = row-major scale[k*N/64 + b].
+ *              unifur_nf4_stripe_weight / unifur_nf4_unstripe_weight convert. */
+enum { UNIFUR_NF4_LAYOUT_ROW_MAJOR = 0, UNIFUR_NF4_LAYOUT_STRIPED = 1 };
+
 /* The packed weight an Nf4Linear holds (src/qwennet.rs:161-178). */
 typedef struct unifur_nf4_weight {
   const uint8_t *packed;
   unifur_nf4_scales scales;
   uint64_t d_in;
   uint64_t d_out;
+  int32_t layout; /* UNIFUR_NF4_LAYOUT_* */
 } unifur_nf4_weight;
 
 /* LoraAdapter factors (src/quantize.rs:556-565): a [d_in, rank] and
@@ -121,6 +133,20 @@ int unifur_nf4_double_quantize(const float *absmax, uint64_t num_blocks, uint8_t
  * rounded to nearest even). */
 int unifur_nf4_dequantize(const uint8_t *packed, const unifur_nf4_scales *scales, uint64_t len, void *out,
                           int out_dtype, void *stream);
+
+/* ---- device layout of a linear weight ------------------------------------------ */
+
+/* Row-major -> striped.  src->layout must be ROW_MAJOR, d_out % 64 == 0 and
+ * src->packed 8-byte aligned.  Writes ceil(d_in*d_out/2) bytes to dst_packed
+ * and the per-block scales (u8 DQ codes or f32 absmax, as src->scales.kind) to
+ * dst_scales; a double-quantized weight keeps its scale_of_scales.  No
+ * counterpart in the reference (which has one layout); it stands in for the
+ * load-time [out, in] -> [in, out] transpose of src/qwennet.rs:1375-1390 as the
+ * place where the resident form is fixed. */
+int unifur_nf4_stripe_weight(const unifur_nf4_weight *src, uint8_t *dst_packed, void *dst_scales, void *stream);
+
+/* Striped -> row-major (the reference's bytes, bit for bit), the inverse. */
+int unifur_nf4_unstripe_weight(const unifur_nf4_weight *src, uint8_t *dst_packed, void *dst_scales, void *stream);
 
 /* ---- linear layers ----------------------------------------------------------- */
 

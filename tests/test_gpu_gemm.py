@@ -33,11 +33,12 @@ def lora_parts(oracle, d_in, d_out, r, seed, device, scaling=2.0):
     return a, b, ad
 
 
-def test_config3_prefill_qlora(device, oracle):
+@pytest.mark.parametrize("striped", [True, False])
+def test_config3_prefill_qlora(device, oracle, striped):
     # X bf16 [2048, 4096], W NF4 4096 -> 4096 with double
     # quantization, LoRA r = 16, scale 2, bf16 output.
     M, K, N, r = 2048, 4096, 4096, 16
-    lin, wdeq = make_linear(oracle, K, N, 0x4E463457 + 3, device, dq=True)
+    lin, wdeq = make_linear(oracle, K, N, 0x4E463457 + 3, device, dq=True, striped=striped)
     x, xt = acts(oracle, M, K, 0x58 + 3, torch.bfloat16, device)
     a, b, ad = lora_parts(oracle, K, N, r, 0x41 + 3, device)
     ql = Q.QloraLinear(lin, ad)
@@ -51,30 +52,33 @@ def test_config3_prefill_qlora(device, oracle):
     assert torch.equal(ql.forward(xt, out_dtype=torch.float32), yf)
 
 
+@pytest.mark.parametrize("striped", [True, False])
 @pytest.mark.parametrize("M", [5, 64, 127, 128, 129, 300])
 @pytest.mark.parametrize("dq", [True, False])
-def test_ragged_rows_and_scale_kinds(device, oracle, M, dq):
+def test_ragged_rows_and_scale_kinds(device, oracle, M, dq, striped):
     K, N = 512, 384
-    lin, wdeq = make_linear(oracle, K, N, 100 + M, device, dq=dq)
+    lin, wdeq = make_linear(oracle, K, N, 100 + M, device, dq=dq, striped=striped)
     x, xt = acts(oracle, M, K, 200 + M, torch.bfloat16, device)
     ref = oracle.linear_ref_f64(x, wdeq)
     check(lin.forward(xt, out_dtype=torch.float32), ref, x, wdeq, TOL_BF16, f"mfma M={M} dq={dq}")
 
 
+@pytest.mark.parametrize("striped", [True, False])
 @pytest.mark.parametrize("shape", [(896, 4864), (4864, 896), (896, 128), (64, 128), (11008, 4096)])
-def test_qwen_and_edge_shapes(device, oracle, shape):
+def test_qwen_and_edge_shapes(device, oracle, shape, striped):
     K, N = shape
     M = 32
-    lin, wdeq = make_linear(oracle, K, N, 300 + K + N, device)
+    lin, wdeq = make_linear(oracle, K, N, 300 + K + N, device, striped=striped)
     x, xt = acts(oracle, M, K, 301, torch.bfloat16, device)
     check(lin.forward(xt, out_dtype=torch.bfloat16), oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_BF16,
           f"mfma {shape}")
 
 
+@pytest.mark.parametrize("striped", [True, False])
 @pytest.mark.parametrize("r", [1, 8, 16, 40, 64])
-def test_bias_and_lora_ranks(device, oracle, r):
+def test_bias_and_lora_ranks(device, oracle, r, striped):
     M, K, N = 200, 1024, 512
-    lin, wdeq = make_linear(oracle, K, N, 400 + r, device)
+    lin, wdeq = make_linear(oracle, K, N, 400 + r, device, striped=striped)
     bias = oracle.fill_normal(401, 0.1, N)
     lin.bias = torch.from_numpy(bias).to(device)
     x, xt = acts(oracle, M, K, 402, torch.bfloat16, device)

@@ -23,8 +23,9 @@ TOL_F32 = 1e-5
 TOL_BF16 = 1e-2
 
 
-def make_linear(oracle, d_in, d_out, seed, device, dq=True, sigma=0.02):
-    """Nf4Linear from seeded [d_in, d_out] values; returns (layer, W_deq f32)."""
+def make_linear(oracle, d_in, d_out, seed, device, dq=True, sigma=0.02, striped=None):
+    """Nf4Linear from seeded [d_in, d_out] values; returns (layer, W_deq f32).
+    striped=None lets the layer pick (striped when d_out % 64 == 0)."""
     v = oracle.fill_normal(seed, sigma, d_in * d_out)
     packed, absmax = oracle.quantize_packed(v)
     if dq:
@@ -36,7 +37,10 @@ def make_linear(oracle, d_in, d_out, seed, device, dq=True, sigma=0.02):
     if dq:
         p = p.with_double_quantization()
     assert np.array_equal(p.codes.cpu().numpy(), packed)
-    return Q.Nf4Linear.from_packed(p, d_in, d_out), wdeq.reshape(d_in, d_out)
+    lin = Q.Nf4Linear.from_packed(p, d_in, d_out, striped=striped)
+    # either layout gives back the reference's packed bytes
+    assert np.array_equal(lin.packed().codes.cpu().numpy(), packed)
+    return lin, wdeq.reshape(d_in, d_out)
 
 
 def check(y, ref, x, wdeq, tol, tag):
@@ -67,11 +71,13 @@ def test_orientation_known_answer(device, oracle):
     assert w[1, 2] == pytest.approx(6.0, abs=6 * 2 / 255)
 
 
+@pytest.mark.parametrize("striped", [True, False])
 @pytest.mark.parametrize("dq", [True, False])
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
-def test_gemv_config2_4096_to_11008(device, oracle, dq, x_dtype):
+def test_gemv_config2_4096_to_11008(device, oracle, dq, x_dtype, striped):
     # x[1, 4096] ~ N(0,1), W logical 11008x4096 stored [4096, 11008]
-    lin, wdeq = make_linear(oracle, 4096, 11008, 0x4E463457 + 1, device, dq=dq)
+    lin, wdeq = make_linear(oracle, 4096, 11008, 0x4E463457 + 1, device, dq=dq, striped=striped)
+    assert lin.is_striped() == striped
     x, xt = acts(oracle, 1, 4096, 0x58 + 1, x_dtype, device)
     ref = oracle.linear_ref_f64(x, wdeq)
     y = lin.forward(xt, out_dtype=torch.float32)
@@ -83,18 +89,21 @@ def test_gemv_config2_4096_to_11008(device, oracle, dq, x_dtype):
     assert torch.equal(lin.forward(xt, out_dtype=torch.float32), y)
 
 
+@pytest.mark.parametrize("striped", [True, False])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4])
-@pytest.mark.parametrize("shape", [(896, 4864), (4864, 896), (896, 128), (256, 64), (4096, 4096)])
-def test_gemv_rows_and_shapes(device, oracle, rows, shape):
+@pytest.mark.parametrize("shape", [(896, 4864), (4864, 896), (896, 128), (256, 64), (4096, 4096), (100, 192),
+                                   (11008, 4096)])
+def test_gemv_rows_and_shapes(device, oracle, rows, shape, striped):
     d_in, d_out = shape
-    lin, wdeq = make_linear(oracle, d_in, d_out, 11 + d_in + d_out, device)
+    lin, wdeq = make_linear(oracle, d_in, d_out, 11 + d_in + d_out, device, striped=striped)
     x, xt = acts(oracle, rows, d_in, 5 + rows, torch.float32, device)
     check(lin.forward(xt), oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_F32, f"gemv rows={rows} {shape}")
 
 
-def test_gemv_bias_and_qlora(device, oracle):
+@pytest.mark.parametrize("striped", [True, False])
+def test_gemv_bias_and_qlora(device, oracle, striped):
     d_in, d_out, r = 4096, 4096, 16
-    lin, wdeq = make_linear(oracle, d_in, d_out, 21, device, dq=True)
+    lin, wdeq = make_linear(oracle, d_in, d_out, 21, device, dq=True, striped=striped)
     bias = oracle.fill_normal(22, 0.1, d_out)
     lin.bias = torch.from_numpy(bias).to(device)
     x, xt = acts(oracle, 2, d_in, 23, torch.float32, device)
@@ -125,12 +134,13 @@ def test_generic_path_dequantize_then_matmul(device, oracle, shape, rows, dt):
           f"generic {shape} rows={rows}")
 
 
+@pytest.mark.parametrize("striped", [True, False])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 7])
-def test_swiglu_small(device, oracle, rows):
+def test_swiglu_small(device, oracle, rows, striped):
     hidden, inter = 256, 512
-    g, wg = make_linear(oracle, hidden, inter, 41, device)
-    u, wu = make_linear(oracle, hidden, inter, 42, device)
-    d, wd = make_linear(oracle, inter, hidden, 43, device)
+    g, wg = make_linear(oracle, hidden, inter, 41, device, striped=striped)
+    u, wu = make_linear(oracle, hidden, inter, 42, device, striped=striped)
+    d, wd = make_linear(oracle, inter, hidden, 43, device, striped=striped)
     mlp = Q.QwenMlp(g, u, d)
     x, xt = acts(oracle, rows, hidden, 44, torch.float32, device)
     ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
@@ -138,16 +148,19 @@ def test_swiglu_small(device, oracle, rows):
     check(mlp.forward(xt), ref, h, wd, TOL_F32, f"swiglu rows={rows}")
 
 
-def test_swiglu_config4_t1(device, oracle):
-    # BASELINE config 4 at T = 1: hidden 4096, intermediate 11008, bf16 x
-    g, wg = make_linear(oracle, 4096, 11008, 0x4E463457 + 4, device)
-    u, wu = make_linear(oracle, 4096, 11008, 0x4E463457 + 5, device)
-    d, wd = make_linear(oracle, 11008, 4096, 0x4E463457 + 6, device)
-    x, xt = acts(oracle, 1, 4096, 0x58 + 4, torch.bfloat16, device)
+@pytest.mark.parametrize("striped", [True, False])
+@pytest.mark.parametrize("T", [1, 16, 512])
+def test_swiglu_config4(device, oracle, T, striped):
+    # hidden 4096, intermediate 11008, bf16 x, T = 1, 16, 512
+    # (T = 1: GEMV pair; T = 16 and 512: the MFMA GEMMs with a bf16 middle)
+    g, wg = make_linear(oracle, 4096, 11008, 0x4E463457 + 4, device, striped=striped)
+    u, wu = make_linear(oracle, 4096, 11008, 0x4E463457 + 5, device, striped=striped)
+    d, wd = make_linear(oracle, 11008, 4096, 0x4E463457 + 6, device, striped=striped)
+    x, xt = acts(oracle, T, 4096, 0x58 + 4, torch.bfloat16, device)
     ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
     h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
     y = Q.QwenMlp(g, u, d).forward(xt, out_dtype=torch.float32)
-    check(y, ref, h, wd, TOL_BF16, "swiglu config4 T=1")
+    check(y, ref, h, wd, TOL_BF16, f"swiglu config4 T={T} striped={striped}")
 
 
 def test_workspace_shared_by_generic_then_gemv_calls(device, oracle):
@@ -157,7 +170,7 @@ def test_workspace_shared_by_generic_then_gemv_calls(device, oracle):
     from unifur_amd import _lib as L
     import ctypes
     small, wsmall = make_linear(oracle, 64, 70, 51, device, sigma=1.0)    # generic (70 % 64 != 0)
-    big, wbig = make_linear(oracle, 4096, 4096, 52, device)               # GEMV, split-K
+    big, wbig = make_linear(oracle, 4096, 4096, 52, device, striped=False)  # row-major GEMV, split-K
     need = max(L.lib().unifur_nf4_linear_workspace_size(1, 64, 70, 0, 0),
                L.lib().unifur_nf4_linear_workspace_size(1, 4096, 4096, 0, 0))
     ws = torch.zeros(need, dtype=torch.uint8, device=device)

@@ -22,6 +22,9 @@ BF16 = 1
 SCALES_F32 = 0
 SCALES_DOUBLE_QUANTIZED = 1
 
+LAYOUT_ROW_MAJOR = 0
+LAYOUT_STRIPED = 1
+
 BLOCK_SIZE = 64
 
 
@@ -40,6 +43,7 @@ class Weight(ctypes.Structure):
         ("scales", Scales),
         ("d_in", ctypes.c_uint64),
         ("d_out", ctypes.c_uint64),
+        ("layout", ctypes.c_int32),
     ]
 
 
@@ -67,6 +71,8 @@ SIGNATURES = {
     "unifur_nf4_quantize": (_I, [_P, _U64, _P, _P, _P]),
     "unifur_nf4_double_quantize": (_I, [_P, _U64, _P, _P, _P]),
     "unifur_nf4_dequantize": (_I, [_P, ctypes.POINTER(Scales), _U64, _P, _I, _P]),
+    "unifur_nf4_stripe_weight": (_I, [ctypes.POINTER(Weight), _P, _P, _P]),
+    "unifur_nf4_unstripe_weight": (_I, [ctypes.POINTER(Weight), _P, _P, _P]),
     "unifur_nf4_linear_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
     "unifur_nf4_linear_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), _P, ctypes.POINTER(Lora), _P, _I,
                                        _P, _U64, _P]),

@@ -17,6 +17,7 @@
 #include "nf4_gemm.hpp"
 #include "nf4_generic.hpp"
 #include "nf4_gemv.hpp"
+#include "nf4_layout.hpp"
 
 namespace unifur {
 namespace {
@@ -68,12 +69,31 @@ int check_scales(const unifur_nf4_scales* s) {
   return UNIFUR_NF4_OK;
 }
 
+bool aligned_to(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
 int check_weight(const unifur_nf4_weight* w, const char* name) {
   UNIFUR_ARG(w != nullptr, std::string(name) + " weight is NULL");
   UNIFUR_ARG(w->packed != nullptr, std::string(name) + " packed codes are NULL");
   UNIFUR_ARG(w->d_in > 0 && w->d_out > 0, std::string(name) + " has a zero dimension");
   UNIFUR_ARG(w->d_in <= 0x7fffffffu && w->d_out <= 0x7fffffffu, std::string(name) + " dimension exceeds 2^31-1");
-  return check_scales(&w->scales);
+  if (int r = check_scales(&w->scales)) return r;
+  if (w->layout == UNIFUR_NF4_LAYOUT_ROW_MAJOR) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(w->layout == UNIFUR_NF4_LAYOUT_STRIPED,
+             std::string(name) + " has unknown layout " + std::to_string(w->layout));
+  UNIFUR_ARG(w->d_out % 64 == 0, std::string(name) + ": the striped layout needs d_out % 64 == 0");
+  UNIFUR_ARG(aligned_to(w->packed, 8), std::string(name) + ": striped codes must be 8-byte aligned");
+  UNIFUR_ARG(w->d_in * w->d_out / 2 < (1ull << 31), std::string(name) + ": striped weight over 2 GiB of codes");
+  if (w->scales.kind == UNIFUR_NF4_SCALES_F32)
+    UNIFUR_ARG(aligned_to(w->scales.absmax, 16), std::string(name) + ": striped absmax must be 16-byte aligned");
+  else
+    UNIFUR_ARG(aligned_to(w->scales.dq_codes, 4), std::string(name) + ": striped DQ codes must be 4-byte aligned");
+  return UNIFUR_NF4_OK;
+}
+
+bool is_striped(const unifur_nf4_weight* w) { return w->layout == UNIFUR_NF4_LAYOUT_STRIPED; }
+
+uint64_t scale_bytes(uint64_t num_blocks, int kind) {
+  return kind == UNIFUR_NF4_SCALES_F32 ? 4 * num_blocks : num_blocks;
 }
 
 // ---------------------------------------------------------------- workspace --
@@ -145,43 +165,52 @@ struct Carver {
 
 // ------------------------------------------------------------- linear plans --
 
-enum class LinearPath { kGemv, kMfma, kGeneric };
+enum class LinearPath { kGemvStriped, kGemv, kMfma, kGeneric };
 
-// The fused GEMV needs whole 64-blocks per weight row (d_out % 64 == 0),
+// The row-major GEMV needs whole 64-blocks per weight row (d_out % 64 == 0),
 // 16-byte aligned code rows and a weight that 32-bit buffer offsets reach
-// (under 2 GiB of codes, 4 G values); every other shape takes the generic path.
+// (under 2 GiB of codes, 4 G values).
 bool gemv_layout_ok(uint64_t d_in, uint64_t d_out, const void* packed) {
-  return d_out % 64 == 0 && (reinterpret_cast<uintptr_t>(packed) & 15u) == 0 && d_in * d_out / 2 < (1ull << 31);
+  return d_out % 64 == 0 && aligned_to(packed, 16) && d_in * d_out / 2 < (1ull << 31);
 }
 
 struct LinearLayout {
   LinearPath path;
   GemvPlan gemv;
-  size_t counters, partials, xa, xa_part, wf32, total;
+  StripedPlan striped;
+  size_t partials, xa, xa_part, wf32, rm_codes, rm_scales, total;
 };
 
-// Decode-sized batches (<= 4 rows) take the fused GEMV; larger bf16 batches
-// the MFMA GEMM; everything else the generic dequantize + f32 matmul.
+// Decode-sized batches (<= 4 rows) take a GEMV (the striped one for striped
+// weights); larger bf16 batches the MFMA GEMM; everything else the generic
+// dequantize + f32 matmul (a striped weight is first put back in row-major
+// order in the workspace).
 LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t lora_rank, const void* packed,
-                         int x_dtype, const void* x) {
+                         int x_dtype, const void* x, bool striped, int scale_kind) {
   LinearLayout L{};
   Carver c;
-  const bool gemv = rows <= (uint64_t)kGemvMaxRows && gemv_layout_ok(d_in, d_out, packed) &&
-                    ceil_div_u64(d_out, 256) <= (uint64_t)kMaxCounters;
-  const bool mfma = !gemv && x_dtype == UNIFUR_NF4_BF16 && gemv_layout_ok(d_in, d_out, packed) &&
-                    rows <= 0x7fffffffu && d_in <= 0x7fffffffu && d_out <= 0x7fffffffu &&
+  const bool small = rows <= (uint64_t)kGemvMaxRows;
+  const bool layout_ok = striped || gemv_layout_ok(d_in, d_out, packed);
+  const bool mfma = !small && x_dtype == UNIFUR_NF4_BF16 && layout_ok && rows <= 0x7fffffffu &&
                     gemm_supported((int)rows, (int)d_in, (int)d_out, x);
-  if (gemv) {
+  if (small && striped) {
+    L.path = LinearPath::kGemvStriped;
+    const int n = (int)d_out;
+    L.striped = plan_gemv_striped((int)rows, (int)d_in, &n, 1, false);
+  } else if (small && layout_ok && ceil_div_u64(d_out, 256) <= (uint64_t)kMaxCounters) {
     L.path = LinearPath::kGemv;
     const int n = (int)d_out;
     L.gemv = plan_gemv((int)rows, (int)d_in, &n, 1, false);
-    L.counters = 0;
     L.partials = c.take(L.gemv.partial_count[0] * sizeof(float));
   } else if (mfma) {
     L.path = LinearPath::kMfma;
   } else {
     L.path = LinearPath::kGeneric;
     L.wf32 = c.take((size_t)d_in * d_out * sizeof(float));
+    if (striped) {
+      L.rm_codes = c.take(ceil_div_u64(d_in * d_out, 2));
+      L.rm_scales = c.take(scale_bytes(ceil_div_u64(d_in * d_out, 64), scale_kind));
+    }
   }
   const uint64_t xa_cols = L.path == LinearPath::kMfma && lora_rank ? (uint64_t)lora_pad((int)lora_rank) : lora_rank;
   L.xa = c.take((size_t)rows * xa_cols * sizeof(float));
@@ -194,6 +223,39 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
 template <typename T>
 T* at(void* base, size_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+// A striped weight put back in row-major order into the workspace (the
+// generic path's input); a row-major weight is returned as it is.
+int row_major_view(const unifur_nf4_weight* w, void* ws, size_t codes_off, size_t scales_off, hipStream_t stream,
+                   const uint8_t** packed, ScalesArg* scales) {
+  *packed = w->packed;
+  *scales = to_scales(w->scales);
+  if (!is_striped(w)) return UNIFUR_NF4_OK;
+  uint8_t* codes = at<uint8_t>(ws, codes_off);
+  const bool dq = w->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED;
+  UNIFUR_HIP(launch_stripe_codes(w->packed, codes, w->d_in, w->d_out, false, stream));
+  void* sc = at<void>(ws, scales_off);
+  UNIFUR_HIP(launch_stripe_scales(dq ? (const void*)w->scales.dq_codes : (const void*)w->scales.absmax, sc, w->d_in,
+                                  w->d_out, dq, false, stream));
+  *packed = codes;
+  if (dq)
+    scales->dq_codes = static_cast<const uint8_t*>(sc);
+  else
+    scales->absmax = static_cast<const float*>(sc);
+  return UNIFUR_NF4_OK;
+}
+
+GemvWeight gemv_weight(const unifur_nf4_weight* w, void* y, bool y_bf16, unsigned* counters, float* partials) {
+  GemvWeight g{};
+  g.packed = w->packed;
+  g.scales = to_scales(w->scales);
+  g.d_out = (int)w->d_out;
+  g.y = y;
+  g.y_bf16 = y_bf16;
+  g.counters = counters;
+  g.partials = partials;
+  return g;
 }
 
 int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w, const float* bias,
@@ -209,10 +271,12 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     UNIFUR_ARG(lora->a != nullptr && lora->b != nullptr, "lora factors are NULL");
     UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
   }
-  const LinearLayout L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x);
+  const LinearLayout L =
+      plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind);
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool xbf = x_dtype == UNIFUR_NF4_BF16;
+  const bool ybf = y_dtype == UNIFUR_NF4_BF16;
   float* xa = nullptr;
   if (L.path == LinearPath::kMfma) {
     const uint16_t* xb = static_cast<const uint16_t*>(x);
@@ -222,88 +286,97 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
                                      at<float>(ws, L.xa_part), xa, stream));
     }
     UNIFUR_HIP(launch_gemm(xb, w->packed, to_scales(w->scales), (int)rows, (int)w->d_in, (int)w->d_out, bias, xa,
-                           lora ? lora->b : nullptr, (int)rank, y, y_dtype == UNIFUR_NF4_BF16, stream));
+                           lora ? lora->b : nullptr, (int)rank, y, ybf, is_striped(w), stream));
     return UNIFUR_NF4_OK;
   }
   if (lora) {
     xa = at<float>(ws, L.xa);
     UNIFUR_HIP(launch_lora_xa(x, xbf, lora->a, (int)rows, (int)w->d_in, (int)rank, xa, stream));
   }
-  if (L.path == LinearPath::kGemv) {
-    GemvWeight gw{};
-    gw.packed = w->packed;
-    gw.scales = to_scales(w->scales);
-    gw.d_out = (int)w->d_out;
-    gw.y = y;
-    gw.y_bf16 = y_dtype == UNIFUR_NF4_BF16;
+  if (L.path == LinearPath::kGemv || L.path == LinearPath::kGemvStriped) {
+    GemvWeight gw = gemv_weight(w, y, ybf, at<unsigned>(ws, 0), at<float>(ws, L.partials));
     gw.bias = bias;
     gw.lora_xa = xa;
     gw.lora_b = lora ? lora->b : nullptr;
     gw.lora_rank = (int)rank;
     gw.lora_scaling = lora ? lora->scaling : 0.0f;
-    gw.counters = at<unsigned>(ws, L.counters);
-    gw.partials = at<float>(ws, L.partials);
-    UNIFUR_HIP(launch_gemv(L.gemv, x, xbf, (int)rows, (int)w->d_in, &gw, 1, stream));
+    if (L.path == LinearPath::kGemvStriped)
+      UNIFUR_HIP(launch_gemv_striped(L.striped, x, xbf, (int)rows, (int)w->d_in, &gw, 1, false, stream));
+    else
+      UNIFUR_HIP(launch_gemv(L.gemv, x, xbf, (int)rows, (int)w->d_in, &gw, 1, stream));
     return UNIFUR_NF4_OK;
   }
   // Generic: the reference's own sequence -- dequantize the whole weight to
   // f32 (bit-exact), then an f32 matmul.
+  const uint8_t* packed = nullptr;
+  ScalesArg scales{};
+  if (int r = row_major_view(w, ws, L.rm_codes, L.rm_scales, stream, &packed, &scales)) return r;
   float* wf = at<float>(ws, L.wf32);
-  UNIFUR_HIP(launch_dequantize(w->packed, to_scales(w->scales), (size_t)w->d_in * w->d_out, wf, false,
-                               u32_aligned(w->packed), stream));
-  Epilogue e{bias, xa, lora ? lora->b : nullptr, (int)rank, lora ? lora->scaling : 0.0f, y,
-             y_dtype == UNIFUR_NF4_BF16};
+  UNIFUR_HIP(launch_dequantize(packed, scales, (size_t)w->d_in * w->d_out, wf, false, u32_aligned(packed), stream));
+  Epilogue e{bias, xa, lora ? lora->b : nullptr, (int)rank, lora ? lora->scaling : 0.0f, y, ybf};
   UNIFUR_HIP(launch_gemm_f32(x, xbf, wf, (int)rows, (int)w->d_in, (int)w->d_out, e, stream));
   return UNIFUR_NF4_OK;
 }
 
 // ------------------------------------------------------------- swiglu plans --
 
-enum class MlpPath { kPairGemv, kGemv, kGeneric };
+enum class MlpPath { kPairStriped, kStriped, kPairGemv, kGemv, kMfma, kGeneric };
 
 struct MlpLayout {
   MlpPath path;
   GemvPlan up_plan, down_plan;
-  size_t counters, partials0, partials1, h, u, wf32, total;
+  StripedPlan s_up, s_down;
+  size_t partials0, partials1, h, u, hb, wf32, rm_codes, rm_scales, total;
 };
 
-MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const void* pg, const void* pu, const void* pd) {
+MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_nf4_weight* g,
+                   const unifur_nf4_weight* u, const unifur_nf4_weight* d, int x_dtype, const void* x) {
   MlpLayout L{};
   Carver c;
-  const bool layout = gemv_layout_ok(hidden, inter, pg) && gemv_layout_ok(hidden, inter, pu) &&
-                      gemv_layout_ok(inter, hidden, pd) &&
-                      ceil_div_u64(std::max(inter, hidden), 256) <= (uint64_t)kMaxCounters;
-  if (layout && rows <= (uint64_t)kGemvMaxRows) {
-    L.path = rows <= (uint64_t)kGemvPairMaxRows ? MlpPath::kPairGemv : MlpPath::kGemv;
-    const int gi[2] = {(int)inter, (int)inter};
-    const int hd = (int)hidden;
+  const bool all_striped = is_striped(g) && is_striped(u) && is_striped(d);
+  const bool row_major_ok = !is_striped(g) && !is_striped(u) && !is_striped(d) &&
+                            gemv_layout_ok(hidden, inter, g->packed) && gemv_layout_ok(hidden, inter, u->packed) &&
+                            gemv_layout_ok(inter, hidden, d->packed) &&
+                            ceil_div_u64(std::max(inter, hidden), 256) <= (uint64_t)kMaxCounters;
+  const bool same_kind = g->scales.kind == u->scales.kind;
+  const bool small = rows <= (uint64_t)kGemvMaxRows;
+  const bool layouts_ok = all_striped || row_major_ok;
+  const bool mfma = !small && x_dtype == UNIFUR_NF4_BF16 && layouts_ok && rows <= 0x7fffffffu &&
+                    gemm_supported((int)rows, (int)hidden, (int)inter, x) &&
+                    gemm_supported((int)rows, (int)inter, (int)hidden, reinterpret_cast<const void*>(uintptr_t{256}));
+  const int gi[2] = {(int)inter, (int)inter};
+  const int hd = (int)hidden;
+  if (small && all_striped) {
+    L.path = rows <= (uint64_t)kGemvPairMaxRows && same_kind ? MlpPath::kPairStriped : MlpPath::kStriped;
+    L.s_up = plan_gemv_striped((int)rows, (int)hidden, gi, 2, L.path == MlpPath::kPairStriped);
+    L.s_down = plan_gemv_striped((int)rows, (int)inter, &hd, 1, false);
+    L.h = c.take((size_t)rows * inter * sizeof(float));
+    L.u = L.path == MlpPath::kStriped ? c.take((size_t)rows * inter * sizeof(float)) : 0;
+  } else if (small && row_major_ok) {
+    L.path = rows <= (uint64_t)kGemvPairMaxRows && same_kind ? MlpPath::kPairGemv : MlpPath::kGemv;
     L.up_plan = plan_gemv((int)rows, (int)hidden, gi, 2, L.path == MlpPath::kPairGemv);
     L.down_plan = plan_gemv((int)rows, (int)inter, &hd, 1, false);
-    L.counters = 0;
     L.partials0 = c.take(std::max(L.up_plan.partial_count[0], L.down_plan.partial_count[0]) * sizeof(float));
     L.partials1 = c.take(L.up_plan.partial_count[1] * sizeof(float));
     L.h = c.take((size_t)rows * inter * sizeof(float));
     L.u = L.path == MlpPath::kGemv ? c.take((size_t)rows * inter * sizeof(float)) : 0;
+  } else if (mfma) {
+    L.path = MlpPath::kMfma;
+    L.h = c.take((size_t)rows * inter * sizeof(float));
+    L.u = c.take((size_t)rows * inter * sizeof(float));
+    L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
   } else {
     L.path = MlpPath::kGeneric;
     L.wf32 = c.take((size_t)hidden * inter * sizeof(float));
     L.h = c.take((size_t)rows * inter * sizeof(float));
     L.u = c.take((size_t)rows * inter * sizeof(float));
+    if (is_striped(g) || is_striped(u) || is_striped(d)) {
+      L.rm_codes = c.take(ceil_div_u64(hidden * inter, 2));
+      L.rm_scales = c.take(4 * ceil_div_u64(hidden * inter, 64));
+    }
   }
   L.total = c.off;
   return L;
-}
-
-GemvWeight gemv_weight(const unifur_nf4_weight* w, void* y, bool y_bf16, unsigned* counters, float* partials) {
-  GemvWeight g{};
-  g.packed = w->packed;
-  g.scales = to_scales(w->scales);
-  g.d_out = (int)w->d_out;
-  g.y = y;
-  g.y_bf16 = y_bf16;
-  g.counters = counters;
-  g.partials = partials;
-  return g;
 }
 
 int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* gate, const unifur_nf4_weight* up,
@@ -319,32 +392,76 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr && y != nullptr, "x or y is NULL");
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
-  const MlpLayout L = plan_mlp(rows, hidden, inter, gate->packed, up->packed, down->packed);
+  const MlpLayout L = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x);
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool xbf = x_dtype == UNIFUR_NF4_BF16;
   const bool ybf = y_dtype == UNIFUR_NF4_BF16;
   float* h = at<float>(ws, L.h);
-  if (L.path == MlpPath::kPairGemv || L.path == MlpPath::kGemv) {
-    unsigned* cnt = at<unsigned>(ws, L.counters);
-    float* p0 = at<float>(ws, L.partials0);
-    float* p1 = at<float>(ws, L.partials1);
-    if (L.path == MlpPath::kPairGemv) {
-      GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, p0), gemv_weight(up, nullptr, false, cnt, p1)};
-      UNIFUR_HIP(launch_gemv(L.up_plan, x, xbf, (int)rows, (int)hidden, gw, 2, stream));
-    } else {
-      float* u = at<float>(ws, L.u);
-      GemvWeight g1 = gemv_weight(gate, h, false, cnt, p0);
-      UNIFUR_HIP(launch_gemv(plan_gemv((int)rows, (int)hidden, &g1.d_out, 1, false), x, xbf, (int)rows,
-                             (int)hidden, &g1, 1, stream));
-      GemvWeight g2 = gemv_weight(up, u, false, cnt, p0);
-      UNIFUR_HIP(launch_gemv(plan_gemv((int)rows, (int)hidden, &g2.d_out, 1, false), x, xbf, (int)rows,
-                             (int)hidden, &g2, 1, stream));
-      UNIFUR_HIP(launch_silu_mul(h, u, (size_t)rows * inter, h, stream));
+  unsigned* cnt = at<unsigned>(ws, 0);
+  switch (L.path) {
+    case MlpPath::kPairStriped: {
+      GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, nullptr), gemv_weight(up, nullptr, false, cnt, nullptr)};
+      UNIFUR_HIP(launch_gemv_striped(L.s_up, x, xbf, (int)rows, (int)hidden, gw, 2, true, stream));
+      GemvWeight dw = gemv_weight(down, y, ybf, cnt, nullptr);
+      UNIFUR_HIP(launch_gemv_striped(L.s_down, h, false, (int)rows, (int)inter, &dw, 1, false, stream));
+      return UNIFUR_NF4_OK;
     }
-    GemvWeight dw = gemv_weight(down, y, ybf, cnt, p0);
-    UNIFUR_HIP(launch_gemv(L.down_plan, h, false, (int)rows, (int)inter, &dw, 1, stream));
-    return UNIFUR_NF4_OK;
+    case MlpPath::kStriped: {
+      float* u = at<float>(ws, L.u);
+      // gate and up in one launch (two weights over the same x) when their
+      // scales are of one kind, else one launch each
+      GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, nullptr), gemv_weight(up, u, false, cnt, nullptr)};
+      if (gate->scales.kind == up->scales.kind) {
+        UNIFUR_HIP(launch_gemv_striped(L.s_up, x, xbf, (int)rows, (int)hidden, gw, 2, false, stream));
+      } else {
+        const StripedPlan one = plan_gemv_striped((int)rows, (int)hidden, &gw[0].d_out, 1, false);
+        UNIFUR_HIP(launch_gemv_striped(one, x, xbf, (int)rows, (int)hidden, &gw[0], 1, false, stream));
+        UNIFUR_HIP(launch_gemv_striped(one, x, xbf, (int)rows, (int)hidden, &gw[1], 1, false, stream));
+      }
+      UNIFUR_HIP(launch_silu_mul(h, u, (size_t)rows * inter, h, stream));
+      GemvWeight dw = gemv_weight(down, y, ybf, cnt, nullptr);
+      UNIFUR_HIP(launch_gemv_striped(L.s_down, h, false, (int)rows, (int)inter, &dw, 1, false, stream));
+      return UNIFUR_NF4_OK;
+    }
+    case MlpPath::kPairGemv:
+    case MlpPath::kGemv: {
+      float* p0 = at<float>(ws, L.partials0);
+      float* p1 = at<float>(ws, L.partials1);
+      if (L.path == MlpPath::kPairGemv) {
+        GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, p0), gemv_weight(up, nullptr, false, cnt, p1)};
+        UNIFUR_HIP(launch_gemv(L.up_plan, x, xbf, (int)rows, (int)hidden, gw, 2, stream));
+      } else {
+        float* u = at<float>(ws, L.u);
+        GemvWeight g1 = gemv_weight(gate, h, false, cnt, p0);
+        UNIFUR_HIP(launch_gemv(plan_gemv((int)rows, (int)hidden, &g1.d_out, 1, false), x, xbf, (int)rows,
+                               (int)hidden, &g1, 1, stream));
+        GemvWeight g2 = gemv_weight(up, u, false, cnt, p0);
+        UNIFUR_HIP(launch_gemv(plan_gemv((int)rows, (int)hidden, &g2.d_out, 1, false), x, xbf, (int)rows,
+                               (int)hidden, &g2, 1, stream));
+        UNIFUR_HIP(launch_silu_mul(h, u, (size_t)rows * inter, h, stream));
+      }
+      GemvWeight dw = gemv_weight(down, y, ybf, cnt, p0);
+      UNIFUR_HIP(launch_gemv(L.down_plan, h, false, (int)rows, (int)inter, &dw, 1, stream));
+      return UNIFUR_NF4_OK;
+    }
+    case MlpPath::kMfma: {
+      // gate and up through the MFMA GEMM (f32 out), silu(g) * u rounded to
+      // bf16, then down through the MFMA GEMM.
+      const uint16_t* xb = static_cast<const uint16_t*>(x);
+      float* u = at<float>(ws, L.u);
+      uint16_t* hb = at<uint16_t>(ws, L.hb);
+      UNIFUR_HIP(launch_gemm(xb, gate->packed, to_scales(gate->scales), (int)rows, (int)hidden, (int)inter, nullptr,
+                             nullptr, nullptr, 0, h, false, is_striped(gate), stream));
+      UNIFUR_HIP(launch_gemm(xb, up->packed, to_scales(up->scales), (int)rows, (int)hidden, (int)inter, nullptr,
+                             nullptr, nullptr, 0, u, false, is_striped(up), stream));
+      UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
+      UNIFUR_HIP(launch_gemm(hb, down->packed, to_scales(down->scales), (int)rows, (int)inter, (int)hidden, nullptr,
+                             nullptr, nullptr, 0, y, ybf, is_striped(down), stream));
+      return UNIFUR_NF4_OK;
+    }
+    case MlpPath::kGeneric:
+      break;
   }
   // Generic: three dequantize + f32 matmul linears and the elementwise middle.
   float* wf = at<float>(ws, L.wf32);
@@ -355,16 +472,21 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   eu.y = u;
   ed.y = y;
   ed.y_bf16 = ybf;
-  UNIFUR_HIP(launch_dequantize(gate->packed, to_scales(gate->scales), hidden * inter, wf, false,
-                               u32_aligned(gate->packed), stream));
-  UNIFUR_HIP(launch_gemm_f32(x, xbf, wf, (int)rows, (int)hidden, (int)inter, eg, stream));
-  UNIFUR_HIP(launch_dequantize(up->packed, to_scales(up->scales), hidden * inter, wf, false,
-                               u32_aligned(up->packed), stream));
-  UNIFUR_HIP(launch_gemm_f32(x, xbf, wf, (int)rows, (int)hidden, (int)inter, eu, stream));
-  UNIFUR_HIP(launch_silu_mul(h, u, (size_t)rows * inter, h, stream));
-  UNIFUR_HIP(launch_dequantize(down->packed, to_scales(down->scales), inter * hidden, wf, false,
-                               u32_aligned(down->packed), stream));
-  UNIFUR_HIP(launch_gemm_f32(h, false, wf, (int)rows, (int)inter, (int)hidden, ed, stream));
+  const unifur_nf4_weight* ws3[3] = {gate, up, down};
+  const Epilogue* es[3] = {&eg, &eu, &ed};
+  for (int i = 0; i < 3; ++i) {
+    const unifur_nf4_weight* w = ws3[i];
+    const uint8_t* packed = nullptr;
+    ScalesArg scales{};
+    if (int r = row_major_view(w, ws, L.rm_codes, L.rm_scales, stream, &packed, &scales)) return r;
+    UNIFUR_HIP(launch_dequantize(packed, scales, w->d_in * w->d_out, wf, false, u32_aligned(packed), stream));
+    if (i < 2) {
+      UNIFUR_HIP(launch_gemm_f32(x, xbf, wf, (int)rows, (int)hidden, (int)inter, *es[i], stream));
+      if (i == 1) UNIFUR_HIP(launch_silu_mul(h, u, (size_t)rows * inter, h, stream));
+    } else {
+      UNIFUR_HIP(launch_gemm_f32(h, false, wf, (int)rows, (int)inter, (int)hidden, *es[i], stream));
+    }
+  }
   return UNIFUR_NF4_OK;
 }
 
@@ -445,7 +567,12 @@ uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t
   // with misaligned buffers may take the generic path, which needs more and
   // reports UNIFUR_NF4_ERR_WORKSPACE with the size when given less
   const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
-  return plan_linear(rows, d_in, d_out, lora_rank, aligned, x_dtype, aligned).total;
+  uint64_t need = 0;
+  for (int striped = 0; striped < 2; ++striped)
+    for (int kind = 0; kind < 2; ++kind)
+      need = std::max<uint64_t>(need, plan_linear(rows, d_in, d_out, lora_rank, aligned, x_dtype, aligned,
+                                                  striped && d_out % 64 == 0, kind).total);
+  return need;
 }
 
 int unifur_nf4_linear_forward(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w,
@@ -464,10 +591,48 @@ int unifur_nf4_qlora_forward(const void* x, int x_dtype, uint64_t rows, const un
 }
 
 uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype) {
-  (void)x_dtype;
   if (rows == 0 || hidden == 0 || intermediate == 0) return 0;
-  const void* p = reinterpret_cast<const void*>(uintptr_t{256});
-  return plan_mlp(rows, hidden, intermediate, p, p, p).total;
+  const uint8_t* p = reinterpret_cast<const uint8_t*>(uintptr_t{256});
+  uint64_t need = 0;
+  for (int striped = 0; striped < 2; ++striped) {
+    if (striped && (hidden % 64 != 0 || intermediate % 64 != 0)) continue;
+    for (int kind = 0; kind < 2; ++kind) {
+      unifur_nf4_weight g{p, {kind, (const float*)p, p, (const float*)p}, hidden, intermediate,
+                          striped ? UNIFUR_NF4_LAYOUT_STRIPED : UNIFUR_NF4_LAYOUT_ROW_MAJOR};
+      unifur_nf4_weight d = g;
+      d.d_in = intermediate;
+      d.d_out = hidden;
+      need = std::max<uint64_t>(need, plan_mlp(rows, hidden, intermediate, &g, &g, &d, x_dtype, p).total);
+    }
+  }
+  return need;
+}
+
+int unifur_nf4_stripe_weight(const unifur_nf4_weight* src, uint8_t* dst_packed, void* dst_scales, void* stream) {
+  if (int r = check_weight(src, "src")) return r;
+  UNIFUR_ARG(src->layout == UNIFUR_NF4_LAYOUT_ROW_MAJOR, "stripe_weight takes a row-major weight");
+  UNIFUR_ARG(src->d_out % 64 == 0, "the striped layout needs d_out % 64 == 0");
+  UNIFUR_ARG(dst_packed && dst_scales, "dst_packed or dst_scales is NULL");
+  UNIFUR_ARG(aligned_to(src->packed, 8) && aligned_to(dst_packed, 8), "packed codes must be 8-byte aligned");
+  const bool dq = src->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  UNIFUR_HIP(launch_stripe_codes(src->packed, dst_packed, src->d_in, src->d_out, true, st));
+  UNIFUR_HIP(launch_stripe_scales(dq ? (const void*)src->scales.dq_codes : (const void*)src->scales.absmax,
+                                  dst_scales, src->d_in, src->d_out, dq, true, st));
+  return UNIFUR_NF4_OK;
+}
+
+int unifur_nf4_unstripe_weight(const unifur_nf4_weight* src, uint8_t* dst_packed, void* dst_scales, void* stream) {
+  if (int r = check_weight(src, "src")) return r;
+  UNIFUR_ARG(src->layout == UNIFUR_NF4_LAYOUT_STRIPED, "unstripe_weight takes a striped weight");
+  UNIFUR_ARG(dst_packed && dst_scales, "dst_packed or dst_scales is NULL");
+  UNIFUR_ARG(aligned_to(dst_packed, 8), "packed codes must be 8-byte aligned");
+  const bool dq = src->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  UNIFUR_HIP(launch_stripe_codes(src->packed, dst_packed, src->d_in, src->d_out, false, st));
+  UNIFUR_HIP(launch_stripe_scales(dq ? (const void*)src->scales.dq_codes : (const void*)src->scales.absmax,
+                                  dst_scales, src->d_in, src->d_out, dq, false, st));
+  return UNIFUR_NF4_OK;
 }
 
 int unifur_nf4_swiglu_forward(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* gate,

@@ -90,32 +90,58 @@ struct BStep {
   uint32_t scale[4];
 };
 
-template <bool DQ>
+// The producer's vmcnt arithmetic counts these: 8 X copies, then the loads
+// below (4 code dwords, and 4 scale loads row-major or 1 striped).
+template <bool STRIPED>
+constexpr int kStepLoads = 8 + 4 + (STRIPED ? 1 : 4);
+
+template <bool DQ, bool STRIPED>
 __device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int k0, int tid) {
   const int c = tid & 15, g4 = tid >> 4;
-  const uint32_t row_bytes = (uint32_t)g.N / 2;
-  const uint32_t bpr = (uint32_t)g.N / kBlock;
-  const uint8_t* cp = g.packed + (size_t)(k0 + 4 * g4) * row_bytes + (n0 + 8 * c) / 2;
+  const int n = n0 + 8 * c, k = k0 + 4 * g4;  // first column and row of this thread's 4 x 8 codes
+  if constexpr (STRIPED) {
+    // stripe n / 16 holds 8 bytes per row; these 8 columns are its half (n % 16) / 8
+    const uint8_t* cp = g.packed + ((size_t)(n / 16) * g.K + k) * 8 + (size_t)(c & 1) * 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) B.code[i] = *reinterpret_cast<const uint32_t*>(cp + (size_t)i * row_bytes);
-  const size_t blk = (size_t)(k0 + 4 * g4) * bpr + (n0 + 8 * c) / kBlock;
+    for (int i = 0; i < 4; ++i) B.code[i] = *reinterpret_cast<const uint32_t*>(cp + (size_t)i * 8);
+    // block-major scales: rows k .. k + 3 of block n / 64 are consecutive (k % 4 == 0, K % 64 == 0)
+    const size_t blk = (size_t)(n / kBlock) * g.K + k;
+    if constexpr (DQ) {
+      B.scale[0] = *reinterpret_cast<const uint32_t*>(g.scales.dq_codes + blk);  // 4 codes, split in store_b
+    } else {
+      const u32x4 s4 = *reinterpret_cast<const u32x4*>(g.scales.absmax + blk);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if constexpr (DQ)
-      B.scale[i] = g.scales.dq_codes[blk + (size_t)i * bpr];
-    else
-      B.scale[i] = __float_as_uint(g.scales.absmax[blk + (size_t)i * bpr]);
+      for (int i = 0; i < 4; ++i) B.scale[i] = s4[i];
+    }
+  } else {
+    const uint32_t row_bytes = (uint32_t)g.N / 2, bpr = (uint32_t)g.N / kBlock;
+    const uint8_t* cp = g.packed + (size_t)k * row_bytes + n / 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) B.code[i] = *reinterpret_cast<const uint32_t*>(cp + (size_t)i * row_bytes);
+    const size_t blk = (size_t)k * bpr + n / kBlock;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DQ)
+        B.scale[i] = g.scales.dq_codes[blk + (size_t)i * bpr];
+      else
+        B.scale[i] = __float_as_uint(g.scales.absmax[blk + (size_t)i * bpr]);
+    }
   }
 }
 
 // Codes -> dequantized bf16 W tile [n][k] in LDS buffer buf.
-template <bool DQ>
+template <bool DQ, bool STRIPED>
 __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int tid) {
   const int c = tid & 15, g4 = tid >> 4;
   const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq);
   float s[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) s[i] = DQ ? dq_lut[B.scale[i] & 0xffu] : __uint_as_float(B.scale[i]);
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (DQ && STRIPED)
+      s[i] = dq_lut[(B.scale[0] >> (8 * i)) & 0xffu];
+    else
+      s[i] = DQ ? dq_lut[B.scale[i] & 0xffu] : __uint_as_float(B.scale[i]);
+  }
   // v[i][j]: row k0 + 4 g4 + i, column n0 + 8 c + j; value level[code] * scale
   // (one f32 multiply, as the reference's dequantize), then bf16.
   float v[4][8];
@@ -189,7 +215,7 @@ __device__ __forceinline__ void mma_step(f32x16 (&acc)[2][4], int abase, int bba
 // tiles into LDS and dequantize the W tiles, one step ahead, so that their
 // VALU / LDS / memory work overlaps the MFMAs on the same SIMD.  One
 // workgroup barrier per K step hands the buffers over.
-template <bool DQ, bool YBF16, bool LORA>
+template <bool DQ, bool YBF16, bool LORA, bool STRIPED>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
@@ -230,28 +256,28 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     // loads and the vmcnt arithmetic holds.
     BStep B0, B1;
     load_a(xr, g.K, row0, 0, awave, lane);
-    load_b<DQ>(B0, g, n0, 0, pt);
+    load_b<DQ, STRIPED>(B0, g, n0, 0, pt);
     load_a(xr, g.K, row0, min(1, nk - 1) * kBK, awave + kATileBytes, lane);
-    load_b<DQ>(B1, g, n0, min(1, nk - 1) * kBK, pt);
+    load_b<DQ, STRIPED>(B1, g, n0, min(1, nk - 1) * kBK, pt);
     __syncthreads();  // LUTs visible
-    store_b<DQ>(B0, smem, 0, pt);
-    UNIFUR_WAIT_VMCNT(16);  // X of step 0 landed (step 1's 16 loads may be in flight)
+    store_b<DQ, STRIPED>(B0, smem, 0, pt);
+    UNIFUR_WAIT_VMCNT(kStepLoads<STRIPED>);  // X of step 0 landed (step 1's 16 loads may be in flight)
     __syncthreads();
     int sa = 0;  // X stage of step kt
     int kt = 0;
     for (; kt + 1 < nk; kt += 2) {
       int s2 = sa >= 1 ? sa - 1 : sa + 2;  // (kt + 2) % 3
       load_a(xr, g.K, row0, min(kt + 2, nk - 1) * kBK, awave + s2 * kATileBytes, lane);
-      load_b<DQ>(B0, g, n0, min(kt + 2, nk - 1) * kBK, pt);
-      store_b<DQ>(B1, smem, 1, pt);
-      UNIFUR_WAIT_VMCNT(16);
+      load_b<DQ, STRIPED>(B0, g, n0, min(kt + 2, nk - 1) * kBK, pt);
+      store_b<DQ, STRIPED>(B1, smem, 1, pt);
+      UNIFUR_WAIT_VMCNT(kStepLoads<STRIPED>);
       __syncthreads();
       sa = sa == 2 ? 0 : sa + 1;
       s2 = sa >= 1 ? sa - 1 : sa + 2;
       load_a(xr, g.K, row0, min(kt + 3, nk - 1) * kBK, awave + s2 * kATileBytes, lane);
-      load_b<DQ>(B1, g, n0, min(kt + 3, nk - 1) * kBK, pt);
-      store_b<DQ>(B0, smem, 0, pt);
-      UNIFUR_WAIT_VMCNT(16);
+      load_b<DQ, STRIPED>(B1, g, n0, min(kt + 3, nk - 1) * kBK, pt);
+      store_b<DQ, STRIPED>(B0, smem, 0, pt);
+      UNIFUR_WAIT_VMCNT(kStepLoads<STRIPED>);
       __syncthreads();
       sa = sa == 2 ? 0 : sa + 1;
     }
@@ -331,21 +357,21 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   }
 }
 
-template <bool DQ, bool YBF16, bool LORA>
+template <bool DQ, bool YBF16, bool LORA, bool STRIPED>
 hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   const uint64_t bit = 1ull << (dev & 63);
-  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<DQ, YBF16, LORA>);
+  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<DQ, YBF16, LORA, STRIPED>);
   if (!(done.load(std::memory_order_acquire) & bit)) {
     e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmSmem);
     if (e != hipSuccess) return e;
     done.fetch_or(bit, std::memory_order_acq_rel);
   }
   const int grid = ((g.M + kBM - 1) / kBM) * g.tiles_n;
-  gemm_kernel<DQ, YBF16, LORA><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
+  gemm_kernel<DQ, YBF16, LORA, STRIPED><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
   return hipGetLastError();
 }
 
@@ -438,7 +464,7 @@ hipError_t launch_lora_xa_bf16(const uint16_t* x, const float* a, int M, int K, 
 
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
                        const float* bias, const float* lora_xa, const float* lora_b, int lora_rank, void* y,
-                       bool y_bf16, hipStream_t stream) {
+                       bool y_bf16, bool striped, hipStream_t stream) {
   GemmArgs g{};
   g.x = x;
   g.packed = packed;
@@ -456,8 +482,9 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
   g.tiles_n = N / kBN;
   const bool dq = scales.kind == kScalesDQ;
   const bool lora = lora_xa != nullptr;
-#define UNIFUR_GEMM_CASE(D, B, R) \
-  if (dq == D && y_bf16 == B && lora == R) return launch_g<D, B, R>(g, stream);
+#define UNIFUR_GEMM_CASE(D, B, R)                                                     \
+  if (dq == D && y_bf16 == B && lora == R)                                          \
+    return striped ? launch_g<D, B, R, true>(g, stream) : launch_g<D, B, R, false>(g, stream);
   UNIFUR_GEMM_CASE(true, true, true)
   UNIFUR_GEMM_CASE(true, true, false)
   UNIFUR_GEMM_CASE(true, false, true)

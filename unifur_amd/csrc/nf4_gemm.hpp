@@ -23,8 +23,10 @@ hipError_t launch_lora_xa_bf16(const uint16_t* x, const float* a, int M, int K, 
                                float* xa, hipStream_t stream);
 
 // Y[M, N] = X deq(W) (+ bias) (+ xa B); xa from launch_lora_xa_bf16 or null.
+// The weight is in the reference's row-major layout, or striped
+// (nf4_layout.hpp) when striped is set.
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
                        const float* bias, const float* lora_xa, const float* lora_b, int lora_rank, void* y,
-                       bool y_bf16, hipStream_t stream);
+                       bool y_bf16, bool striped, hipStream_t stream);
 
 }  // namespace unifur

@@ -44,4 +44,29 @@ GemvPlan plan_gemv(int rows, int d_in, const int* d_out, int nweights, bool pair
 hipError_t launch_gemv(const GemvPlan& p, const void* x, bool x_bf16, int rows, int d_in, const GemvWeight* weights,
                        int nweights, hipStream_t stream);
 
+// ---- the same GEMV over weights in the striped layout (nf4_layout.hpp) ----
+// No workspace: each workgroup reduces its 16-column stripe over all of d_in.
+// d_out of every weight a multiple of 64; x [rows, d_in], rows in 1..4 (1..2
+// for the SwiGLU pair); the GemvWeight fields counters and partials are unused.
+
+struct StripedPlan {
+  int waves;          // waves per workgroup: 4, 8 or 16
+  int rows_per_wave;  // a multiple of 64
+  int stripes;        // workgroups
+};
+
+struct StripedArgs {
+  const void* x;  // [rows, d_in] f32 or bf16
+  int d_in;
+  int rows_per_wave;
+  int nweights;
+  GemvWeight w[kMaxGemvWeights];
+  int stripe_begin[kMaxGemvWeights + 1];  // prefix sums of stripes per weight
+};
+
+StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights, bool pair);
+
+hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16, int rows, int d_in,
+                               const GemvWeight* weights, int nweights, bool pair, hipStream_t stream);
+
 }  // namespace unifur

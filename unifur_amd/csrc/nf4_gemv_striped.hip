@@ -1,0 +1,420 @@
+// nf4_gemv_striped.hip -- decode GEMV over the column-striped weight layout.
+//
+// y[t][o] = sum_i x[t][i] * deq(W)[i][o] (+ bias[o]) (+ LoRA), W an NF4
+// weight [d_in = K, d_out = N] stored striped (nf4_layout.hip): 16-column
+// stripe s holds K rows of 8 code bytes back to back, scales are [N/64][K].
+// This is Nf4Linear::forward (src/qwennet.rs:238-241, dequantize then
+// linear) and QloraLinear::forward (src/qwennet.rs:325-345) for a few rows
+// of x, without materialising the weight.
+//
+// One workgroup owns one stripe over all of K, so there is no cross-workgroup
+// reduction: its W waves take consecutive row ranges, and inside a wave lane
+// l takes row 64 c + l of every 64-row chunk c -- a wave's load of a chunk is
+// 512 contiguous bytes of codes, 64 contiguous scale codes and 64 contiguous
+// activations per x row.  Each wave keeps D chunks in flight in a register
+// ring: chunk c + D is requested as soon as chunk c has been consumed, so the
+// memory stream and the decode overlap.  (Requesting everything up front
+// stalls the issue of the later loads behind the memory system, and the
+// decode then starts only once most data has arrived.)
+//
+// Decode: a byte of codes is looked up in a 256-entry LDS table holding
+// {level[lo], level[hi]} (32 copies, lane l reads copy l % 32, so the 64-bit
+// reads of 32 lanes hit distinct bank pairs); the address is one v_perm_b32
+// (byte << 8 | lane offset).  Per row and 64-block the activation is folded
+// with the block scale once (xs = x * scale), then one FMA per code.  The
+// lookups of chunk c + 1 are issued before the FMAs of chunk c.
+//
+// Reduction: the 16 column sums of each lane are added over the 64 lanes by
+// a butterfly that halves the live columns at each step (permlane32 and
+// permlane16 swaps, then row_mirror and row_half_mirror DPP), so every lane
+// ends with one column; the W waves are then added through LDS in a fixed
+// order.  Results are deterministic run to run.
+//
+// PAIR mode computes gate and up of a SwiGLU block in the same pass over x
+// and stores silu(gate x) * (up x) (src/qwennet.rs:816-819,
+// src/tensor_ext.rs:87-90).
+#include "nf4_gemv.hpp"
+#include "nf4_layout.hpp"
+
+#include <atomic>
+
+namespace unifur {
+namespace {
+
+constexpr int kLutCopies = 32;
+constexpr int kLutBytes = 256 * kLutCopies * 8;  // 64 KiB, at LDS address 0
+constexpr int kDqLutOffset = kLutBytes;          // one 256-entry DQ scale table per weight
+constexpr int kLevelsOffset = kDqLutOffset + 2 * 256 * 4;
+constexpr int kStripedSmem = kLevelsOffset + 16 * 4;
+
+typedef const __attribute__((address_space(4))) float const_f32;
+typedef __attribute__((address_space(3))) const f32x2 lds_f32x2;
+
+__device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t as_u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float silu_f32(float z) { return z * (1.0f / (1.0f + __expf(-z))); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// One chunk of one weight in flight: this lane's 8 code bytes and its scale.
+struct ChunkW {
+  u32x2 code;
+  uint32_t scale;  // f32 absmax bits, or the u8 DQ scale code
+};
+
+template <int T, int NW>
+struct Chunk {
+  ChunkW w[NW];
+  uint32_t x[T];  // f32 bits, or bf16 in the low half
+};
+
+// Wave-uniform resources of one weight, bounded to this wave's rows so that
+// every load past them reads zero (and touches no memory).
+struct WaveW {
+  __amdgpu_buffer_rsrc_t codes, scales;
+};
+
+template <int T, int NW, bool XBF16, bool DQ>
+__device__ __forceinline__ void issue_chunk(Chunk<T, NW>& c, const WaveW (&ww)[NW],
+                                            const __amdgpu_buffer_rsrc_t (&xr)[T], int chunk, int lane) {
+  const uint32_t row = (uint32_t)(chunk * 64 + lane);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    c.w[w].code = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
+    if constexpr (DQ)
+      c.w[w].scale = __builtin_amdgcn_raw_buffer_load_b8(ww[w].scales, row, 0, 0);
+    else
+      c.w[w].scale = __builtin_amdgcn_raw_buffer_load_b32(ww[w].scales, row * 4u, 0, 0);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    if constexpr (XBF16)
+      c.x[t] = __builtin_amdgcn_raw_buffer_load_b16(xr[t], row * 2u, 0, 0);
+    else
+      c.x[t] = __builtin_amdgcn_raw_buffer_load_b32(xr[t], row * 4u, 0, 0);
+  }
+}
+
+// Level pairs of this lane's 8 code bytes and the block scale, per weight.
+template <int NW>
+struct Looked {
+  f32x2 lv[NW][8];
+  float scale[NW];
+};
+
+template <int T, int NW, bool DQ>
+__device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW>& c, const float* dq_lut,
+                                       uint32_t lane_off) {
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    o.scale[w] = DQ ? dq_lut[w * 256 + (c.w[w].scale & 0xffu)] : as_f(c.w[w].scale);
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        // LDS byte address = (byte b of the dword) << 8 | lane_off; the LUT
+        // sits at LDS address 0 (this kernel has no static LDS)
+        const uint32_t addr = perm_b32(c.w[w].code[d], lane_off, 0x0c0c0000u | ((4u + b) << 8));
+        o.lv[w][d * 4 + b] = *reinterpret_cast<lds_f32x2*>((size_t)addr);
+      }
+  }
+}
+
+// Sum v[16] over the 64 lanes; lane l ends with column ci(l) (see below) in
+// its return value (lanes l, l^1, l^2, l^3 hold the same column).
+__device__ __forceinline__ float wave_column_sum(const float (&acc)[16], int lane) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {  // lane bit 5: lanes 0-31 keep columns 0-7, 32-63 keep 8-15
+    auto r = __builtin_amdgcn_permlane32_swap(as_u(acc[i]), as_u(acc[i + 8]), false, false);
+    v[i] = as_f(r[0]) + as_f(r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // lane bit 4 (odd rows of 16 keep the upper half)
+    auto r = __builtin_amdgcn_permlane16_swap(as_u(v[i]), as_u(v[i + 4]), false, false);
+    v[i] = as_f(r[0]) + as_f(r[1]);
+  }
+  {  // lane bit 3: partner 15 - l within the row (row_mirror)
+    const bool hi = (lane & 8) != 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float send = hi ? v[i] : v[i + 2];
+      const float keep = hi ? v[i + 2] : v[i];
+      v[i] = keep + as_f(__builtin_amdgcn_update_dpp(0u, as_u(send), 0x140, 0xF, 0xF, false));
+    }
+  }
+  float col;
+  {  // lane bit 2: partner 7 - l within the half row (row_half_mirror)
+    const bool hi = (lane & 4) != 0;
+    const float send = hi ? v[0] : v[1];
+    const float keep = hi ? v[1] : v[0];
+    col = keep + as_f(__builtin_amdgcn_update_dpp(0u, as_u(send), 0x141, 0xF, 0xF, false));
+  }
+  // the four lanes of a quad now hold the same column: add them
+  col += as_f(__builtin_amdgcn_update_dpp(0u, as_u(col), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  col += as_f(__builtin_amdgcn_update_dpp(0u, as_u(col), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  return col;
+}
+
+__device__ __forceinline__ int wave_column_index(int lane) {
+  return ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
+}
+
+__device__ __forceinline__ float epilogue_value(const GemvWeight& W, float base, int t, int gcol) {
+  float y = base;
+  if (W.bias) y += W.bias[gcol];
+  if (W.lora_xa) {
+    // base(x) + ((x A) B) * scaling (src/qwennet.rs:325-344, src/quantize.rs:619-624)
+    float l = 0.0f;
+    for (int j = 0; j < W.lora_rank; ++j)
+      l = __builtin_fmaf(W.lora_xa[t * W.lora_rank + j], W.lora_b[(size_t)j * W.d_out + gcol], l);
+    y += l * W.lora_scaling;
+  }
+  return y;
+}
+
+__device__ __forceinline__ void store_y(const GemvWeight& W, size_t idx, float y) {
+  if (W.y_bf16)
+    reinterpret_cast<uint16_t*>(W.y)[idx] = (uint16_t)(pack_bf16x2(y, 0.0f) & 0xffffu);
+  else
+    reinterpret_cast<float*>(W.y)[idx] = y;
+}
+
+template <int T, int W, int D, bool XBF16, bool DQ, bool PAIR>
+__global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
+  constexpr int NW = PAIR ? 2 : 1;
+  static_assert(D % 2 == 0, "the lookup double buffer is indexed by chunk parity");
+  static_assert(W >= 4, "the LUT build needs 256 threads");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // which weight (several weights of one x can share a launch) and stripe
+  int wi = 0;
+  if constexpr (!PAIR) {
+#pragma unroll
+    for (int i = 1; i < kMaxGemvWeights; ++i)
+      if (i < a.nweights && (int)blockIdx.x >= a.stripe_begin[i]) wi = i;
+  }
+  const int s = blockIdx.x - a.stripe_begin[wi];
+  const int K = a.d_in;
+  const int kw = wave * a.rows_per_wave;
+  const int nrows = max(0, min(a.rows_per_wave, K - kw));
+  const int nchunks = (nrows + 63) / 64;
+
+  WaveW ww[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const GemvWeight& G = a.w[PAIR ? w : wi];
+    ww[w].codes = make_rsrc(G.packed + ((size_t)s * K + kw) * 8, (uint32_t)nrows * 8u);
+    const size_t srow = (size_t)(s / 4) * K + kw;
+    ww[w].scales = DQ ? make_rsrc(G.scales.dq_codes + srow, (uint32_t)nrows)
+                      : make_rsrc(G.scales.absmax + srow, (uint32_t)nrows * 4u);
+  }
+  __amdgpu_buffer_rsrc_t xr[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const size_t off = (size_t)t * K + kw;
+    xr[t] = XBF16 ? make_rsrc(static_cast<const uint16_t*>(a.x) + off, (uint32_t)nrows * 2u)
+                  : make_rsrc(static_cast<const float*>(a.x) + off, (uint32_t)nrows * 4u);
+  }
+
+  // prologue: the first D chunks
+  Chunk<T, NW> ring[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, j, lane);
+
+  // LUTs.  The scale of scales is read through the scalar cache so that it
+  // does not queue behind the chunk loads.
+  float* lv16 = reinterpret_cast<float*>(smem + kLevelsOffset);
+  if (tid == 0) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) lv16[c] = __uint_as_float(level_bits(c));
+  }
+  __syncthreads();
+  if (tid < 256) {
+    const float lo = lv16[tid & 15], hi = lv16[tid >> 4];
+    const f32x4 v = {lo, hi, lo, hi};
+    f32x4* dst = reinterpret_cast<f32x4*>(smem + tid * (kLutCopies * 8));
+#pragma unroll
+    for (int j = 0; j < kLutCopies / 2; ++j) dst[(j + tid) & (kLutCopies / 2 - 1)] = v;
+    if constexpr (DQ) {
+      float* dq_lut = reinterpret_cast<float*>(smem + kDqLutOffset);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        // ((float)q / 255.0f) * scale_of_scales (src/quantize.rs:349)
+        const float sos = *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales);
+        dq_lut[w * 256 + tid] = ((float)tid / 255.0f) * sos;
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+
+  const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
+  const uint32_t lane_off = (uint32_t)(lane & (kLutCopies - 1)) * 8u;
+  float acc[NW][T][16];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[w][t][i] = 0.0f;
+
+  Looked<NW> lk[2];
+  lookup<T, NW, DQ>(lk[0], ring[0], dq_lut, lane_off);
+  for (int c0 = 0; c0 < nchunks; c0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      // chunk c0 + j is in ring[j] and already looked up in lk[j & 1];
+      // chunk c0 + j + 1 is in ring[(j + 1) % D] (refilled at step 0 when
+      // j + 1 == D).  Chunks past this wave's rows read as zero: x = 0.
+      __builtin_amdgcn_sched_barrier(0);
+      lookup<T, NW, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, lane_off);
+      float xs[NW][T];
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const float xv = XBF16 ? bf16_bits_to_f32(ring[j].x[t] & 0xffffu) : as_f(ring[j].x[t]);
+          xs[w][t] = xv * lk[j & 1].scale[w];  // x * block scale, once per row
+        }
+      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, c0 + j + D, lane);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            acc[w][t][2 * i] = __builtin_fmaf(xs[w][t], lk[j & 1].lv[w][i].x, acc[w][t][2 * i]);
+            acc[w][t][2 * i + 1] = __builtin_fmaf(xs[w][t], lk[j & 1].lv[w][i].y, acc[w][t][2 * i + 1]);
+          }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // reduce: over the lanes of each wave, then over the waves (LUT space reused)
+  float col[NW][T];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int t = 0; t < T; ++t) col[w][t] = wave_column_sum(acc[w][t], lane);
+  __syncthreads();  // every wave is done with the LUT
+  float* red = reinterpret_cast<float*>(smem);
+  if ((lane & 3) == 0) {
+    const int ci = wave_column_index(lane);
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int t = 0; t < T; ++t) red[((w * T + t) * W + wave) * 16 + ci] = col[w][t];
+  }
+  __syncthreads();
+  if (tid >= T * 16) return;
+  const int t = tid / 16, cc = tid % 16;
+  const GemvWeight& G = a.w[wi];
+  const int gcol = s * kStripeCols + cc;
+  float sum[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    float v = 0.0f;
+#pragma unroll
+    for (int q = 0; q < W; ++q) v += red[((w * T + t) * W + q) * 16 + cc];
+    sum[w] = v;
+  }
+  float y = epilogue_value(G, sum[0], t, gcol);
+  if constexpr (PAIR) y = silu_f32(y) * epilogue_value(a.w[1], sum[1], t, gcol);  // silu(gate x) * up x
+  store_y(G, (size_t)t * G.d_out + gcol, y);
+}
+
+// ================================================================ launching ==
+
+constexpr int kDepth = 4;
+
+template <int T, int W, bool XBF16, bool DQ, bool PAIR>
+hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
+  auto* fn = &gemv_striped_kernel<T, W, kDepth, XBF16, DQ, PAIR>;
+  static std::atomic<uint64_t> done{0};  // dynamic LDS above 64 KiB: once per device
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(done.load(std::memory_order_acquire) & bit)) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kStripedSmem);
+    if (e != hipSuccess) return e;
+    done.fetch_or(bit, std::memory_order_acq_rel);
+  }
+  fn<<<grid, W * 64, kStripedSmem, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <int T, int W, bool PAIR>
+hipError_t launch_flags(const StripedArgs& a, int grid, bool xbf16, bool dq, hipStream_t stream) {
+  if (xbf16) return dq ? launch_t<T, W, true, true, PAIR>(a, grid, stream) : launch_t<T, W, true, false, PAIR>(a, grid, stream);
+  return dq ? launch_t<T, W, false, true, PAIR>(a, grid, stream) : launch_t<T, W, false, false, PAIR>(a, grid, stream);
+}
+
+// 16 waves only where the registers fit at four waves per SIMD: one or two
+// activation rows of a single weight (the plan never asks for more).
+template <int T, bool PAIR>
+hipError_t dispatch_w(const StripedArgs& a, int grid, int waves, bool xbf16, bool dq, hipStream_t stream) {
+  if (waves == 4) return launch_flags<T, 4, PAIR>(a, grid, xbf16, dq, stream);
+  if (waves == 8) return launch_flags<T, 8, PAIR>(a, grid, xbf16, dq, stream);
+  if constexpr (T <= 2 && !PAIR) {
+    if (waves == 16) return launch_flags<T, 16, PAIR>(a, grid, xbf16, dq, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights, bool pair) {
+  StripedPlan p{};
+  int stripes = 0;
+  for (int i = 0; i < (pair ? 1 : nweights); ++i) stripes += d_out[i] / kStripeCols;
+  const int chunks = (d_in + 63) / 64;
+  // Enough waves for about 16 per CU over 256 CUs, but no more waves than
+  // 64-row chunks.
+  const int max_waves = (pair || rows > 2) ? 8 : 16;
+  int waves = 4;
+  while (waves < max_waves && (long)stripes * waves < 4096 && waves * 2 <= chunks) waves *= 2;
+  p.waves = waves;
+  p.rows_per_wave = (chunks + waves - 1) / waves * 64;
+  p.stripes = stripes;
+  return p;
+}
+
+hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16, int rows, int d_in,
+                               const GemvWeight* weights, int nweights, bool pair, hipStream_t stream) {
+  StripedArgs a{};
+  a.x = x;
+  a.d_in = d_in;
+  a.rows_per_wave = p.rows_per_wave;
+  a.nweights = nweights;
+  int s = 0;
+  for (int i = 0; i < nweights; ++i) {
+    a.w[i] = weights[i];
+    a.stripe_begin[i] = pair ? 0 : s;
+    if (!pair || i == 0) s += weights[i].d_out / kStripeCols;
+  }
+  for (int i = nweights; i <= kMaxGemvWeights; ++i) a.stripe_begin[i] = s;
+  const bool dq = weights[0].scales.kind == kScalesDQ;
+  if (pair) {
+    if (rows == 1) return dispatch_w<1, true>(a, s, p.waves, x_bf16, dq, stream);
+    if (rows == 2) return dispatch_w<2, true>(a, s, p.waves, x_bf16, dq, stream);
+    return hipErrorInvalidValue;
+  }
+  switch (rows) {
+    case 1: return dispatch_w<1, false>(a, s, p.waves, x_bf16, dq, stream);
+    case 2: return dispatch_w<2, false>(a, s, p.waves, x_bf16, dq, stream);
+    case 3: return dispatch_w<3, false>(a, s, p.waves, x_bf16, dq, stream);
+    case 4: return dispatch_w<4, false>(a, s, p.waves, x_bf16, dq, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace unifur

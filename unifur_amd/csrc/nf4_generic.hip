@@ -11,7 +11,8 @@
 //     (src/quantize.rs:619-624); the second factor and the scaling are
 //     applied in the consuming kernel's epilogue.
 //   * silu_mul: h = silu(g) * u, the middle of QwenMlp::forward
-//     (src/qwennet.rs:816-819) when gate and up ran as separate launches.
+//     (src/qwennet.rs:816-819) when gate and up ran as separate launches;
+//     the bf16 variant feeds the MFMA GEMM of the down projection.
 #include "nf4_generic.hpp"
 
 namespace unifur {
@@ -122,6 +123,14 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
   }
 }
 
+__global__ void silu_mul_bf16_kernel(const float* __restrict__ g, const float* __restrict__ u, size_t n,
+                                     uint16_t* __restrict__ h) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const float z = g[i];
+    h[i] = (uint16_t)(pack_bf16x2((z * (1.0f / (1.0f + __expf(-z)))) * u[i], 0.0f) & 0xffffu);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_gemm_f32(const void* x, bool x_bf16, const float* w, int M, int K, int N, const Epilogue& e,
@@ -150,6 +159,14 @@ hipError_t launch_silu_mul(const float* g, const float* u, size_t n, float* h, h
   if (blocks > 4096) blocks = 4096;
   if (blocks == 0) return hipSuccess;
   silu_mul_kernel<<<(unsigned)blocks, 256, 0, stream>>>(g, u, n, h);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_bf16(const float* g, const float* u, size_t n, uint16_t* h, hipStream_t stream) {
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks == 0) return hipSuccess;
+  silu_mul_bf16_kernel<<<(unsigned)blocks, 256, 0, stream>>>(g, u, n, h);
   return hipGetLastError();
 }
 

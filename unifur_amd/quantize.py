@@ -266,14 +266,21 @@ class LoraAdapter:
 # ------------------------------------------------------------------- linears --
 
 def _weight_struct(packed: PackedNf4Tensor, d_in: int, d_out: int) -> L.Weight:
-    return L.Weight(packed.codes.data_ptr(), packed.scales_struct(), d_in, d_out)
+    return L.Weight(packed.codes.data_ptr(), packed.scales_struct(), d_in, d_out, L.LAYOUT_ROW_MAJOR)
 
 
 class Nf4Linear:
     """A frozen NF4-resident linear with weight [d_input, d_output]
-    (src/qwennet.rs:161-242); forward never materialises the weight."""
+    (src/qwennet.rs:161-242); forward never materialises the weight.
 
-    def __init__(self, packed: PackedNf4Tensor, d_input: int, d_output: int, bias: Optional[torch.Tensor] = None):
+    The packed weight is held on the device in the column-striped layout
+    when d_output % 64 == 0 (``striped=None`` picks it then): a byte
+    permutation of the reference's packed codes and scales, same size, that
+    the decode GEMV streams contiguously.  ``packed()`` rebuilds the
+    reference-layout tensor bit for bit."""
+
+    def __init__(self, packed: PackedNf4Tensor, d_input: int, d_output: int, bias: Optional[torch.Tensor] = None,
+                 striped: Optional[bool] = None):
         if len(packed) != d_input * d_output:
             raise ValueError(f"packed weight holds {len(packed)} values, [{d_input}, {d_output}] needs "
                              f"{d_input * d_output}")
@@ -281,22 +288,40 @@ class Nf4Linear:
             _require_cuda(bias, "bias")
             if bias.dtype != torch.float32 or bias.numel() != d_output:
                 raise ValueError("bias must be float32 [d_output]")
-        self._packed = packed
+        if striped is None:
+            striped = d_output % 64 == 0
+        if striped and d_output % 64 != 0:
+            raise ValueError("the striped layout needs d_output % 64 == 0")
         self._d_in = int(d_input)
         self._d_out = int(d_output)
         self.bias = bias
+        self._striped = bool(striped)
+        self._len = len(packed)
+        self._dq = packed.is_double_quantized()
+        self._sos = packed.scale_of_scales
+        if self._striped:
+            src = _weight_struct(packed, d_input, d_output)
+            self._codes = torch.empty_like(packed.codes)
+            self._scales = torch.empty_like(packed.dq_codes if self._dq else packed.absmax)
+            L.check(L.lib().unifur_nf4_stripe_weight(ctypes.byref(src), self._codes.data_ptr(),
+                                                     self._scales.data_ptr(), _stream()))
+            self._packed = None
+        else:
+            self._codes = packed.codes
+            self._scales = packed.dq_codes if self._dq else packed.absmax
+            self._packed = packed
 
     @staticmethod
     def from_packed(packed: PackedNf4Tensor, d_input: int, d_output: int,
-                    bias: Optional[torch.Tensor] = None) -> "Nf4Linear":
-        return Nf4Linear(packed, d_input, d_output, bias)
+                    bias: Optional[torch.Tensor] = None, striped: Optional[bool] = None) -> "Nf4Linear":
+        return Nf4Linear(packed, d_input, d_output, bias, striped)
 
     @staticmethod
-    def from_values(values: torch.Tensor, d_input: int, d_output: int) -> "Nf4Linear":
+    def from_values(values: torch.Tensor, d_input: int, d_output: int, striped: Optional[bool] = None) -> "Nf4Linear":
         """src/qwennet.rs:198-205: quantize [d_input, d_output] row-major values,
         always with double quantization."""
         return Nf4Linear(PackedNf4Tensor.quantize(values.contiguous().view(-1)).with_double_quantization(),
-                         d_input, d_output)
+                         d_input, d_output, striped=striped)
 
     def d_input(self) -> int:
         return self._d_in
@@ -304,18 +329,36 @@ class Nf4Linear:
     def d_output(self) -> int:
         return self._d_out
 
+    def is_striped(self) -> bool:
+        return self._striped
+
     def resident_bytes(self) -> int:
-        return self._packed.resident_bytes()
+        return PackedNf4Tensor.estimated_resident_bytes(self._len, self._dq)
 
     def packed(self) -> PackedNf4Tensor:
-        return self._packed
+        """The reference-layout packed tensor (rebuilt on the device from the
+        striped copy when the layer holds that)."""
+        if self._packed is not None:
+            return self._packed
+        codes = torch.empty_like(self._codes)
+        scales = torch.empty_like(self._scales)
+        w = self.weight_struct()
+        L.check(L.lib().unifur_nf4_unstripe_weight(ctypes.byref(w), codes.data_ptr(), scales.data_ptr(), _stream()))
+        if self._dq:
+            return PackedNf4Tensor(codes, self._len, dq_codes=scales, scale_of_scales=self._sos)
+        return PackedNf4Tensor(codes, self._len, absmax=scales)
 
     def dequantized_weight(self) -> torch.Tensor:
         """src/qwennet.rs:230-236."""
-        return self._packed.dequantize().view(self._d_in, self._d_out)
+        return self.packed().dequantize().view(self._d_in, self._d_out)
 
     def weight_struct(self) -> L.Weight:
-        return _weight_struct(self._packed, self._d_in, self._d_out)
+        if self._dq:
+            sc = L.Scales(L.SCALES_DOUBLE_QUANTIZED, None, self._scales.data_ptr(), self._sos.data_ptr())
+        else:
+            sc = L.Scales(L.SCALES_F32, self._scales.data_ptr(), None, None)
+        return L.Weight(self._codes.data_ptr(), sc, self._d_in, self._d_out,
+                        L.LAYOUT_STRIPED if self._striped else L.LAYOUT_ROW_MAJOR)
 
     def _forward(self, x: torch.Tensor, lora: Optional[LoraAdapter], out_dtype: Optional[torch.dtype]):
         _require_cuda(x, "x")
