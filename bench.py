@@ -1,20 +1,24 @@
 """Benchmark of the NF4 quantized-linear hot path on one MI355X.
 
 Headline (BASELINE.json metric, configs[1]): the decode GEMV
-y[1, 11008] = x[1, 4096] . deq(W), W the reference's [4096, 11008] packed NF4
-weight with double-quantized scales (as Nf4Linear::from_values builds it,
-src/qwennet.rs:198-205), f32 activations and accumulation.  One step = one
-GEMV launch over one batch.  Weights are resident in HBM and rotated over
+y[1, 11008] = x[1, 4096] . deq(W), W the reference's [4096, 11008] NF4
+weight (logical 11008 x 4096, blocks of 64 along d_out) with double-quantized
+scales, as Nf4Linear::from_values builds it (src/qwennet.rs:198-205), held on
+the device in the column-striped layout; f32 activations and accumulation.
+One step = one GEMV launch.  The weights are resident in HBM and rotated over
 enough copies (>= 512 MiB, twice the 256 MiB Infinity Cache) that every step
 streams its weight from HBM ("cold").  value = algorithmic bytes per step *
-steps / timed seconds.
+steps / timed seconds, the steps replayed from a HIP graph.
 
-Also reported in the same JSON line (not the headline): warm GEMV, NF4
-dequantize and quantize of the config-1 4096x4096 matrix, each with its
-kernel's roofline fraction, and the CPU baseline (the oracle's restatement
-of the reference's CPU path, timed on this host).
+The same JSON line carries the GEMV kernel's roofline (HIP events on its
+launch stream), the CPU baseline (the oracle's restatement of the
+reference's CPU path, timed on this host) and secondary figures for every
+BASELINE config: quantize / dequantize (config 1), the MFMA prefill GEMM
+with LoRA (config 3, TFLOP/s), the SwiGLU block at T = 1, 16, 512
+(config 4) and the Qwen2-0.5B-shaped projection set (config 5: whole-model
+quantize pass, per-token decode at batch 1 and 32).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
 from __future__ import annotations
 
@@ -33,22 +37,22 @@ METRIC = "NF4 dequant/GEMV GB/s and prefill GEMM TFLOP/s, % of MI355X roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 MALL_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemv_config2.txt")
 
 
-def gemv_bytes(d_in: int, d_out: int, dq: bool, x_bytes: int = 4, y_bytes: int = 4) -> int:
+def gemv_bytes(d_in: int, d_out: int, dq: bool, x_bytes: int = 4, y_bytes: int = 4, rows: int = 1) -> int:
     """Algorithmic HBM bytes of one GEMV: packed codes + scales + x + y."""
     n = d_in * d_out
     nb = (n + 63) // 64
     scales = nb + 4 if dq else 4 * nb
-    return (n + 1) // 2 + scales + d_in * x_bytes + d_out * y_bytes
+    return (n + 1) // 2 + scales + rows * (d_in * x_bytes + d_out * y_bytes)
 
 
-def kernel_ms(torch, fn, iters: int) -> float:
-    """Average GPU time of fn() measured with event pairs on the launch stream.
-
-    A long sleep kernel is queued first so that every launch below is already
-    enqueued when the GPU reaches it: the event pairs then bracket the kernel
-    itself, not host-side launch latency."""
+def event_ms(torch, fn, iters: int) -> float:
+    """Median GPU time of fn(i) from one event pair per launch on the launch
+    stream.  A long sleep kernel is queued first so that every launch is
+    enqueued before the GPU reaches it: the pairs bracket the kernels, not
+    host launch latency."""
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     torch.cuda.synchronize()
@@ -62,90 +66,138 @@ def kernel_ms(torch, fn, iters: int) -> float:
     return times[len(times) // 2]
 
 
+def capture(torch, fn, n: int):
+    """A HIP graph of fn(0) .. fn(n - 1) on a side stream (None if capture fails)."""
+    try:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            # one eager pass on the capture stream first: the library sizes its
+            # per-stream workspace (hipMalloc) outside the capture
+            for i in range(n):
+                fn(i)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                for i in range(n):
+                    fn(i)
+        torch.cuda.current_stream().wait_stream(s)
+        g.replay()
+        torch.cuda.synchronize()
+        return g
+    except Exception as e:  # noqa: BLE001 - report and time eagerly
+        print(f"# graph capture unavailable ({e}); timing eager launches", file=sys.stderr)
+        return None
+
+
+def replay_event_ms(torch, graph, launches: int, reps: int = 20) -> float:
+    """Per-launch GPU time of a graph of `launches` kernels: one HIP event pair
+    on the replay stream around `reps` back-to-back replays."""
+    graph.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * launches)
+
+
+def graph_ms(torch, graph, reps: int) -> float:
+    """Average wall time of one graph replay over reps back-to-back replays."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / reps
+
+
+def rand_weights(torch, Q, d_in, d_out, gen, dq=True, striped=True):
+    w = torch.randn(d_in * d_out, device="cuda", generator=gen) * 0.02
+    p = Q.PackedNf4Tensor.quantize(w)
+    if dq:
+        p = p.with_double_quantization()
+    del w
+    return Q.Nf4Linear.from_packed(p, d_in, d_out, striped=striped)
+
+
+# --------------------------------------------------------------- config 2 --
+
 def bench_gemv(torch, Q, L, args) -> dict:
     d_in, d_out = 4096, 11008
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(0x4E463458)
-    w = torch.randn(d_in * d_out, device=dev, generator=g) * 0.02
-    base = Q.PackedNf4Tensor.quantize(w).with_double_quantization()
-    del w
+    base = rand_weights(torch, Q, d_in, d_out, g)
     nbytes = gemv_bytes(d_in, d_out, dq=True)
     copies = max(2, -(-(2 * MALL_BYTES) // nbytes))  # >= 512 MiB of weights
-    layers = []
-    for _ in range(copies):
-        p = Q.PackedNf4Tensor(base.codes.clone(), len(base), dq_codes=base.dq_codes.clone(),
-                              scale_of_scales=base.scale_of_scales.clone())
-        layers.append(Q.Nf4Linear.from_packed(p, d_in, d_out))
+    layers = [base] + [Q.Nf4Linear.from_packed(base.packed(), d_in, d_out) for _ in range(copies - 1)]
     x = torch.randn(1, d_in, device=dev, generator=g)
     y = torch.empty(1, d_out, device=dev)
-    ws_bytes = L.lib().unifur_nf4_linear_workspace_size(1, d_in, d_out, L.F32, 0)
-    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     structs = [lay.weight_struct() for lay in layers]
     lib = L.lib()
 
     def launch(i: int) -> None:
         st = lib.unifur_nf4_linear_forward(x.data_ptr(), L.F32, 1, ctypes.byref(structs[i % copies]), None, None,
-                                           y.data_ptr(), L.F32, ws.data_ptr(), ws_bytes,
-                                           torch.cuda.current_stream().cuda_stream)
+                                           y.data_ptr(), L.F32, None, 0, torch.cuda.current_stream().cuda_stream)
         if st != 0:
             L.check(st)
 
-    # sanity: GEMV of copy 0 against torch's f32 matvec of the dequantized weight
+    # sanity: against torch's f32 matvec of the dequantized weight
     launch(0)
     ref = x @ layers[0].dequantized_weight()
     torch.cuda.synchronize()
     rel = float((y - ref).abs().max() / ref.abs().max())
     if not rel < 1e-4:
         raise RuntimeError(f"GEMV sanity check failed: max rel error {rel:.3e}")
-
     for i in range(args.warmup):
         launch(i)
+    graph = capture(torch, launch, copies)
     steps = args.steps
-    # Whole-job timing: K launches replayed from a HIP graph (launch-bound
-    # otherwise: one GEMV is a few microseconds), falling back to eager.
-    graph = None
-    try:
-        graph = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            with torch.cuda.graph(graph, stream=s):
-                for i in range(copies):
-                    launch(i)
-        torch.cuda.current_stream().wait_stream(s)
-        graph.replay()
-        torch.cuda.synchronize()
-    except Exception as e:  # noqa: BLE001 - report and time eagerly
-        print(f"# graph capture unavailable ({e}); timing eager launches", file=sys.stderr)
-        graph = None
-    reps = -(-steps // copies) if graph is not None else 0
-    if graph is not None:
-        steps = reps * copies
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     if graph is not None:
+        reps = -(-steps // copies)
+        steps = reps * copies
+        t0 = time.perf_counter()
         for _ in range(reps):
             graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
     else:
+        t0 = time.perf_counter()
         for i in range(steps):
             launch(i)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-
-    cold_ms = kernel_ms(torch, lambda i: launch(i % copies), 2 * copies)
-    warm_ms = kernel_ms(torch, lambda i: launch(0), 2 * copies)
-    # re-check after the timed work
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    # per-launch kernel time: HIP events on the launch stream around graph
+    # replays of the rotating launches (cold), and of one weight (warm)
+    cold_ms = replay_event_ms(torch, graph, copies) if graph is not None else event_ms(
+        torch, lambda i: launch(i % copies), 4 * copies)
+    warm = capture(torch, lambda i: launch(0), copies)
+    warm_ms = replay_event_ms(torch, warm, copies) if warm is not None else event_ms(torch, lambda i: launch(0), 4 * copies)
     launch(1)
     torch.cuda.synchronize()
     if not float((y - ref).abs().max() / ref.abs().max()) < 1e-4:
         raise RuntimeError("GEMV result drifted during timing")
-    return {
-        "steps": steps, "elapsed_s": elapsed, "bytes": nbytes, "copies": copies,
-        "value_gbs": nbytes * steps / elapsed / 1e9, "ms_per_step": elapsed * 1e3 / steps,
-        "kernel_cold_ms": cold_ms, "kernel_warm_ms": warm_ms, "graph": graph is not None,
-    }
+    out = {"steps": steps, "elapsed_s": elapsed, "bytes": nbytes, "copies": copies,
+           "value_gbs": nbytes * steps / elapsed / 1e9, "ms_per_step": elapsed * 1e3 / steps,
+           "kernel_cold_ms": cold_ms, "kernel_warm_ms": warm_ms, "graph": graph is not None}
+    # bf16 activations (same weight bytes, x half the size)
+    xb = x.to(torch.bfloat16)
 
+    def launch_b(i: int) -> None:
+        L.check(lib.unifur_nf4_linear_forward(xb.data_ptr(), L.BF16, 1, ctypes.byref(structs[i % copies]), None,
+                                              None, y.data_ptr(), L.F32, None, 0,
+                                              torch.cuda.current_stream().cuda_stream))
+    gb = capture(torch, launch_b, copies)
+    out["kernel_cold_ms_bf16x"] = replay_event_ms(torch, gb, copies) if gb is not None else event_ms(
+        torch, launch_b, 4 * copies)
+    return out
+
+
+# --------------------------------------------------------------- config 1 --
 
 def bench_codec(torch, Q, L) -> dict:
     """Config 1 (4096 x 4096 f32): quantize and dequantize kernels."""
@@ -153,12 +205,17 @@ def bench_codec(torch, Q, L) -> dict:
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(0x4E463457)
-    copies = 4
+    copies = 8  # 8 x (64 MiB + 8 MiB) > the Infinity Cache
     vals = [torch.randn(n, device=dev, generator=g) * 0.02 for _ in range(copies)]
     packs = [Q.PackedNf4Tensor.quantize(v) for v in vals]
     outs = [torch.empty(n, device=dev) for _ in range(copies)]
-    q_ms = kernel_ms(torch, lambda i: Q.PackedNf4Tensor.quantize(vals[i % copies]), 16)
     lib = L.lib()
+
+    def quant(i: int) -> None:
+        p = packs[i % copies]
+        L.check(lib.unifur_nf4_quantize(vals[i % copies].data_ptr(), n, p.codes.data_ptr(), p.absmax.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream))
+
     structs = [p.scales_struct() for p in packs]
 
     def deq(i: int) -> None:
@@ -167,18 +224,142 @@ def bench_codec(torch, Q, L) -> dict:
                                           outs[i % copies].data_ptr(), L.F32,
                                           torch.cuda.current_stream().cuda_stream))
 
-    d_ms = kernel_ms(torch, deq, 16)
+    gq, gd = capture(torch, quant, copies), capture(torch, deq, copies)
+    q_ms = replay_event_ms(torch, gq, copies) if gq is not None else event_ms(torch, quant, 4 * copies)
+    d_ms = replay_event_ms(torch, gd, copies) if gd is not None else event_ms(torch, deq, 4 * copies)
     codec_bytes = 4 * n + n // 2 + 4 * (n // 64)  # f32 values + packed codes + f32 absmax
     return {"quantize_ms": q_ms, "dequant_ms": d_ms, "bytes": codec_bytes,
             "quantize_gbs": codec_bytes / q_ms / 1e6, "dequant_gbs": codec_bytes / d_ms / 1e6}
 
 
+# --------------------------------------------------------------- config 3 --
+
+def bench_gemm(torch, Q, L) -> dict:
+    """Config 3: X bf16 [2048, 4096] . NF4 W [4096, 4096] + LoRA r 16 (scale 2), bf16 Y."""
+    M, K, N, r = 2048, 4096, 4096, 16
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x4E463457 + 3)
+    lin = rand_weights(torch, Q, K, N, g)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    a = torch.randn(K, r, device=dev, generator=g) * 0.01
+    b = torch.randn(r, N, device=dev, generator=g) * 0.01
+    ql = Q.QloraLinear(lin, Q.LoraAdapter.from_parts(a, b, 2.0))
+    y = ql.forward(x)
+    ref = (x.float() @ lin.dequantized_weight()) + (x.float() @ a) @ b * 2.0
+    err = float((y.float() - ref).abs().max() / ref.abs().max())
+    if not err < 1e-2:
+        raise RuntimeError(f"GEMM sanity check failed: {err:.3e}")
+    flops = 2 * M * N * K + 2 * M * K * r + 2 * M * r * N
+    w = lin.weight_struct()
+    lo = ql.adapter.struct()
+    lib = L.lib()
+    ws_bytes = lib.unifur_nf4_linear_workspace_size(M, K, N, L.BF16, r)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+
+    def launch(i: int) -> None:
+        L.check(lib.unifur_nf4_qlora_forward(x.data_ptr(), L.BF16, M, ctypes.byref(w), ctypes.byref(lo), y.data_ptr(),
+                                             L.BF16, ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream))
+
+    for i in range(3):
+        launch(i)
+    graph = capture(torch, launch, 8)
+    ms = graph_ms(torch, graph, 10) / 8 if graph is not None else event_ms(torch, launch, 16)
+    # the base GEMM kernel alone (no LoRA: one launch)
+    ybase = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+    def base(i: int) -> None:
+        L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), L.BF16, M, ctypes.byref(w), None, None, ybase.data_ptr(),
+                                              L.BF16, None, 0, torch.cuda.current_stream().cuda_stream))
+    gbase = capture(torch, base, 8)
+    base_ms = replay_event_ms(torch, gbase, 8, reps=10) if gbase is not None else event_ms(torch, base, 16)
+    base_flops = 2 * M * N * K
+    return {"ms": ms, "tflops": flops / ms / 1e9, "frac": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+            "base_kernel_ms": base_ms, "base_tflops": base_flops / base_ms / 1e9, "max_rel_err": err}
+
+
+# --------------------------------------------------------------- config 4 --
+
+def bench_swiglu(torch, Q, L, tokens) -> dict:
+    hidden, inter = 4096, 11008
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x4E463457 + 4)
+    copies = 3  # 3 x 38 MB of packed weights per block: > the Infinity Cache
+    blocks = [Q.QwenMlp(rand_weights(torch, Q, hidden, inter, g), rand_weights(torch, Q, hidden, inter, g),
+                        rand_weights(torch, Q, inter, hidden, g)) for _ in range(copies)]
+    wbytes = 2 * gemv_bytes(hidden, inter, True, 0, 0) + gemv_bytes(inter, hidden, True, 0, 0)
+    out = {}
+    for T in tokens:
+        x = torch.randn(T, hidden, device=dev, generator=g).to(torch.bfloat16)
+        ys = [None] * copies
+
+        def run(i: int) -> None:
+            ys[i % copies] = blocks[i % copies].forward(x)
+
+        for i in range(copies):
+            run(i)
+        graph = capture(torch, run, copies * 2)
+        ms = graph_ms(torch, graph, 20) / (copies * 2) if graph is not None else event_ms(torch, run, 12)
+        flops = T * 270_532_608
+        out[f"T{T}"] = {"ms": round(ms, 5), "weight_gbs": round(wbytes / ms / 1e6, 1),
+                        "tflops": round(flops / ms / 1e9, 2)}
+    return out
+
+
+# --------------------------------------------------------------- config 5 --
+
+QWEN_PROJ = [("q", 896, 896), ("k", 896, 128), ("v", 896, 128), ("o", 896, 896),
+             ("gate", 896, 4864), ("up", 896, 4864), ("down", 4864, 896)]
+
+
+def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x4E463457 + 5)
+    # whole-model quantize pass: quantize + double-quantize + stripe, 168 weights
+    vals = [(torch.randn(di * do, device=dev, generator=g) * 0.02, di, do)
+            for _ in range(layers) for (_, di, do) in QWEN_PROJ]
+    torch.cuda.synchronize()
+
+    def quantize_all():
+        return [Q.Nf4Linear.from_values(v, di, do) for (v, di, do) in vals]
+
+    quantize_all()  # warm
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    lins = quantize_all()
+    torch.cuda.synchronize()
+    q_s = time.perf_counter() - t0
+    params = sum(di * do for (_, di, do) in vals)
+    q_bytes = 4 * params + params // 2 + 4 * (params // 64)  # f32 in, codes + f32 absmax out (config 5 unit)
+    del vals
+    out = {"quantize_pass_ms": round(q_s * 1e3, 3), "quantize_pass_gbs": round(q_bytes / q_s / 1e9, 1),
+           "params": params}
+    wbytes = sum(gemv_bytes(lin.d_input(), lin.d_output(), True, 0, 0) for lin in lins)
+    for b in (1, 32):
+        xs = {di: torch.randn(b, di, device=dev, generator=g).to(torch.bfloat16 if b > 4 else torch.float32)
+              for (_, di, _) in QWEN_PROJ}
+
+        def step(i: int) -> None:
+            for lin in lins:
+                lin.forward(xs[lin.d_input()])
+
+        step(0)
+        graph = capture(torch, step, 1)
+        ms = graph_ms(torch, graph, 20) if graph is not None else event_ms(torch, step, 5)
+        out[f"decode_b{b}"] = {"ms_per_token_step": round(ms, 4), "weight_gbs": round(wbytes / ms / 1e6, 1),
+                               "tokens_per_s": round(b / ms * 1e3, 1)}
+    out["weight_bytes"] = wbytes
+    return out
+
+
+# ------------------------------------------------------------- CPU baseline --
+
 def cpu_baseline(sample_s: float) -> dict:
     """The reference's CPU path restated (oracle): serial dequantize of the
     whole weight, then an f32 matmul on all host cores, timed on the config-2
     GEMV for about `sample_s` seconds."""
-    import numpy as np
-
     from oracle import oracle as O
 
     d_in, d_out = 4096, 11008
@@ -196,26 +377,39 @@ def cpu_baseline(sample_s: float) -> dict:
         if time.perf_counter() - t0 >= sample_s:
             break
     dt = (time.perf_counter() - t0) / iters
-    del w
-    _ = np.zeros(1)
-    return {"value": gemv_bytes(d_in, d_out, dq=True) / dt / 1e9, "unit": "GB/s", "cores": threads,
+    return {"value": round(gemv_bytes(d_in, d_out, dq=True) / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"{iters} x (1-thread dequantize of the 4096x11008 DQ weight + {threads}-thread f32 "
-                      f"GEMV), {dt * 1e3:.1f} ms each, oracle/nf4_oracle.c restatement of "
+            "sample": f"{iters} x config-2 GEMV (1-thread dequantize of the 4096x11008 DQ weight + {threads}-thread "
+                      f"f32 GEMV), {dt * 1e3:.1f} ms each; oracle/nf4_oracle.c restatement of "
                       f"PackedNf4Tensor::dequantize + burn linear"}
+
+
+def read_traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2400)
+    ap.add_argument("--steps", type=int, default=4800)
     ap.add_argument("--warmup", type=int, default=96)
     ap.add_argument("--cpu-sample-s", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--quick", action="store_true", help="headline GEMV and codec only")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 20 device copies of 256 MiB (the reference kernel for scaling HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the NF4 path would shard); run with --gpus 1", file=sys.stderr)
+              "(every kernel runs on one GPU's share of a layer); run with --gpus 1", file=sys.stderr)
         return 2
 
     import torch
@@ -226,9 +420,38 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        # a plain copy of known size: 256 MiB read + 256 MiB written per launch
+        a = torch.ones(64 << 20, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(20):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": a.numel() * 4, "copy_calibration_bytes_written": b.numel() * 4,
+                          "launches": 20}))
+        return 0
     L.lib()
     gemv = bench_gemv(torch, Q, L, args)
     codec = bench_codec(torch, Q, L)
+    secondary = {
+        "gemv_warm": {"kernel_ms": round(gemv["kernel_warm_ms"], 5),
+                      "gbs": round(gemv["bytes"] / gemv["kernel_warm_ms"] / 1e6, 1)},
+        "gemv_bf16_activations_cold": {
+            "kernel_ms": round(gemv["kernel_cold_ms_bf16x"], 5),
+            "gbs": round(gemv_bytes(4096, 11008, True, 2, 4) / gemv["kernel_cold_ms_bf16x"] / 1e6, 1)},
+        "dequantize_f32_config1": {"kernel_ms": round(codec["dequant_ms"], 5), "gbs": round(codec["dequant_gbs"], 1),
+                                   "frac": round(codec["dequant_gbs"] / HBM_PEAK_GBS, 4)},
+        "quantize_config1": {"kernel_ms": round(codec["quantize_ms"], 5), "gbs": round(codec["quantize_gbs"], 1),
+                             "frac": round(codec["quantize_gbs"] / HBM_PEAK_GBS, 4)},
+    }
+    if not args.quick:
+        gemm = bench_gemm(torch, Q, L)
+        secondary["prefill_qlora_gemm_config3"] = {
+            "ms": round(gemm["ms"], 5), "tflops": round(gemm["tflops"], 1), "frac": round(gemm["frac"], 4),
+            "base_gemm_kernel_ms": round(gemm["base_kernel_ms"], 5), "base_tflops": round(gemm["base_tflops"], 1),
+            "max_rel_err": gemm["max_rel_err"]}
+        secondary["swiglu_config4"] = bench_swiglu(torch, Q, L, (1, 16, 512))
+        secondary["qwen05b_config5"] = bench_qwen(torch, Q, L)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample_s)
 
     achieved = gemv["bytes"] / gemv["kernel_cold_ms"] / 1e6
@@ -246,8 +469,8 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "config 2: NF4 decode GEMV x[1x4096] f32 . W[4096x11008] (Wt of the logical "
-                        "11008x4096), block 64, double-quantized scales, y f32; "
+            "workload": "config 2: NF4 decode GEMV x[1x4096] f32 . W[4096x11008] (Wt of the logical 11008x4096), "
+                        "block 64, double-quantized scales, y f32; weight held striped; "
                         f"{gemv['copies']} weight copies rotated (cold HBM)",
             "timing": "HIP-graph replay of the launches" if gemv["graph"] else "eager launches",
             "d_in": 4096, "d_out": 11008, "rows": 1, "block_size": 64, "double_quantized": True,
@@ -255,24 +478,15 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_kernel<1,16,f32,dq>",
+            "kernel": "gemv_striped_kernel<1,4,4,f32,dq>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": read_traffic(),
         },
         "cpu_baseline": cpu,
-        "secondary": {
-            "gemv_warm": {"kernel_ms": round(gemv["kernel_warm_ms"], 5),
-                          "gbs": round(gemv["bytes"] / gemv["kernel_warm_ms"] / 1e6, 1)},
-            "dequantize_f32_config1": {"kernel_ms": round(codec["dequant_ms"], 5),
-                                       "gbs": round(codec["dequant_gbs"], 1),
-                                       "frac": round(codec["dequant_gbs"] / HBM_PEAK_GBS, 4)},
-            "quantize_config1": {"kernel_ms": round(codec["quantize_ms"], 5),
-                                 "gbs": round(codec["quantize_gbs"], 1),
-                                 "frac": round(codec["quantize_gbs"] / HBM_PEAK_GBS, 4)},
-        },
+        "secondary": secondary,
     }
     print(json.dumps(line))
     return 0

@@ -6,7 +6,7 @@
  * src/quantize.rs and the NF4-resident linear layers in src/qwennet.rs.  Each
  * entry point names the reference item it stands in for (file:line).  The
  * reference has no FFI for this path today (it is in-process Rust); these are
- * the symbols its FFI crate would bind -- see INTEGRATION.md.
+ * the symbols its FFI crate would bind.
  *
  * Conventions (all entry points):
  *   - Data buffers are DEVICE pointers owned by the caller; `stream` is a

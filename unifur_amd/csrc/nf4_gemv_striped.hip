@@ -18,9 +18,9 @@
 // decode then starts only once most data has arrived.)
 //
 // Decode: a byte of codes is looked up in a 256-entry LDS table holding
-// {level[lo], level[hi]} (32 copies, lane l reads copy l % 32, so the 64-bit
-// reads of 32 lanes hit distinct bank pairs); the address is one v_perm_b32
-// (byte << 8 | lane offset).  Per row and 64-block the activation is folded
+// {level[lo], level[hi]} (16 copies, lane l reads copy l % 16, so the 64-bit
+// reads of 16 lanes hit distinct bank pairs; 32 KiB, so four workgroups fit
+// a CU); the address is one v_perm_b32 (byte << 8 | lane offset) and a shift.  Per row and 64-block the activation is folded
 // with the block scale once (xs = x * scale), then one FMA per code.  The
 // lookups of chunk c + 1 are issued before the FMAs of chunk c.
 //
@@ -41,16 +41,27 @@
 namespace unifur {
 namespace {
 
-constexpr int kLutCopies = 32;
-constexpr int kLutBytes = 256 * kLutCopies * 8;  // 64 KiB, at LDS address 0
+#ifndef UNIFUR_GEMV_LUT_COPIES
+#define UNIFUR_GEMV_LUT_COPIES 16
+#endif
+constexpr int kLutCopies = UNIFUR_GEMV_LUT_COPIES;
+static_assert(kLutCopies == 8 || kLutCopies == 16 || kLutCopies == 32, "LUT copies");
+constexpr int kLutBytes = 256 * kLutCopies * 8;  // at LDS address 0
 constexpr int kDqLutOffset = kLutBytes;          // one 256-entry DQ scale table per weight
-constexpr int kLevelsOffset = kDqLutOffset + 2 * 256 * 4;
-constexpr int kStripedSmem = kLevelsOffset + 16 * 4;
+constexpr int kStripedSmem = kDqLutOffset + 2 * 256 * 4;
 
 typedef const __attribute__((address_space(4))) float const_f32;
 typedef __attribute__((address_space(3))) const f32x2 lds_f32x2;
 
 __device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
+
+// NF4_LEVELS[c] for a per-lane c from immediates (no memory access).
+__device__ __forceinline__ float level_select(int c) {
+  float v = __uint_as_float(level_bits(0));
+#pragma unroll
+  for (int i = 1; i < 16; ++i) v = c == i ? __uint_as_float(level_bits(i)) : v;
+  return v;
+}
 __device__ __forceinline__ uint32_t as_u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float silu_f32(float z) { return z * (1.0f / (1.0f + __expf(-z))); }
 
@@ -107,6 +118,10 @@ struct Looked {
 template <int T, int NW, bool DQ>
 __device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW>& c, const float* dq_lut,
                                        uint32_t lane_off) {
+  // lane_off is (copy * 8) << (8 - log2(kLutCopies * 8 / 32)): the v_perm
+  // puts the code byte in bits 8-15, and a shift brings the entry stride down
+  // to kLutCopies * 8 bytes when that is under 256.
+  constexpr int kShift = kLutCopies == 32 ? 0 : (kLutCopies == 16 ? 1 : 2);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     o.scale[w] = DQ ? dq_lut[w * 256 + (c.w[w].scale & 0xffu)] : as_f(c.w[w].scale);
@@ -116,7 +131,7 @@ __device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW>& c, con
       for (int b = 0; b < 4; ++b) {
         // LDS byte address = (byte b of the dword) << 8 | lane_off; the LUT
         // sits at LDS address 0 (this kernel has no static LDS)
-        const uint32_t addr = perm_b32(c.w[w].code[d], lane_off, 0x0c0c0000u | ((4u + b) << 8));
+        const uint32_t addr = perm_b32(c.w[w].code[d], lane_off, 0x0c0c0000u | ((4u + b) << 8)) >> kShift;
         o.lv[w][d * 4 + b] = *reinterpret_cast<lds_f32x2*>((size_t)addr);
       }
   }
@@ -191,14 +206,19 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
+  // XCD-aware order: workgroup b runs on XCD b % 8, so each XCD takes a
+  // contiguous run of stripes and the four stripes of a 64-column block
+  // (which share their scale codes) meet in one L2.
+  const int nb = gridDim.x;
+  const int b = (nb % 8 == 0) ? ((int)blockIdx.x % 8) * (nb / 8) + (int)blockIdx.x / 8 : (int)blockIdx.x;
   // which weight (several weights of one x can share a launch) and stripe
   int wi = 0;
   if constexpr (!PAIR) {
 #pragma unroll
     for (int i = 1; i < kMaxGemvWeights; ++i)
-      if (i < a.nweights && (int)blockIdx.x >= a.stripe_begin[i]) wi = i;
+      if (i < a.nweights && b >= a.stripe_begin[i]) wi = i;
   }
-  const int s = blockIdx.x - a.stripe_begin[wi];
+  const int s = b - a.stripe_begin[wi];
   const int K = a.d_in;
   const int kw = wave * a.rows_per_wave;
   const int nrows = max(0, min(a.rows_per_wave, K - kw));
@@ -221,21 +241,11 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
                   : make_rsrc(static_cast<const float*>(a.x) + off, (uint32_t)nrows * 4u);
   }
 
-  // prologue: the first D chunks
-  Chunk<T, NW> ring[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j) issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, j, lane);
-
-  // LUTs.  The scale of scales is read through the scalar cache so that it
-  // does not queue behind the chunk loads.
-  float* lv16 = reinterpret_cast<float*>(smem + kLevelsOffset);
-  if (tid == 0) {
-#pragma unroll
-    for (int c = 0; c < 16; ++c) lv16[c] = __uint_as_float(level_bits(c));
-  }
-  __syncthreads();
+  // LUTs first: their barrier must not wait for the issue of the chunk
+  // loads, which the memory system back-pressures when every workgroup
+  // starts at once.  The scale of scales is read through the scalar cache.
   if (tid < 256) {
-    const float lo = lv16[tid & 15], hi = lv16[tid >> 4];
+    const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
     const f32x4 v = {lo, hi, lo, hi};
     f32x4* dst = reinterpret_cast<f32x4*>(smem + tid * (kLutCopies * 8));
 #pragma unroll
@@ -254,8 +264,13 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
 
+  // prologue: the first D chunks
+  Chunk<T, NW> ring[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, j, lane);
+
   const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
-  const uint32_t lane_off = (uint32_t)(lane & (kLutCopies - 1)) * 8u;
+  const uint32_t lane_off = ((uint32_t)(lane & (kLutCopies - 1)) * 8u) << (kLutCopies == 32 ? 0 : kLutCopies == 16 ? 1 : 2);
   float acc[NW][T][16];
 #pragma unroll
   for (int w = 0; w < NW; ++w)
@@ -332,7 +347,10 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 
 // ================================================================ launching ==
 
-constexpr int kDepth = 4;
+#ifndef UNIFUR_GEMV_DEPTH
+#define UNIFUR_GEMV_DEPTH 4
+#endif
+constexpr int kDepth = UNIFUR_GEMV_DEPTH;
 
 template <int T, int W, bool XBF16, bool DQ, bool PAIR>
 hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
@@ -377,11 +395,12 @@ StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights
   int stripes = 0;
   for (int i = 0; i < (pair ? 1 : nweights); ++i) stripes += d_out[i] / kStripeCols;
   const int chunks = (d_in + 63) / 64;
-  // Enough waves for about 16 per CU over 256 CUs, but no more waves than
-  // 64-row chunks.
+  // About 4096 waves over the GPU (16 per CU): waves per workgroup = the
+  // power of two at most 4096 / stripes, within [4, 16] (8 for the pair or
+  // more than two rows, for registers) and no more than the 64-row chunks.
   const int max_waves = (pair || rows > 2) ? 8 : 16;
   int waves = 4;
-  while (waves < max_waves && (long)stripes * waves < 4096 && waves * 2 <= chunks) waves *= 2;
+  while (waves < max_waves && (long)stripes * waves * 2 <= 4096 && waves * 2 <= chunks) waves *= 2;
   p.waves = waves;
   p.rows_per_wave = (chunks + waves - 1) / waves * 64;
   p.stripes = stripes;
