@@ -134,6 +134,16 @@ int unifur_nf4_double_quantize(const float *absmax, uint64_t num_blocks, uint8_t
 int unifur_nf4_dequantize(const uint8_t *packed, const unifur_nf4_scales *scales, uint64_t len, void *out,
                           int out_dtype, void *stream);
 
+/* Loader step of qwen_linear (src/qwennet.rs:1687-1726): a checkpoint weight
+ * src [out_features, in_features] row-major (PyTorch order), f32 or bf16
+ * (bf16 decoded exactly, src/import.rs:323-327), is transposed to
+ * [in_features, out_features] (transpose2d, src/qwennet.rs:1375-1390) and
+ * quantized (PackedNf4Tensor::quantize, src/quantize.rs:262-279) in one pass:
+ * packed/absmax are bit-identical to quantizing the transposed copy.
+ * out_features % 64 == 0; packed 8-byte aligned. */
+int unifur_nf4_quantize_transposed(const void *src, int src_dtype, uint64_t out_features, uint64_t in_features,
+                                   uint8_t *packed, float *absmax, void *stream);
+
 /* ---- device layout of a linear weight ------------------------------------------ */
 
 /* Row-major -> striped.  src->layout must be ROW_MAJOR, d_out % 64 == 0 and
@@ -170,6 +180,21 @@ int unifur_nf4_linear_forward(const void *x, int x_dtype, uint64_t rows, const u
 int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,
                              const unifur_nf4_lora *lora, void *y, int y_dtype, void *workspace,
                              uint64_t workspace_bytes, void *stream);
+
+/* Linear with an f32-resident weight w [d_in, d_out] row-major: the F32 arm of
+ * QwenLinear (src/qwennet.rs:293-355) and the dequantized base of the
+ * simulated QLoraLinear (src/quantize.rs:637-700); y = x w (+ bias)
+ * (+ (x a) b * scaling).  Same conventions as unifur_nf4_linear_forward. */
+uint64_t unifur_nf4_dense_linear_workspace_size(uint64_t rows, uint32_t lora_rank);
+int unifur_nf4_dense_linear_forward(const void *x, int x_dtype, uint64_t rows, const float *w, uint64_t d_in,
+                                    uint64_t d_out, const float *bias, const unifur_nf4_lora *lora, void *y,
+                                    int y_dtype, void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* QLoraLinear::merged (src/quantize.rs:716-726): out = w + (a b) * scaling,
+ * LoraAdapter::delta_weight (src/quantize.rs:626-634) folded into an f32
+ * weight [d_in, d_out]. */
+int unifur_nf4_lora_merge(const float *w, uint64_t d_in, uint64_t d_out, const unifur_nf4_lora *lora, float *out,
+                          void *stream);
 
 /* Workspace bytes of unifur_nf4_swiglu_forward (same contract as above). */
 uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype);

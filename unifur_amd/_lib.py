@@ -71,6 +71,11 @@ SIGNATURES = {
     "unifur_nf4_quantize": (_I, [_P, _U64, _P, _P, _P]),
     "unifur_nf4_double_quantize": (_I, [_P, _U64, _P, _P, _P]),
     "unifur_nf4_dequantize": (_I, [_P, ctypes.POINTER(Scales), _U64, _P, _I, _P]),
+    "unifur_nf4_quantize_transposed": (_I, [_P, _I, _U64, _U64, _P, _P, _P]),
+    "unifur_nf4_dense_linear_workspace_size": (_U64, [_U64, ctypes.c_uint32]),
+    "unifur_nf4_dense_linear_forward": (_I, [_P, _I, _U64, _P, _U64, _U64, _P, ctypes.POINTER(Lora), _P, _I, _P,
+                                             _U64, _P]),
+    "unifur_nf4_lora_merge": (_I, [_P, _U64, _U64, ctypes.POINTER(Lora), _P, _P]),
     "unifur_nf4_stripe_weight": (_I, [ctypes.POINTER(Weight), _P, _P, _P]),
     "unifur_nf4_unstripe_weight": (_I, [ctypes.POINTER(Weight), _P, _P, _P]),
     "unifur_nf4_linear_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),

@@ -608,6 +608,69 @@ uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64
   return need;
 }
 
+int unifur_nf4_quantize_transposed(const void* src, int src_dtype, uint64_t out_features, uint64_t in_features,
+                                   uint8_t* packed, float* absmax, void* stream) {
+  UNIFUR_ARG(valid_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  if (out_features == 0 || in_features == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(src && packed && absmax, "src, packed or absmax is NULL");
+  UNIFUR_ARG(out_features % 64 == 0, "quantize_transposed needs out_features % 64 == 0");
+  UNIFUR_ARG(out_features / 64 <= 65535u && in_features <= 0x7fffffffffull, "quantize_transposed: shape too large");
+  UNIFUR_ARG(aligned_to(packed, 8), "packed must be 8-byte aligned");
+  UNIFUR_ARG(aligned_to(src, src_dtype == UNIFUR_NF4_BF16 ? 2 : 4), "src is misaligned for its dtype");
+  UNIFUR_HIP(launch_quantize_transposed(src, src_dtype == UNIFUR_NF4_BF16, out_features, in_features, packed, absmax,
+                                        static_cast<hipStream_t>(stream)));
+  return UNIFUR_NF4_OK;
+}
+
+uint64_t unifur_nf4_dense_linear_workspace_size(uint64_t rows, uint32_t lora_rank) {
+  if (rows == 0 || lora_rank == 0) return 0;
+  Carver c;
+  c.take((size_t)rows * lora_rank * sizeof(float));
+  return c.off;
+}
+
+int unifur_nf4_dense_linear_forward(const void* x, int x_dtype, uint64_t rows, const float* w, uint64_t d_in,
+                                    uint64_t d_out, const float* bias, const unifur_nf4_lora* lora, void* y,
+                                    int y_dtype, void* workspace, uint64_t workspace_bytes, void* stream) {
+  UNIFUR_ARG(valid_dtype(x_dtype) && valid_dtype(y_dtype), "dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  UNIFUR_ARG(d_in > 0 && d_out > 0 && d_in <= 0x7fffffffu && d_out <= 0x7fffffffu, "bad weight shape");
+  if (rows == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(x && y && w, "x, y or w is NULL");
+  UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  const uint32_t rank = lora ? lora->rank : 0;
+  if (lora) {
+    UNIFUR_ARG(lora->a != nullptr && lora->b != nullptr, "lora factors are NULL");
+    UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t need = lora ? (size_t)rows * rank * sizeof(float) : 0;
+  void* ws = nullptr;
+  if (need) {
+    // the counter region keeps its offset-0 meaning for shared workspaces
+    Carver c;
+    const size_t off = c.take(need);
+    if (int r = resolve_workspace(workspace, workspace_bytes, c.off, st, &ws)) return r;
+    ws = at<char>(ws, off);
+  }
+  float* xa = static_cast<float*>(ws);
+  if (lora) UNIFUR_HIP(launch_lora_xa(x, x_dtype == UNIFUR_NF4_BF16, lora->a, (int)rows, (int)d_in, (int)rank, xa, st));
+  Epilogue e{bias, xa, lora ? lora->b : nullptr, (int)rank, lora ? lora->scaling : 0.0f, y,
+             y_dtype == UNIFUR_NF4_BF16};
+  UNIFUR_HIP(launch_gemm_f32(x, x_dtype == UNIFUR_NF4_BF16, w, (int)rows, (int)d_in, (int)d_out, e, st));
+  return UNIFUR_NF4_OK;
+}
+
+int unifur_nf4_lora_merge(const float* w, uint64_t d_in, uint64_t d_out, const unifur_nf4_lora* lora, float* out,
+                          void* stream) {
+  UNIFUR_ARG(lora != nullptr && lora->a && lora->b, "lora factors are NULL");
+  UNIFUR_ARG(lora->rank >= 1, "lora rank must be positive");
+  if (d_in == 0 || d_out == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(w && out, "w or out is NULL");
+  UNIFUR_HIP(launch_lora_merge(w, lora->a, lora->b, (int)lora->rank, lora->scaling, d_in, d_out, out,
+                               static_cast<hipStream_t>(stream)));
+  return UNIFUR_NF4_OK;
+}
+
 int unifur_nf4_stripe_weight(const unifur_nf4_weight* src, uint8_t* dst_packed, void* dst_scales, void* stream) {
   if (int r = check_weight(src, "src")) return r;
   UNIFUR_ARG(src->layout == UNIFUR_NF4_LAYOUT_ROW_MAJOR, "stripe_weight takes a row-major weight");

@@ -214,6 +214,67 @@ __global__ void dequantize_tail_kernel(const uint8_t* __restrict__ packed, Scale
   }
 }
 
+// ------------------------------------------------------ transpose-quantize --
+// The loader's step (src/qwennet.rs:1687-1726): a checkpoint weight
+// src[out_f][in_f] (PyTorch [out, in], f32 or bf16 decoded exactly as
+// src/import.rs:323-327) is transposed to [in_f][out_f] (transpose2d,
+// src/qwennet.rs:1375-1390) and quantized (PackedNf4Tensor::quantize) -- here
+// in one pass, without the transposed f32 copy.  With out_f % 64 == 0 every
+// 64-value block of the transposed buffer is 64 consecutive output features
+// of one input feature, i.e. one column segment of a 64 x 64 source tile.
+// Tile in LDS (padded rows), then wave lane l takes block row k = l / 4 of
+// its 16 and the quarter l % 4 of the block: a 4-lane absmax, 16 codes, one
+// 8-byte store.  Arithmetic identical to quantize_full_kernel.
+template <bool kBf16In>
+__global__ __launch_bounds__(256) void quantize_transposed_kernel(const void* __restrict__ src, uint64_t out_f,
+                                                                  uint64_t in_f, uint8_t* __restrict__ packed,
+                                                                  float* __restrict__ absmax) {
+  __shared__ BucketEntry tab[33];
+  __shared__ float tile[64][65];
+  build_bucket_table(tab);
+  const int tid = threadIdx.x;
+  const uint64_t o0 = (uint64_t)blockIdx.y * 64, k0 = (uint64_t)blockIdx.x * 64;
+  // load: tile[o][k] = src[o0 + o][k0 + k], rows of 64 consecutive values
+  for (int i = tid; i < 64 * 64; i += 256) {
+    const int o = i >> 6, k = i & 63;
+    float v = 0.0f;
+    if (k0 + k < in_f) {
+      const uint64_t idx = (o0 + o) * in_f + k0 + k;
+      v = kBf16In ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(src)[idx])
+                  : reinterpret_cast<const float*>(src)[idx];
+    }
+    tile[o][k] = v;
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  const int q = lane & 3;              // quarter of the 64-value block
+  const int kr = wave * 16 + (lane >> 2);  // tile row k: four waves x 16 rows
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = tile[q * 16 + i][kr];
+  // absmax = fold(0, max(acc, |v|)) over the block (src/quantize.rs:103),
+  // NaN-ignoring maxNum as Rust's f32::max
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+  m = fmaxf(m, __shfl_xor(m, 1, 4));
+  m = fmaxf(m, __shfl_xor(m, 2, 4));
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t c = m == 0.0f ? 7u : code_of(v[i] / m, tab);  // src/quantize.rs:104-114
+    if (i < 8)
+      lo |= c << (4 * i);
+    else
+      hi |= c << (4 * (i - 8));
+  }
+  if (k0 + kr < in_f) {
+    const uint64_t base = (k0 + kr) * out_f + o0 + (uint64_t)q * 16;  // value index in [in_f][out_f]
+    reinterpret_cast<uint2*>(packed)[base / 16] = make_uint2(lo, hi);
+    if (q == 0) absmax[base / 64] = m;
+  }
+}
+
 int grid_for(size_t work_items, int threads, int max_blocks) {
   size_t g = (work_items + threads - 1) / threads;
   if (g > (size_t)max_blocks) g = max_blocks;
@@ -277,6 +338,20 @@ hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, siz
     else
       dequantize_tail_kernel<false><<<g, 64, 0, stream>>>(packed, scales, first, n, out);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_transposed(const void* src, bool bf16_in, uint64_t out_f, uint64_t in_f, uint8_t* packed,
+                                      float* absmax, hipStream_t stream) {
+  if (out_f == 0 || in_f == 0) return hipSuccess;
+  const uint64_t gx = (in_f + 63) / 64, gy = out_f / 64;
+  if (out_f % 64 != 0 || gx > 0x7fffffffu || gy > 65535u) return hipErrorInvalidValue;
+  if (bf16_in)
+    quantize_transposed_kernel<true><<<dim3((unsigned)gx, (unsigned)gy), 256, 0, stream>>>(src, out_f, in_f, packed,
+                                                                                           absmax);
+  else
+    quantize_transposed_kernel<false><<<dim3((unsigned)gx, (unsigned)gy), 256, 0, stream>>>(src, out_f, in_f, packed,
+                                                                                            absmax);
   return hipGetLastError();
 }
 

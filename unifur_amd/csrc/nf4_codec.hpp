@@ -19,6 +19,10 @@ hipError_t launch_quantize(const float* values, size_t n, uint8_t* packed, float
                            hipStream_t stream);
 hipError_t launch_double_quantize(const float* absmax, size_t nb, uint8_t* q, float* scale_of_scales,
                                   hipStream_t stream);
+// src[out_f][in_f] (f32 or bf16) -> packed NF4 codes and f32 absmax of its
+// [in_f][out_f] transpose; out_f % 64 == 0, packed 8-byte aligned.
+hipError_t launch_quantize_transposed(const void* src, bool bf16_in, uint64_t out_f, uint64_t in_f, uint8_t* packed,
+                                      float* absmax, hipStream_t stream);
 hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, size_t n, void* out, bool bf16_out,
                              bool aligned, hipStream_t stream);
 

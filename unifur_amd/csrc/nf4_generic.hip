@@ -131,7 +131,33 @@ __global__ void silu_mul_bf16_kernel(const float* __restrict__ g, const float* _
   }
 }
 
+// out[k][n] = w[k][n] + (sum_j a[k][j] b[j][n]) * scaling: QLoraLinear::merged
+// (src/quantize.rs:716-726) with LoraAdapter::delta_weight (src/quantize.rs:626-634)
+// evaluated in that order (product, then the scale, then the sum).
+__global__ void lora_merge_kernel(const float* __restrict__ w, const float* __restrict__ a,
+                                  const float* __restrict__ b, int rank, float scaling, uint64_t K, uint64_t N,
+                                  float* __restrict__ out) {
+  const uint64_t total = K * N;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t k = i / N, n = i % N;
+    float d = 0.0f;
+    for (int j = 0; j < rank; ++j) d = __builtin_fmaf(a[k * rank + j], b[(uint64_t)j * N + n], d);
+    out[i] = w[i] + d * scaling;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_lora_merge(const float* w, const float* a, const float* b, int rank, float scaling, uint64_t K,
+                             uint64_t N, float* out, hipStream_t stream) {
+  const uint64_t total = K * N;
+  if (total == 0) return hipSuccess;
+  uint64_t blocks = (total + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  lora_merge_kernel<<<(unsigned)blocks, 256, 0, stream>>>(w, a, b, rank, scaling, K, N, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm_f32(const void* x, bool x_bf16, const float* w, int M, int K, int N, const Epilogue& e,
                            hipStream_t stream) {

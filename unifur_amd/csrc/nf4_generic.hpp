@@ -20,6 +20,8 @@ hipError_t launch_gemm_f32(const void* x, bool x_bf16, const float* w, int M, in
                            hipStream_t stream);
 hipError_t launch_lora_xa(const void* x, bool x_bf16, const float* a, int M, int K, int rank, float* xa,
                           hipStream_t stream);
+hipError_t launch_lora_merge(const float* w, const float* a, const float* b, int rank, float scaling, uint64_t K,
+                             uint64_t N, float* out, hipStream_t stream);
 hipError_t launch_silu_mul(const float* g, const float* u, size_t n, float* h, hipStream_t stream);
 hipError_t launch_silu_mul_bf16(const float* g, const float* u, size_t n, uint16_t* h, hipStream_t stream);
 

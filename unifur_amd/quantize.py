@@ -425,3 +425,171 @@ class QwenMlp:
         return y
 
     __call__ = forward
+
+
+# ------------------------------------------------------- dense f32 linears --
+
+class DenseLinear:
+    """A plain linear with an f32-resident weight [d_input, d_output] and
+    optional bias: Burn's ``Linear`` as the reference uses it for the F32 arm
+    of ``QwenLinear`` (src/qwennet.rs:293-355) and for the output of
+    ``QLoRALinear::merged`` (src/quantize.rs:716-726).  Forward runs the
+    library's f32 GEMM (``unifur_nf4_dense_linear_forward``)."""
+
+    def __init__(self, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
+        _require_cuda(weight, "weight")
+        if weight.dtype != torch.float32 or weight.dim() != 2:
+            raise ValueError("weight must be float32 [d_input, d_output]")
+        if bias is not None:
+            _require_cuda(bias, "bias")
+            if bias.dtype != torch.float32 or bias.numel() != weight.shape[1]:
+                raise ValueError("bias must be float32 [d_output]")
+        self.weight = weight
+        self.bias = bias
+
+    def d_input(self) -> int:
+        return self.weight.shape[0]
+
+    def d_output(self) -> int:
+        return self.weight.shape[1]
+
+    def _forward(self, x: torch.Tensor, lora: Optional["LoraAdapter"], out_dtype: Optional[torch.dtype]):
+        _require_cuda(x, "x")
+        d_in, d_out = self.weight.shape
+        if x.shape[-1] != d_in:
+            raise ValueError(f"x has last dim {x.shape[-1]}, the layer takes {d_in}")
+        rows = x.numel() // d_in
+        out_dtype = out_dtype or x.dtype
+        y = torch.empty(*x.shape[:-1], d_out, dtype=out_dtype, device=x.device)
+        lo = lora.struct() if lora is not None else None
+        L.check(L.lib().unifur_nf4_dense_linear_forward(
+            x.data_ptr(), _dtype_code(x.dtype), rows, self.weight.data_ptr(), d_in, d_out,
+            self.bias.data_ptr() if self.bias is not None else None,
+            ctypes.byref(lo) if lo is not None else None, y.data_ptr(), _dtype_code(out_dtype), None, 0,
+            _stream()))
+        return y
+
+    def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        return self._forward(x, None, out_dtype)
+
+    __call__ = forward
+
+
+def _linear_init(d_in: int, d_out: int, generator: Optional[torch.Generator], device) -> tuple:
+    """Burn's default ``LinearConfig`` initialisation (Kaiming-uniform with
+    gain 1/sqrt(3), i.e. U(-1/sqrt(d_in), 1/sqrt(d_in)) for weight and bias)."""
+    bound = 1.0 / math.sqrt(max(d_in, 1))
+    w = (torch.rand(d_in, d_out, generator=generator) * 2 - 1) * bound
+    b = (torch.rand(d_out, generator=generator) * 2 - 1) * bound
+    return w.to(device), b.to(device)
+
+
+def _quantize_dequantize_flat(values: torch.Tensor, double_quantization: bool) -> torch.Tensor:
+    q = PackedNf4Tensor.quantize(values.contiguous().view(-1))
+    if double_quantization:
+        q = q.with_double_quantization()
+    return q.dequantize().view(values.shape)
+
+
+class QLoRALinear:
+    """The simulated QLoRA layer of src/quantize.rs:637-727: an f32-stored
+    base whose weight holds NF4-grid values (``quantize_dequantize_tensor``),
+    an f32 bias, and a LoRA adapter.  ``resident_bits`` reports what the base
+    would occupy packed; ``merged`` folds ``scaling * A B`` into the weight.
+    (The NF4-resident form is ``QloraLinear`` above.)"""
+
+    def __init__(self, base: DenseLinear, adapter: LoraAdapter, quantized_values: int, double_quantized: bool):
+        self.base = base
+        self._adapter = adapter
+        self.quantized_values = int(quantized_values)
+        self.double_quantized = bool(double_quantized)
+
+    @staticmethod
+    def from_linear(base: DenseLinear, config: LoraConfig, double_quantization: bool, device="cuda",
+                    generator: Optional[torch.Generator] = None) -> "QLoRALinear":
+        """src/quantize.rs:653-676: quantize the base weight to NF4 (values
+        kept dequantized in f32), keep the bias, attach a fresh adapter."""
+        n = base.weight.numel()
+        q = _quantize_dequantize_flat(base.weight, double_quantization)
+        return QLoRALinear(DenseLinear(q, base.bias), LoraAdapter.new(config, device, generator), n,
+                           double_quantization)
+
+    @staticmethod
+    def new(in_features: int, out_features: int, config: LoraConfig, double_quantization: bool, device="cuda",
+            generator: Optional[torch.Generator] = None) -> "QLoRALinear":
+        """src/quantize.rs:679-690: a fresh biased linear, quantized and adapted."""
+        w, b = _linear_init(in_features, out_features, generator, device)
+        return QLoRALinear.from_linear(DenseLinear(w, b), config, double_quantization, device, generator)
+
+    def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """base(x) + adapter(x) (src/quantize.rs:692-694), one fused launch chain."""
+        return self.base._forward(x, self._adapter, out_dtype)
+
+    __call__ = forward
+
+    def adapter(self) -> LoraAdapter:
+        return self._adapter
+
+    def resident_bits(self) -> tuple:
+        """src/quantize.rs:700-713: (packed NF4 bits, f32 bits) of the base weight."""
+        blocks = float((self.quantized_values + BLOCK_SIZE - 1) // BLOCK_SIZE)
+        scale_bits = 8.0 * blocks + 32.0 if self.double_quantized else 32.0 * blocks
+        return 4.0 * self.quantized_values + scale_bits, 32.0 * self.quantized_values
+
+    def merged(self) -> DenseLinear:
+        """src/quantize.rs:716-726: a plain linear with W + scaling * (A B)."""
+        out = torch.empty_like(self.base.weight)
+        d_in, d_out = self.base.weight.shape
+        lo = self._adapter.struct()
+        L.check(L.lib().unifur_nf4_lora_merge(self.base.weight.data_ptr(), d_in, d_out, ctypes.byref(lo),
+                                              out.data_ptr(), _stream()))
+        return DenseLinear(out, self.base.bias)
+
+
+# ---------------------------------------------------- module-level quantize --
+
+class Nf4Quantizer:
+    """src/quantize.rs:418-493: quantize every weight-shaped parameter of a
+    module to the NF4 grid in place.  Parameters of rank < 2, with fewer than
+    BLOCK_SIZE values, or under a module whose path contains a ``skip``
+    needle are left alone.  A module is a mapping of dotted parameter names
+    to device tensors; the module path of ``a.b.weight`` is ``[a, b]``."""
+
+    def __init__(self, double_quantization: bool):
+        self.double_quantization = bool(double_quantization)
+        self.skip: list[str] = []
+        self.quantized_values = 0
+        self.skipped_params = 0
+
+    def skipping(self, name: str) -> "Nf4Quantizer":
+        self.skip.append(name)
+        return self
+
+    def is_skipped(self, path: list) -> bool:
+        return any(needle in part for needle in self.skip for part in path)
+
+    def should_quantize(self, name: str, shape) -> bool:
+        """The map_float decision (src/quantize.rs:469-475), host-side."""
+        numel = 1
+        for d in shape:
+            numel *= int(d)
+        path = name.split(".")[:-1]
+        return len(shape) >= 2 and numel >= BLOCK_SIZE and not self.is_skipped(path)
+
+    def map_float(self, name: str, param: torch.Tensor) -> torch.Tensor:
+        if not self.should_quantize(name, tuple(param.shape)):
+            self.skipped_params += 1
+            return param
+        if param.dtype != torch.float32:
+            raise ValueError(f"{name}: the quantizer takes float32 parameters")
+        self.quantized_values += param.numel()
+        return _quantize_dequantize_flat(param, self.double_quantization)
+
+
+def quantize_module(module: dict, double_quantization: bool, skip=()) -> tuple:
+    """src/quantize.rs:498-511: (quantized module, values quantized)."""
+    mapper = Nf4Quantizer(double_quantization)
+    for s in skip:
+        mapper.skipping(s)
+    out = {name: mapper.map_float(name, p) for name, p in module.items()}
+    return out, mapper.quantized_values
