@@ -1,0 +1,114 @@
+"""GPU parity of the skinny MFMA path: 5..64 bf16 activation rows over a
+striped NF4 weight (the medium batches between the decode GEMV and the
+prefill GEMM: speculative decode, small batches, config 4 at T = 16).
+
+The weight operand is bf16(level * scale), x is bf16: the bf16 tolerance of
+BASELINE.json's north star applies (normwise and max|y - r| / max|r| both
+<= 1e-2 against the float64 product with the oracle's dequantized weight).
+Token counts straddle the 16-token MFMA tiles; d_in values leave partial
+64-row chunks and partial 16-row lane groups (d_in % 64 = 8, 40), which is
+where a transposed-operand index mistake would show.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from unifur_amd import _lib as L
+from unifur_amd import quantize as Q
+
+from test_gpu_gemm import lora_parts
+from test_gpu_linear import TOL_BF16, acts, check, make_linear
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("T", [5, 8, 16, 17, 31, 32, 33, 48, 63, 64])
+@pytest.mark.parametrize("dq", [True, False])
+def test_token_counts_and_scale_kinds(device, oracle, T, dq):
+    K, N = 1024, 512
+    lin, wdeq = make_linear(oracle, K, N, 700 + T, device, dq=dq, striped=True)
+    x, xt = acts(oracle, T, K, 701 + T, torch.bfloat16, device)
+    ref = oracle.linear_ref_f64(x, wdeq)
+    check(lin.forward(xt, out_dtype=torch.float32), ref, x, wdeq, TOL_BF16, f"skinny T={T} dq={dq}")
+    check(lin.forward(xt, out_dtype=torch.bfloat16), ref, x, wdeq, TOL_BF16, f"skinny T={T} dq={dq} bf16-out")
+
+
+@pytest.mark.parametrize("shape", [(904, 192), (200, 128), (40, 64), (8, 64), (896, 4864), (4864, 896),
+                                   (4096, 1024)])
+@pytest.mark.parametrize("T", [7, 32, 64])
+def test_ragged_d_in_and_qwen_shapes(device, oracle, shape, T):
+    K, N = shape
+    lin, wdeq = make_linear(oracle, K, N, 800 + K + N + T, device, striped=True)
+    x, xt = acts(oracle, T, K, 801 + T, torch.bfloat16, device)
+    check(lin.forward(xt, out_dtype=torch.float32), oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_BF16,
+          f"skinny {shape} T={T}")
+
+
+@pytest.mark.parametrize("r", [1, 16, 64])
+@pytest.mark.parametrize("T", [12, 40])
+def test_bias_and_lora(device, oracle, r, T):
+    K, N = 512, 256
+    lin, wdeq = make_linear(oracle, K, N, 900 + r, device, striped=True)
+    bias = oracle.fill_normal(901, 0.1, N)
+    lin.bias = torch.from_numpy(bias).to(device)
+    x, xt = acts(oracle, T, K, 902 + T, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 903 + r, device, scaling=16.0 / r)
+    ref = oracle.linear_ref_f64(x, wdeq, bias) + oracle.lora_ref_f64(x, a, b, 16.0 / r)
+    y = Q.QloraLinear(lin, ad).forward(xt, out_dtype=torch.float32)
+    check(y, ref, x, wdeq, TOL_BF16, f"skinny bias+lora r={r} T={T}")
+    # fixed accumulation order: bit-identical on a second call
+    assert torch.equal(Q.QloraLinear(lin, ad).forward(xt, out_dtype=torch.float32), y)
+
+
+def test_misaligned_or_odd_d_in_falls_back_with_the_same_result(device, oracle):
+    # d_in % 8 != 0 cannot take 16-byte activation loads: another path
+    # serves it, within the same tolerance
+    K, N, T = 100, 64, 9
+    lin, wdeq = make_linear(oracle, K, N, 950, device, striped=True)
+    x, xt = acts(oracle, T, K, 951, torch.bfloat16, device)
+    check(lin.forward(xt, out_dtype=torch.float32), oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_BF16,
+          "odd d_in")
+
+
+def _swiglu_parts(oracle, hidden, inter, seed, device, kinds=(True, True, True)):
+    ws, deqs = [], []
+    for i, (din, dout) in enumerate([(hidden, inter), (hidden, inter), (inter, hidden)]):
+        lin, wd = make_linear(oracle, din, dout, seed + i, device, dq=kinds[i], striped=True)
+        ws.append(lin)
+        deqs.append(wd)
+    return ws, deqs
+
+
+@pytest.mark.parametrize("T", [5, 16, 33, 64])
+@pytest.mark.parametrize("kinds", [(True, True, True), (True, False, True), (False, False, False)])
+def test_swiglu_pair_and_mixed_scale_kinds(device, oracle, T, kinds):
+    hidden, inter = 256, 704
+    (g, u, d), (wg, wu, wd) = _swiglu_parts(oracle, hidden, inter, 1000 + T, device, kinds)
+    x, xt = acts(oracle, T, hidden, 1010 + T, torch.bfloat16, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    mlp = Q.QwenMlp(g, u, d)
+    y = mlp.forward(xt, out_dtype=torch.float32)
+    # the down projection reads bf16(silu(g) * u); bound with |h| from the reference
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    check(y, ref, h, wd, TOL_BF16, f"skinny swiglu T={T} kinds={kinds}")
+    assert torch.equal(mlp.forward(xt, out_dtype=torch.float32), y)
+
+
+def test_user_workspace_covers_mixed_kinds(device, oracle):
+    hidden, inter, T = 256, 704, 24
+    (g, u, d), (wg, wu, wd) = _swiglu_parts(oracle, hidden, inter, 1100, device, (True, False, True))
+    x, xt = acts(oracle, T, hidden, 1101, torch.bfloat16, device)
+    need = L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16)
+    assert need >= 65536 + T * inter * (2 + 4 + 4)
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    y = torch.empty(T, hidden, device=device)
+    gs, us, ds = g.weight_struct(), u.weight_struct(), d.weight_struct()
+    stream = torch.cuda.current_stream().cuda_stream
+    L.check(L.lib().unifur_nf4_swiglu_forward(xt.data_ptr(), L.BF16, T, ctypes.byref(gs), ctypes.byref(us),
+                                              ctypes.byref(ds), y.data_ptr(), L.F32, ws.data_ptr(), need, stream))
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    check(y, oracle.swiglu_ref_f64(x, wg, wu, wd), h, wd, TOL_BF16, "skinny swiglu user workspace")

@@ -165,7 +165,7 @@ struct Carver {
 
 // ------------------------------------------------------------- linear plans --
 
-enum class LinearPath { kGemvStriped, kGemv, kMfma, kGeneric };
+enum class LinearPath { kGemvStriped, kGemv, kSkinny, kMfma, kGeneric };
 
 // The row-major GEMV needs whole 64-blocks per weight row (d_out % 64 == 0),
 // 16-byte aligned code rows and a weight that 32-bit buffer offsets reach
@@ -182,7 +182,8 @@ struct LinearLayout {
 };
 
 // Decode-sized batches (<= 4 rows) take a GEMV (the striped one for striped
-// weights); larger bf16 batches the MFMA GEMM; everything else the generic
+// weights); bf16 batches up to 64 rows over a striped weight the skinny MFMA
+// kernel; larger bf16 batches the MFMA GEMM; everything else the generic
 // dequantize + f32 matmul (a striped weight is first put back in row-major
 // order in the workspace).
 LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t lora_rank, const void* packed,
@@ -193,10 +194,16 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
   const bool layout_ok = striped || gemv_layout_ok(d_in, d_out, packed);
   const bool mfma = !small && x_dtype == UNIFUR_NF4_BF16 && layout_ok && rows <= 0x7fffffffu &&
                     gemm_supported((int)rows, (int)d_in, (int)d_out, x);
+  const bool skinny = !small && striped && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
+                      d_in <= 0x7fffffffu && skinny_supported((int)rows, (int)d_in, x);
   if (small && striped) {
     L.path = LinearPath::kGemvStriped;
     const int n = (int)d_out;
     L.striped = plan_gemv_striped((int)rows, (int)d_in, &n, 1, false);
+  } else if (skinny) {
+    L.path = LinearPath::kSkinny;
+    const int n = (int)d_out;
+    L.striped = plan_skinny((int)rows, (int)d_in, &n, 1, false);
   } else if (small && layout_ok && ceil_div_u64(d_out, 256) <= (uint64_t)kMaxCounters) {
     L.path = LinearPath::kGemv;
     const int n = (int)d_out;
@@ -293,7 +300,7 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     xa = at<float>(ws, L.xa);
     UNIFUR_HIP(launch_lora_xa(x, xbf, lora->a, (int)rows, (int)w->d_in, (int)rank, xa, stream));
   }
-  if (L.path == LinearPath::kGemv || L.path == LinearPath::kGemvStriped) {
+  if (L.path == LinearPath::kGemv || L.path == LinearPath::kGemvStriped || L.path == LinearPath::kSkinny) {
     GemvWeight gw = gemv_weight(w, y, ybf, at<unsigned>(ws, 0), at<float>(ws, L.partials));
     gw.bias = bias;
     gw.lora_xa = xa;
@@ -302,6 +309,9 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     gw.lora_scaling = lora ? lora->scaling : 0.0f;
     if (L.path == LinearPath::kGemvStriped)
       UNIFUR_HIP(launch_gemv_striped(L.striped, x, xbf, (int)rows, (int)w->d_in, &gw, 1, false, stream));
+    else if (L.path == LinearPath::kSkinny)
+      UNIFUR_HIP(launch_skinny(L.striped, static_cast<const uint16_t*>(x), (int)rows, (int)w->d_in, &gw, 1, false,
+                               stream));
     else
       UNIFUR_HIP(launch_gemv(L.gemv, x, xbf, (int)rows, (int)w->d_in, &gw, 1, stream));
     return UNIFUR_NF4_OK;
@@ -320,7 +330,7 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
 
 // ------------------------------------------------------------- swiglu plans --
 
-enum class MlpPath { kPairStriped, kStriped, kPairGemv, kGemv, kMfma, kGeneric };
+enum class MlpPath { kPairStriped, kStriped, kPairGemv, kGemv, kSkinny, kMfma, kGeneric };
 
 struct MlpLayout {
   MlpPath path;
@@ -346,7 +356,21 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
                     gemm_supported((int)rows, (int)inter, (int)hidden, reinterpret_cast<const void*>(uintptr_t{256}));
   const int gi[2] = {(int)inter, (int)inter};
   const int hd = (int)hidden;
-  if (small && all_striped) {
+  // the skinny kernel for up to 64 bf16 rows; h lives 256-byte aligned in the workspace
+  const bool skinny = !small && all_striped && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
+                      hidden <= 0x7fffffffu && inter <= 0x7fffffffu &&
+                      skinny_supported((int)rows, (int)hidden, x) &&
+                      skinny_supported((int)rows, (int)inter, reinterpret_cast<const void*>(uintptr_t{256}));
+  if (skinny) {
+    L.path = MlpPath::kSkinny;
+    L.s_up = plan_skinny((int)rows, (int)hidden, gi, 2, same_kind);
+    L.s_down = plan_skinny((int)rows, (int)inter, &hd, 1, false);
+    L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
+    if (!same_kind) {
+      L.h = c.take((size_t)rows * inter * sizeof(float));
+      L.u = c.take((size_t)rows * inter * sizeof(float));
+    }
+  } else if (small && all_striped) {
     L.path = rows <= (uint64_t)kGemvPairMaxRows && same_kind ? MlpPath::kPairStriped : MlpPath::kStriped;
     L.s_up = plan_gemv_striped((int)rows, (int)hidden, gi, 2, L.path == MlpPath::kPairStriped);
     L.s_down = plan_gemv_striped((int)rows, (int)inter, &hd, 1, false);
@@ -443,6 +467,26 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       }
       GemvWeight dw = gemv_weight(down, y, ybf, cnt, p0);
       UNIFUR_HIP(launch_gemv(L.down_plan, h, false, (int)rows, (int)inter, &dw, 1, stream));
+      return UNIFUR_NF4_OK;
+    }
+    case MlpPath::kSkinny: {
+      // gate and up in one pass storing silu(g) * u as bf16 (two passes and
+      // the elementwise kernel when their scales differ in kind), then down
+      const uint16_t* xb = static_cast<const uint16_t*>(x);
+      uint16_t* hb = at<uint16_t>(ws, L.hb);
+      if (gate->scales.kind == up->scales.kind) {
+        GemvWeight gw[2] = {gemv_weight(gate, hb, true, cnt, nullptr), gemv_weight(up, nullptr, true, cnt, nullptr)};
+        UNIFUR_HIP(launch_skinny(L.s_up, xb, (int)rows, (int)hidden, gw, 2, true, stream));
+      } else {
+        float* u = at<float>(ws, L.u);
+        GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, nullptr), gemv_weight(up, u, false, cnt, nullptr)};
+        const StripedPlan one = plan_skinny((int)rows, (int)hidden, &gw[0].d_out, 1, false);
+        UNIFUR_HIP(launch_skinny(one, xb, (int)rows, (int)hidden, &gw[0], 1, false, stream));
+        UNIFUR_HIP(launch_skinny(one, xb, (int)rows, (int)hidden, &gw[1], 1, false, stream));
+        UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
+      }
+      GemvWeight dw = gemv_weight(down, y, ybf, cnt, nullptr);
+      UNIFUR_HIP(launch_skinny(L.s_down, hb, (int)rows, (int)inter, &dw, 1, false, stream));
       return UNIFUR_NF4_OK;
     }
     case MlpPath::kMfma: {
@@ -596,13 +640,15 @@ uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64
   uint64_t need = 0;
   for (int striped = 0; striped < 2; ++striped) {
     if (striped && (hidden % 64 != 0 || intermediate % 64 != 0)) continue;
-    for (int kind = 0; kind < 2; ++kind) {
-      unifur_nf4_weight g{p, {kind, (const float*)p, p, (const float*)p}, hidden, intermediate,
+    for (int kind = 0; kind < 4; ++kind) {  // gate and up scale kinds, alike or not
+      unifur_nf4_weight g{p, {kind & 1, (const float*)p, p, (const float*)p}, hidden, intermediate,
                           striped ? UNIFUR_NF4_LAYOUT_STRIPED : UNIFUR_NF4_LAYOUT_ROW_MAJOR};
+      unifur_nf4_weight u = g;
+      u.scales.kind = kind >> 1;
       unifur_nf4_weight d = g;
       d.d_in = intermediate;
       d.d_out = hidden;
-      need = std::max<uint64_t>(need, plan_mlp(rows, hidden, intermediate, &g, &g, &d, x_dtype, p).total);
+      need = std::max<uint64_t>(need, plan_mlp(rows, hidden, intermediate, &g, &u, &d, x_dtype, p).total);
     }
   }
   return need;

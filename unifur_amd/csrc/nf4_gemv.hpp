@@ -57,6 +57,7 @@ struct StripedPlan {
 
 struct StripedArgs {
   const void* x;  // [rows, d_in] f32 or bf16
+  int rows;
   int d_in;
   int rows_per_wave;
   int nweights;
@@ -68,5 +69,20 @@ StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights
 
 hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16, int rows, int d_in,
                                const GemvWeight* weights, int nweights, bool pair, hipStream_t stream);
+
+// ---- 5..64 bf16 rows over striped weights, on MFMA ----
+// Same decomposition (a workgroup per stripe over all of d_in, waves split
+// d_in) with the products on v_mfma_f32_16x16x32_bf16: the weight operand is
+// bf16(level * scale) (the rounding of the MFMA GEMM path), x is used as it
+// is.  Needs bf16 x with d_in % 8 == 0, 16-byte aligned, rows * d_in * 2 under
+// 2^31; the SwiGLU pair mode stores silu(gate x) * (up x).
+constexpr int kSkinnyMaxRows = 64;
+
+bool skinny_supported(int rows, int d_in, const void* x);
+
+StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool pair);
+
+hipError_t launch_skinny(const StripedPlan& p, const uint16_t* x, int rows, int d_in, const GemvWeight* weights,
+                         int nweights, bool pair, hipStream_t stream);
 
 }  // namespace unifur

@@ -388,6 +388,268 @@ hipError_t dispatch_w(const StripedArgs& a, int grid, int waves, bool xbf16, boo
   return hipErrorInvalidValue;
 }
 
+// ============================================== 5..64 rows on MFMA (skinny) ==
+//
+// Same workgroup / wave / chunk decomposition and LUT as above, with the
+// products on v_mfma_f32_16x16x32_bf16 (C[token][column] += A[token][k] B[k][column]):
+//   * a wave writes its 64 x 8 code bytes of a chunk to a private LDS slot
+//     (lane = row) and reads them back with ds_read_b64_tr_b4, which
+//     transposes 16 x 16 nibbles inside each group of 16 lanes: lane 16 G + c
+//     receives column c of rows 16 G .. 16 G + 15 -- the MFMA operand layout
+//     (8 consecutive k per lane), rows 16 G + j, j < 8 for the first MFMA of
+//     the chunk and j >= 8 for the second;
+//   * each byte (two rows of one column) is looked up in the level-pair LUT,
+//     multiplied by the two row scales -- the scale of row 16 G + j is decoded
+//     by lane 16 G + j and broadcast with DPP row_newbcast:j -- and rounded to
+//     a bf16 pair: the B operand is bf16(level * scale), exactly what the MFMA
+//     GEMM path stages in LDS;
+//   * the A operand is x itself: lane 16 G + t loads x[t][k .. k + 15] for
+//     the 16 rows of its group (two 16-byte loads), for up to four 16-token
+//     tiles; loads outside the wave's rows or past the tokens read zero.
+// Per 64-row chunk and weight a wave issues 2 MFMAs per token tile.  The
+// waves' accumulators are added through LDS in a fixed order.
+
+typedef int v2i32 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2_w;
+
+constexpr int kSkStageOffset = kStripedSmem;  // after the level and DQ LUTs
+
+// the value of lane 16 (l / 16) + J, in every lane l
+template <int J>
+__device__ __forceinline__ float row_bcast(float v) {
+  return as_f(__builtin_amdgcn_update_dpp(0u, as_u(v), 0x150 + J, 0xF, 0xF, false));
+}
+template <int J>
+__device__ __forceinline__ void row_bcast_all(float v, float (&o)[16]) {
+  o[J] = row_bcast<J>(v);
+  if constexpr (J + 1 < 16) row_bcast_all<J + 1>(v, o);
+}
+
+template <int NT, int NW>
+struct SkChunk {
+  u32x2 code[NW];
+  uint32_t scale[NW];
+  u32x4 x[NT][2];
+};
+
+template <int NW>
+struct SkLooked {
+  f32x2 lv[NW][8];
+  float s[NW];
+};
+
+// Loads of chunk `chunk` of this wave: codes and scale of row 64 chunk + lane
+// (bounded to the wave's rows), and for each token tile x[t][k0 .. k0 + 15]
+// with t = 16 tt + lane % 16, k0 = kw + 64 chunk + 16 (lane / 16): offsets
+// past the wave's rows are sent out of the buffer (zero), tokens past `rows`
+// fall out of it by themselves.
+template <int NT, int NW, bool DQ>
+__device__ __forceinline__ void sk_issue(SkChunk<NT, NW>& c, const WaveW (&ww)[NW], __amdgpu_buffer_rsrc_t xr,
+                                         int K, int kw, int kend, int chunk, int lane) {
+  const uint32_t row = (uint32_t)(chunk * 64 + lane);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    c.code[w] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
+    if constexpr (DQ)
+      c.scale[w] = __builtin_amdgcn_raw_buffer_load_b8(ww[w].scales, row, 0, 0);
+    else
+      c.scale[w] = __builtin_amdgcn_raw_buffer_load_b32(ww[w].scales, row * 4u, 0, 0);
+  }
+  const int k0 = kw + chunk * 64 + 16 * (lane >> 4);
+  const uint32_t off = (uint32_t)((lane & 15) * K + k0) * 2u;
+  const uint32_t out = 0x80000000u;  // beyond num_records: reads zero
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const uint32_t o = off + (uint32_t)(16 * tt * K) * 2u;
+    c.x[tt][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, k0 + 8 <= kend ? o : out, 0, 0));
+    c.x[tt][1] =
+        __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, k0 + 16 <= kend ? o + 16u : out, 0, 0));
+  }
+}
+
+// Stage the codes, transpose them, look the bytes up; decode the row scale.
+template <int NT, int NW, bool DQ>
+__device__ __forceinline__ void sk_prep(SkLooked<NW>& o, const SkChunk<NT, NW>& c, uint32_t stage, const float* dq_lut,
+                                        uint32_t lane_off) {
+  constexpr int kShift = kLutCopies == 32 ? 0 : (kLutCopies == 16 ? 1 : 2);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    *reinterpret_cast<lds_u32x2_w*>((size_t)(stage + w * 512)) = c.code[w];
+    o.s[w] = DQ ? dq_lut[w * 256 + (c.scale[w] & 0xffu)] : as_f(c.scale[w]);
+  }
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const v2i32 nib = __builtin_amdgcn_ds_read_tr4_b64_v2i32(reinterpret_cast<lds_v2i32*>((size_t)(stage + w * 512)));
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t addr = perm_b32((uint32_t)nib[d], lane_off, 0x0c0c0000u | ((4u + b) << 8)) >> kShift;
+        o.lv[w][d * 4 + b] = *reinterpret_cast<lds_f32x2*>((size_t)addr);
+      }
+  }
+}
+
+template <int NT, int W, int D, bool DQ, bool PAIR>
+__global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
+  constexpr int NW = PAIR ? 2 : 1;
+  static_assert(D % 2 == 0, "the lookup double buffer is indexed by chunk parity");
+  static_assert(W >= 4, "the LUT build and the epilogue need 256 threads");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const int nb = gridDim.x;
+  const int b = (nb % 8 == 0) ? ((int)blockIdx.x % 8) * (nb / 8) + (int)blockIdx.x / 8 : (int)blockIdx.x;
+  int wi = 0;
+  if constexpr (!PAIR) {
+#pragma unroll
+    for (int i = 1; i < kMaxGemvWeights; ++i)
+      if (i < a.nweights && b >= a.stripe_begin[i]) wi = i;
+  }
+  const int s = b - a.stripe_begin[wi];
+  const int K = a.d_in;
+  const int kw = wave * a.rows_per_wave;
+  const int nrows = max(0, min(a.rows_per_wave, K - kw));
+  const int nchunks = (nrows + 63) / 64;
+
+  WaveW ww[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const GemvWeight& G = a.w[PAIR ? w : wi];
+    ww[w].codes = make_rsrc(G.packed + ((size_t)s * K + kw) * 8, (uint32_t)nrows * 8u);
+    const size_t srow = (size_t)(s / 4) * K + kw;
+    ww[w].scales = DQ ? make_rsrc(G.scales.dq_codes + srow, (uint32_t)nrows)
+                      : make_rsrc(G.scales.absmax + srow, (uint32_t)nrows * 4u);
+  }
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.rows * (uint32_t)K * 2u);
+
+  if (tid < 256) {  // level-pair LUT and DQ scale table, as in the GEMV
+    const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
+    const f32x4 v = {lo, hi, lo, hi};
+    f32x4* dst = reinterpret_cast<f32x4*>(smem + tid * (kLutCopies * 8));
+#pragma unroll
+    for (int j = 0; j < kLutCopies / 2; ++j) dst[(j + tid) & (kLutCopies / 2 - 1)] = v;
+    if constexpr (DQ) {
+      float* dq_lut = reinterpret_cast<float*>(smem + kDqLutOffset);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float sos = *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales);
+        dq_lut[w * 256 + tid] = ((float)tid / 255.0f) * sos;  // src/quantize.rs:349
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+
+  SkChunk<NT, NW> ring[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) sk_issue<NT, NW, DQ>(ring[j], ww, xr, K, kw, kw + nrows, j, lane);
+
+  const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
+  const uint32_t lane_off = ((uint32_t)(lane & (kLutCopies - 1)) * 8u)
+                            << (kLutCopies == 32 ? 0 : kLutCopies == 16 ? 1 : 2);
+  const uint32_t stage = (uint32_t)(kSkStageOffset + wave * NW * 512 + lane * 8);
+  f32x4 acc[NW][NT];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) acc[w][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  SkLooked<NW> lk[2];
+  sk_prep<NT, NW, DQ>(lk[0], ring[0], stage, dq_lut, lane_off);
+  for (int c0 = 0; c0 < nchunks; c0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      sk_prep<NT, NW, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], stage, dq_lut, lane_off);
+      const SkLooked<NW>& L = lk[j & 1];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        float sc[16];
+        row_bcast_all<0>(L.s[w], sc);
+        u32x4 b0, b1;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          b0[m] = pack_bf16x2(L.lv[w][m].x * sc[2 * m], L.lv[w][m].y * sc[2 * m + 1]);
+          b1[m] = pack_bf16x2(L.lv[w][4 + m].x * sc[8 + 2 * m], L.lv[w][4 + m].y * sc[9 + 2 * m]);
+        }
+        const bf16x8_t B0 = __builtin_bit_cast(bf16x8_t, b0), B1 = __builtin_bit_cast(bf16x8_t, b1);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+          acc[w][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][0]), B0,
+                                                               acc[w][tt], 0, 0, 0);
+          acc[w][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][1]), B1,
+                                                               acc[w][tt], 0, 0, 0);
+        }
+      }
+      sk_issue<NT, NW, DQ>(ring[j], ww, xr, K, kw, kw + nrows, c0 + j + D, lane);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // acc[w][tt][e] = C[token 16 tt + 4 (lane / 16) + e][column lane % 16];
+  // waves added through LDS (LUT space), one token tile at a time
+  float* red = reinterpret_cast<float*>(smem);
+  const GemvWeight& G = a.w[wi];
+  const int t_l = tid >> 4, cc = tid & 15;  // epilogue element of this thread (tid < 256)
+  const int src = ((t_l >> 2) * 16 + cc) * 4 + (t_l & 3);
+  const int gcol = s * kStripeCols + cc;
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      *reinterpret_cast<f32x4*>(red + ((w * W + wave) * 64 + lane) * 4) = acc[w][tt];
+    __syncthreads();
+    const int t = 16 * tt + t_l;
+    if (tid < 256 && t < a.rows) {
+      float sum[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < W; ++q) v += red[(w * W + q) * 256 + src];
+        sum[w] = v;
+      }
+      float y = epilogue_value(G, sum[0], t, gcol);
+      if constexpr (PAIR) y = silu_f32(y) * epilogue_value(a.w[1], sum[1], t, gcol);
+      store_y(G, (size_t)t * G.d_out + gcol, y);
+    }
+  }
+}
+
+template <int NT, int W, bool DQ, bool PAIR>
+hipError_t sk_launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
+  constexpr int NW = PAIR ? 2 : 1;
+  constexpr int D = NT <= 2 ? 4 : 2;
+  constexpr int smem = kSkStageOffset + W * NW * 512;
+  static_assert(smem <= 65536, "skinny LDS");
+  static_assert(W * NW * 1024 <= kLutBytes, "the reduction reuses the LUT space");
+  skinny_kernel<NT, W, D, DQ, PAIR><<<grid, W * 64, smem, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <int NT, bool PAIR>
+hipError_t sk_dispatch(const StripedArgs& a, int grid, int waves, bool dq, hipStream_t stream) {
+  if (waves == 4) return dq ? sk_launch_t<NT, 4, true, PAIR>(a, grid, stream) : sk_launch_t<NT, 4, false, PAIR>(a, grid, stream);
+  if (waves == 8) return dq ? sk_launch_t<NT, 8, true, PAIR>(a, grid, stream) : sk_launch_t<NT, 8, false, PAIR>(a, grid, stream);
+  return hipErrorInvalidValue;
+}
+
+template <bool PAIR>
+hipError_t sk_dispatch_rows(const StripedArgs& a, int grid, int waves, bool dq, hipStream_t stream) {
+  switch ((a.rows + 15) / 16) {
+    case 1: return sk_dispatch<1, PAIR>(a, grid, waves, dq, stream);
+    case 2: return sk_dispatch<2, PAIR>(a, grid, waves, dq, stream);
+    case 3: return sk_dispatch<3, PAIR>(a, grid, waves, dq, stream);
+    case 4: return sk_dispatch<4, PAIR>(a, grid, waves, dq, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
 StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights, bool pair) {
@@ -411,6 +673,7 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
                                const GemvWeight* weights, int nweights, bool pair, hipStream_t stream) {
   StripedArgs a{};
   a.x = x;
+  a.rows = rows;
   a.d_in = d_in;
   a.rows_per_wave = p.rows_per_wave;
   a.nweights = nweights;
@@ -434,6 +697,46 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
     case 4: return dispatch_w<4, false>(a, s, p.waves, x_bf16, dq, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+bool skinny_supported(int rows, int d_in, const void* x) {
+  return rows >= 1 && rows <= kSkinnyMaxRows && d_in > 0 && d_in % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (uint64_t)rows * (uint64_t)d_in * 2u < (1ull << 31);
+}
+
+StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool pair) {
+  StripedPlan p{};
+  int stripes = 0;
+  for (int i = 0; i < (pair ? 1 : nweights); ++i) stripes += d_out[i] / kStripeCols;
+  const int chunks = (d_in + 63) / 64;
+  (void)rows;
+  int waves = 4;  // 4 or 8 waves per workgroup, about 4096 waves over the GPU
+  if ((long)stripes * 16 <= 4096 && chunks >= 16) waves = 8;
+  p.waves = waves;
+  p.rows_per_wave = (chunks + waves - 1) / waves * 64;
+  p.stripes = stripes;
+  return p;
+}
+
+hipError_t launch_skinny(const StripedPlan& p, const uint16_t* x, int rows, int d_in, const GemvWeight* weights,
+                         int nweights, bool pair, hipStream_t stream) {
+  if (!skinny_supported(rows, d_in, x) || nweights < 1 || nweights > kMaxGemvWeights || (pair && nweights != 2))
+    return hipErrorInvalidValue;
+  StripedArgs a{};
+  a.x = x;
+  a.rows = rows;
+  a.d_in = d_in;
+  a.rows_per_wave = p.rows_per_wave;
+  a.nweights = nweights;
+  int s = 0;
+  for (int i = 0; i < nweights; ++i) {
+    a.w[i] = weights[i];
+    a.stripe_begin[i] = pair ? 0 : s;
+    if (!pair || i == 0) s += weights[i].d_out / kStripeCols;
+  }
+  for (int i = nweights; i <= kMaxGemvWeights; ++i) a.stripe_begin[i] = s;
+  const bool dq = weights[0].scales.kind == kScalesDQ;
+  return pair ? sk_dispatch_rows<true>(a, s, p.waves, dq, stream) : sk_dispatch_rows<false>(a, s, p.waves, dq, stream);
 }
 
 }  // namespace unifur
