@@ -37,8 +37,10 @@ def test_token_counts_and_scale_kinds(device, oracle, T, dq):
     check(lin.forward(xt, out_dtype=torch.bfloat16), ref, x, wdeq, TOL_BF16, f"skinny T={T} dq={dq} bf16-out")
 
 
+# d_out 11008 and 8192 put four and two stripes on each wave (one activation
+# load feeds them all); the others one
 @pytest.mark.parametrize("shape", [(904, 192), (200, 128), (40, 64), (8, 64), (896, 4864), (4864, 896),
-                                   (4096, 1024)])
+                                   (4096, 1024), (904, 11008), (200, 8192)])
 @pytest.mark.parametrize("T", [7, 32, 64])
 def test_ragged_d_in_and_qwen_shapes(device, oracle, shape, T):
     K, N = shape
@@ -112,3 +114,40 @@ def test_user_workspace_covers_mixed_kinds(device, oracle):
                                               ctypes.byref(ds), y.data_ptr(), L.F32, ws.data_ptr(), need, stream))
     h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
     check(y, oracle.swiglu_ref_f64(x, wg, wu, wd), h, wd, TOL_BF16, "skinny swiglu user workspace")
+
+
+@pytest.mark.parametrize("T", [9, 24, 64])
+def test_swiglu_pair_with_grouped_stripes(device, oracle, T):
+    # intermediate 10240 (640 stripes): the gate/up pair runs four stripes per
+    # wave at one token tile and two at more
+    hidden, inter = 128, 10240
+    (g, u, d), (wg, wu, wd) = _swiglu_parts(oracle, hidden, inter, 1200 + T, device)
+    x, xt = acts(oracle, T, hidden, 1210 + T, torch.bfloat16, device)
+    y = Q.QwenMlp(g, u, d).forward(xt, out_dtype=torch.float32)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    check(y, oracle.swiglu_ref_f64(x, wg, wu, wd), h, wd, TOL_BF16, f"skinny swiglu grouped T={T}")
+
+
+@pytest.mark.parametrize("T", [16, 64])
+def test_split_d_in_hand_off_with_user_workspace(device, oracle, T):
+    # d_out 4096 over d_in 11008: four stripes per wave leave 64 stripe groups,
+    # so d_in is split over workgroups and the last slab to arrive adds the
+    # partial sums; the arrival counters must be left zeroed for the next call
+    K, N = 11008, 4096
+    lin, wdeq = make_linear(oracle, K, N, 1300 + T, device, striped=True)
+    x, xt = acts(oracle, T, K, 1301 + T, torch.bfloat16, device)
+    need = L.lib().unifur_nf4_linear_workspace_size(T, K, N, L.BF16, 0)
+    assert need > 65536  # the counters and the partials
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    w = lin.weight_struct()
+    stream = torch.cuda.current_stream().cuda_stream
+    ref = oracle.linear_ref_f64(x, wdeq)
+    outs = []
+    for _ in range(2):
+        y = torch.empty(T, N, device=device)
+        L.check(L.lib().unifur_nf4_linear_forward(xt.data_ptr(), L.BF16, T, ctypes.byref(w), None, None, y.data_ptr(),
+                                                  L.F32, ws.data_ptr(), need, stream))
+        check(y, ref, x, wdeq, TOL_BF16, f"skinny split T={T}")
+        assert int(ws[:65536].count_nonzero()) == 0
+        outs.append(y)
+    assert torch.equal(outs[0], outs[1])  # slabs added in a fixed order

@@ -195,7 +195,8 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
   const bool mfma = !small && x_dtype == UNIFUR_NF4_BF16 && layout_ok && rows <= 0x7fffffffu &&
                     gemm_supported((int)rows, (int)d_in, (int)d_out, x);
   const bool skinny = !small && striped && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
-                      d_in <= 0x7fffffffu && skinny_supported((int)rows, (int)d_in, x);
+                      d_in <= 0x7fffffffu && skinny_supported((int)rows, (int)d_in, x) &&
+                      d_out / 64 <= (uint64_t)kMaxCounters;
   if (small && striped) {
     L.path = LinearPath::kGemvStriped;
     const int n = (int)d_out;
@@ -204,6 +205,7 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
     L.path = LinearPath::kSkinny;
     const int n = (int)d_out;
     L.striped = plan_skinny((int)rows, (int)d_in, &n, 1, false);
+    L.partials = c.take(skinny_partial_floats(L.striped, (int)rows, n) * sizeof(float));
   } else if (small && layout_ok && ceil_div_u64(d_out, 256) <= (uint64_t)kMaxCounters) {
     L.path = LinearPath::kGemv;
     const int n = (int)d_out;
@@ -360,11 +362,19 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
   const bool skinny = !small && all_striped && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
                       hidden <= 0x7fffffffu && inter <= 0x7fffffffu &&
                       skinny_supported((int)rows, (int)hidden, x) &&
-                      skinny_supported((int)rows, (int)inter, reinterpret_cast<const void*>(uintptr_t{256}));
+                      skinny_supported((int)rows, (int)inter, reinterpret_cast<const void*>(uintptr_t{256})) &&
+                      std::max(inter, hidden) / 64 <= (uint64_t)kMaxCounters;
   if (skinny) {
     L.path = MlpPath::kSkinny;
-    L.s_up = plan_skinny((int)rows, (int)hidden, gi, 2, same_kind);
+    // same_kind: gate/up in one pair launch; else one launch each (the plan
+    // of a single weight), both followed by down -- launches run in stream
+    // order, so they take turns on the partials
+    L.s_up = same_kind ? plan_skinny((int)rows, (int)hidden, gi, 2, true)
+                       : plan_skinny((int)rows, (int)hidden, gi, 1, false);
     L.s_down = plan_skinny((int)rows, (int)inter, &hd, 1, false);
+    const size_t up_part = skinny_partial_floats(L.s_up, (int)rows, (int)inter);
+    L.partials0 = c.take(std::max(up_part, skinny_partial_floats(L.s_down, (int)rows, (int)hidden)) * sizeof(float));
+    L.partials1 = c.take(up_part * sizeof(float));
     L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
     if (!same_kind) {
       L.h = c.take((size_t)rows * inter * sizeof(float));
@@ -474,18 +484,19 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       // the elementwise kernel when their scales differ in kind), then down
       const uint16_t* xb = static_cast<const uint16_t*>(x);
       uint16_t* hb = at<uint16_t>(ws, L.hb);
+      float* p0 = at<float>(ws, L.partials0);
+      float* p1 = at<float>(ws, L.partials1);
       if (gate->scales.kind == up->scales.kind) {
-        GemvWeight gw[2] = {gemv_weight(gate, hb, true, cnt, nullptr), gemv_weight(up, nullptr, true, cnt, nullptr)};
+        GemvWeight gw[2] = {gemv_weight(gate, hb, true, cnt, p0), gemv_weight(up, nullptr, true, cnt, p1)};
         UNIFUR_HIP(launch_skinny(L.s_up, xb, (int)rows, (int)hidden, gw, 2, true, stream));
       } else {
         float* u = at<float>(ws, L.u);
-        GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, nullptr), gemv_weight(up, u, false, cnt, nullptr)};
-        const StripedPlan one = plan_skinny((int)rows, (int)hidden, &gw[0].d_out, 1, false);
-        UNIFUR_HIP(launch_skinny(one, xb, (int)rows, (int)hidden, &gw[0], 1, false, stream));
-        UNIFUR_HIP(launch_skinny(one, xb, (int)rows, (int)hidden, &gw[1], 1, false, stream));
+        GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, p0), gemv_weight(up, u, false, cnt, p0)};
+        UNIFUR_HIP(launch_skinny(L.s_up, xb, (int)rows, (int)hidden, &gw[0], 1, false, stream));
+        UNIFUR_HIP(launch_skinny(L.s_up, xb, (int)rows, (int)hidden, &gw[1], 1, false, stream));
         UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
       }
-      GemvWeight dw = gemv_weight(down, y, ybf, cnt, nullptr);
+      GemvWeight dw = gemv_weight(down, y, ybf, cnt, p0);
       UNIFUR_HIP(launch_skinny(L.s_down, hb, (int)rows, (int)inter, &dw, 1, false, stream));
       return UNIFUR_NF4_OK;
     }

@@ -52,7 +52,10 @@ hipError_t launch_gemv(const GemvPlan& p, const void* x, bool x_bf16, int rows, 
 struct StripedPlan {
   int waves;          // waves per workgroup: 4, 8 or 16
   int rows_per_wave;  // a multiple of 64
-  int stripes;        // workgroups
+  int stripes;        // stripes of the launch (workgroups = stripes / group)
+  int group;          // skinny kernel: stripes per wave (1, 2 or 4); the GEMV takes 1
+  int splits;         // skinny kernel: d_in slabs over workgroups (1 for the GEMV)
+  int rows_per_split; // skinny kernel: waves * rows_per_wave
 };
 
 struct StripedArgs {
@@ -60,6 +63,7 @@ struct StripedArgs {
   int rows;
   int d_in;
   int rows_per_wave;
+  int rows_per_split;  // skinny kernel: d_in rows per workgroup along gridDim.y
   int nweights;
   GemvWeight w[kMaxGemvWeights];
   int stripe_begin[kMaxGemvWeights + 1];  // prefix sums of stripes per weight
@@ -75,7 +79,11 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
 // d_in) with the products on v_mfma_f32_16x16x32_bf16: the weight operand is
 // bf16(level * scale) (the rounding of the MFMA GEMM path), x is used as it
 // is.  Needs bf16 x with d_in % 8 == 0, 16-byte aligned, rows * d_in * 2 under
-// 2^31; the SwiGLU pair mode stores silu(gate x) * (up x).
+// 2^31; the SwiGLU pair mode stores silu(gate x) * (up x).  With
+// plan.splits > 1 the workgroups of a stripe group split d_in and hand their
+// partial sums over through the GemvWeight fields partials (splits * rows *
+// d_out floats per weight) and counters (one zeroed u32 per stripe group,
+// left zeroed): the last to arrive adds them in slab order.
 constexpr int kSkinnyMaxRows = 64;
 
 bool skinny_supported(int rows, int d_in, const void* x);
@@ -84,5 +92,8 @@ StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool
 
 hipError_t launch_skinny(const StripedPlan& p, const uint16_t* x, int rows, int d_in, const GemvWeight* weights,
                          int nweights, bool pair, hipStream_t stream);
+
+// floats of GemvWeight::partials one weight of a skinny launch needs (0 without splits)
+size_t skinny_partial_floats(const StripedPlan& p, int rows, int d_out);
 
 }  // namespace unifur

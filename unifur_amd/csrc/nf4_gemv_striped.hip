@@ -37,6 +37,7 @@
 #include "nf4_layout.hpp"
 
 #include <atomic>
+#include <type_traits>
 
 namespace unifur {
 namespace {
@@ -70,15 +71,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 // One chunk of one weight in flight: this lane's 8 code bytes and its scale.
+// Narrow loads are kept in narrow fields: the ring is carried around the
+// chunk loop, and a widening of a loaded byte placed at the loop head would
+// wait there for the newest loads instead of the ones the step consumes.
+template <bool DQ>
 struct ChunkW {
   u32x2 code;
-  uint32_t scale;  // f32 absmax bits, or the u8 DQ scale code
+  std::conditional_t<DQ, uint8_t, uint32_t> scale;  // the u8 DQ scale code, or f32 absmax bits
 };
 
-template <int T, int NW>
+template <int T, int NW, bool XBF16, bool DQ>
 struct Chunk {
-  ChunkW w[NW];
-  uint32_t x[T];  // f32 bits, or bf16 in the low half
+  ChunkW<DQ> w[NW];
+  std::conditional_t<XBF16, uint16_t, uint32_t> x[T];  // bf16 or f32 bits
 };
 
 // Wave-uniform resources of one weight, bounded to this wave's rows so that
@@ -88,7 +93,7 @@ struct WaveW {
 };
 
 template <int T, int NW, bool XBF16, bool DQ>
-__device__ __forceinline__ void issue_chunk(Chunk<T, NW>& c, const WaveW (&ww)[NW],
+__device__ __forceinline__ void issue_chunk(Chunk<T, NW, XBF16, DQ>& c, const WaveW (&ww)[NW],
                                             const __amdgpu_buffer_rsrc_t (&xr)[T], int chunk, int lane) {
   const uint32_t row = (uint32_t)(chunk * 64 + lane);
 #pragma unroll
@@ -115,8 +120,8 @@ struct Looked {
   float scale[NW];
 };
 
-template <int T, int NW, bool DQ>
-__device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW>& c, const float* dq_lut,
+template <int T, int NW, bool XBF16, bool DQ>
+__device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW, XBF16, DQ>& c, const float* dq_lut,
                                        uint32_t lane_off) {
   // lane_off is (copy * 8) << (8 - log2(kLutCopies * 8 / 32)): the v_perm
   // puts the code byte in bits 8-15, and a shift brings the entry stride down
@@ -124,7 +129,7 @@ __device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW>& c, con
   constexpr int kShift = kLutCopies == 32 ? 0 : (kLutCopies == 16 ? 1 : 2);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    o.scale[w] = DQ ? dq_lut[w * 256 + (c.w[w].scale & 0xffu)] : as_f(c.w[w].scale);
+    o.scale[w] = DQ ? dq_lut[w * 256 + (uint32_t)c.w[w].scale] : as_f((uint32_t)c.w[w].scale);
 #pragma unroll
     for (int d = 0; d < 2; ++d)
 #pragma unroll
@@ -264,10 +269,15 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
 
-  // prologue: the first D chunks
-  Chunk<T, NW> ring[D];
+  // prologue: the first D chunks, issued in chunk order like the steady
+  // state (a load of chunk 0 issued last would make every pass through the
+  // loop head wait for the newest loads)
+  Chunk<T, NW, XBF16, DQ> ring[D];
 #pragma unroll
-  for (int j = 0; j < D; ++j) issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, j, lane);
+  for (int j = 0; j < D; ++j) {
+    issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, j, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
   const uint32_t lane_off = ((uint32_t)(lane & (kLutCopies - 1)) * 8u) << (kLutCopies == 32 ? 0 : kLutCopies == 16 ? 1 : 2);
@@ -280,7 +290,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
       for (int i = 0; i < 16; ++i) acc[w][t][i] = 0.0f;
 
   Looked<NW> lk[2];
-  lookup<T, NW, DQ>(lk[0], ring[0], dq_lut, lane_off);
+  lookup<T, NW, XBF16, DQ>(lk[0], ring[0], dq_lut, lane_off);
   for (int c0 = 0; c0 < nchunks; c0 += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
@@ -288,13 +298,13 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
       // chunk c0 + j + 1 is in ring[(j + 1) % D] (refilled at step 0 when
       // j + 1 == D).  Chunks past this wave's rows read as zero: x = 0.
       __builtin_amdgcn_sched_barrier(0);
-      lookup<T, NW, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, lane_off);
+      lookup<T, NW, XBF16, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, lane_off);
       float xs[NW][T];
 #pragma unroll
       for (int w = 0; w < NW; ++w)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-          const float xv = XBF16 ? bf16_bits_to_f32(ring[j].x[t] & 0xffffu) : as_f(ring[j].x[t]);
+          const float xv = XBF16 ? bf16_bits_to_f32((uint32_t)ring[j].x[t]) : as_f((uint32_t)ring[j].x[t]);
           xs[w][t] = xv * lk[j & 1].scale[w];  // x * block scale, once per row
         }
       issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, c0 + j + D, lane);
@@ -390,9 +400,13 @@ hipError_t dispatch_w(const StripedArgs& a, int grid, int waves, bool xbf16, boo
 
 // ============================================== 5..64 rows on MFMA (skinny) ==
 //
-// Same workgroup / wave / chunk decomposition and LUT as above, with the
-// products on v_mfma_f32_16x16x32_bf16 (C[token][column] += A[token][k] B[k][column]):
-//   * a wave writes its 64 x 8 code bytes of a chunk to a private LDS slot
+// The GEMV's decomposition (waves split d_in, 64-row chunks, register ring)
+// with the products on v_mfma_f32_16x16x32_bf16 (C[token][column] +=
+// A[token][k] B[k][column]).  A wave owns S consecutive stripes (S = 1, 2 or
+// 4, inside one 64-column block, so they share the row scales) of NW weights
+// (2 for the SwiGLU gate/up pair): every activation load feeds NW * S
+// stripes.  For each chunk and each (weight, stripe) unit:
+//   * the wave writes the unit's 64 x 8 code bytes to a private LDS slot
 //     (lane = row) and reads them back with ds_read_b64_tr_b4, which
 //     transposes 16 x 16 nibbles inside each group of 16 lanes: lane 16 G + c
 //     receives column c of rows 16 G .. 16 G + 15 -- the MFMA operand layout
@@ -401,16 +415,34 @@ hipError_t dispatch_w(const StripedArgs& a, int grid, int waves, bool xbf16, boo
 //   * each byte (two rows of one column) is looked up in the level-pair LUT,
 //     multiplied by the two row scales -- the scale of row 16 G + j is decoded
 //     by lane 16 G + j and broadcast with DPP row_newbcast:j -- and rounded to
-//     a bf16 pair: the B operand is bf16(level * scale), exactly what the MFMA
-//     GEMM path stages in LDS;
-//   * the A operand is x itself: lane 16 G + t loads x[t][k .. k + 15] for
-//     the 16 rows of its group (two 16-byte loads), for up to four 16-token
-//     tiles; loads outside the wave's rows or past the tokens read zero.
-// Per 64-row chunk and weight a wave issues 2 MFMAs per token tile.  The
-// waves' accumulators are added through LDS in a fixed order.
+//     a bf16 pair: the B operand is bf16(level * scale), what the MFMA GEMM
+//     path stages in LDS;
+//   * the A operand is x itself: lane 16 G + t holds x[t][k .. k + 15] of its
+//     group's 16 rows (two 16-byte loads per 16-token tile, up to four
+//     tiles); loads outside the wave's rows or past the tokens read zero.
+// The units are software-pipelined: the LDS work of the next unit is issued
+// before the MFMAs of the current one.  The waves' accumulators are added
+// through LDS in a fixed order.
 
 typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
+
+// Split-d_in hand-off: partial sums are written with agent-scope atomic
+// stores (coherent across the XCDs' L2s) and the writer waits for them to
+// complete before it counts itself in; the last arrival reads them back with
+// agent-scope atomic loads (release / acquire at agent scope without the L2
+// write-back and invalidate that only non-atomic data would need).
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_all_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt = expcnt = lgkmcnt = 0: every store acknowledged
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2_w;
 
 constexpr int kSkStageOffset = kStripedSmem;  // after the level and DQ LUTs
@@ -426,31 +458,30 @@ __device__ __forceinline__ void row_bcast_all(float v, float (&o)[16]) {
   if constexpr (J + 1 < 16) row_bcast_all<J + 1>(v, o);
 }
 
-template <int NT, int NW>
+template <int NT, int NW, int S, bool DQ>
 struct SkChunk {
-  u32x2 code[NW];
-  uint32_t scale[NW];
+  u32x2 code[NW][S];
+  std::conditional_t<DQ, uint8_t, uint32_t> scale[NW];  // narrow, as in the GEMV ring
   u32x4 x[NT][2];
 };
 
-template <int NW>
-struct SkLooked {
-  f32x2 lv[NW][8];
-  float s[NW];
-};
-
-// Loads of chunk `chunk` of this wave: codes and scale of row 64 chunk + lane
-// (bounded to the wave's rows), and for each token tile x[t][k0 .. k0 + 15]
-// with t = 16 tt + lane % 16, k0 = kw + 64 chunk + 16 (lane / 16): offsets
-// past the wave's rows are sent out of the buffer (zero), tokens past `rows`
-// fall out of it by themselves.
-template <int NT, int NW, bool DQ>
-__device__ __forceinline__ void sk_issue(SkChunk<NT, NW>& c, const WaveW (&ww)[NW], __amdgpu_buffer_rsrc_t xr,
+// Loads of chunk `chunk` of this wave: codes of row 64 chunk + lane of each
+// stripe and its scale, and for each token tile x[t][k0 .. k0 + 15] with
+// t = 16 tt + lane % 16, k0 = kw + 64 chunk + 16 (lane / 16).  The code and
+// scale buffers end at the wave's last row (stripes before the last read the
+// next rows of their stripe, which meet zero scales and zero activations);
+// activation offsets past the wave's rows are sent out of the buffer (zero),
+// tokens past `rows` fall out of it by themselves.
+template <int NT, int NW, int S, bool DQ>
+__device__ __forceinline__ void sk_issue(SkChunk<NT, NW, S, DQ>& c, const WaveW (&ww)[NW], __amdgpu_buffer_rsrc_t xr,
                                          int K, int kw, int kend, int chunk, int lane) {
   const uint32_t row = (uint32_t)(chunk * 64 + lane);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    c.code[w] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+      c.code[w][i] = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, ((uint32_t)(i * K) + row) * 8u, 0, 0));
     if constexpr (DQ)
       c.scale[w] = __builtin_amdgcn_raw_buffer_load_b8(ww[w].scales, row, 0, 0);
     else
@@ -468,49 +499,45 @@ __device__ __forceinline__ void sk_issue(SkChunk<NT, NW>& c, const WaveW (&ww)[N
   }
 }
 
-// Stage the codes, transpose them, look the bytes up; decode the row scale.
-template <int NT, int NW, bool DQ>
-__device__ __forceinline__ void sk_prep(SkLooked<NW>& o, const SkChunk<NT, NW>& c, uint32_t stage, const float* dq_lut,
-                                        uint32_t lane_off) {
+// One unit's code bytes: stage, transpose, look up (level pairs of rows
+// 16 G + 2 m, 16 G + 2 m + 1 of this lane's column, m = 0..7).
+__device__ __forceinline__ void sk_lookup(f32x2 (&lv)[8], u32x2 code, uint32_t stage, uint32_t lane_off) {
   constexpr int kShift = kLutCopies == 32 ? 0 : (kLutCopies == 16 ? 1 : 2);
+  *reinterpret_cast<lds_u32x2_w*>((size_t)stage) = code;
+  const v2i32 nib = __builtin_amdgcn_ds_read_tr4_b64_v2i32(reinterpret_cast<lds_v2i32*>((size_t)stage));
 #pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    *reinterpret_cast<lds_u32x2_w*>((size_t)(stage + w * 512)) = c.code[w];
-    o.s[w] = DQ ? dq_lut[w * 256 + (c.scale[w] & 0xffu)] : as_f(c.scale[w]);
-  }
+  for (int d = 0; d < 2; ++d)
 #pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    const v2i32 nib = __builtin_amdgcn_ds_read_tr4_b64_v2i32(reinterpret_cast<lds_v2i32*>((size_t)(stage + w * 512)));
-#pragma unroll
-    for (int d = 0; d < 2; ++d)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t addr = perm_b32((uint32_t)nib[d], lane_off, 0x0c0c0000u | ((4u + b) << 8)) >> kShift;
-        o.lv[w][d * 4 + b] = *reinterpret_cast<lds_f32x2*>((size_t)addr);
-      }
-  }
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t addr = perm_b32((uint32_t)nib[d], lane_off, 0x0c0c0000u | ((4u + b) << 8)) >> kShift;
+      lv[d * 4 + b] = *reinterpret_cast<lds_f32x2*>((size_t)addr);
+    }
 }
 
-template <int NT, int W, int D, bool DQ, bool PAIR>
+template <int NT, int W, int D, int S, bool DQ, bool PAIR>
 __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   constexpr int NW = PAIR ? 2 : 1;
-  static_assert(D % 2 == 0, "the lookup double buffer is indexed by chunk parity");
+  constexpr int U = NW * S;  // units per chunk
+  static_assert(D % 2 == 0, "the scale double buffer is indexed by chunk parity");
   static_assert(W >= 4, "the LUT build and the epilogue need 256 threads");
+  static_assert(S == 1 || S == 2 || S == 4, "stripes per wave stay inside one 64-column block");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   const int nb = gridDim.x;
   const int b = (nb % 8 == 0) ? ((int)blockIdx.x % 8) * (nb / 8) + (int)blockIdx.x / 8 : (int)blockIdx.x;
+  const int gs = b * S;  // first stripe of this workgroup over the launch
   int wi = 0;
   if constexpr (!PAIR) {
 #pragma unroll
     for (int i = 1; i < kMaxGemvWeights; ++i)
-      if (i < a.nweights && b >= a.stripe_begin[i]) wi = i;
+      if (i < a.nweights && gs >= a.stripe_begin[i]) wi = i;
   }
-  const int s = b - a.stripe_begin[wi];
+  const int s0 = gs - a.stripe_begin[wi];
   const int K = a.d_in;
-  const int kw = wave * a.rows_per_wave;
+  const int P = gridDim.y, p = blockIdx.y;  // d_in slabs
+  const int kw = p * a.rows_per_split + wave * a.rows_per_wave;
   const int nrows = max(0, min(a.rows_per_wave, K - kw));
   const int nchunks = (nrows + 63) / 64;
 
@@ -518,8 +545,8 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     const GemvWeight& G = a.w[PAIR ? w : wi];
-    ww[w].codes = make_rsrc(G.packed + ((size_t)s * K + kw) * 8, (uint32_t)nrows * 8u);
-    const size_t srow = (size_t)(s / 4) * K + kw;
+    ww[w].codes = make_rsrc(G.packed + ((size_t)s0 * K + kw) * 8, (uint32_t)((S - 1) * K + nrows) * 8u);
+    const size_t srow = (size_t)(s0 / 4) * K + kw;
     ww[w].scales = DQ ? make_rsrc(G.scales.dq_codes + srow, (uint32_t)nrows)
                       : make_rsrc(G.scales.absmax + srow, (uint32_t)nrows * 4u);
   }
@@ -544,108 +571,205 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
 
-  SkChunk<NT, NW> ring[D];
+  SkChunk<NT, NW, S, DQ> ring[D];
 #pragma unroll
-  for (int j = 0; j < D; ++j) sk_issue<NT, NW, DQ>(ring[j], ww, xr, K, kw, kw + nrows, j, lane);
+  for (int j = 0; j < D; ++j) {  // in chunk order, as in the GEMV
+    sk_issue<NT, NW, S, DQ>(ring[j], ww, xr, K, kw, kw + nrows, j, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
   const uint32_t lane_off = ((uint32_t)(lane & (kLutCopies - 1)) * 8u)
                             << (kLutCopies == 32 ? 0 : kLutCopies == 16 ? 1 : 2);
-  const uint32_t stage = (uint32_t)(kSkStageOffset + wave * NW * 512 + lane * 8);
-  f32x4 acc[NW][NT];
+  const uint32_t stage = (uint32_t)(kSkStageOffset + wave * 512 + lane * 8);
+  f32x4 acc[NW][S][NT];
 #pragma unroll
   for (int w = 0; w < NW; ++w)
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt) acc[w][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < S; ++i)
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) acc[w][i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  SkLooked<NW> lk[2];
-  sk_prep<NT, NW, DQ>(lk[0], ring[0], stage, dq_lut, lane_off);
+  auto decode_scale = [&](const SkChunk<NT, NW, S, DQ>& c, int w) {
+    return DQ ? dq_lut[w * 256 + (uint32_t)c.scale[w]] : as_f((uint32_t)c.scale[w]);
+  };
+  float sdec[2][NW];  // this lane's row scale, per chunk parity
+  f32x2 lk[2][8];     // level pairs, per unit parity
+#pragma unroll
+  for (int w = 0; w < NW; ++w) sdec[0][w] = decode_scale(ring[0], w);
+  sk_lookup(lk[0], ring[0].code[0][0], stage, lane_off);
   for (int c0 = 0; c0 < nchunks; c0 += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      __builtin_amdgcn_sched_barrier(0);
-      sk_prep<NT, NW, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], stage, dq_lut, lane_off);
-      const SkLooked<NW>& L = lk[j & 1];
+      float sc[NW][16];
 #pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        float sc[16];
-        row_bcast_all<0>(L.s[w], sc);
+      for (int w = 0; w < NW; ++w) row_bcast_all<0>(sdec[j & 1][w], sc[w]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int w = u / S, i = u % S;
+        const int q = j * U + u;  // unit parity (c0 * U is even)
+        __builtin_amdgcn_sched_barrier(0);
+        if (u + 1 < U) {
+          sk_lookup(lk[(q + 1) & 1], ring[j].code[(u + 1) / S][(u + 1) % S], stage, lane_off);
+        } else {
+#pragma unroll
+          for (int v = 0; v < NW; ++v) sdec[(j + 1) & 1][v] = decode_scale(ring[(j + 1) % D], v);
+          sk_lookup(lk[(q + 1) & 1], ring[(j + 1) % D].code[0][0], stage, lane_off);
+        }
+        const f32x2(&L)[8] = lk[q & 1];
         u32x4 b0, b1;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          b0[m] = pack_bf16x2(L.lv[w][m].x * sc[2 * m], L.lv[w][m].y * sc[2 * m + 1]);
-          b1[m] = pack_bf16x2(L.lv[w][4 + m].x * sc[8 + 2 * m], L.lv[w][4 + m].y * sc[9 + 2 * m]);
+          b0[m] = pack_bf16x2(L[m].x * sc[w][2 * m], L[m].y * sc[w][2 * m + 1]);
+          b1[m] = pack_bf16x2(L[4 + m].x * sc[w][8 + 2 * m], L[4 + m].y * sc[w][9 + 2 * m]);
         }
         const bf16x8_t B0 = __builtin_bit_cast(bf16x8_t, b0), B1 = __builtin_bit_cast(bf16x8_t, b1);
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
-          acc[w][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][0]), B0,
-                                                               acc[w][tt], 0, 0, 0);
-          acc[w][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][1]), B1,
-                                                               acc[w][tt], 0, 0, 0);
+          acc[w][i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][0]), B0,
+                                                                  acc[w][i][tt], 0, 0, 0);
+          acc[w][i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][1]), B1,
+                                                                  acc[w][i][tt], 0, 0, 0);
         }
       }
-      sk_issue<NT, NW, DQ>(ring[j], ww, xr, K, kw, kw + nrows, c0 + j + D, lane);
+      sk_issue<NT, NW, S, DQ>(ring[j], ww, xr, K, kw, kw + nrows, c0 + j + D, lane);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // acc[w][tt][e] = C[token 16 tt + 4 (lane / 16) + e][column lane % 16];
-  // waves added through LDS (LUT space), one token tile at a time
+  // acc[w][i][tt][e] = C[token 16 tt + 4 (lane / 16) + e][column lane % 16 of
+  // stripe s0 + i]; waves added through LDS (LUT space), one (tile, stripe)
+  // at a time, both weights of a pair together.  Thread tid < 256 owns
+  // token 16 tt + tid / 16, column tid % 16 of every (tile, stripe).
   float* red = reinterpret_cast<float*>(smem);
   const GemvWeight& G = a.w[wi];
-  const int t_l = tid >> 4, cc = tid & 15;  // epilogue element of this thread (tid < 256)
+  const int t_l = tid >> 4, cc = tid & 15;
   const int src = ((t_l >> 2) * 16 + cc) * 4 + (t_l & 3);
-  const int gcol = s * kStripeCols + cc;
+  float sums[NW][S][NT];
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    __syncthreads();
+  for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-      *reinterpret_cast<f32x4*>(red + ((w * W + wave) * 64 + lane) * 4) = acc[w][tt];
-    __syncthreads();
-    const int t = 16 * tt + t_l;
-    if (tid < 256 && t < a.rows) {
-      float sum[NW];
+    for (int i = 0; i < S; ++i) {
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+        *reinterpret_cast<f32x4*>(red + ((w * W + wave) * 64 + lane) * 4) = acc[w][i][tt];
+      __syncthreads();
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
         float v = 0.0f;
+        if (tid < 256) {
 #pragma unroll
-        for (int q = 0; q < W; ++q) v += red[(w * W + q) * 256 + src];
-        sum[w] = v;
+          for (int qq = 0; qq < W; ++qq) v += red[(w * W + qq) * 256 + src];
+        }
+        sums[w][i][tt] = v;
       }
-      float y = epilogue_value(G, sum[0], t, gcol);
-      if constexpr (PAIR) y = silu_f32(y) * epilogue_value(a.w[1], sum[1], t, gcol);
+    }
+  const bool mine = tid < 256;
+  if (P > 1) {
+    // slab p's sums to the partials, then the last slab to arrive adds all
+    // of them in slab order
+    if (mine) {
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        const int t = 16 * tt + t_l;
+        if (t >= a.rows) continue;
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          const size_t idx = ((size_t)p * a.rows + t) * G.d_out + (s0 + i) * kStripeCols + cc;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) store_coherent(&a.w[PAIR ? w : wi].partials[idx], sums[w][i][tt]);
+        }
+      }
+    }
+    wait_all_memory();
+    int* is_last = reinterpret_cast<int*>(smem + kSkStageOffset);
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(&G.counters[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *is_last = prev == (unsigned)(P - 1);
+    }
+    __syncthreads();
+    if (!*is_last) return;
+    if (mine) {
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        const int t = 16 * tt + t_l;
+        if (t >= a.rows) continue;
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          const size_t idx = (size_t)t * G.d_out + (s0 + i) * kStripeCols + cc;
+          const size_t stride = (size_t)a.rows * G.d_out;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const float* part = a.w[PAIR ? w : wi].partials + idx;
+            float v = 0.0f;
+            for (int q = 0; q < P; ++q) v += load_coherent(part + q * stride);
+            sums[w][i][tt] = v;
+          }
+        }
+      }
+    }
+    if (tid == 0) __hip_atomic_store(&G.counters[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!mine) return;
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int t = 16 * tt + t_l;
+    if (t >= a.rows) continue;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int gcol = (s0 + i) * kStripeCols + cc;
+      float y = epilogue_value(G, sums[0][i][tt], t, gcol);
+      if constexpr (PAIR) y = silu_f32(y) * epilogue_value(a.w[1], sums[1][i][tt], t, gcol);
       store_y(G, (size_t)t * G.d_out + gcol, y);
     }
   }
 }
 
-template <int NT, int W, bool DQ, bool PAIR>
-hipError_t sk_launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
+template <int NT, int W, int S, bool DQ, bool PAIR>
+hipError_t sk_launch_t(const StripedArgs& a, int grid, int splits, hipStream_t stream) {
   constexpr int NW = PAIR ? 2 : 1;
-  constexpr int D = NT <= 2 ? 4 : 2;
-  constexpr int smem = kSkStageOffset + W * NW * 512;
+  constexpr int D = (NT == 1 && S == 1) ? 4 : 2;
+  constexpr int smem = kSkStageOffset + W * 512;
   static_assert(smem <= 65536, "skinny LDS");
   static_assert(W * NW * 1024 <= kLutBytes, "the reduction reuses the LUT space");
-  skinny_kernel<NT, W, D, DQ, PAIR><<<grid, W * 64, smem, stream>>>(a);
+  skinny_kernel<NT, W, D, S, DQ, PAIR><<<dim3(grid, splits), W * 64, smem, stream>>>(a);
   return hipGetLastError();
 }
 
-template <int NT, bool PAIR>
-hipError_t sk_dispatch(const StripedArgs& a, int grid, int waves, bool dq, hipStream_t stream) {
-  if (waves == 4) return dq ? sk_launch_t<NT, 4, true, PAIR>(a, grid, stream) : sk_launch_t<NT, 4, false, PAIR>(a, grid, stream);
-  if (waves == 8) return dq ? sk_launch_t<NT, 8, true, PAIR>(a, grid, stream) : sk_launch_t<NT, 8, false, PAIR>(a, grid, stream);
+template <int NT, int S, bool PAIR>
+hipError_t sk_dispatch_w(const StripedArgs& a, int grid, int splits, int waves, bool dq, hipStream_t stream) {
+  if (waves == 4)
+    return dq ? sk_launch_t<NT, 4, S, true, PAIR>(a, grid, splits, stream)
+              : sk_launch_t<NT, 4, S, false, PAIR>(a, grid, splits, stream);
+  if (waves == 8)
+    return dq ? sk_launch_t<NT, 8, S, true, PAIR>(a, grid, splits, stream)
+              : sk_launch_t<NT, 8, S, false, PAIR>(a, grid, splits, stream);
   return hipErrorInvalidValue;
 }
 
+template <int NT, bool PAIR>
+hipError_t sk_dispatch_s(const StripedArgs& a, int grid, int splits, int waves, int group, bool dq,
+                         hipStream_t stream) {
+  if (group == 1) return sk_dispatch_w<NT, 1, PAIR>(a, grid, splits, waves, dq, stream);
+  if (group == 2) return sk_dispatch_w<NT, 2, PAIR>(a, grid, splits, waves, dq, stream);
+  if constexpr (!PAIR || NT == 1) {
+    if (group == 4) return sk_dispatch_w<NT, 4, PAIR>(a, grid, splits, waves, dq, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+// token tiles of 16: 1, 2 or 4 (33..48 tokens run as four tiles)
+int skinny_tiles(int rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : 4; }
+
 template <bool PAIR>
-hipError_t sk_dispatch_rows(const StripedArgs& a, int grid, int waves, bool dq, hipStream_t stream) {
-  switch ((a.rows + 15) / 16) {
-    case 1: return sk_dispatch<1, PAIR>(a, grid, waves, dq, stream);
-    case 2: return sk_dispatch<2, PAIR>(a, grid, waves, dq, stream);
-    case 3: return sk_dispatch<3, PAIR>(a, grid, waves, dq, stream);
-    case 4: return sk_dispatch<4, PAIR>(a, grid, waves, dq, stream);
+hipError_t sk_dispatch_rows(const StripedArgs& a, int grid, int splits, int waves, int group, bool dq,
+                            hipStream_t stream) {
+  switch (skinny_tiles(a.rows)) {
+    case 1: return sk_dispatch_s<1, PAIR>(a, grid, splits, waves, group, dq, stream);
+    case 2: return sk_dispatch_s<2, PAIR>(a, grid, splits, waves, group, dq, stream);
+    case 4: return sk_dispatch_s<4, PAIR>(a, grid, splits, waves, group, dq, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -709,11 +833,30 @@ StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool
   int stripes = 0;
   for (int i = 0; i < (pair ? 1 : nweights); ++i) stripes += d_out[i] / kStripeCols;
   const int chunks = (d_in + 63) / 64;
-  (void)rows;
-  int waves = 4;  // 4 or 8 waves per workgroup, about 4096 waves over the GPU
-  if ((long)stripes * 16 <= 4096 && chunks >= 16) waves = 8;
+  const int tiles = skinny_tiles(rows);
+  // Stripes per wave (group): each activation load then feeds that many
+  // stripes, which pays while the workgroups still cover the GPU (>= ~160);
+  // the pair keeps its registers in bounds with two past one token tile.
+  // With few stripes and a long d_in, d_in is split over workgroups (slabs
+  // of >= 32 chunks) up to ~256 workgroups: the hand-off costs a few
+  // microseconds of latency, which only a long d_in repays.
+  const int g = (pair && tiles > 1) ? 2 : 4;
+  int group = 1, splits = 1;
+  if (stripes / g >= 160) {
+    group = g;
+  } else if (chunks >= 64) {
+    group = g;
+    while ((stripes / group) * splits < 256 && chunks / (splits * 2) >= 32) splits *= 2;
+  } else if (stripes / 2 >= 160) {
+    group = 2;
+  }
+  const int waves = (tiles <= 2 && chunks / splits >= 16) ? 8 : 4;
+  p.group = group;
   p.waves = waves;
-  p.rows_per_wave = (chunks + waves - 1) / waves * 64;
+  p.splits = splits;
+  const int chunks_per_split = (chunks + splits - 1) / splits;
+  p.rows_per_wave = (chunks_per_split + waves - 1) / waves * 64;
+  p.rows_per_split = p.rows_per_wave * waves;
   p.stripes = stripes;
   return p;
 }
@@ -722,21 +865,32 @@ hipError_t launch_skinny(const StripedPlan& p, const uint16_t* x, int rows, int 
                          int nweights, bool pair, hipStream_t stream) {
   if (!skinny_supported(rows, d_in, x) || nweights < 1 || nweights > kMaxGemvWeights || (pair && nweights != 2))
     return hipErrorInvalidValue;
+  if ((p.group != 1 && p.group != 2 && p.group != 4) || p.splits < 1 || p.splits > 65535 ||
+      (long)p.rows_per_split * p.splits < d_in || p.rows_per_split != p.rows_per_wave * p.waves)
+    return hipErrorInvalidValue;
   StripedArgs a{};
   a.x = x;
   a.rows = rows;
   a.d_in = d_in;
   a.rows_per_wave = p.rows_per_wave;
+  a.rows_per_split = p.rows_per_split;
   a.nweights = nweights;
   int s = 0;
   for (int i = 0; i < nweights; ++i) {
     a.w[i] = weights[i];
+    if (p.splits > 1 && (!weights[i].partials || !weights[i].counters)) return hipErrorInvalidValue;
     a.stripe_begin[i] = pair ? 0 : s;
-    if (!pair || i == 0) s += weights[i].d_out / kStripeCols;
+    if (!pair || i == 0) s += weights[i].d_out / kStripeCols;  // a multiple of 4: groups never straddle weights
   }
   for (int i = nweights; i <= kMaxGemvWeights; ++i) a.stripe_begin[i] = s;
   const bool dq = weights[0].scales.kind == kScalesDQ;
-  return pair ? sk_dispatch_rows<true>(a, s, p.waves, dq, stream) : sk_dispatch_rows<false>(a, s, p.waves, dq, stream);
+  const int grid = s / p.group;
+  return pair ? sk_dispatch_rows<true>(a, grid, p.splits, p.waves, p.group, dq, stream)
+              : sk_dispatch_rows<false>(a, grid, p.splits, p.waves, p.group, dq, stream);
+}
+
+size_t skinny_partial_floats(const StripedPlan& p, int rows, int d_out) {
+  return p.splits > 1 ? (size_t)p.splits * rows * d_out : 0;
 }
 
 }  // namespace unifur
