@@ -163,3 +163,50 @@ def test_every_f32_in_unit_interval_gets_the_scan_code(device):
             lo = hi
         print(f"sign {hex(sign)} done, {checked} values", flush=True)
     assert checked == 2 * (0x3F800000 + 1)
+
+
+THRESHOLD_BITS = [
+    0xbf591cd8, 0xbf1c5270, 0xbeeb847f, 0xbeadea76, 0xbe703cec, 0xbe0d38bb, 0xbd3a7870, 0x3d22fb00,
+    0x3df64863, 0x3e5067e1, 0x3e9582d5, 0x3ec753fa, 0x3f006d04, 0x3f248db0, 0x3f5c89da,
+]
+
+
+def near_threshold_blocks(seed: int, nblocks: int) -> np.ndarray:
+    """Blocks whose values sit within a few ulp of threshold * absmax, for
+    absmax over the whole normal range and its ends (subnormal, 2^126 and
+    beyond, zero, with inf and NaN entries): the values the kernel's fast
+    reciprocal classification must hand to the exact division."""
+    rng = np.random.default_rng(seed)
+    T = np.array(THRESHOLD_BITS, np.uint32).view(np.float32)
+    exps = rng.integers(-130, 128, nblocks)
+    m = (rng.uniform(1.0, 2.0, nblocks) * np.exp2(exps.astype(np.float64))).astype(np.float32)
+    m[:8] = np.array([0.0, 1e-45, 1e-40, 1.1754944e-38, 8.507059e37, 1.7e38, 3.4028235e38, 1.0], np.float32)
+    m[~np.isfinite(m)] = np.float32(3.0e38)
+    blocks = np.zeros((nblocks, 64), np.float32)
+    blocks[:, 0] = m
+    with np.errstate(over="ignore", invalid="ignore"):
+        for j in range(1, 64):
+            t = T[rng.integers(0, 15, nblocks)]
+            v = (t.astype(np.float64) * m.astype(np.float64)).astype(np.float32)
+            k = rng.integers(-6, 7, nblocks)
+            for step in range(6):  # nudge by up to 6 ulp either way
+                v = np.where(k > step, np.nextafter(v, np.float32(np.inf)), v)
+                v = np.where(-k > step, np.nextafter(v, np.float32(-np.inf)), v)
+            blocks[:, j] = np.where(np.abs(v) <= m, v, np.float32(0.0))
+    blocks[8, 5] = np.inf
+    blocks[9, 7] = -np.inf
+    blocks[10, 3] = np.nan
+    blocks[11] = 0.0
+    return blocks.ravel()
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_values_next_to_thresholds_at_every_scale_bit_exact(device, oracle, seed):
+    v = near_threshold_blocks(seed, 4096)
+    x = torch.from_numpy(v).to(device)
+    p = Q.PackedNf4Tensor.quantize(x)
+    packed, absmax = oracle.quantize_packed(v)
+    got = p.codes.cpu().numpy()
+    bad = np.nonzero(got != packed)[0]
+    assert bad.size == 0, f"seed {seed}: {bad.size} code bytes differ, first at byte {bad[:5]}"
+    assert np.array_equal(u32(p.absmax.cpu().numpy()), u32(absmax))

@@ -321,3 +321,16 @@ def test_round_bf16_is_round_to_nearest_even(oracle):
     x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -3.0, np.inf], np.float32)
     r = oracle.round_bf16(x)
     assert list(r) == [1.0, 1.0, 1.0 + 2 ** -6, -3.0, np.inf]
+
+
+def test_thresholds_sit_far_from_bucket_edges_and_from_each_other():
+    # The GPU quantizer classifies v * rcp(absmax), which is within 2^-22 of
+    # fl(v / absmax), through a table over floor(16 u), and divides exactly
+    # only within 2^-20 of the threshold inside the bucket.  That is exact if
+    # every threshold is more than 2^-20 + 2^-22 from each bucket edge j / 16
+    # and the thresholds are more than 1/16 apart (one per bucket).
+    T = np.array(THRESHOLD_BITS, np.uint32).view(np.float32).astype(np.float64)
+    edge = np.abs(T * 16 - np.round(T * 16)) / 16
+    assert edge.min() > 2.0 ** -20 + 2.0 ** -22
+    assert edge.min() > 2.0 ** -10  # in fact more than 2^-10
+    assert np.diff(np.sort(T)).min() > 1.0 / 16

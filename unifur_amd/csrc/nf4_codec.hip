@@ -13,6 +13,11 @@
 namespace unifur {
 namespace {
 
+// Half-width of the window around a threshold where the quantizer's fast
+// reciprocal path defers to the exact division: 2^-20 >= 4x the 2^-22 by
+// which v * rcp(absmax) can differ from fl(v / absmax) for |u| <= 1.
+constexpr float kNear = 9.5367431640625e-07f;
+
 // Exact decision thresholds of nearest_level_code (src/quantize.rs:208-219):
 // for u in [-1, 1], scan(u) == #{t : u >= T[t]}.  Each T[t] is the smallest
 // f32 at which the strict-< scan over f32 distances first returns code t+1;
@@ -59,17 +64,54 @@ __device__ __forceinline__ uint32_t code_of(float u, const BucketEntry* tab) {
 // q of lane l reads float4 #(q*64 + l) of the wave's span, so every load is a
 // contiguous 1 KiB across the wave and block (q*4 + l/16) lives in the 16
 // consecutive lanes of one instruction: absmax is a 16-lane max reduction.
+//
+// The code of v is scan(fl(v / absmax)).  The IEEE division costs a dozen
+// instructions, so the kernel first classifies u' = v * rcp(absmax), which
+// is within 3 ulp of fl(v / absmax) whenever absmax is a normal f32 (rcp is
+// 1 ulp, the product 1/2 ulp).  scan is a step function whose steps sit at
+// the 15 thresholds, none of them within 2^-9 of a bucket edge, so u' and
+// fl(v / absmax) get the same code unless u' lies within kNear of the
+// threshold inside its bucket; those values, and every value of a block
+// whose absmax is zero, subnormal or not finite, take the exact division.
 constexpr int kQuantWaves = 4;  // waves per workgroup
 constexpr int kQuantThreads = kQuantWaves * 64;
 
-__device__ __forceinline__ float max16(float v) {
-  // NaN never reaches here (inputs pass through fabs + fmax with 0 start),
-  // so the order of the butterfly does not matter.
-  v = fmaxf(v, __shfl_xor(v, 1, 16));
-  v = fmaxf(v, __shfl_xor(v, 2, 16));
-  v = fmaxf(v, __shfl_xor(v, 4, 16));
-  v = fmaxf(v, __shfl_xor(v, 8, 16));
-  return v;
+// Max over the 16 lanes of each row, in every lane: DPP quad_perm [1,0,3,2]
+// and [2,3,0,1], then row_half_mirror and row_mirror (every lane of a quad,
+// then of a half row, then of the row holds the max of the span so far).
+// NaN never reaches here (inputs pass through fabs + fmax with 0 start), so
+// the order of the butterfly does not matter.
+// The values are >= 0 and never NaN, so their bit patterns order like the
+// values and the steps are integer maxes (no canonicalisation).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return __builtin_amdgcn_update_dpp(0u, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float max16(float f) {
+  uint32_t v = __float_as_uint(f);
+  v = max(v, dpp_u<0xB1>(v));
+  v = max(v, dpp_u<0x4E>(v));
+  v = max(v, dpp_u<0x141>(v));
+  v = max(v, dpp_u<0x140>(v));
+  return __uint_as_float(v);
+}
+
+// Code of v from u = v * rcp(absmax); `near` is set when u lies within kNear
+// of the threshold of its bucket (the caller then divides exactly).
+__device__ __forceinline__ uint32_t code_fast(float v, float r, const BucketEntry* tab, bool& near) {
+  const float u = v * r;
+  // bucket floor(16 u) + 16, by truncation of 16 u + 16 >= 0 (u >= -1 - 3 ulp;
+  // a bucket off by one next to an edge gives the same code, see above);
+  // a NaN u takes bucket 0: code 0, as the scan
+  const float t = __builtin_fmaf(u, 16.0f, 16.0f);
+  const uint32_t b = (uint32_t)fminf(fmaxf(t, 0.0f), 32.0f);  // < 0 and NaN -> 0 (maxNum)
+  const BucketEntry e = tab[b];
+  near = near || fabsf(u - e.t_in) <= kNear;
+  return e.base + (u >= e.t_in ? 1u : 0u);
+}
+
+__device__ __forceinline__ uint32_t code_exact(float v, float m, const BucketEntry* tab) {
+  return m == 0.0f ? 7u : code_of(v / m, tab);
 }
 
 __global__ __launch_bounds__(kQuantThreads) void quantize_full_kernel(
@@ -86,23 +128,33 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_full_kernel(
     f32x4 v[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) v[q] = __builtin_nontemporal_load(src + q * 64 + lane);
+    float m[4];
+    uint32_t nib[4];
+    bool exact = false;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       // absmax = fold(0, max(acc, |v|)) (src/quantize.rs:103); fmaxf is
       // IEEE maxNum, so NaN inputs are ignored exactly as Rust's f32::max.
-      float m = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v[q].x)), fmaxf(fabsf(v[q].y), fabsf(v[q].z))),
-                      fabsf(v[q].w));
-      m = max16(m);
-      uint32_t nib = 0;
-      if (m == 0.0f) {
-        nib = 0x7777u;  // all-zero block -> scan(0) = 7 (src/quantize.rs:108-110)
-      } else {
-        nib = code_of(v[q].x / m, tab) | (code_of(v[q].y / m, tab) << 4) |
-              (code_of(v[q].z / m, tab) << 8) | (code_of(v[q].w / m, tab) << 12);
-      }
+      m[q] = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v[q].x)), fmaxf(fabsf(v[q].y), fabsf(v[q].z))), fabsf(v[q].w));
+      m[q] = max16(m[q]);
+      // rcp(m) is a normal f32 for m in [2^-126, 2^126]; outside (m == 0:
+      // all codes 7, src/quantize.rs:108-110) the block takes the exact path
+      exact = exact || !(m[q] >= 1.1754943508222875e-38f && m[q] <= 8.507059173023462e+37f);
+      const float r = __builtin_amdgcn_rcpf(m[q]);
+      nib[q] = code_fast(v[q].x, r, tab, exact) | (code_fast(v[q].y, r, tab, exact) << 4) |
+               (code_fast(v[q].z, r, tab, exact) << 8) | (code_fast(v[q].w, r, tab, exact) << 12);
+    }
+    if (exact) {  // rare: this lane's 16 values by the exact division
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        nib[q] = code_exact(v[q].x, m[q], tab) | (code_exact(v[q].y, m[q], tab) << 4) |
+                 (code_exact(v[q].z, m[q], tab) << 8) | (code_exact(v[q].w, m[q], tab) << 12);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
       const size_t f4 = span * 256 + q * 64 + lane;  // float4 index == u16 index of packed
-      reinterpret_cast<uint16_t*>(packed)[f4] = (uint16_t)nib;
-      if ((lane & 15) == 0) absmax[f4 / 16] = m;
+      reinterpret_cast<uint16_t*>(packed)[f4] = (uint16_t)nib[q];
+      if ((lane & 15) == 0) absmax[f4 / 16] = m[q];
     }
   }
 }
@@ -145,6 +197,8 @@ __global__ void dq_max_kernel(const float* __restrict__ absmax, size_t nb, uint3
   if ((threadIdx.x & 63) == 0) atomicMax(max_bits, __float_as_uint(m));
 }
 
+__global__ void zero_u32_kernel(uint32_t* p) { *p = 0u; }
+
 __global__ void dq_encode_kernel(const float* __restrict__ absmax, size_t nb, const uint32_t* __restrict__ max_bits,
                                  uint8_t* __restrict__ q) {
   const float M = __uint_as_float(*max_bits);
@@ -160,10 +214,18 @@ __global__ void dq_encode_kernel(const float* __restrict__ absmax, size_t nb, co
 }
 
 // -------------------------------------------------------------- dequantize --
-// LUT in LDS: byte b -> {level[b & 15], level[b >> 4]}.  The DQ scale is
-// ((float)q / 255.0f) * sos, evaluated per block exactly as the reference.
-__device__ __forceinline__ void build_byte_lut(f32x2* lut) {
-  for (int b = threadIdx.x; b < 256; b += blockDim.x) lut[b] = f32x2{level(b & 15), level(b >> 4)};
+// LUT in LDS: byte b -> {level[b & 15], level[b >> 4]}, kDeqLutCopies copies
+// (lane l reads copy l % kDeqLutCopies: the random 8-byte reads of a wave
+// spread over the banks).  The DQ scale is ((float)q / 255.0f) * sos,
+// evaluated as the reference does, once per code in an LDS table.
+constexpr int kDeqLutCopies = 8;
+
+// NF4_LEVELS[c] for a per-lane c from immediates (no memory access)
+__device__ __forceinline__ float level_of(int c) {
+  float v = level(0);
+#pragma unroll
+  for (int i = 1; i < 16; ++i) v = c == i ? level(i) : v;
+  return v;
 }
 
 __device__ __forceinline__ float block_scale(const ScalesArg& s, size_t blk) {
@@ -171,29 +233,62 @@ __device__ __forceinline__ float block_scale(const ScalesArg& s, size_t blk) {
   return ((float)s.dq_codes[blk] / 255.0f) * (*s.scale_of_scales);
 }
 
-// Each thread expands 8 codes (4 bytes, one u32) per step; one block of 64
-// values is 8 threads.  Lanes read consecutive u32 (256 B per wave load).
-template <bool kBf16Out>
+// A wave covers kDeqTiles tiles of 512 values (128 float4) per step: lane l
+// expands the four values of float4 l and of float4 64 + l of each tile (two
+// code bytes each), so each store is a contiguous 1 KiB across the wave and
+// each code load a contiguous 128 bytes; 16 lanes share a 64-value block.
+// All loads of a step are issued before its lookups and stores.
+constexpr int kDeqTiles = 4;
+
+template <bool kBf16Out, bool kDQ>
 __global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* __restrict__ packed, ScalesArg scales,
-                                                         size_t n8, void* __restrict__ out) {
-  __shared__ f32x2 lut[256];
-  build_byte_lut(lut);
+                                                         size_t n_tiles, void* __restrict__ out) {
+  __shared__ f32x2 lut[256 * kDeqLutCopies];
+  __shared__ float dq_lut[256];
+  {
+    const int b = threadIdx.x;  // 256 threads: entry b, all its copies
+    const f32x2 e = {level_of(b & 15), level_of(b >> 4)};
+#pragma unroll
+    for (int c = 0; c < kDeqLutCopies; ++c) lut[b * kDeqLutCopies + c] = e;
+    if constexpr (kDQ) dq_lut[b] = ((float)b / 255.0f) * (*scales.scale_of_scales);  // src/quantize.rs:349
+  }
   __syncthreads();
-  const uint32_t* src = reinterpret_cast<const uint32_t*>(packed);
-  for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < n8; g += (size_t)gridDim.x * blockDim.x) {
-    uint32_t w = __builtin_nontemporal_load(src + g);
-    float s = block_scale(scales, g / 8);
-    f32x2 p0 = lut[w & 0xff], p1 = lut[(w >> 8) & 0xff], p2 = lut[(w >> 16) & 0xff], p3 = lut[w >> 24];
-    // out = NF4_LEVELS[c] * scale: one f32 multiply, as src/quantize.rs:362
-    float o0 = p0.x * s, o1 = p0.y * s, o2 = p1.x * s, o3 = p1.y * s;
-    float o4 = p2.x * s, o5 = p2.y * s, o6 = p3.x * s, o7 = p3.y * s;
-    if constexpr (kBf16Out) {
-      u32x4 r = {pack_bf16x2(o0, o1), pack_bf16x2(o2, o3), pack_bf16x2(o4, o5), pack_bf16x2(o6, o7)};
-      __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(out) + g);
-    } else {
-      f32x4* d = reinterpret_cast<f32x4*>(out) + 2 * g;
-      __builtin_nontemporal_store(f32x4{o0, o1, o2, o3}, d);
-      __builtin_nontemporal_store(f32x4{o4, o5, o6, o7}, d + 1);
+  const int lane = threadIdx.x & 63;
+  const int copy = lane % kDeqLutCopies;
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(packed);
+  const size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const size_t nwaves = (size_t)gridDim.x * 4;
+  for (size_t t0 = wave * kDeqTiles; t0 < n_tiles; t0 += nwaves * kDeqTiles) {
+    uint32_t w[kDeqTiles][2], sc[kDeqTiles][2];  // code bytes; scale (f32 bits or DQ code)
+#pragma unroll
+    for (int u = 0; u < kDeqTiles; ++u)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const size_t f4 = (t0 + u) * 128 + h * 64 + lane;  // float4 index == u16 index of the codes
+        const bool ok = t0 + u < n_tiles;
+        w[u][h] = ok ? __builtin_nontemporal_load(src + f4) : 0u;
+        if constexpr (kDQ)
+          sc[u][h] = ok ? scales.dq_codes[f4 / 16] : 0u;
+        else
+          sc[u][h] = ok ? __float_as_uint(scales.absmax[f4 / 16]) : 0u;
+      }
+#pragma unroll
+    for (int u = 0; u < kDeqTiles; ++u) {
+      if (t0 + u >= n_tiles) break;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const size_t f4 = (t0 + u) * 128 + h * 64 + lane;
+        const float s = kDQ ? dq_lut[sc[u][h]] : __uint_as_float(sc[u][h]);
+        const f32x2 p0 = lut[(w[u][h] & 0xff) * kDeqLutCopies + copy], p1 = lut[(w[u][h] >> 8) * kDeqLutCopies + copy];
+        // out = NF4_LEVELS[c] * scale: one f32 multiply, as src/quantize.rs:362
+        const float o0 = p0.x * s, o1 = p0.y * s, o2 = p1.x * s, o3 = p1.y * s;
+        if constexpr (kBf16Out) {
+          const u32x2 r = {pack_bf16x2(o0, o1), pack_bf16x2(o2, o3)};
+          __builtin_nontemporal_store(r, reinterpret_cast<u32x2*>(out) + f4);
+        } else {
+          __builtin_nontemporal_store(f32x4{o0, o1, o2, o3}, reinterpret_cast<f32x4*>(out) + f4);
+        }
+      }
     }
   }
 }
@@ -308,10 +403,11 @@ hipError_t launch_double_quantize(const float* absmax, size_t nb, uint8_t* q, fl
                                   hipStream_t stream) {
   // The scale of scales is the max itself, so its own storage is the
   // accumulator of the integer atomic max (non-negative f32 bits order as u32).
+  // (zeroed by a kernel rather than a memset node, so that the call can be
+  // captured in a graph)
   uint32_t* max_bits = reinterpret_cast<uint32_t*>(scale_of_scales);
-  hipError_t e = hipMemsetAsync(max_bits, 0, sizeof(uint32_t), stream);
-  if (e != hipSuccess) return e;
-  if (nb == 0) return hipSuccess;
+  zero_u32_kernel<<<1, 1, 0, stream>>>(max_bits);
+  if (nb == 0) return hipGetLastError();
   dq_max_kernel<<<grid_for(nb, 256, 1024), 256, 0, stream>>>(absmax, nb, max_bits);
   dq_encode_kernel<<<grid_for(nb, 256, 4096), 256, 0, stream>>>(absmax, nb, max_bits, q);
   return hipGetLastError();
@@ -320,17 +416,21 @@ hipError_t launch_double_quantize(const float* absmax, size_t nb, uint8_t* q, fl
 hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, size_t n, void* out, bool bf16_out,
                              bool aligned, hipStream_t stream) {
   if (n == 0) return hipSuccess;
-  // groups of 8 values take the vector kernel (4-byte aligned codes, 16-byte
-  // aligned output); the remainder, or everything if misaligned, the scalar one.
-  const size_t n8 = aligned ? n / 8 : 0;
-  if (n8) {
-    int grid = grid_for(n8, 256, 16384);
+  // tiles of 512 values take the vector kernel (2-byte aligned codes,
+  // 16-byte aligned output); the remainder, or everything if misaligned, the
+  // scalar one.
+  const size_t tiles = aligned ? n / 512 : 0;
+  if (tiles) {
+    const int grid = grid_for(tiles, 4 * kDeqTiles, 8192);
+    const bool dq = scales.kind == kScalesDQ;
     if (bf16_out)
-      dequantize_kernel<true><<<grid, 256, 0, stream>>>(packed, scales, n8, out);
+      dq ? dequantize_kernel<true, true><<<grid, 256, 0, stream>>>(packed, scales, tiles, out)
+         : dequantize_kernel<true, false><<<grid, 256, 0, stream>>>(packed, scales, tiles, out);
     else
-      dequantize_kernel<false><<<grid, 256, 0, stream>>>(packed, scales, n8, out);
+      dq ? dequantize_kernel<false, true><<<grid, 256, 0, stream>>>(packed, scales, tiles, out)
+         : dequantize_kernel<false, false><<<grid, 256, 0, stream>>>(packed, scales, tiles, out);
   }
-  const size_t first = n8 * 8;
+  const size_t first = tiles * 512;
   if (first < n) {
     unsigned g = (unsigned)((n - first + 63) / 64);
     if (bf16_out)
