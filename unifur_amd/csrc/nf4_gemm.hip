@@ -90,10 +90,10 @@ struct BStep {
   uint32_t scale[4];
 };
 
-// The producer's vmcnt arithmetic counts these: 8 X copies, then the loads
-// below (4 code dwords, and 4 scale loads row-major or 1 striped).
+// The producer's vmcnt arithmetic counts these: the B loads of one step (4
+// code dwords, and 4 scale loads row-major or 1 striped).
 template <bool STRIPED>
-constexpr int kStepLoads = 8 + 4 + (STRIPED ? 1 : 4);
+constexpr int kStepLoads = 4 + (STRIPED ? 1 : 4);
 
 template <bool DQ, bool STRIPED>
 __device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int k0, int tid) {
@@ -220,9 +220,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const bool producer = wave >= 4;
-  const int w4 = wave & 3;   // MFMA wave index, or the MFMA wave a producer copies X for
-  const int pt = tid & 255;  // producer thread index
+  const int w4 = wave & 3;  // MFMA wave index (waves 0-3)
 
   // XCD-aware tile order: workgroup b runs on XCD b % 8; each XCD takes a
   // contiguous run of tiles in row-major (m, n) order, so the workgroups
@@ -247,40 +245,73 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   const int nk = g.K / kBK;
   const int awave = kLdsA + w4 * (kATileBytes / 4);
 
-  // Both roles pass the same number of workgroup barriers: 2 before the
-  // loop and one per K step.
-  if (producer) {
-    // Loads per step, in issue order: 8 X copies, then 4 code + 4 scale
-    // loads.  Load indices are clamped to the last step (a harmless
-    // in-bounds reload into a free stage) so that every step issues the same
-    // loads and the vmcnt arithmetic holds.
-    BStep B0, B1;
-    load_a(xr, g.K, row0, 0, awave, lane);
-    load_b<DQ, STRIPED>(B0, g, n0, 0, pt);
-    load_a(xr, g.K, row0, min(1, nk - 1) * kBK, awave + kATileBytes, lane);
-    load_b<DQ, STRIPED>(B1, g, n0, min(1, nk - 1) * kBK, pt);
+  // Every role passes the same workgroup barriers: 2 before the K loop, one
+  // per step handed over (nk - 1), and one more when nk is even (the MFMA
+  // waves' loop runs steps in pairs and ends with a barrier).
+  if (wave == 4 || wave == 5) {
+    // Copy waves: X tiles of MFMA waves 2 (wave - 4) and 2 (wave - 4) + 1,
+    // two steps ahead in three LDS stages.  These waves issue nothing but
+    // the LDS copies, so the only waits on them are the explicit ones.
+    const int c0 = 2 * (wave - 4);
+    const int base0 = kLdsA + c0 * (kATileBytes / 4), base1 = base0 + kATileBytes / 4;
+    const int r0 = m0 + 64 * c0, r1 = r0 + 64;
+    auto copy = [&](int step, int stage) {
+      load_a(xr, g.K, r0, min(step, nk - 1) * kBK, base0 + stage * kATileBytes, lane);
+      load_a(xr, g.K, r1, min(step, nk - 1) * kBK, base1 + stage * kATileBytes, lane);
+    };
+    copy(0, 0);
+    copy(1, 1);
     __syncthreads();  // LUTs visible
-    store_b<DQ, STRIPED>(B0, smem, 0, pt);
-    UNIFUR_WAIT_VMCNT(kStepLoads<STRIPED>);  // X of step 0 landed (step 1's 16 loads may be in flight)
+    UNIFUR_WAIT_VMCNT(16);  // step 0 landed (step 1's 16 copies may fly)
     __syncthreads();
-    int sa = 0;  // X stage of step kt
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-      int s2 = sa >= 1 ? sa - 1 : sa + 2;  // (kt + 2) % 3
-      load_a(xr, g.K, row0, min(kt + 2, nk - 1) * kBK, awave + s2 * kATileBytes, lane);
-      load_b<DQ, STRIPED>(B0, g, n0, min(kt + 2, nk - 1) * kBK, pt);
-      store_b<DQ, STRIPED>(B1, smem, 1, pt);
-      UNIFUR_WAIT_VMCNT(kStepLoads<STRIPED>);
+    int stage = 2;  // stage of step s1 + 1
+    for (int s1 = 1; s1 < nk; ++s1) {
+      copy(s1 + 1, stage);  // clamped past the last step: a harmless reload into a free stage
+      UNIFUR_WAIT_VMCNT(16);  // step s1 landed
       __syncthreads();
-      sa = sa == 2 ? 0 : sa + 1;
-      s2 = sa >= 1 ? sa - 1 : sa + 2;
-      load_a(xr, g.K, row0, min(kt + 3, nk - 1) * kBK, awave + s2 * kATileBytes, lane);
-      load_b<DQ, STRIPED>(B1, g, n0, min(kt + 3, nk - 1) * kBK, pt);
-      store_b<DQ, STRIPED>(B0, smem, 0, pt);
-      UNIFUR_WAIT_VMCNT(kStepLoads<STRIPED>);
-      __syncthreads();
-      sa = sa == 2 ? 0 : sa + 1;
+      stage = stage == 2 ? 0 : stage + 1;
     }
+    if ((nk & 1) == 0) __syncthreads();
+    UNIFUR_WAIT_VMCNT(0);
+    return;
+  }
+  if (wave >= 6) {
+    // Dequantizing waves: thread d expands the W-tile parts of producer
+    // indices d and d + 128, from codes loaded kBRing steps ahead.
+    constexpr int kBRing = 4;
+    const int d = tid - 384;
+    BStep Br[2][kBRing];
+#pragma unroll
+    for (int r = 0; r < kBRing; ++r)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) load_b<DQ, STRIPED>(Br[h][r], g, n0, min(r, nk - 1) * kBK, d + 128 * h);
+    __syncthreads();  // LUTs visible
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      store_b<DQ, STRIPED>(Br[h][0], smem, 0, d + 128 * h);
+      load_b<DQ, STRIPED>(Br[h][0], g, n0, min(kBRing, nk - 1) * kBK, d + 128 * h);
+    }
+    __syncthreads();  // step 0 ready
+    auto handoff = [&](int s1, int slot) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        store_b<DQ, STRIPED>(Br[h][slot], smem, s1 & 1, d + 128 * h);
+        load_b<DQ, STRIPED>(Br[h][slot], g, n0, min(s1 + kBRing, nk - 1) * kBK, d + 128 * h);
+      }
+      __syncthreads();
+    };
+    // whole rounds of kBRing handoffs (static ring slots), then the rest
+    int s1 = 1;
+    for (; s1 + kBRing <= nk; s1 += kBRing) {
+#pragma unroll
+      for (int u = 0; u < kBRing; ++u) handoff(s1 + u, (u + 1) % kBRing);
+    }
+    for (int u = 0; s1 < nk; ++s1, ++u) {  // slot of step s1 = (u + 1) % kBRing
+      if (u == 0) handoff(s1, 1);
+      else if (u == 1) handoff(s1, 2);
+      else handoff(s1, 3);
+    }
+    if ((nk & 1) == 0) __syncthreads();
     UNIFUR_WAIT_VMCNT(0);  // drain the clamped reloads before the wave exits
     return;
   }
