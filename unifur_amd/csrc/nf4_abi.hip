@@ -178,7 +178,7 @@ struct LinearLayout {
   LinearPath path;
   GemvPlan gemv;
   StripedPlan striped;
-  size_t partials, xa, xa_part, wf32, rm_codes, rm_scales, total;
+  size_t partials, xa, lora_at, lora_bt, wf32, rm_codes, rm_scales, total;
 };
 
 // Decode-sized batches (<= 4 rows) take a GEMV (the striped one for striped
@@ -221,10 +221,15 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
       L.rm_scales = c.take(scale_bytes(ceil_div_u64(d_in * d_out, 64), scale_kind));
     }
   }
-  const uint64_t xa_cols = L.path == LinearPath::kMfma && lora_rank ? (uint64_t)lora_pad((int)lora_rank) : lora_rank;
-  L.xa = c.take((size_t)rows * xa_cols * sizeof(float));
-  if (L.path == LinearPath::kMfma && lora_rank)
-    L.xa_part = c.take(lora_xa_partial_floats((int)rows, (int)d_in, (int)lora_rank) * sizeof(float));
+  if (L.path == LinearPath::kMfma && lora_rank) {
+    // bf16 operands of the fused epilogue: xa [rows, pad], A^T [pad, d_in], B^T [d_out, pad]
+    const size_t pad = (size_t)lora_pad((int)lora_rank);
+    L.xa = c.take((size_t)rows * pad * 2);
+    L.lora_at = c.take(pad * d_in * 2);
+    L.lora_bt = c.take((size_t)d_out * pad * 2);
+  } else {
+    L.xa = c.take((size_t)rows * lora_rank * sizeof(float));
+  }
   L.total = c.off;
   return L;
 }
@@ -289,13 +294,15 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   float* xa = nullptr;
   if (L.path == LinearPath::kMfma) {
     const uint16_t* xb = static_cast<const uint16_t*>(x);
+    uint16_t *xa16 = nullptr, *bt16 = nullptr;
     if (lora) {
-      xa = at<float>(ws, L.xa);
-      UNIFUR_HIP(launch_lora_xa_bf16(xb, lora->a, (int)rows, (int)w->d_in, (int)rank, lora->scaling,
-                                     at<float>(ws, L.xa_part), xa, stream));
+      xa16 = at<uint16_t>(ws, L.xa);
+      bt16 = at<uint16_t>(ws, L.lora_bt);
+      UNIFUR_HIP(launch_lora_operands(xb, lora->a, lora->b, (int)rows, (int)w->d_in, (int)w->d_out, (int)rank,
+                                      lora->scaling, at<uint16_t>(ws, L.lora_at), bt16, xa16, stream));
     }
-    UNIFUR_HIP(launch_gemm(xb, w->packed, to_scales(w->scales), (int)rows, (int)w->d_in, (int)w->d_out, bias, xa,
-                           lora ? lora->b : nullptr, (int)rank, y, ybf, is_striped(w), stream));
+    UNIFUR_HIP(launch_gemm(xb, w->packed, to_scales(w->scales), (int)rows, (int)w->d_in, (int)w->d_out, bias, xa16,
+                           bt16, (int)rank, y, ybf, is_striped(w), stream));
     return UNIFUR_NF4_OK;
   }
   if (lora) {

@@ -51,8 +51,8 @@ struct GemmArgs {
   ScalesArg scales;
   int M, K, N;
   const float* bias;     // [N] or null
-  const float* lora_xa;  // [M, lora_pad]: scaling * (x A), zero past lora_rank; or null
-  const float* lora_b;   // [lora_rank, N]
+  const uint16_t* lora_xa;  // bf16 [M, lora_pad]: scaling * (x A), zero past lora_rank; or null
+  const uint16_t* lora_bt;  // bf16 [N, lora_pad]: B transposed, zero past lora_rank
   int lora_rank, lora_pad;
   void* y;  // [M, N] f32 or bf16
   int y_bf16;
@@ -336,30 +336,27 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   if (kt < nk) mma_step(acc, awave + sa * kATileBytes, kLdsB, lane);  // odd step count: last W in buffer 0
 
   if constexpr (LORA) {
-    // acc += xa[rows, r] . B[r, cols], xa already scaled: one 32x32x16 MFMA
-    // per tile and 16 adapter columns (columns past lora_rank contribute zero).
+    // acc += xa[rows, r] . B[r, cols] (xa already scaled), one 32x32x16 MFMA
+    // per tile and 16 adapter columns; both operands are bf16 laid out so
+    // that each fragment is one 16-byte load (columns past the rank are zero).
     const int kr = (lane >> 5) * 8;
-    for (int r0 = 0; r0 < g.lora_rank; r0 += 16) {
-      bf16x8 bfr[4];
+    for (int r0 = 0; r0 < g.lora_pad; r0 += 16) {
+      bf16x8 bfr[4], af[2];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = n0 + 32 * j + (lane & 31);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int r = r0 + kr + q;
-          bfr[j][q] = r < g.lora_rank ? (__bf16)g.lora_b[(size_t)r * g.N + n] : (__bf16)0.0f;
-        }
+        bfr[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(g.lora_bt + (size_t)n * g.lora_pad + r0 + kr));
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int m = row0 + 32 * i + (lane & 31);
-        bf16x8 af;
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          af[q] = m < g.M ? (__bf16)g.lora_xa[(size_t)m * g.lora_pad + r0 + kr + q] : (__bf16)0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bfr[j], acc[i][j], 0, 0, 0);
+        af[i] = m < g.M ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(g.lora_xa + (size_t)m * g.lora_pad + r0 + kr))
+                        : bf16x8{};
       }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
   }
 
@@ -407,61 +404,67 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
 }
 
 // ------------------------------------------------------------ LoRA x A ------
-// xa[m][j] = scaling * sum_k x[m][k] a[k][j], the first factor of
-// LoraAdapter::forward (src/quantize.rs:619-624) with the scaling folded in,
-// laid out [M, pad] (pad = rank rounded up to 16, zero past the rank) for the
-// fused epilogue.  Two launches: partial products over 256-wide K slices
-// (one workgroup per 64 rows x 16 adapter columns x slice; the slice of a is
-// staged in LDS as bf16 and is the B operand of 16x16x32 MFMAs whose A
-// operand is read straight from X, all eight loads of a wave issued before
-// its MFMAs), then a fixed-order sum over the slices.
-constexpr int kXaK = 256;
-constexpr int kXaRowsPerWg = 64;
-constexpr int kXaColStride = kXaK + 8;  // bf16 elements: 16-byte pad per column row
+// The adapter operands of the fused epilogue, in bf16 layouts whose MFMA
+// fragments are single 16-byte loads (pad = rank rounded up to 16, zero past
+// the rank): at[pad][K] = A transposed and bt[N][pad] = B transposed (one
+// small prep kernel), then xa[M][pad] = bf16(scaling * (X A)) -- the first
+// factor of LoraAdapter::forward (src/quantize.rs:619-624) with the scaling
+// folded in -- by a kernel of 16-row x 16-column tiles whose four waves split
+// K into quarters (v_mfma_f32_16x16x32_bf16, X and at straight from memory,
+// eight steps of loads in flight) and add their quarters through LDS.
 
-__global__ __launch_bounds__(256) void lora_xa_partial_kernel(const uint16_t* __restrict__ x,
-                                                              const float* __restrict__ a, int M, int K, int rank,
-                                                              int pad, float* __restrict__ part) {
-  __shared__ __attribute__((aligned(16))) __bf16 as[16 * kXaColStride];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int m0 = blockIdx.x * kXaRowsPerWg, s = blockIdx.y, c0 = blockIdx.z * 16;
-  const int k0 = s * kXaK;
-  const int kl = min(kXaK, K - k0);  // a multiple of 32
-  for (int i = tid; i < kXaK * 16; i += 256) {  // zero past the slice end and the rank
-    const int k = i >> 4, c = i & 15;
-    const float v = (k < kl && c0 + c < rank) ? a[(size_t)(k0 + k) * rank + c0 + c] : 0.0f;
-    as[c * kXaColStride + k] = (__bf16)v;
-  }
-  __syncthreads();
-  const int row = m0 + 16 * w + (lane & 15);
-  const uint16_t* xr = x + (size_t)row * K + k0 + (lane >> 4) * 8;
-  const __bf16* ar = as + (lane & 15) * kXaColStride + (lane >> 4) * 8;
-  bf16x8 xv[kXaK / 32];
-#pragma unroll
-  for (int q = 0; q < kXaK / 32; ++q)
-    xv[q] = (row < M && 32 * q < kl) ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xr + 32 * q))
-                                     : bf16x8{};
-  f32x4 acc = {};
-#pragma unroll
-  for (int q = 0; q < kXaK / 32; ++q) {
-    const bf16x8 bf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ar + 32 * q));
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[q], bf, acc, 0, 0, 0);
-  }
-  // acc[e] = C[row 4 (lane / 16) + e][col lane % 16]
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int m = m0 + 16 * w + 4 * (lane >> 4) + e;
-    if (m < M) part[((size_t)s * M + m) * pad + c0 + (lane & 15)] = acc[e];
+__global__ void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b, int K, int N, int rank,
+                                 int pad, uint16_t* __restrict__ at, uint16_t* __restrict__ bt) {
+  const size_t na = (size_t)pad * K, total = na + (size_t)N * pad;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    if (i < na) {
+      const int j = (int)(i / K), k = (int)(i % K);  // at[j][k] = a[k][j]
+      at[i] = j < rank ? (uint16_t)(pack_bf16x2(a[(size_t)k * rank + j], 0.0f) & 0xffffu) : (uint16_t)0;
+    } else {
+      const size_t q = i - na;
+      const int n = (int)(q / pad), j = (int)(q % pad);  // bt[n][j] = b[j][n]
+      bt[q] = j < rank ? (uint16_t)(pack_bf16x2(b[(size_t)j * N + n], 0.0f) & 0xffffu) : (uint16_t)0;
+    }
   }
 }
 
-__global__ void lora_xa_reduce_kernel(const float* __restrict__ part, int slices, int M, int rank, int pad,
-                                      float scaling, float* __restrict__ xa) {
-  const size_t n = (size_t)M * pad;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-    float v = 0.0f;
-    for (int s = 0; s < slices; ++s) v += part[(size_t)s * n + i];
-    xa[i] = (int)(i % pad) < rank ? v * scaling : 0.0f;
+constexpr int kXaBatch = 8;  // k32 steps whose loads are in flight together
+
+__global__ __launch_bounds__(256) void lora_xa_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ at,
+                                                      int M, int K, int pad, float scaling, uint16_t* __restrict__ xa) {
+  __shared__ float red[4][256];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int m0 = blockIdx.x * 16, c0 = blockIdx.y * 16;
+  const int kq = K / 4;  // a multiple of 16 (K % 64 == 0)
+  const int kbeg = w * kq, kend = kbeg + kq;
+  // rows past M read as zero (buffer bound)
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), 0x00020000);
+  const uint32_t xrow = (uint32_t)(m0 + (lane & 15)) * (uint32_t)K * 2u;
+  const uint16_t* arow = at + (size_t)(c0 + (lane & 15)) * K;
+  const int kl = 8 * (lane >> 4);  // this lane's 8 k of each 32
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = kbeg; k0 < kend; k0 += 32 * kXaBatch) {
+    bf16x8 xv[kXaBatch], av[kXaBatch];
+#pragma unroll
+    for (int q = 0; q < kXaBatch; ++q) {
+      const int k = k0 + 32 * q + kl;
+      const bool ok = k < kend;  // K / 4 may be an odd multiple of 16: mask per 8-k group
+      xv[q] = ok ? __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, xrow + (uint32_t)k * 2u, 0, 0))
+                 : bf16x8{};
+      av[q] = ok ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(arow + k)) : bf16x8{};
+    }
+#pragma unroll
+    for (int q = 0; q < kXaBatch; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[q], av[q], acc, 0, 0, 0);
+  }
+  // acc[e] = C[row 4 (lane / 16) + e][col lane % 16]; add the four K quarters
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[w][(4 * (lane >> 4) + e) * 16 + (lane & 15)] = acc[e];
+  __syncthreads();
+  const int t = threadIdx.x, m = m0 + t / 16;
+  if (m < M) {
+    const float v = (red[0][t] + red[1][t] + red[2][t] + red[3][t]) * scaling;
+    xa[(size_t)m * pad + c0 + (t & 15)] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
   }
 }
 
@@ -475,26 +478,21 @@ bool gemm_supported(int M, int K, int N, const void* x) {
 
 int lora_pad(int rank) { return (rank + 15) / 16 * 16; }
 
-size_t lora_xa_partial_floats(int M, int K, int rank) {
-  return (size_t)((K + kXaK - 1) / kXaK) * (size_t)M * (size_t)lora_pad(rank);
-}
-
-hipError_t launch_lora_xa_bf16(const uint16_t* x, const float* a, int M, int K, int rank, float scaling, float* part,
-                               float* xa, hipStream_t stream) {
-  if (rank < 1 || rank > 64 || K % 32 != 0) return hipErrorInvalidValue;
-  const int pad = lora_pad(rank), slices = (K + kXaK - 1) / kXaK;
-  const dim3 grid((M + kXaRowsPerWg - 1) / kXaRowsPerWg, slices, pad / 16);
-  lora_xa_partial_kernel<<<grid, 256, 0, stream>>>(x, a, M, K, rank, pad, part);
+hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* b, int M, int K, int N, int rank,
+                                float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa, hipStream_t stream) {
+  if (rank < 1 || rank > 64 || K % 64 != 0) return hipErrorInvalidValue;
+  const int pad = lora_pad(rank);
+  const size_t total = (size_t)pad * K + (size_t)N * pad;
+  lora_prep_kernel<<<(unsigned)std::min<size_t>((total + 255) / 256, 2048), 256, 0, stream>>>(a, b, K, N, rank, pad,
+                                                                                             at, bt);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t n = (size_t)M * pad;
-  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 2048);
-  lora_xa_reduce_kernel<<<blocks, 256, 0, stream>>>(part, slices, M, rank, pad, scaling, xa);
+  lora_xa_kernel<<<dim3((M + 15) / 16, pad / 16), 256, 0, stream>>>(x, at, M, K, pad, scaling, xa);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
-                       const float* bias, const float* lora_xa, const float* lora_b, int lora_rank, void* y,
+                       const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
                        bool y_bf16, bool striped, hipStream_t stream) {
   GemmArgs g{};
   g.x = x;
@@ -505,7 +503,7 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
   g.N = N;
   g.bias = bias;
   g.lora_xa = lora_xa;
-  g.lora_b = lora_b;
+  g.lora_bt = lora_bt;
   g.lora_rank = lora_rank;
   g.lora_pad = lora_pad(lora_rank);
   g.y = y;

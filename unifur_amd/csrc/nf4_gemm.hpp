@@ -11,22 +11,21 @@ namespace unifur {
 // offsets).
 bool gemm_supported(int M, int K, int N, const void* x);
 
-// Row stride (in floats) of the xa buffer launch_lora_xa_bf16 writes.
+// Adapter columns padded to a multiple of 16 (the row stride of the LoRA
+// operand buffers below).
 int lora_pad(int rank);
 
-// Floats of split-K partial products launch_lora_xa_bf16 needs.
-size_t lora_xa_partial_floats(int M, int K, int rank);
+// The fused LoRA epilogue's operands, bf16: at[pad][K] (A transposed),
+// bt[N][pad] (B transposed) and xa[M][pad] = scaling * (X A), zero past the
+// rank; rank <= 64, K a multiple of 64.
+hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* b, int M, int K, int N, int rank,
+                                float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa, hipStream_t stream);
 
-// xa[M, lora_pad(rank)] = scaling * (X A), zero past the rank, via
-// part[lora_xa_partial_floats]; rank <= 64, K a multiple of 32.
-hipError_t launch_lora_xa_bf16(const uint16_t* x, const float* a, int M, int K, int rank, float scaling, float* part,
-                               float* xa, hipStream_t stream);
-
-// Y[M, N] = X deq(W) (+ bias) (+ xa B); xa from launch_lora_xa_bf16 or null.
+// Y[M, N] = X deq(W) (+ bias) (+ xa B); xa and bt from launch_lora_operands, or null.
 // The weight is in the reference's row-major layout, or striped
 // (nf4_layout.hpp) when striped is set.
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
-                       const float* bias, const float* lora_xa, const float* lora_b, int lora_rank, void* y,
+                       const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
                        bool y_bf16, bool striped, hipStream_t stream);
 
 }  // namespace unifur
