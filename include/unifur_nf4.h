@@ -166,6 +166,17 @@ int unifur_nf4_unstripe_weight(const unifur_nf4_weight *src, uint8_t *dst_packed
 uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
                                           uint32_t lora_rank);
 
+/* The least workspace a call with these arguments accepts.  Batches of more
+ * than 64 bf16 rows normally expand the weight (plus the LoRA update) to
+ * bf16 in the workspace -- d_in * d_out * 2 bytes, plus the BLAS GEMM's
+ * scratch -- and multiply with a BLAS GEMM; given a workspace smaller than
+ * unifur_nf4_linear_workspace_size but at least this size, they take the
+ * fused MFMA kernel instead, which dequantizes W tiles on chip and needs no
+ * weight-sized scratch.  Has no counterpart in the reference (which
+ * allocates freely); it is for callers with bounded device memory. */
+uint64_t unifur_nf4_linear_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
+                                              uint32_t lora_rank);
+
 /* Nf4Linear::forward (src/qwennet.rs:238-241): y = x deq(W) (+ bias), and with
  * lora != NULL QloraLinear::forward (src/qwennet.rs:325-345): base(x) +
  * (x a) b * scaling.  x [rows, d_in] (f32 or bf16), y [rows, d_out]
@@ -198,6 +209,9 @@ int unifur_nf4_lora_merge(const float *w, uint64_t d_in, uint64_t d_out, const u
 
 /* Workspace bytes of unifur_nf4_swiglu_forward (same contract as above). */
 uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype);
+/* The least workspace unifur_nf4_swiglu_forward accepts (the fused MFMA
+ * kernels for more than 64 bf16 rows; see unifur_nf4_linear_min_workspace_size). */
+uint64_t unifur_nf4_swiglu_min_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype);
 
 /* QwenMlp::forward (src/qwennet.rs:816-819): y = down(silu(gate x) * up x),
  * silu(z) = z * sigmoid(z) (src/tensor_ext.rs:87-90).  gate and up are

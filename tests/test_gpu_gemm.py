@@ -111,22 +111,49 @@ def test_misaligned_activations_take_the_generic_path(device, oracle):
     check(aligned, oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_BF16, "aligned x")
 
 
-def test_workspace_for_mfma_lora_is_small(device, oracle):
-    # the MFMA path needs only the LoRA xa buffer and its partial products
-    # over 256-wide K slices (16 of them for K = 4096)
-    need = L.lib().unifur_nf4_linear_workspace_size(2048, 4096, 4096, L.BF16, 16)
-    assert need <= 65536 + (1 + 16) * 2048 * 16 * 4 + 512
-    M, K, N, r = 256, 512, 256, 16
-    lin, wdeq = make_linear(oracle, K, N, 600, device)
-    x, xt = acts(oracle, M, K, 601, torch.bfloat16, device)
-    a, b, ad = lora_parts(oracle, K, N, r, 602, device)
-    need = L.lib().unifur_nf4_linear_workspace_size(M, K, N, L.BF16, r)
+def _qlora_with_workspace(device, oracle, M, K, N, r, need, seed, striped=True):
+    lin, wdeq = make_linear(oracle, K, N, seed, device, striped=striped)
+    x, xt = acts(oracle, M, K, seed + 1, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, seed + 2, device)
+    bias = oracle.fill_normal(seed + 3, 0.1, N)
+    bt = torch.from_numpy(bias).to(device)
     ws = torch.zeros(need, dtype=torch.uint8, device=device)
-    y = torch.empty(M, N, device=device)
     w, lo = lin.weight_struct(), ad.struct()
     stream = torch.cuda.current_stream().cuda_stream
-    L.check(L.lib().unifur_nf4_qlora_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w), ctypes.byref(lo),
-                                             y.data_ptr(), L.F32, ws.data_ptr(), need, stream))
-    ref = oracle.linear_ref_f64(x, wdeq) + oracle.lora_ref_f64(x, a, b, 2.0)
-    check(y, ref, x, wdeq, TOL_BF16, "mfma user workspace")
+    ref = oracle.linear_ref_f64(x, wdeq, bias) + oracle.lora_ref_f64(x, a, b, 2.0)
+    outs = []
+    for _ in range(2):
+        y = torch.empty(M, N, device=device)
+        L.check(L.lib().unifur_nf4_linear_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w),
+                                                  bt.data_ptr(),
+                                                  ctypes.byref(lo), y.data_ptr(), L.F32, ws.data_ptr(), need, stream))
+        check(y, ref, x, wdeq, TOL_BF16, f"prefill workspace {need}")
+        outs.append(y)
+    assert torch.equal(outs[0], outs[1])
     assert int(ws[:65536].count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("striped", [True, False])
+def test_workspace_sizes_select_expanded_or_fused_prefill(device, oracle, striped):
+    # the default size holds the bf16 expansion of W (d_in d_out 2 bytes) and
+    # the BLAS scratch; the minimum only the fused kernel's LoRA operands
+    M, K, N, r = 256, 512, 256, 16
+    full = L.lib().unifur_nf4_linear_workspace_size(M, K, N, L.BF16, r)
+    lean = L.lib().unifur_nf4_linear_min_workspace_size(M, K, N, L.BF16, r)
+    assert full >= 65536 + K * N * 2
+    assert lean < K * N * 2 and lean <= 65536 + M * 16 * 2 + 16 * K * 2 + N * 16 * 2 + 3 * 256
+    assert L.lib().unifur_nf4_linear_min_workspace_size(4, K, N, L.F32, 0) == \
+        L.lib().unifur_nf4_linear_workspace_size(4, K, N, L.F32, 0)
+    _qlora_with_workspace(device, oracle, M, K, N, r, full, 600, striped)   # expanded + BLAS
+    _qlora_with_workspace(device, oracle, M, K, N, r, lean, 610, striped)   # fused kernel
+    with pytest.raises(RuntimeError):
+        _qlora_with_workspace(device, oracle, M, K, N, r, lean - 256, 620, striped)
+
+
+@pytest.mark.parametrize("M", [65, 128, 300, 2048])
+def test_fused_prefill_kernel_config3_shapes(device, oracle, M):
+    # the fused MFMA kernel (what a caller with bounded scratch gets) at the
+    # config-3 weight shape, with bias and LoRA, against the same reference
+    K, N, r = 4096, 4096, 16
+    lean = L.lib().unifur_nf4_linear_min_workspace_size(M, K, N, L.BF16, r)
+    _qlora_with_workspace(device, oracle, M, K, N, r, lean, 700 + M)

@@ -163,6 +163,33 @@ def test_swiglu_config4(device, oracle, T, striped):
     check(y, ref, h, wd, TOL_BF16, f"swiglu config4 T={T} striped={striped}")
 
 
+@pytest.mark.parametrize("striped", [True, False])
+def test_swiglu_prefill_expanded_and_fused(device, oracle, striped):
+    # more than 64 rows: with the default workspace each weight is expanded to
+    # bf16 and multiplied by the BLAS GEMM; with the minimum workspace the
+    # fused MFMA kernel runs; both within the bf16 tolerance
+    from unifur_amd import _lib as L
+    import ctypes
+    T, hidden, inter = 200, 1024, 2816
+    g, wg = make_linear(oracle, hidden, inter, 61, device, striped=striped)
+    u, wu = make_linear(oracle, hidden, inter, 62, device, striped=striped)
+    d, wd = make_linear(oracle, inter, hidden, 63, device, striped=striped)
+    x, xt = acts(oracle, T, hidden, 64, torch.bfloat16, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    full = L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16)
+    lean = L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)
+    assert lean < hidden * inter * 2 < full
+    gs, us, ds = g.weight_struct(), u.weight_struct(), d.weight_struct()
+    stream = torch.cuda.current_stream().cuda_stream
+    for need in (full, lean):
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        y = torch.empty(T, hidden, device=device)
+        L.check(L.lib().unifur_nf4_swiglu_forward(xt.data_ptr(), L.BF16, T, ctypes.byref(gs), ctypes.byref(us),
+                                                  ctypes.byref(ds), y.data_ptr(), L.F32, ws.data_ptr(), need, stream))
+        check(y, ref, h, wd, TOL_BF16, f"swiglu T={T} workspace {need}")
+
+
 def test_workspace_shared_by_generic_then_gemv_calls(device, oracle):
     # A generic-path call writes an f32 weight copy into the workspace; the
     # GEMV's split-K arrival counters live in a region nothing else touches,

@@ -14,6 +14,7 @@
 
 #include "../../include/unifur_nf4.h"
 #include "nf4_codec.hpp"
+#include "nf4_expand.hpp"
 #include "nf4_gemm.hpp"
 #include "nf4_generic.hpp"
 #include "nf4_gemv.hpp"
@@ -176,18 +177,22 @@ bool gemv_layout_ok(uint64_t d_in, uint64_t d_out, const void* packed) {
 
 struct LinearLayout {
   LinearPath path;
+  bool expand;  // kMfma: bf16 weight expanded in the workspace + BLAS GEMM (else the fused kernel)
   GemvPlan gemv;
   StripedPlan striped;
-  size_t partials, xa, lora_at, lora_bt, wf32, rm_codes, rm_scales, total;
+  size_t partials, xa, lora_at, lora_bt, wt, blas, wf32, rm_codes, rm_scales, total;
 };
 
 // Decode-sized batches (<= 4 rows) take a GEMV (the striped one for striped
 // weights); bf16 batches up to 64 rows over a striped weight the skinny MFMA
-// kernel; larger bf16 batches the MFMA GEMM; everything else the generic
-// dequantize + f32 matmul (a striped weight is first put back in row-major
-// order in the workspace).
+// kernel; larger bf16 batches the prefill path: with `expand`, the weight
+// (plus the LoRA update) expanded once to bf16 in the workspace and a BLAS
+// GEMM, else the fused MFMA kernel that dequantizes W tiles in LDS (no
+// weight-sized scratch); everything else the generic dequantize + f32
+// matmul (a striped weight is first put back in row-major order in the
+// workspace).
 LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t lora_rank, const void* packed,
-                         int x_dtype, const void* x, bool striped, int scale_kind) {
+                         int x_dtype, const void* x, bool striped, int scale_kind, bool expand = true) {
   LinearLayout L{};
   Carver c;
   const bool small = rows <= (uint64_t)kGemvMaxRows;
@@ -213,6 +218,11 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
     L.partials = c.take(L.gemv.partial_count[0] * sizeof(float));
   } else if (mfma) {
     L.path = LinearPath::kMfma;
+    L.expand = expand && expand_supported((int)d_in, (int)d_out, (int)lora_rank);
+    if (L.expand) {
+      L.wt = c.take(d_in * d_out * sizeof(uint16_t));
+      L.blas = c.take(kBlasWorkspace);
+    }
   } else {
     L.path = LinearPath::kGeneric;
     L.wf32 = c.take((size_t)d_in * d_out * sizeof(float));
@@ -221,7 +231,9 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
       L.rm_scales = c.take(scale_bytes(ceil_div_u64(d_in * d_out, 64), scale_kind));
     }
   }
-  if (L.path == LinearPath::kMfma && lora_rank) {
+  if (L.path == LinearPath::kMfma && L.expand) {
+    // the adapter is merged into the expanded weight
+  } else if (L.path == LinearPath::kMfma && lora_rank) {
     // bf16 operands of the fused epilogue: xa [rows, pad], A^T [pad, d_in], B^T [d_out, pad]
     const size_t pad = (size_t)lora_pad((int)lora_rank);
     L.xa = c.take((size_t)rows * pad * 2);
@@ -285,13 +297,29 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     UNIFUR_ARG(lora->a != nullptr && lora->b != nullptr, "lora factors are NULL");
     UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
   }
-  const LinearLayout L =
-      plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind);
+  LinearLayout L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind);
+  if (L.path == LinearPath::kMfma && L.expand &&
+      ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
+    // a workspace too small for the expanded weight (or an output the BLAS
+    // kernels cannot take with 16-byte accesses): the fused kernel
+    const LinearLayout lean =
+        plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false);
+    if (!workspace || workspace_bytes >= lean.total) L = lean;
+  }
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool xbf = x_dtype == UNIFUR_NF4_BF16;
   const bool ybf = y_dtype == UNIFUR_NF4_BF16;
   float* xa = nullptr;
+  if (L.path == LinearPath::kMfma && L.expand) {
+    uint16_t* wt = at<uint16_t>(ws, L.wt);
+    UNIFUR_HIP(launch_expand_bf16(w->packed, to_scales(w->scales), (int)w->d_in, (int)w->d_out, is_striped(w),
+                                  lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
+                                  lora ? lora->scaling : 0.0f, wt, stream));
+    UNIFUR_HIP(blas_gemm_xwt(static_cast<const uint16_t*>(x), wt, bias, (int)rows, (int)w->d_out, (int)w->d_in, y,
+                             ybf, at<void>(ws, L.blas), kBlasWorkspace, stream));
+    return UNIFUR_NF4_OK;
+  }
   if (L.path == LinearPath::kMfma) {
     const uint16_t* xb = static_cast<const uint16_t*>(x);
     uint16_t *xa16 = nullptr, *bt16 = nullptr;
@@ -343,13 +371,15 @@ enum class MlpPath { kPairStriped, kStriped, kPairGemv, kGemv, kSkinny, kMfma, k
 
 struct MlpLayout {
   MlpPath path;
+  bool expand;  // kMfma: each weight expanded to bf16 in turn + BLAS GEMMs (else the fused kernel)
   GemvPlan up_plan, down_plan;
   StripedPlan s_up, s_down;
-  size_t partials0, partials1, h, u, hb, wf32, rm_codes, rm_scales, total;
+  size_t partials0, partials1, h, u, hb, wt, blas, wf32, rm_codes, rm_scales, total;
 };
 
 MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_nf4_weight* g,
-                   const unifur_nf4_weight* u, const unifur_nf4_weight* d, int x_dtype, const void* x) {
+                   const unifur_nf4_weight* u, const unifur_nf4_weight* d, int x_dtype, const void* x,
+                   bool expand = true) {
   MlpLayout L{};
   Carver c;
   const bool all_striped = is_striped(g) && is_striped(u) && is_striped(d);
@@ -406,6 +436,11 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
     L.h = c.take((size_t)rows * inter * sizeof(float));
     L.u = c.take((size_t)rows * inter * sizeof(float));
     L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
+    L.expand = expand && expand_supported((int)hidden, (int)inter, 0) && expand_supported((int)inter, (int)hidden, 0);
+    if (L.expand) {
+      L.wt = c.take(hidden * inter * sizeof(uint16_t));  // one weight at a time
+      L.blas = c.take(kBlasWorkspace);
+    }
   } else {
     L.path = MlpPath::kGeneric;
     L.wf32 = c.take((size_t)hidden * inter * sizeof(float));
@@ -433,7 +468,13 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr && y != nullptr, "x or y is NULL");
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
-  const MlpLayout L = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x);
+  MlpLayout L = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x);
+  if (L.path == MlpPath::kMfma && L.expand && ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
+    // a workspace too small for an expanded weight, or an output the BLAS
+    // kernels cannot take with 16-byte accesses: the fused kernel
+    const MlpLayout lean = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x, false);
+    if (workspace_bytes >= lean.total || !workspace) L = lean;
+  }
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool xbf = x_dtype == UNIFUR_NF4_BF16;
@@ -508,11 +549,27 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       return UNIFUR_NF4_OK;
     }
     case MlpPath::kMfma: {
-      // gate and up through the MFMA GEMM (f32 out), silu(g) * u rounded to
-      // bf16, then down through the MFMA GEMM.
+      // gate and up (f32 out), silu(g) * u rounded to bf16, then down: each
+      // weight expanded to bf16 in turn and a BLAS GEMM, or the fused kernel.
       const uint16_t* xb = static_cast<const uint16_t*>(x);
       float* u = at<float>(ws, L.u);
       uint16_t* hb = at<uint16_t>(ws, L.hb);
+      if (L.expand) {
+        uint16_t* wt = at<uint16_t>(ws, L.wt);
+        void* bw = at<void>(ws, L.blas);
+        const int hd = (int)hidden, in = (int)inter, m = (int)rows;
+        UNIFUR_HIP(launch_expand_bf16(gate->packed, to_scales(gate->scales), hd, in, is_striped(gate), nullptr,
+                                      nullptr, 0, 0.0f, wt, stream));
+        UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, in, hd, h, false, bw, kBlasWorkspace, stream));
+        UNIFUR_HIP(launch_expand_bf16(up->packed, to_scales(up->scales), hd, in, is_striped(up), nullptr, nullptr, 0,
+                                      0.0f, wt, stream));
+        UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, in, hd, u, false, bw, kBlasWorkspace, stream));
+        UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
+        UNIFUR_HIP(launch_expand_bf16(down->packed, to_scales(down->scales), in, hd, is_striped(down), nullptr,
+                                      nullptr, 0, 0.0f, wt, stream));
+        UNIFUR_HIP(blas_gemm_xwt(hb, wt, nullptr, m, hd, in, y, ybf, bw, kBlasWorkspace, stream));
+        return UNIFUR_NF4_OK;
+      }
       UNIFUR_HIP(launch_gemm(xb, gate->packed, to_scales(gate->scales), (int)rows, (int)hidden, (int)inter, nullptr,
                              nullptr, nullptr, 0, h, false, is_striped(gate), stream));
       UNIFUR_HIP(launch_gemm(xb, up->packed, to_scales(up->scales), (int)rows, (int)hidden, (int)inter, nullptr,
@@ -550,6 +607,26 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     }
   }
   return UNIFUR_NF4_OK;
+}
+
+uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype, bool expand) {
+  if (rows == 0 || hidden == 0 || intermediate == 0) return 0;
+  const uint8_t* p = reinterpret_cast<const uint8_t*>(uintptr_t{256});
+  uint64_t need = 0;
+  for (int striped = 0; striped < 2; ++striped) {
+    if (striped && (hidden % 64 != 0 || intermediate % 64 != 0)) continue;
+    for (int kind = 0; kind < 4; ++kind) {  // gate and up scale kinds, alike or not
+      unifur_nf4_weight g{p, {kind & 1, (const float*)p, p, (const float*)p}, hidden, intermediate,
+                          striped ? UNIFUR_NF4_LAYOUT_STRIPED : UNIFUR_NF4_LAYOUT_ROW_MAJOR};
+      unifur_nf4_weight u = g;
+      u.scales.kind = kind >> 1;
+      unifur_nf4_weight d = g;
+      d.d_in = intermediate;
+      d.d_out = hidden;
+      need = std::max<uint64_t>(need, plan_mlp(rows, hidden, intermediate, &g, &u, &d, x_dtype, p, expand).total);
+    }
+  }
+  return need;
 }
 
 }  // namespace
@@ -637,6 +714,22 @@ uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t
   return need;
 }
 
+uint64_t unifur_nf4_linear_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
+                                              uint32_t lora_rank) {
+  if (rows == 0 || d_in == 0 || d_out == 0) return 0;
+  const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
+  uint64_t need = 0;
+  for (int striped = 0; striped < 2; ++striped)
+    for (int kind = 0; kind < 2; ++kind)
+      need = std::max<uint64_t>(need, plan_linear(rows, d_in, d_out, lora_rank, aligned, x_dtype, aligned,
+                                                  striped && d_out % 64 == 0, kind, false).total);
+  return need;
+}
+
+uint64_t unifur_nf4_swiglu_min_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype) {
+  return swiglu_workspace(rows, hidden, intermediate, x_dtype, false);
+}
+
 int unifur_nf4_linear_forward(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w,
                               const float* bias, const unifur_nf4_lora* lora, void* y, int y_dtype, void* workspace,
                               uint64_t workspace_bytes, void* stream) {
@@ -653,25 +746,8 @@ int unifur_nf4_qlora_forward(const void* x, int x_dtype, uint64_t rows, const un
 }
 
 uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype) {
-  if (rows == 0 || hidden == 0 || intermediate == 0) return 0;
-  const uint8_t* p = reinterpret_cast<const uint8_t*>(uintptr_t{256});
-  uint64_t need = 0;
-  for (int striped = 0; striped < 2; ++striped) {
-    if (striped && (hidden % 64 != 0 || intermediate % 64 != 0)) continue;
-    for (int kind = 0; kind < 4; ++kind) {  // gate and up scale kinds, alike or not
-      unifur_nf4_weight g{p, {kind & 1, (const float*)p, p, (const float*)p}, hidden, intermediate,
-                          striped ? UNIFUR_NF4_LAYOUT_STRIPED : UNIFUR_NF4_LAYOUT_ROW_MAJOR};
-      unifur_nf4_weight u = g;
-      u.scales.kind = kind >> 1;
-      unifur_nf4_weight d = g;
-      d.d_in = intermediate;
-      d.d_out = hidden;
-      need = std::max<uint64_t>(need, plan_mlp(rows, hidden, intermediate, &g, &u, &d, x_dtype, p).total);
-    }
-  }
-  return need;
+  return swiglu_workspace(rows, hidden, intermediate, x_dtype, true);
 }
-
 int unifur_nf4_quantize_transposed(const void* src, int src_dtype, uint64_t out_features, uint64_t in_features,
                                    uint8_t* packed, float* absmax, void* stream) {
   UNIFUR_ARG(valid_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");

@@ -1,0 +1,196 @@
+// nf4_blas.hip -- the plain bf16 GEMM of the prefill path, through hipBLASLt.
+//
+// Y[M][N] = X[M][K] Wt[N][K]^T (+ bias): in hipBLASLt's column-major terms
+// D (N x M, ld N) = op(A) B with A = Wt seen as a K x N matrix (ld K,
+// transposed) and B = X seen as K x M (ld K) -- the "TN" form, both
+// operands K-contiguous.  f32 accumulation (HIPBLAS_COMPUTE_32F), alpha 1,
+// beta 0, the bias added by the library's epilogue.
+//
+// The library's heuristic ranks candidates without running them and its
+// first choice is often not the fastest on this part, so the first call of a
+// shape on a device times every candidate it returns (one warm-up and three
+// timed launches each, on the caller's stream) and keeps the fastest.
+#include "nf4_expand.hpp"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace unifur {
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr int kCandidates = 8;
+
+struct Key {
+  int dev, M, N, K;
+  bool y_bf16, bias;
+  bool operator<(const Key& o) const {
+    return std::tie(dev, M, N, K, y_bf16, bias) < std::tie(o.dev, o.M, o.N, o.K, o.y_bf16, o.bias);
+  }
+};
+
+struct State {
+  std::mutex mu;
+  hipblasLtHandle_t handle[kMaxDevices] = {};
+  std::map<Key, hipblasLtMatmulAlgo_t> tuned;
+};
+
+State& state() {
+  static State s;
+  return s;
+}
+
+hipError_t to_hip(hipblasStatus_t s) {
+  switch (s) {
+    case HIPBLAS_STATUS_SUCCESS: return hipSuccess;
+    case HIPBLAS_STATUS_NOT_SUPPORTED: return hipErrorNotSupported;
+    case HIPBLAS_STATUS_INVALID_VALUE: return hipErrorInvalidValue;
+    case HIPBLAS_STATUS_ALLOC_FAILED: return hipErrorOutOfMemory;
+    default: return hipErrorUnknown;
+  }
+}
+
+#define BLAS_TRY(expr)                                   \
+  do {                                                   \
+    const hipblasStatus_t st_ = (expr);                  \
+    if (st_ != HIPBLAS_STATUS_SUCCESS) return to_hip(st_); \
+  } while (0)
+#define HIP_TRY(expr)                  \
+  do {                                 \
+    const hipError_t e_ = (expr);      \
+    if (e_ != hipSuccess) return e_;   \
+  } while (0)
+
+// The descriptors of one product (they hold the bias pointer, so each call
+// builds its own).
+struct Desc {
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+  ~Desc() {
+    if (d) hipblasLtMatrixLayoutDestroy(d);
+    if (b) hipblasLtMatrixLayoutDestroy(b);
+    if (a) hipblasLtMatrixLayoutDestroy(a);
+    if (op) hipblasLtMatmulDescDestroy(op);
+  }
+  hipblasStatus_t make(int M, int N, int K, const float* bias, bool y_bf16) {
+    hipblasStatus_t s = hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    if (s != HIPBLAS_STATUS_SUCCESS) return s;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)))) return s;
+    if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)))) return s;
+    if (bias) {
+      const hipblasLtEpilogue_t epi = HIPBLASLT_EPILOGUE_BIAS;
+      const hipDataType bt = HIP_R_32F;
+      if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi)))) return s;
+      if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)))) return s;
+      if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt)))) return s;
+    }
+    if ((s = hipblasLtMatrixLayoutCreate(&a, HIP_R_16BF, K, N, K))) return s;
+    if ((s = hipblasLtMatrixLayoutCreate(&b, HIP_R_16BF, K, M, K))) return s;
+    return hipblasLtMatrixLayoutCreate(&d, y_bf16 ? HIP_R_16BF : HIP_R_32F, N, M, N);
+  }
+};
+
+hipError_t handle_for(int dev, bool capturing, hipblasLtHandle_t* out) {
+  State& st = state();
+  std::lock_guard<std::mutex> lock(st.mu);
+  if (!st.handle[dev]) {
+    // creating a handle allocates device memory: not under stream capture
+    if (capturing) return hipErrorStreamCaptureUnsupported;
+    BLAS_TRY(hipblasLtCreate(&st.handle[dev]));
+  }
+  *out = st.handle[dev];
+  return hipSuccess;
+}
+
+hipError_t time_candidate(hipblasLtHandle_t h, const Desc& dsc, const hipblasLtMatmulAlgo_t& algo, const uint16_t* x,
+                          const uint16_t* wt, void* y, void* ws, size_t ws_bytes, hipStream_t stream, float* ms) {
+  const float alpha = 1.0f, beta = 0.0f;
+  auto run = [&]() {
+    return hipblasLtMatmul(h, dsc.op, &alpha, wt, dsc.a, x, dsc.b, &beta, y, dsc.d, y, dsc.d, &algo, ws, ws_bytes,
+                           stream);
+  };
+  BLAS_TRY(run());
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  HIP_TRY(hipEventCreate(&e0));
+  hipError_t e = hipEventCreate(&e1);
+  if (e == hipSuccess) e = hipEventRecord(e0, stream);
+  for (int i = 0; i < 3 && e == hipSuccess; ++i) e = to_hip(run());
+  if (e == hipSuccess) e = hipEventRecord(e1, stream);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  return e;
+}
+
+}  // namespace
+
+hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
+                         bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0 || !x || !wt || !y) return hipErrorInvalidValue;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(stream, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  hipblasLtHandle_t h = nullptr;
+  HIP_TRY(handle_for(dev, capturing, &h));
+
+  Desc dsc;
+  BLAS_TRY(dsc.make(M, N, K, bias, y_bf16));
+  const Key key{dev, M, N, K, y_bf16, bias != nullptr};
+  hipblasLtMatmulAlgo_t algo{};
+  bool have = false;
+  {
+    State& st = state();
+    std::lock_guard<std::mutex> lock(st.mu);
+    auto it = st.tuned.find(key);
+    if (it != st.tuned.end()) {
+      algo = it->second;
+      have = true;
+    }
+  }
+  if (!have) {
+    hipblasLtMatmulPreference_t pref = nullptr;
+    BLAS_TRY(hipblasLtMatmulPreferenceCreate(&pref));
+    const uint64_t limit = ws_bytes;
+    hipblasStatus_t s =
+        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &limit, sizeof(limit));
+    hipblasLtMatmulHeuristicResult_t res[kCandidates] = {};
+    int n = 0;
+    if (s == HIPBLAS_STATUS_SUCCESS)
+      s = hipblasLtMatmulAlgoGetHeuristic(h, dsc.op, dsc.a, dsc.b, dsc.d, dsc.d, pref, kCandidates, res, &n);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    BLAS_TRY(s);
+    if (n <= 0) return hipErrorNotSupported;
+    int best = 0;
+    if (!capturing) {
+      float best_ms = -1.0f;
+      for (int i = 0; i < n; ++i) {
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > ws_bytes) continue;
+        float ms = 0.0f;
+        if (time_candidate(h, dsc, res[i].algo, x, wt, y, ws, ws_bytes, stream, &ms) != hipSuccess) continue;
+        if (best_ms < 0.0f || ms < best_ms) {
+          best_ms = ms;
+          best = i;
+        }
+      }
+      if (best_ms < 0.0f) return hipErrorNotSupported;
+      State& st = state();
+      std::lock_guard<std::mutex> lock(st.mu);
+      st.tuned[key] = res[best].algo;
+    }
+    algo = res[best].algo;
+  }
+  const float alpha = 1.0f, beta = 0.0f;
+  BLAS_TRY(hipblasLtMatmul(h, dsc.op, &alpha, wt, dsc.a, x, dsc.b, &beta, y, dsc.d, y, dsc.d, &algo, ws, ws_bytes,
+                           stream));
+  return hipSuccess;
+}
+
+}  // namespace unifur
