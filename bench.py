@@ -354,6 +354,48 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
     return out
 
 
+# ------------------------------------------------------ next: embedding ----
+
+def bench_embedding(torch, Q, L) -> dict:
+    """Nf4Embedding::forward on the Qwen2-0.5B vocabulary table (151936 x 896,
+    double quantized): the gather-dequantize of 32 and 2048 token ids against
+    the reference's sequence, a whole-table dequantize per forward
+    (src/qwennet.rs:279-290) timed with the same dequantize kernel."""
+    from unifur_amd import qwennet as QN
+    n_emb, d = 151936, 896
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x4E463457 + 6)
+    emb = QN.Nf4Embedding.from_values(torch.randn(n_emb * d, device=dev, generator=g) * 0.02, n_emb, d)
+    out = {"table": f"{n_emb}x{d}", "resident_bytes": emb.resident_bytes()}
+    for t in (32, 2048):
+        ids = torch.randint(0, n_emb, (t,), device=dev, generator=g)
+        rows = torch.empty(t, d, device=dev)
+        s = emb.packed.scales_struct()
+
+        def gather(i: int) -> None:
+            L.check(L.lib().unifur_nf4_embedding_forward(
+                emb.packed.codes.data_ptr(), ctypes.byref(s), n_emb, d, ids.data_ptr(), L.IDS_I64, t,
+                rows.data_ptr(), L.F32, torch.cuda.current_stream().cuda_stream))
+
+        gather(0)
+        graph = capture(torch, gather, 16)
+        ms = graph_ms(torch, graph, 10) / 16 if graph is not None else event_ms(torch, gather, 16)
+        moved = t * (d // 2 + d // 64 + 4 * d) + 8 * t
+        out[f"gather_T{t}_us"] = round(ms * 1e3, 2)
+        out[f"gather_T{t}_gbs"] = round(moved / ms / 1e6, 1)
+    full = torch.empty(n_emb * d, device=dev)
+    sf = emb.packed.scales_struct()
+
+    def whole(i: int) -> None:
+        L.check(L.lib().unifur_nf4_dequantize(emb.packed.codes.data_ptr(), ctypes.byref(sf), n_emb * d,
+                                              full.data_ptr(), L.F32, torch.cuda.current_stream().cuda_stream))
+
+    whole(0)
+    out["whole_table_dequantize_us"] = round(event_ms(torch, whole, 5) * 1e3, 1)
+    return out
+
+
 # ------------------------------------------------------------- CPU baseline --
 
 def cpu_baseline(sample_s: float) -> dict:
@@ -452,6 +494,7 @@ def main() -> int:
             "max_rel_err": gemm["max_rel_err"]}
         secondary["swiglu_config4"] = bench_swiglu(torch, Q, L, (1, 16, 512))
         secondary["qwen05b_config5"] = bench_qwen(torch, Q, L)
+        secondary["embedding_qwen05b"] = bench_embedding(torch, Q, L)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample_s)
 
     achieved = gemv["bytes"] / gemv["kernel_cold_ms"] / 1e6

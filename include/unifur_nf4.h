@@ -52,6 +52,9 @@ enum {
 /* Element types of activations and outputs. */
 enum { UNIFUR_NF4_F32 = 0, UNIFUR_NF4_BF16 = 1 };
 
+/* Index types of embedding lookups. */
+enum { UNIFUR_NF4_IDS_I32 = 0, UNIFUR_NF4_IDS_I64 = 1 };
+
 /* PackedScales (src/quantize.rs:221-233). */
 enum { UNIFUR_NF4_SCALES_F32 = 0, UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED = 1 };
 
@@ -133,6 +136,18 @@ int unifur_nf4_double_quantize(const float *absmax, uint64_t num_blocks, uint8_t
  * rounded to nearest even). */
 int unifur_nf4_dequantize(const uint8_t *packed, const unifur_nf4_scales *scales, uint64_t len, void *out,
                           int out_dtype, void *stream);
+
+/* Nf4Embedding::forward (src/qwennet.rs:288-290): out[t][:] = row ids[t] of
+ * the dequantized [n_embedding, d_model] table, held as one packed tensor
+ * with its scales (Nf4Embedding::from_values, src/qwennet.rs:265-271); f32
+ * bit-identical to the reference's dequantized table, or bf16.  Only the
+ * gathered rows are dequantized (the reference dequantizes the whole table
+ * per call, src/qwennet.rs:280-286).  ids: n_ids device indices, int32 or
+ * int64 (UNIFUR_NF4_IDS_*); an id outside [0, n_embedding) yields a row of
+ * NaN, where burn's embedding would panic. */
+int unifur_nf4_embedding_forward(const uint8_t *packed, const unifur_nf4_scales *scales, uint64_t n_embedding,
+                                 uint64_t d_model, const void *ids, int ids_dtype, uint64_t n_ids, void *out,
+                                 int out_dtype, void *stream);
 
 /* Loader step of qwen_linear (src/qwennet.rs:1687-1726): a checkpoint weight
  * src [out_features, in_features] row-major (PyTorch order), f32 or bf16

@@ -19,6 +19,9 @@ ERR_WORKSPACE = -3
 F32 = 0
 BF16 = 1
 
+IDS_I32 = 0
+IDS_I64 = 1
+
 SCALES_F32 = 0
 SCALES_DOUBLE_QUANTIZED = 1
 
@@ -78,6 +81,7 @@ SIGNATURES = {
     "unifur_nf4_lora_merge": (_I, [_P, _U64, _U64, ctypes.POINTER(Lora), _P, _P]),
     "unifur_nf4_stripe_weight": (_I, [ctypes.POINTER(Weight), _P, _P, _P]),
     "unifur_nf4_unstripe_weight": (_I, [ctypes.POINTER(Weight), _P, _P, _P]),
+    "unifur_nf4_embedding_forward": (_I, [_P, ctypes.POINTER(Scales), _U64, _U64, _P, _I, _U64, _P, _I, _P]),
     "unifur_nf4_linear_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
     "unifur_nf4_linear_min_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
     "unifur_nf4_linear_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), _P, ctypes.POINTER(Lora), _P, _I,

@@ -14,6 +14,7 @@
 
 #include "../../include/unifur_nf4.h"
 #include "nf4_codec.hpp"
+#include "nf4_embedding.hpp"
 #include "nf4_expand.hpp"
 #include "nf4_gemm.hpp"
 #include "nf4_generic.hpp"
@@ -696,6 +697,27 @@ int unifur_nf4_dequantize(const uint8_t* packed, const unifur_nf4_scales* scales
                        (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
   UNIFUR_HIP(launch_dequantize(packed, to_scales(*scales), len, out, out_dtype == UNIFUR_NF4_BF16, aligned,
                                static_cast<hipStream_t>(stream)));
+  return UNIFUR_NF4_OK;
+}
+
+int unifur_nf4_embedding_forward(const uint8_t* packed, const unifur_nf4_scales* scales, uint64_t n_embedding,
+                                 uint64_t d_model, const void* ids, int ids_dtype, uint64_t n_ids, void* out,
+                                 int out_dtype, void* stream) {
+  UNIFUR_ARG(valid_dtype(out_dtype), "out_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  UNIFUR_ARG(ids_dtype == UNIFUR_NF4_IDS_I32 || ids_dtype == UNIFUR_NF4_IDS_I64,
+             "ids_dtype must be UNIFUR_NF4_IDS_I32 or UNIFUR_NF4_IDS_I64");
+  if (n_ids == 0 || d_model == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(ids && out, "ids or out is NULL");
+  UNIFUR_ARG(n_embedding == 0 || d_model <= ~0ull / n_embedding, "table size overflows");
+  if (n_embedding > 0) {
+    if (int r = check_scales(scales)) return r;
+    UNIFUR_ARG(packed != nullptr, "packed is NULL");
+  }
+  UNIFUR_ARG(aligned_to(ids, ids_dtype == UNIFUR_NF4_IDS_I64 ? 8 : 4), "ids misaligned for its type");
+  UNIFUR_ARG(aligned_to(out, out_dtype == UNIFUR_NF4_BF16 ? 2 : 4), "out misaligned for its dtype");
+  const ScalesArg sc = n_embedding > 0 ? to_scales(*scales) : ScalesArg{};
+  UNIFUR_HIP(launch_embedding(packed, sc, n_embedding, d_model, ids, ids_dtype == UNIFUR_NF4_IDS_I64, n_ids, out,
+                              out_dtype == UNIFUR_NF4_BF16, static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
 }
 

@@ -5,6 +5,7 @@ this module                            reference (s-b-repo/unifur)
 =====================================  ==========================================
 ``QwenLoraConfig``                     ``QwenLoraConfig`` (src/qwennet.rs:703-747)
 ``QwenLinear``                         ``QwenLinear`` (src/qwennet.rs:293-435)
+``Nf4Embedding``                       ``Nf4Embedding`` (src/qwennet.rs:244-291)
 ``WeightStore``                        ``WeightStore`` (src/qwennet.rs:1598-1607)
 ``Nf4ResidencyReport``                 ``Nf4ResidencyReport`` (src/qwennet.rs:1609-1681)
 ``qwen_linear``                        ``qwen_linear`` (src/qwennet.rs:1683-1726)
@@ -100,6 +101,55 @@ class QwenLinear:
         if self.kind == self.F32:
             raise ValueError("LoRA adapters attach to NF4-resident weights only")
         raise ValueError("weight already carries a LoRA adapter")
+
+
+class Nf4Embedding:
+    """NF4-resident embedding table (src/qwennet.rs:244-291): the
+    ``[n_embedding, d_model]`` table as one packed tensor with double
+    quantization.  ``forward`` gathers and dequantizes only the selected rows
+    (the reference dequantizes the whole table per call, then gathers);
+    the rows are the reference's f32 values bit for bit."""
+
+    def __init__(self, packed: Q.PackedNf4Tensor, n_embedding: int, d_model: int):
+        if len(packed) != n_embedding * d_model:
+            raise ValueError(f"packed table holds {len(packed)} values, not {n_embedding} x {d_model}")
+        self.packed = packed
+        self.n_embedding = int(n_embedding)
+        self.d_model = int(d_model)
+
+    @staticmethod
+    def from_values(values: torch.Tensor, n_embedding: int, d_model: int) -> "Nf4Embedding":
+        """src/qwennet.rs:265-271: quantize the row-major table, then double quantization."""
+        v = values.reshape(-1)
+        if v.numel() != n_embedding * d_model:
+            raise ValueError(f"{v.numel()} values for a {n_embedding} x {d_model} table")
+        return Nf4Embedding(Q.PackedNf4Tensor.quantize(v.contiguous()).with_double_quantization(), n_embedding,
+                            d_model)
+
+    def resident_bytes(self) -> int:
+        """src/qwennet.rs:274-276."""
+        return self.packed.resident_bytes()
+
+    def dequantized_weight(self) -> torch.Tensor:
+        """src/qwennet.rs:279-286: the whole ``[n_embedding, d_model]`` f32 table."""
+        return self.packed.dequantize().view(self.n_embedding, self.d_model)
+
+    def forward(self, ids: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """src/qwennet.rs:288-290: ``ids`` int64 or int32 of any shape ->
+        ``[*ids.shape, d_model]``.  An id outside ``[0, n_embedding)`` yields
+        a row of NaN (burn would panic)."""
+        if ids.dtype not in (torch.int64, torch.int32):
+            raise ValueError("ids must be int64 or int32")
+        if not ids.is_cuda:
+            raise ValueError("ids must be a device tensor")
+        flat = ids.reshape(-1).contiguous()
+        out = torch.empty(flat.numel(), self.d_model, dtype=dtype, device=flat.device)
+        s = self.packed.scales_struct()
+        L.check(L.lib().unifur_nf4_embedding_forward(
+            self.packed.codes.data_ptr(), ctypes.byref(s), self.n_embedding, self.d_model, flat.data_ptr(),
+            L.IDS_I64 if flat.dtype == torch.int64 else L.IDS_I32, flat.numel(), out.data_ptr(),
+            L.BF16 if dtype == torch.bfloat16 else L.F32, torch.cuda.current_stream().cuda_stream))
+        return out.view(*ids.shape, self.d_model)
 
 
 class WeightStore(Enum):
