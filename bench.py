@@ -354,6 +354,45 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
     return out
 
 
+# ------------------------------------------------------- next: backward ----
+
+def bench_backward(torch, Q, L) -> dict:
+    """Adapter-only training step of one config-3 layer in reverse: dy bf16
+    [2048, 4096] through the 4096 x 4096 DQ weight with the r = 16 adapter:
+    dx (bf16) and both adapter gradients (f32)."""
+    M, K, N, r = 2048, 4096, 4096, 16
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x4E463457 + 7)
+    lin = rand_weights(torch, Q, K, N, g)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    dy = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+    a = torch.randn(K, r, device=dev, generator=g) * 0.01
+    b = torch.randn(r, N, device=dev, generator=g) * 0.01
+    ql = Q.QloraLinear(lin, Q.LoraAdapter.from_parts(a, b, 2.0))
+    lib = L.lib()
+    ws_bytes = lib.unifur_nf4_linear_backward_workspace_size(M, K, N, L.BF16, r)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    dx = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
+    ga = torch.empty(K, r, device=dev)
+    gb = torch.empty(r, N, device=dev)
+    w, lo = lin.weight_struct(), ql.adapter.struct()
+
+    def step(i: int) -> None:
+        L.check(lib.unifur_nf4_linear_backward(dy.data_ptr(), L.BF16, M, ctypes.byref(w), ctypes.byref(lo),
+                                               x.data_ptr(), L.BF16, dx.data_ptr(), L.BF16, ga.data_ptr(),
+                                               gb.data_ptr(), ws.data_ptr(), ws_bytes,
+                                               torch.cuda.current_stream().cuda_stream))
+
+    for i in range(3):
+        step(i)
+    graph = capture(torch, step, 4)
+    ms = graph_ms(torch, graph, 10) / 4 if graph is not None else event_ms(torch, step, 8)
+    flops = 2 * M * N * K + 2 * K * r * N + 4 * M * r * (K + N)
+    return {"ms": round(ms, 5), "tflops": round(flops / ms / 1e9, 1),
+            "frac": round(flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+
+
 # ------------------------------------------------------ next: embedding ----
 
 def bench_embedding(torch, Q, L) -> dict:
@@ -495,6 +534,7 @@ def main() -> int:
         secondary["swiglu_config4"] = bench_swiglu(torch, Q, L, (1, 16, 512))
         secondary["qwen05b_config5"] = bench_qwen(torch, Q, L)
         secondary["embedding_qwen05b"] = bench_embedding(torch, Q, L)
+        secondary["qlora_backward_config3"] = bench_backward(torch, Q, L)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample_s)
 
     achieved = gemv["bytes"] / gemv["kernel_cold_ms"] / 1e6

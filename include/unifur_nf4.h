@@ -207,6 +207,26 @@ int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const un
                              const unifur_nf4_lora *lora, void *y, int y_dtype, void *workspace,
                              uint64_t workspace_bytes, void *stream);
 
+/* Backward of Nf4Linear::forward / QloraLinear::forward for adapter-only
+ * training (src/qwentrain.rs:421-470 runs burn's autodiff through the
+ * detached dequantized weight; the packed base weight is #[module(skip)],
+ * src/qwennet.rs:168-178, so it has no gradient).  Given dy [rows, d_out]
+ * (f32 or bf16) and, with lora, x [rows, d_in] (f32 or bf16):
+ *   dx     [rows, d_in]   = dy W^T + ((dy scaling) B^T) A^T   (dx may be NULL)
+ *   grad_b [rank, d_out]  = (x A)^T (dy scaling)             (f32, may be NULL)
+ *   grad_a [d_in, rank]   = x^T ((dy scaling) B^T)           (f32, may be NULL)
+ * the vector-Jacobian products of LoraAdapter::forward ((x A) B scaling,
+ * src/quantize.rs:619-624) and of the base product.  bf16 dy goes through
+ * the weight expanded to bf16 (with the adapter merged) and a BLAS GEMM;
+ * f32 dy through the f32 dequantized weight.  The adapter gradients are
+ * summed over the rows in a fixed order (deterministic). */
+uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
+                                                   uint32_t lora_rank);
+int unifur_nf4_linear_backward(const void *dy, int dy_dtype, uint64_t rows, const unifur_nf4_weight *w,
+                               const unifur_nf4_lora *lora, const void *x, int x_dtype, void *dx, int dx_dtype,
+                               float *grad_a, float *grad_b, void *workspace, uint64_t workspace_bytes,
+                               void *stream);
+
 /* Linear with an f32-resident weight w [d_in, d_out] row-major: the F32 arm of
  * QwenLinear (src/qwennet.rs:293-355) and the dequantized base of the
  * simulated QLoraLinear (src/quantize.rs:637-700); y = x w (+ bias)

@@ -77,3 +77,22 @@ def test_workspace_sizes_are_consistent(lib):
     # every non-empty plan starts with the 64 KiB counter region
     assert lib.unifur_nf4_linear_workspace_size(1, 64, 64, 0, 0) >= 65536
     assert lib.unifur_nf4_swiglu_workspace_size(1, 4096, 11008, 1) >= 11008 * 4
+
+
+def test_backward_and_prefill_workspace_sizes(lib):
+    # host-only planning, including empty batches (no division by a zero
+    # tile count)
+    for rows in (0, 1, 5, 64, 65, 2048):
+        bw = lib.unifur_nf4_linear_backward_workspace_size(rows, 4096, 4096, 1, 16)
+        assert bw >= 65536
+        if rows:  # bf16 dy: the expanded bf16 weight is part of it
+            assert bw >= 4096 * 4096 * 2
+        assert lib.unifur_nf4_linear_backward_workspace_size(rows, 100, 70, 0, 3) >= 65536
+    # f32 dy: the f32 dequantized weight
+    assert lib.unifur_nf4_linear_backward_workspace_size(8, 256, 128, 0, 0) >= 256 * 128 * 4
+    # prefill: the default holds the bf16 expansion, the minimum does not
+    full = lib.unifur_nf4_linear_workspace_size(2048, 4096, 4096, 1, 16)
+    lean = lib.unifur_nf4_linear_min_workspace_size(2048, 4096, 4096, 1, 16)
+    assert lean < 4096 * 4096 * 2 <= full
+    assert lib.unifur_nf4_swiglu_min_workspace_size(512, 4096, 11008, 1) < \
+        lib.unifur_nf4_swiglu_workspace_size(512, 4096, 11008, 1)

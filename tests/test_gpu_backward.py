@@ -1,0 +1,136 @@
+"""GPU parity of the NF4 linear backward for adapter-only training: the
+vector-Jacobian products of Nf4Linear::forward / QloraLinear::forward
+(src/qwennet.rs:238-241, :325-345; LoraAdapter::forward (x A) B s,
+src/quantize.rs:619-624) that burn's autodiff takes under
+src/qwentrain.rs:421-470, the base weight frozen:
+
+    dx     = dy W^T + ((dy s) B^T) A^T
+    grad_b = (x A)^T (dy s)
+    grad_a = x^T ((dy s) B^T)
+
+Each is checked against the float64 evaluation of those formulas with the
+oracle's dequantized weight (bit-identical to the reference's), normwise
+(max |got - ref| over the sum of absolute products): f32 dy through the f32
+dequantized weight within 1e-5; bf16 dy through the bf16-expanded weight
+within 1e-2 (the forward GEMM's bar); the adapter gradients, summed in f32,
+within 1e-5 whatever the input types.  A transposed factor, a dropped
+scaling or a wrong reduction axis fails these by orders of magnitude.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from unifur_amd import _lib as L
+from unifur_amd import quantize as Q
+
+from test_gpu_gemm import lora_parts
+from test_gpu_linear import acts, make_linear
+
+pytestmark = pytest.mark.gpu
+
+
+def normwise(got, ref, bound):
+    got = np.asarray(got, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(float(np.max(bound)), 1e-30))
+
+
+def refs(x, dy, wdeq, a, b, s):
+    x = np.asarray(x, np.float64)
+    dy = np.asarray(dy, np.float64)
+    w = np.asarray(wdeq, np.float64)
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    g = dy * s
+    dx = dy @ w.T + (g @ b.T) @ a.T
+    dx_bound = np.abs(dy) @ np.abs(w).T + (np.abs(g) @ np.abs(b).T) @ np.abs(a).T
+    gb = (x @ a).T @ g
+    gb_bound = (np.abs(x) @ np.abs(a)).T @ np.abs(g)
+    ga = x.T @ (g @ b.T)
+    ga_bound = np.abs(x).T @ (np.abs(g) @ np.abs(b).T)
+    return dx, dx_bound, ga, ga_bound, gb, gb_bound
+
+
+@pytest.mark.parametrize("case", [
+    # (M, K, N, r, dy dtype, x dtype, striped, dq)
+    (37, 256, 384, 8, torch.float32, torch.float32, True, True),
+    (37, 256, 384, 8, torch.float32, torch.bfloat16, False, False),
+    (300, 512, 256, 16, torch.bfloat16, torch.bfloat16, True, True),
+    (300, 512, 256, 16, torch.bfloat16, torch.float32, False, True),
+    (5, 1024, 128, 64, torch.bfloat16, torch.bfloat16, True, False),
+    (129, 896, 4864, 16, torch.bfloat16, torch.bfloat16, True, True),
+    (64, 100, 70, 3, torch.float32, torch.float32, False, True),  # ragged: generic path, d_out % 64 != 0
+])
+def test_qlora_backward(device, oracle, case):
+    M, K, N, r, dyt, xt_dtype, striped, dq = case
+    lin, wdeq = make_linear(oracle, K, N, 1400 + M + K, device, dq=dq, striped=striped and N % 64 == 0)
+    s = 16.0 / r
+    a, b, ad = lora_parts(oracle, K, N, r, 1401 + r, device, scaling=s)
+    x, xt = acts(oracle, M, K, 1402, xt_dtype, device)
+    dy, dyt_ = acts(oracle, M, N, 1403, dyt, device)
+    ql = Q.QloraLinear(lin, ad)
+    dx, ga, gb = ql.backward(xt, dyt_, dx_dtype=torch.float32)
+    rdx, bdx, rga, bga, rgb, bgb = refs(x, dy, wdeq, a, b, s)
+    tol_dx = 1e-2 if dyt == torch.bfloat16 else 1e-5
+    e_dx, e_ga, e_gb = normwise(dx.cpu(), rdx, bdx), normwise(ga.cpu(), rga, bga), normwise(gb.cpu(), rgb, bgb)
+    print(f"backward {case}: dx {e_dx:.2e} grad_a {e_ga:.2e} grad_b {e_gb:.2e}", flush=True)
+    assert e_dx <= tol_dx and e_ga <= 1e-5 and e_gb <= 1e-5
+    assert ga.shape == (K, r) and gb.shape == (r, N) and dx.shape == (M, K)
+    # deterministic: fixed reduction order
+    dx2, ga2, gb2 = ql.backward(xt, dyt_, dx_dtype=torch.float32)
+    assert torch.equal(dx, dx2) and torch.equal(ga, ga2) and torch.equal(gb, gb2)
+
+
+@pytest.mark.parametrize("dyt", [torch.float32, torch.bfloat16])
+def test_base_backward_without_adapter(device, oracle, dyt):
+    M, K, N = 200, 512, 384
+    lin, wdeq = make_linear(oracle, K, N, 1500, device)
+    dy, dyt_ = acts(oracle, M, N, 1501, dyt, device)
+    dx = lin.backward(dyt_, dx_dtype=torch.float32)
+    ref = np.asarray(dy, np.float64) @ np.asarray(wdeq, np.float64).T
+    bound = np.abs(np.asarray(dy, np.float64)) @ np.abs(np.asarray(wdeq, np.float64)).T
+    assert normwise(dx.cpu(), ref, bound) <= (1e-2 if dyt == torch.bfloat16 else 1e-5)
+    # bf16 out is that result rounded
+    dxb = lin.backward(dyt_, dx_dtype=torch.bfloat16)
+    assert normwise(dxb.float().cpu(), ref, bound) <= 1e-2
+
+
+def test_config3_backward(device, oracle):
+    # the config-3 shapes in reverse: dy bf16 [2048, 4096] through the
+    # 4096 x 4096 DQ weight with the r = 16 adapter (scale 2)
+    M, K, N, r = 2048, 4096, 4096, 16
+    lin, wdeq = make_linear(oracle, K, N, 0x4E463457 + 3, device, dq=True, striped=True)
+    a, b, ad = lora_parts(oracle, K, N, r, 0x41 + 3, device)
+    x, xt = acts(oracle, M, K, 0x58 + 3, torch.bfloat16, device)
+    dy, dyt_ = acts(oracle, M, N, 0x59 + 3, torch.bfloat16, device)
+    dx, ga, gb = Q.QloraLinear(lin, ad).backward(xt, dyt_, dx_dtype=torch.bfloat16)
+    rdx, bdx, rga, bga, rgb, bgb = refs(x, dy, wdeq, a, b, 2.0)
+    assert normwise(dx.float().cpu(), rdx, bdx) <= 1e-2
+    assert normwise(ga.cpu(), rga, bga) <= 1e-5 and normwise(gb.cpu(), rgb, bgb) <= 1e-5
+
+
+def test_gradients_only_and_empty_batch(device, oracle):
+    M, K, N, r = 50, 256, 128, 4
+    lin, wdeq = make_linear(oracle, K, N, 1600, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 1601, device)
+    x, xt = acts(oracle, M, K, 1602, torch.float32, device)
+    dy, dyt_ = acts(oracle, M, N, 1603, torch.float32, device)
+    dx, ga, gb = Q.QloraLinear(lin, ad).backward(xt, dyt_, want_dx=False)
+    assert dx is None
+    _, _, rga, bga, rgb, bgb = refs(x, dy, wdeq, a, b, 2.0)
+    assert normwise(ga.cpu(), rga, bga) <= 1e-5 and normwise(gb.cpu(), rgb, bgb) <= 1e-5
+    # no rows: zero gradients, nothing else touched
+    dx0, ga0, gb0 = Q.QloraLinear(lin, ad).backward(xt[:0], dyt_[:0])
+    assert dx0.shape == (0, K) and not ga0.any() and not gb0.any()
+    # gradients without the adapter or without x are refused
+    w = lin.weight_struct()
+    g = torch.empty(K, r, device=device)
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.lib().unifur_nf4_linear_backward(dyt_.data_ptr(), L.F32, M, ctypes.byref(w), None, xt.data_ptr(), L.F32,
+                                              None, L.F32, g.data_ptr(), None, None, 0, st) == L.ERR_INVALID
+    lo = ad.struct()
+    assert L.lib().unifur_nf4_linear_backward(dyt_.data_ptr(), L.F32, M, ctypes.byref(w), ctypes.byref(lo), None,
+                                              L.F32, None, L.F32, g.data_ptr(), None, None, 0, st) == L.ERR_INVALID

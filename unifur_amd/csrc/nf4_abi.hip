@@ -630,6 +630,115 @@ uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate,
   return need;
 }
 
+
+// ------------------------------------------------------------ backward -----
+
+// dX through the expanded bf16 weight and the BLAS GEMM (bf16 dY), or the
+// generic dequantize (+ merge) and f32 GEMM; the adapter gradients through
+// x A, dY B^T and two row reductions.
+struct BackwardLayout {
+  bool blas;
+  size_t wt, blas_ws, wf32, rm_codes, rm_scales, xa, u, partials, total;
+};
+
+BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t rank, int dy_dtype, bool want_dx,
+                             bool want_grads, bool striped, int scale_kind, bool aligned) {
+  BackwardLayout L{};
+  Carver c;
+  if (want_dx) {
+    L.blas = dy_dtype == UNIFUR_NF4_BF16 && aligned && rows <= 0x7fffffffu && d_in <= 0x7fffffffu &&
+             d_out <= 0x7fffffffu && expand_supported((int)d_in, (int)d_out, (int)rank);
+    if (L.blas) {
+      L.wt = c.take(d_in * d_out * sizeof(uint16_t));
+      L.blas_ws = c.take(kBlasWorkspace);
+    } else {
+      L.wf32 = c.take(d_in * d_out * sizeof(float));
+      if (striped) {
+        L.rm_codes = c.take(ceil_div_u64(d_in * d_out, 2));
+        L.rm_scales = c.take(scale_bytes(ceil_div_u64(d_in * d_out, 64), scale_kind));
+      }
+    }
+  }
+  if (want_grads && rank) {
+    L.xa = c.take((size_t)rows * rank * sizeof(float));
+    L.u = c.take((size_t)rows * rank * sizeof(float));
+    const int m = (int)std::min<uint64_t>(rows, 0x7fffffffu);
+    const int k = (int)std::min<uint64_t>(d_in, 0x7fffffffu), n = (int)std::min<uint64_t>(d_out, 0x7fffffffu);
+    const size_t p_mm = (size_t)std::max(narrow_mm_slabs(m, k), narrow_mm_slabs(m, n)) * rows * rank;
+    const size_t p_atb = std::max((size_t)narrow_atb_slabs(m, n) * d_out, (size_t)narrow_atb_slabs(m, k) * d_in) * rank;
+    L.partials = c.take(std::max(p_mm, p_atb) * sizeof(float));
+  }
+  L.total = c.off;
+  return L;
+}
+
+int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_weight* w, const unifur_nf4_lora* lora,
+                 const void* x, int x_dtype, void* dx, int dx_dtype, float* grad_a, float* grad_b, void* workspace,
+                 uint64_t workspace_bytes, hipStream_t stream) {
+  UNIFUR_ARG(valid_dtype(dy_dtype) && valid_dtype(dx_dtype) && valid_dtype(x_dtype),
+             "dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  if (int r = check_weight(w, "linear_backward")) return r;
+  const uint32_t rank = lora ? lora->rank : 0;
+  if (lora) {
+    UNIFUR_ARG(lora->a != nullptr && lora->b != nullptr, "lora factors are NULL");
+    UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
+  }
+  const bool want_dx = dx != nullptr;
+  const bool want_grads = lora && (grad_a || grad_b);
+  UNIFUR_ARG(!(grad_a || grad_b) || lora, "adapter gradients need the adapter");
+  UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  UNIFUR_ARG(rows == 0 || dy != nullptr, "dy is NULL");
+  UNIFUR_ARG(!want_grads || rows == 0 || x != nullptr, "adapter gradients need x");
+  const uint64_t K = w->d_in, N = w->d_out;
+  UNIFUR_ARG(K <= 0x7fffffffu && N <= 0x7fffffffu, "weight too large");
+  const bool aligned = aligned_to(dy, 16) && aligned_to(dx, 16);
+  const BackwardLayout L = plan_backward(rows, K, N, rank, dy_dtype, want_dx && rows > 0, want_grads, is_striped(w),
+                                         w->scales.kind, aligned);
+  void* ws = nullptr;
+  if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
+  const bool dybf = dy_dtype == UNIFUR_NF4_BF16, xbf = x_dtype == UNIFUR_NF4_BF16;
+  const int m = (int)rows, k = (int)K, n = (int)N;
+  if (want_dx && rows > 0) {
+    // dX = dY (W + scaling A B)^T = dY W^T + ((dY scaling) B^T) A^T
+    if (L.blas) {
+      uint16_t* wt = at<uint16_t>(ws, L.wt);
+      UNIFUR_HIP(launch_expand_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w), lora ? lora->a : nullptr,
+                                    lora ? lora->b : nullptr, (int)rank, lora ? lora->scaling : 0.0f, wt, stream));
+      UNIFUR_HIP(blas_gemm_dyw(static_cast<const uint16_t*>(dy), wt, m, n, k, dx, dx_dtype == UNIFUR_NF4_BF16,
+                               at<void>(ws, L.blas_ws), kBlasWorkspace, stream));
+    } else {
+      const uint8_t* packed = nullptr;
+      ScalesArg scales{};
+      if (int r = row_major_view(w, ws, L.rm_codes, L.rm_scales, stream, &packed, &scales)) return r;
+      float* wf = at<float>(ws, L.wf32);
+      UNIFUR_HIP(launch_dequantize(packed, scales, (size_t)K * N, wf, false, u32_aligned(packed), stream));
+      if (lora) UNIFUR_HIP(launch_lora_merge(wf, lora->a, lora->b, (int)rank, lora->scaling, K, N, wf, stream));
+      Epilogue e{};
+      e.y = dx;
+      e.y_bf16 = dx_dtype == UNIFUR_NF4_BF16;
+      // W' [K][N] row-major is the transposed [N_out = K][K_in = N] operand
+      UNIFUR_HIP(launch_gemm_f32_wt(dy, dybf, wf, m, n, k, e, stream));
+    }
+  }
+  if (want_grads) {
+    float* xa = at<float>(ws, L.xa);
+    float* u = at<float>(ws, L.u);
+    float* part = at<float>(ws, L.partials);
+    const int r = (int)rank;
+    if (grad_b) {
+      // grad_B [r][N] = (x A)^T (dY scaling)
+      UNIFUR_HIP(launch_narrow_mm(x, xbf, lora->a, false, m, k, r, part, xa, stream));
+      UNIFUR_HIP(launch_narrow_atb(dy, dybf, xa, m, n, r, true, lora->scaling, part, grad_b, stream));
+    }
+    if (grad_a) {
+      // grad_A [K][r] = x^T ((dY scaling) B^T)
+      UNIFUR_HIP(launch_narrow_mm(dy, dybf, lora->b, true, m, n, r, part, u, stream));
+      UNIFUR_HIP(launch_narrow_atb(x, xbf, u, m, k, r, false, lora->scaling, part, grad_a, stream));
+    }
+  }
+  return UNIFUR_NF4_OK;
+}
+
 }  // namespace
 }  // namespace unifur
 
@@ -698,6 +807,26 @@ int unifur_nf4_dequantize(const uint8_t* packed, const unifur_nf4_scales* scales
   UNIFUR_HIP(launch_dequantize(packed, to_scales(*scales), len, out, out_dtype == UNIFUR_NF4_BF16, aligned,
                                static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
+}
+
+uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
+                                                   uint32_t lora_rank) {
+  if (d_in == 0 || d_out == 0) return 0;
+  uint64_t need = 0;
+  for (int striped = 0; striped < 2; ++striped)
+    for (int kind = 0; kind < 2; ++kind)
+      need = std::max<uint64_t>(need, plan_backward(rows, d_in, d_out, lora_rank, dy_dtype, rows > 0, lora_rank > 0,
+                                                    striped && d_out % 64 == 0, kind, true)
+                                          .total);
+  return need;
+}
+
+int unifur_nf4_linear_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_weight* w,
+                               const unifur_nf4_lora* lora, const void* x, int x_dtype, void* dx, int dx_dtype,
+                               float* grad_a, float* grad_b, void* workspace, uint64_t workspace_bytes,
+                               void* stream) {
+  return run_backward(dy, dy_dtype, rows, w, lora, x, x_dtype, dx, dx_dtype, grad_a, grad_b, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int unifur_nf4_embedding_forward(const uint8_t* packed, const unifur_nf4_scales* scales, uint64_t n_embedding,

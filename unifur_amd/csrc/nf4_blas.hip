@@ -1,10 +1,14 @@
-// nf4_blas.hip -- the plain bf16 GEMM of the prefill path, through hipBLASLt.
+// nf4_blas.hip -- the plain bf16 GEMMs of the prefill and backward paths,
+// through hipBLASLt.
 //
-// Y[M][N] = X[M][K] Wt[N][K]^T (+ bias): in hipBLASLt's column-major terms
-// D (N x M, ld N) = op(A) B with A = Wt seen as a K x N matrix (ld K,
-// transposed) and B = X seen as K x M (ld K) -- the "TN" form, both
-// operands K-contiguous.  f32 accumulation (HIPBLAS_COMPUTE_32F), alpha 1,
-// beta 0, the bias added by the library's epilogue.
+// Row-major products in hipBLASLt's column-major terms (a row-major [R][C]
+// array is the column-major C x R matrix with leading dimension C):
+//   forward   Y[M][N] = X[M][K] Wt[N][K]^T (+ bias): D (N x M, ld N) =
+//             op_T(Wt as K x N, ld K) * (X as K x M, ld K) -- the "TN" form;
+//   backward  dX[M][K] = dY[M][N] Wt[N][K]: D (K x M, ld K) =
+//             (Wt as K x N, ld K) * (dY as N x M, ld N) -- the "NN" form.
+// bf16 operands, f32 accumulation (HIPBLAS_COMPUTE_32F), alpha 1, beta 0,
+// the bias added by the library's epilogue.
 //
 // The library's heuristic ranks candidates without running them and its
 // first choice is often not the fastest on this part, so the first call of a
@@ -24,11 +28,19 @@ namespace {
 constexpr int kMaxDevices = 64;
 constexpr int kCandidates = 8;
 
+// One product in column-major terms: D (m x n) = op(A) op(B), op(A) m x k.
+struct Shape {
+  bool ta, tb;
+  int m, n, k, lda, ldb, ldd;
+};
+
 struct Key {
-  int dev, M, N, K;
+  int dev;
+  Shape s;
   bool y_bf16, bias;
   bool operator<(const Key& o) const {
-    return std::tie(dev, M, N, K, y_bf16, bias) < std::tie(o.dev, o.M, o.N, o.K, o.y_bf16, o.bias);
+    return std::tie(dev, s.ta, s.tb, s.m, s.n, s.k, s.lda, s.ldb, s.ldd, y_bf16, bias) <
+           std::tie(o.dev, o.s.ta, o.s.tb, o.s.m, o.s.n, o.s.k, o.s.lda, o.s.ldb, o.s.ldd, o.y_bf16, o.bias);
   }
 };
 
@@ -75,10 +87,10 @@ struct Desc {
     if (a) hipblasLtMatrixLayoutDestroy(a);
     if (op) hipblasLtMatmulDescDestroy(op);
   }
-  hipblasStatus_t make(int M, int N, int K, const float* bias, bool y_bf16) {
+  hipblasStatus_t make(const Shape& sh, const float* bias, bool y_bf16) {
     hipblasStatus_t s = hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     if (s != HIPBLAS_STATUS_SUCCESS) return s;
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    const hipblasOperation_t ta = sh.ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, tb = sh.tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
     if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)))) return s;
     if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)))) return s;
     if (bias) {
@@ -88,9 +100,10 @@ struct Desc {
       if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)))) return s;
       if ((s = hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt)))) return s;
     }
-    if ((s = hipblasLtMatrixLayoutCreate(&a, HIP_R_16BF, K, N, K))) return s;
-    if ((s = hipblasLtMatrixLayoutCreate(&b, HIP_R_16BF, K, M, K))) return s;
-    return hipblasLtMatrixLayoutCreate(&d, y_bf16 ? HIP_R_16BF : HIP_R_32F, N, M, N);
+    // stored shapes: A is m x k (k x m when transposed), B k x n (n x k)
+    if ((s = hipblasLtMatrixLayoutCreate(&a, HIP_R_16BF, sh.ta ? sh.k : sh.m, sh.ta ? sh.m : sh.k, sh.lda))) return s;
+    if ((s = hipblasLtMatrixLayoutCreate(&b, HIP_R_16BF, sh.tb ? sh.n : sh.k, sh.tb ? sh.k : sh.n, sh.ldb))) return s;
+    return hipblasLtMatrixLayoutCreate(&d, y_bf16 ? HIP_R_16BF : HIP_R_32F, sh.m, sh.n, sh.ldd);
   }
 };
 
@@ -106,11 +119,11 @@ hipError_t handle_for(int dev, bool capturing, hipblasLtHandle_t* out) {
   return hipSuccess;
 }
 
-hipError_t time_candidate(hipblasLtHandle_t h, const Desc& dsc, const hipblasLtMatmulAlgo_t& algo, const uint16_t* x,
-                          const uint16_t* wt, void* y, void* ws, size_t ws_bytes, hipStream_t stream, float* ms) {
+hipError_t time_candidate(hipblasLtHandle_t h, const Desc& dsc, const hipblasLtMatmulAlgo_t& algo, const void* A,
+                          const void* B, void* y, void* ws, size_t ws_bytes, hipStream_t stream, float* ms) {
   const float alpha = 1.0f, beta = 0.0f;
   auto run = [&]() {
-    return hipblasLtMatmul(h, dsc.op, &alpha, wt, dsc.a, x, dsc.b, &beta, y, dsc.d, y, dsc.d, &algo, ws, ws_bytes,
+    return hipblasLtMatmul(h, dsc.op, &alpha, A, dsc.a, B, dsc.b, &beta, y, dsc.d, y, dsc.d, &algo, ws, ws_bytes,
                            stream);
   };
   BLAS_TRY(run());
@@ -129,9 +142,11 @@ hipError_t time_candidate(hipblasLtHandle_t h, const Desc& dsc, const hipblasLtM
 
 }  // namespace
 
-hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
-                         bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream) {
-  if (M <= 0 || N <= 0 || K <= 0 || !x || !wt || !y) return hipErrorInvalidValue;
+namespace {
+
+hipError_t gemm_cm(const Shape& sh, const void* A, const void* B, const float* bias, void* y, bool y_bf16, void* ws,
+                   size_t ws_bytes, hipStream_t stream) {
+  if (sh.m <= 0 || sh.n <= 0 || sh.k <= 0 || !A || !B || !y) return hipErrorInvalidValue;
   int dev = 0;
   HIP_TRY(hipGetDevice(&dev));
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
@@ -142,8 +157,8 @@ hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bia
   HIP_TRY(handle_for(dev, capturing, &h));
 
   Desc dsc;
-  BLAS_TRY(dsc.make(M, N, K, bias, y_bf16));
-  const Key key{dev, M, N, K, y_bf16, bias != nullptr};
+  BLAS_TRY(dsc.make(sh, bias, y_bf16));
+  const Key key{dev, sh, y_bf16, bias != nullptr};
   hipblasLtMatmulAlgo_t algo{};
   bool have = false;
   {
@@ -174,7 +189,7 @@ hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bia
       for (int i = 0; i < n; ++i) {
         if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > ws_bytes) continue;
         float ms = 0.0f;
-        if (time_candidate(h, dsc, res[i].algo, x, wt, y, ws, ws_bytes, stream, &ms) != hipSuccess) continue;
+        if (time_candidate(h, dsc, res[i].algo, A, B, y, ws, ws_bytes, stream, &ms) != hipSuccess) continue;
         if (best_ms < 0.0f || ms < best_ms) {
           best_ms = ms;
           best = i;
@@ -188,9 +203,23 @@ hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bia
     algo = res[best].algo;
   }
   const float alpha = 1.0f, beta = 0.0f;
-  BLAS_TRY(hipblasLtMatmul(h, dsc.op, &alpha, wt, dsc.a, x, dsc.b, &beta, y, dsc.d, y, dsc.d, &algo, ws, ws_bytes,
+  BLAS_TRY(hipblasLtMatmul(h, dsc.op, &alpha, A, dsc.a, B, dsc.b, &beta, y, dsc.d, y, dsc.d, &algo, ws, ws_bytes,
                            stream));
   return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
+                         bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const Shape sh{true, false, N, M, K, K, K, N};
+  return gemm_cm(sh, wt, x, bias, y, y_bf16, ws, ws_bytes, stream);
+}
+
+hipError_t blas_gemm_dyw(const uint16_t* dy, const uint16_t* wt, int M, int N, int K, void* dx, bool dx_bf16,
+                         void* ws, size_t ws_bytes, hipStream_t stream) {
+  const Shape sh{false, false, K, M, N, K, N, K};
+  return gemm_cm(sh, wt, dy, nullptr, dx, dx_bf16, ws, ws_bytes, stream);
 }
 
 }  // namespace unifur

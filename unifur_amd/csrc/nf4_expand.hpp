@@ -26,4 +26,9 @@ constexpr size_t kBlasWorkspace = 32u << 20;
 hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
                          bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream);
 
+// dX[M][K] = dY[M][N] Wt[N][K] (the backward of the product above with
+// respect to X), bf16 operands, dX f32 or bf16; same kernel choice rule.
+hipError_t blas_gemm_dyw(const uint16_t* dy, const uint16_t* wt, int M, int N, int K, void* dx, bool dx_bf16,
+                         void* ws, size_t ws_bytes, hipStream_t stream);
+
 }  // namespace unifur

@@ -382,6 +382,43 @@ class Nf4Linear:
 
     __call__ = forward
 
+    def _backward(self, dy: torch.Tensor, lora: Optional[LoraAdapter], x: Optional[torch.Tensor], want_dx: bool,
+                  dx_dtype: Optional[torch.dtype]):
+        _require_cuda(dy, "dy")
+        if dy.shape[-1] != self._d_out:
+            raise ValueError(f"dy has last dim {dy.shape[-1]}, the layer gives {self._d_out}")
+        rows = dy.numel() // self._d_out
+        if lora is not None:
+            if x is None:
+                raise ValueError("the adapter gradients need the forward input x")
+            _require_cuda(x, "x")
+            if x.shape[-1] != self._d_in or x.numel() // self._d_in != rows:
+                raise ValueError("x must be [..., d_input] with the rows of dy")
+        dx = None
+        if want_dx:
+            dx = torch.empty(*dy.shape[:-1], self._d_in, dtype=dx_dtype or dy.dtype, device=dy.device)
+        ga = gb = None
+        lo = None
+        if lora is not None:
+            lo = lora.struct()
+            ga = torch.empty(self._d_in, lora.rank(), dtype=torch.float32, device=dy.device)
+            gb = torch.empty(lora.rank(), self._d_out, dtype=torch.float32, device=dy.device)
+        w = self.weight_struct()
+        L.check(L.lib().unifur_nf4_linear_backward(
+            dy.data_ptr(), _dtype_code(dy.dtype), rows, ctypes.byref(w),
+            ctypes.byref(lo) if lo is not None else None,
+            x.data_ptr() if x is not None else None, _dtype_code(x.dtype) if x is not None else L.F32,
+            dx.data_ptr() if dx is not None else None, _dtype_code(dx.dtype) if dx is not None else L.F32,
+            ga.data_ptr() if ga is not None else None, gb.data_ptr() if gb is not None else None,
+            None, 0, _stream()))
+        return dx, ga, gb
+
+    def backward(self, dy: torch.Tensor, dx_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """dL/dx = dy W^T for dy = dL/dy: the gradient burn's autodiff
+        takes through the detached dequantized weight (src/qwennet.rs:238-241
+        under src/qwentrain.rs:421-470); the frozen weight gets none."""
+        return self._backward(dy, None, None, True, dx_dtype)[0]
+
 
 class QloraLinear:
     """Frozen packed NF4 base plus a LoRA adapter (src/qwennet.rs:311-345):
@@ -397,6 +434,14 @@ class QloraLinear:
         return self.base._forward(x, self.adapter, out_dtype)
 
     __call__ = forward
+
+    def backward(self, x: torch.Tensor, dy: torch.Tensor, want_dx: bool = True,
+                 dx_dtype: Optional[torch.dtype] = None):
+        """Vector-Jacobian products of forward for dy = dL/dy: returns
+        (dx, grad_a, grad_b), dx = dy W^T + ((dy s) B^T) A^T,
+        grad_b = (x A)^T (dy s), grad_a = x^T ((dy s) B^T) (f32); dx is None
+        when want_dx is False.  The base weight is frozen."""
+        return self.base._backward(dy, self.adapter, x, want_dx, dx_dtype)
 
 
 class QwenMlp:
