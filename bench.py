@@ -477,6 +477,15 @@ def read_traffic():
     return None
 
 
+PARTS = {
+    "gemm": lambda torch, Q, L: bench_gemm(torch, Q, L),
+    "swiglu": lambda torch, Q, L: bench_swiglu(torch, Q, L, (1, 16, 512)),
+    "qwen": lambda torch, Q, L: bench_qwen(torch, Q, L),
+    "embedding": lambda torch, Q, L: bench_embedding(torch, Q, L),
+    "backward": lambda torch, Q, L: bench_backward(torch, Q, L),
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -487,6 +496,8 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline GEMV and codec only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 20 device copies of 256 MiB (the reference kernel for scaling HBM byte counters)")
+    ap.add_argument("--parts", nargs="+", choices=sorted(PARTS),
+                    help="only these secondary workloads, one JSON object of their figures (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -512,6 +523,9 @@ def main() -> int:
                           "launches": 20}))
         return 0
     L.lib()
+    if args.parts:
+        print(json.dumps({name: PARTS[name](torch, Q, L) for name in args.parts}))
+        return 0
     gemv = bench_gemv(torch, Q, L, args)
     codec = bench_codec(torch, Q, L)
     secondary = {
