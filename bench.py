@@ -350,6 +350,24 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
         ms = graph_ms(torch, graph, 20) if graph is not None else event_ms(torch, step, 5)
         out[f"decode_b{b}"] = {"ms_per_token_step": round(ms, 4), "weight_gbs": round(wbytes / ms / 1e6, 1),
                                "tokens_per_s": round(b / ms * 1e3, 1)}
+
+        # the same weights as a decoder layer drives them: q, k, v in one
+        # shared-input launch, o, and the SwiGLU block (gate/up pair + down)
+        layers_ = [(lins[7 * l:7 * l + 3], lins[7 * l + 3], Q.QwenMlp(*lins[7 * l + 4:7 * l + 7]))
+                   for l in range(layers)]
+
+        def layer_step(i: int) -> None:
+            for qkv, o, mlp in layers_:
+                Q.forward_shared_input(xs[896], qkv)
+                o.forward(xs[896])
+                mlp.forward(xs[896])
+
+        layer_step(0)
+        graph = capture(torch, layer_step, 1)
+        ms = graph_ms(torch, graph, 20) if graph is not None else event_ms(torch, layer_step, 5)
+        out[f"decode_b{b}_layer_launches"] = {"ms_per_token_step": round(ms, 4),
+                                              "weight_gbs": round(wbytes / ms / 1e6, 1),
+                                              "tokens_per_s": round(b / ms * 1e3, 1), "launches": 4 * layers}
     out["weight_bytes"] = wbytes
     return out
 

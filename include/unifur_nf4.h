@@ -201,6 +201,20 @@ int unifur_nf4_linear_forward(const void *x, int x_dtype, uint64_t rows, const u
                               const float *bias, const unifur_nf4_lora *lora, void *y, int y_dtype,
                               void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* n <= 3 linears over one input: y[i] = x w[i] (+ bias[i]) with a shared
+ * d_in -- the q, k and v projections of QwenFullAttention::forward
+ * (src/qwennet.rs:927-956), each an Nf4Linear.  For decode-sized batches
+ * (<= 4 rows, or 5..64 bf16 rows) over striped weights of one scale kind
+ * a single kernel launch serves all of them and each activation load feeds
+ * every weight; other calls run the linears in turn.  w points to n
+ * weights, bias to n pointers (or is NULL; entries may be NULL), y to n
+ * outputs [rows, w[i].d_out]. */
+uint64_t unifur_nf4_linear_multi_workspace_size(uint64_t rows, uint64_t d_in, const uint64_t *d_out, uint32_t n,
+                                                int x_dtype);
+int unifur_nf4_linear_forward_multi(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,
+                                    const float *const *bias, void *const *y, int y_dtype, uint32_t n,
+                                    void *workspace, uint64_t workspace_bytes, void *stream);
+
 /* QloraLinear::forward (src/qwennet.rs:325-345); identical to
  * unifur_nf4_linear_forward with a non-NULL lora. */
 int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,

@@ -739,6 +739,87 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
   return UNIFUR_NF4_OK;
 }
 
+
+// ---------------------------------------------------- linears sharing x -----
+
+// Up to three striped weights of one scale kind over the same x: one GEMV
+// (<= 4 rows) or skinny (5..64 bf16 rows) launch covers them all, every
+// activation load feeding every weight; otherwise the linears run in turn.
+struct MultiLayout {
+  bool fused, skinny;
+  StripedPlan plan;
+  size_t partials[kMaxGemvWeights];
+  size_t total;  // fused plans; the sequential fallback sizes itself per linear
+};
+
+MultiLayout plan_multi(uint64_t rows, uint64_t d_in, const uint64_t* d_out, const unifur_nf4_weight* w, uint32_t n,
+                       int x_dtype, const void* x) {
+  MultiLayout L{};
+  Carver c;
+  bool ok = n >= 1 && n <= (uint32_t)kMaxGemvWeights && rows >= 1 && d_in <= 0x7fffffffu;
+  for (uint32_t i = 0; ok && i < n; ++i)
+    ok = d_out[i] % 64 == 0 && d_out[i] <= 0x7fffffffu && (!w || (is_striped(&w[i]) && w[i].d_in == d_in &&
+                                                                    w[i].scales.kind == w[0].scales.kind));
+  int dn[kMaxGemvWeights] = {};
+  uint64_t stripes = 0;
+  for (uint32_t i = 0; ok && i < n; ++i) {
+    dn[i] = (int)d_out[i];
+    stripes += d_out[i] / 16;
+  }
+  ok = ok && stripes / 4 <= (uint64_t)kMaxCounters;
+  if (ok && rows <= (uint64_t)kGemvMaxRows) {
+    L.fused = true;
+    L.plan = plan_gemv_striped((int)rows, (int)d_in, dn, (int)n, false);
+  } else if (ok && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
+             skinny_supported((int)rows, (int)d_in, x)) {
+    L.fused = L.skinny = true;
+    L.plan = plan_skinny((int)rows, (int)d_in, dn, (int)n, false);
+    for (uint32_t i = 0; i < n; ++i)
+      L.partials[i] = c.take(skinny_partial_floats(L.plan, (int)rows, dn[i]) * sizeof(float));
+  }
+  L.total = c.off;
+  return L;
+}
+
+int run_linear_multi(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w, const float* const* bias,
+                     void* const* y, int y_dtype, uint32_t n, void* workspace, uint64_t workspace_bytes,
+                     hipStream_t stream) {
+  UNIFUR_ARG(valid_dtype(x_dtype) && valid_dtype(y_dtype), "dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  UNIFUR_ARG(n >= 1 && n <= (uint32_t)kMaxGemvWeights, "linear_forward_multi takes 1 to 3 weights");
+  UNIFUR_ARG(w != nullptr && y != nullptr, "weights or outputs are NULL");
+  for (uint32_t i = 0; i < n; ++i) {
+    if (int r = check_weight(&w[i], "linear_forward_multi")) return r;
+    UNIFUR_ARG(w[i].d_in == w[0].d_in, "the weights must share d_in");
+    UNIFUR_ARG(rows == 0 || y[i] != nullptr, "an output is NULL");
+  }
+  if (rows == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(x != nullptr, "x is NULL");
+  uint64_t d_out[kMaxGemvWeights] = {};
+  for (uint32_t i = 0; i < n; ++i) d_out[i] = w[i].d_out;
+  const MultiLayout L = plan_multi(rows, w[0].d_in, d_out, w, n, x_dtype, x);
+  if (!L.fused) {
+    for (uint32_t i = 0; i < n; ++i)
+      if (int r = run_linear(x, x_dtype, rows, &w[i], bias ? bias[i] : nullptr, nullptr, y[i], y_dtype, workspace,
+                             workspace_bytes, stream))
+        return r;
+    return UNIFUR_NF4_OK;
+  }
+  void* ws = nullptr;
+  if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
+  GemvWeight gw[kMaxGemvWeights];
+  for (uint32_t i = 0; i < n; ++i) {
+    gw[i] = gemv_weight(&w[i], y[i], y_dtype == UNIFUR_NF4_BF16, at<unsigned>(ws, 0), at<float>(ws, L.partials[i]));
+    gw[i].bias = bias ? bias[i] : nullptr;
+  }
+  if (L.skinny)
+    UNIFUR_HIP(launch_skinny(L.plan, static_cast<const uint16_t*>(x), (int)rows, (int)w[0].d_in, gw, (int)n, false,
+                             stream));
+  else
+    UNIFUR_HIP(launch_gemv_striped(L.plan, x, x_dtype == UNIFUR_NF4_BF16, (int)rows, (int)w[0].d_in, gw, (int)n,
+                                   false, stream));
+  return UNIFUR_NF4_OK;
+}
+
 }  // namespace
 }  // namespace unifur
 
@@ -807,6 +888,24 @@ int unifur_nf4_dequantize(const uint8_t* packed, const unifur_nf4_scales* scales
   UNIFUR_HIP(launch_dequantize(packed, to_scales(*scales), len, out, out_dtype == UNIFUR_NF4_BF16, aligned,
                                static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
+}
+
+uint64_t unifur_nf4_linear_multi_workspace_size(uint64_t rows, uint64_t d_in, const uint64_t* d_out, uint32_t n,
+                                                int x_dtype) {
+  if (rows == 0 || d_in == 0 || !d_out || n == 0 || n > (uint32_t)kMaxGemvWeights) return 0;
+  const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
+  const MultiLayout L = plan_multi(rows, d_in, d_out, nullptr, n, x_dtype, aligned);
+  uint64_t need = L.total;
+  for (uint32_t i = 0; i < n; ++i)  // the linears one at a time, when not fused
+    need = std::max<uint64_t>(need, unifur_nf4_linear_workspace_size(rows, d_in, d_out[i], x_dtype, 0));
+  return need;
+}
+
+int unifur_nf4_linear_forward_multi(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w,
+                                    const float* const* bias, void* const* y, int y_dtype, uint32_t n,
+                                    void* workspace, uint64_t workspace_bytes, void* stream) {
+  return run_linear_multi(x, x_dtype, rows, w, bias, y, y_dtype, n, workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream));
 }
 
 uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,

@@ -420,6 +420,29 @@ class Nf4Linear:
         return self._backward(dy, None, None, True, dx_dtype)[0]
 
 
+def forward_shared_input(x: torch.Tensor, layers, out_dtype: Optional[torch.dtype] = None) -> list:
+    """y_i = layers[i].forward(x) for up to three Nf4Linears sharing d_input,
+    as QwenFullAttention applies q_proj, k_proj and v_proj to one hidden state
+    (src/qwennet.rs:927-956): decode-sized batches over striped weights of one
+    scale kind take a single launch that reads x once for all of them."""
+    _require_cuda(x, "x")
+    layers = list(layers)
+    if not 1 <= len(layers) <= 3:
+        raise ValueError("forward_shared_input takes one to three layers")
+    d_in = layers[0].d_input()
+    if any(l.d_input() != d_in for l in layers) or x.shape[-1] != d_in:
+        raise ValueError("the layers must share d_input with x's last dim")
+    rows = x.numel() // d_in
+    out_dtype = out_dtype or x.dtype
+    ys = [torch.empty(*x.shape[:-1], l.d_output(), dtype=out_dtype, device=x.device) for l in layers]
+    ws = (L.Weight * len(layers))(*[l.weight_struct() for l in layers])
+    biases = (ctypes.c_void_p * len(layers))(*[l.bias.data_ptr() if l.bias is not None else None for l in layers])
+    outs = (ctypes.c_void_p * len(layers))(*[y.data_ptr() for y in ys])
+    L.check(L.lib().unifur_nf4_linear_forward_multi(x.data_ptr(), _dtype_code(x.dtype), rows, ws, biases, outs,
+                                                    _dtype_code(out_dtype), len(layers), None, 0, _stream()))
+    return ys
+
+
 class QloraLinear:
     """Frozen packed NF4 base plus a LoRA adapter (src/qwennet.rs:311-345):
     forward(x) = base(x) + (x a) b * scaling, fused into one launch chain."""
