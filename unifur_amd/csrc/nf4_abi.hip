@@ -181,7 +181,7 @@ struct LinearLayout {
   bool expand;  // kMfma: bf16 weight expanded in the workspace + BLAS GEMM (else the fused kernel)
   GemvPlan gemv;
   StripedPlan striped;
-  size_t partials, xa, lora_at, lora_bt, wt, blas, wf32, rm_codes, rm_scales, total;
+  size_t partials, xa, lora_at, lora_bt, wt, blas, lora_ops, wf32, rm_codes, rm_scales, total;
 };
 
 // Decode-sized batches (<= 4 rows) take a GEMV (the striped one for striped
@@ -223,6 +223,7 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
     if (L.expand) {
       L.wt = c.take(d_in * d_out * sizeof(uint16_t));
       L.blas = c.take(kBlasWorkspace);
+      L.lora_ops = c.take(expand_lora_scratch_bytes((int)d_in, (int)d_out, (int)lora_rank));
     }
   } else {
     L.path = LinearPath::kGeneric;
@@ -316,7 +317,7 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     uint16_t* wt = at<uint16_t>(ws, L.wt);
     UNIFUR_HIP(launch_expand_bf16(w->packed, to_scales(w->scales), (int)w->d_in, (int)w->d_out, is_striped(w),
                                   lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
-                                  lora ? lora->scaling : 0.0f, wt, stream));
+                                  lora ? lora->scaling : 0.0f, at<void>(ws, L.lora_ops), wt, stream));
     UNIFUR_HIP(blas_gemm_xwt(static_cast<const uint16_t*>(x), wt, bias, (int)rows, (int)w->d_out, (int)w->d_in, y,
                              ybf, at<void>(ws, L.blas), kBlasWorkspace, stream));
     return UNIFUR_NF4_OK;
@@ -560,14 +561,14 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
         void* bw = at<void>(ws, L.blas);
         const int hd = (int)hidden, in = (int)inter, m = (int)rows;
         UNIFUR_HIP(launch_expand_bf16(gate->packed, to_scales(gate->scales), hd, in, is_striped(gate), nullptr,
-                                      nullptr, 0, 0.0f, wt, stream));
+                                      nullptr, 0, 0.0f, nullptr, wt, stream));
         UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, in, hd, h, false, bw, kBlasWorkspace, stream));
         UNIFUR_HIP(launch_expand_bf16(up->packed, to_scales(up->scales), hd, in, is_striped(up), nullptr, nullptr, 0,
-                                      0.0f, wt, stream));
+                                      0.0f, nullptr, wt, stream));
         UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, in, hd, u, false, bw, kBlasWorkspace, stream));
         UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
         UNIFUR_HIP(launch_expand_bf16(down->packed, to_scales(down->scales), in, hd, is_striped(down), nullptr,
-                                      nullptr, 0, 0.0f, wt, stream));
+                                      nullptr, 0, 0.0f, nullptr, wt, stream));
         UNIFUR_HIP(blas_gemm_xwt(hb, wt, nullptr, m, hd, in, y, ybf, bw, kBlasWorkspace, stream));
         return UNIFUR_NF4_OK;
       }
@@ -638,7 +639,7 @@ uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate,
 // x A, dY B^T and two row reductions.
 struct BackwardLayout {
   bool blas;
-  size_t wt, blas_ws, wf32, rm_codes, rm_scales, xa, u, partials, total;
+  size_t wt, blas_ws, lora_ops, wf32, rm_codes, rm_scales, xa, u, partials, total;
 };
 
 BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t rank, int dy_dtype, bool want_dx,
@@ -651,6 +652,7 @@ BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint3
     if (L.blas) {
       L.wt = c.take(d_in * d_out * sizeof(uint16_t));
       L.blas_ws = c.take(kBlasWorkspace);
+      L.lora_ops = c.take(expand_lora_scratch_bytes((int)d_in, (int)d_out, (int)rank));
     } else {
       L.wf32 = c.take(d_in * d_out * sizeof(float));
       if (striped) {
@@ -703,7 +705,8 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
     if (L.blas) {
       uint16_t* wt = at<uint16_t>(ws, L.wt);
       UNIFUR_HIP(launch_expand_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w), lora ? lora->a : nullptr,
-                                    lora ? lora->b : nullptr, (int)rank, lora ? lora->scaling : 0.0f, wt, stream));
+                                    lora ? lora->b : nullptr, (int)rank, lora ? lora->scaling : 0.0f,
+                                    at<void>(ws, L.lora_ops), wt, stream));
       UNIFUR_HIP(blas_gemm_dyw(static_cast<const uint16_t*>(dy), wt, m, n, k, dx, dx_dtype == UNIFUR_NF4_BF16,
                                at<void>(ws, L.blas_ws), kBlasWorkspace, stream));
     } else {

@@ -22,6 +22,8 @@
 // along K, their loads all issued first.
 #include "nf4_expand.hpp"
 
+#include <algorithm>
+
 namespace unifur {
 namespace {
 
@@ -38,9 +40,9 @@ struct ExpandArgs {
   const uint8_t* packed;
   ScalesArg scales;
   int K, N;
-  const float* lora_a;  // [K][rank] or null
-  const float* lora_b;  // [rank][N]
-  int rank;
+  const uint16_t* a16;   // bf16 A [K][rp], zero past the rank (lora_prep_kernel)
+  const uint16_t* bt16;  // bf16 B transposed [N][rp]
+  int rank, rp;
   float scaling;
   uint16_t* wt;  // [N][K]
   int tiles_k;   // K / 64
@@ -86,24 +88,27 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 
   float* lut = reinterpret_cast<float*>(smem + kLdsLut);
   if (tid < 16) lut[tid] = level(tid);
-  // LoRA operands after the transpose tiles, bf16, zero past the rank (rank
-  // rounded up to rp = 16, 32 or 64): A rows [64 KT][rp] and B transposed
-  // [64 columns][rp], so that every MFMA fragment is one 16-byte read; then
-  // the f32 product tile C [64][68]
-  const int rp = a.rank <= 16 ? 16 : a.rank <= 32 ? 32 : 64;
-  const int lds_a = kLdsT + KT * kTBytes, lds_b = lds_a + kTile * KT * rp * 2, lds_c = lds_b + kTile * rp * 2;
+  // LoRA: the MFMA fragments straight from the prepared bf16 operands (one
+  // 16-byte load each, issued with the code loads); the f32 product tile
+  // C [64][68] after the transpose tiles
+  const int lane = tid & 63, wv = tid >> 6, bi = wv >> 1, bj = wv & 1, h = lane >> 5;
+  const int lds_c = kLdsT + KT * kTBytes;
+  // adapter fragments per tile: up to rank 64 in the one-tile kernel, rank
+  // 16 (one fragment) when a workgroup takes several tiles
+  constexpr int kMaxFr = (LORA && KT == 1) ? kMaxRank / 16 : 1;
+  bf16x8_t bfr[kMaxFr];
+  bf16x8_t afr[KT][kMaxFr];
   if constexpr (LORA) {
-    uint16_t* As = reinterpret_cast<uint16_t*>(smem + lds_a);
-    uint16_t* Bt = reinterpret_cast<uint16_t*>(smem + lds_b);
-    // A: four threads per row (columns tid % 4 + 4 j); B: one column per
-    // thread (rows tid / 64 + 4 j)
-    for (int kk = tid >> 2; kk < kTile * KT; kk += 64) {
-      const float* arow = a.lora_a + (size_t)(k0 + kk) * a.rank;
-      for (int r = tid & 3; r < rp; r += 4) As[kk * rp + r] = (uint16_t)pack_bf16x2(r < a.rank ? arow[r] : 0.0f, 0.0f);
+    const int nf = a.rp / 16;
+#pragma unroll
+    for (int f = 0; f < kMaxFr; ++f) {
+      if (f >= nf) break;
+      bfr[f] = *reinterpret_cast<const bf16x8_t*>(a.bt16 + (size_t)(n0 + 32 * bj + (lane & 31)) * a.rp + 16 * f + 8 * h);
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+        afr[t][f] = *reinterpret_cast<const bf16x8_t*>(
+            a.a16 + (size_t)(k0 + kTile * t + 32 * bi + (lane & 31)) * a.rp + 16 * f + 8 * h);
     }
-    const int nn = tid & 63;
-    for (int r = tid >> 6; r < rp; r += 4)
-      Bt[nn * rp + r] = (uint16_t)pack_bf16x2(r < a.rank ? a.lora_b[(size_t)r * a.N + n0 + nn] : 0.0f, 0.0f);
   }
   __syncthreads();
 
@@ -120,15 +125,12 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       // C = A_t B for this tile: wave w computes the 32 x 32 block
       // (w / 2, w % 2) with rp / 16 v_mfma_f32_32x32x16_bf16 (bf16 factors,
       // f32 sums); C passes through LDS to the (k, k + 1) x 8-column layout
-      const int lane = tid & 63, w = tid >> 6, bi = w >> 1, bj = w & 1, h = lane >> 5;
-      const uint16_t* As = reinterpret_cast<const uint16_t*>(smem + lds_a);
-      const uint16_t* Bt = reinterpret_cast<const uint16_t*>(smem + lds_b);
       float* C = reinterpret_cast<float*>(smem + lds_c);
       f32x16 acc = {};
-      for (int r0 = 0; r0 < rp; r0 += 16) {
-        const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(As + (kTile * t + 32 * bi + (lane & 31)) * rp + r0 + 8 * h);
-        const bf16x8_t bf = *reinterpret_cast<const bf16x8_t*>(Bt + (32 * bj + (lane & 31)) * rp + r0 + 8 * h);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc, 0, 0, 0);
+#pragma unroll
+      for (int f = 0; f < kMaxFr; ++f) {
+        if (f >= a.rp / 16) break;
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[t][f], bfr[f], acc, 0, 0, 0);
       }
       if (t > 0) __syncthreads();  // the previous tile's C has been read
       // acc[4 q + e] = C[8 q + 4 h + e][lane % 32] of the block
@@ -166,30 +168,51 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   }
 }
 
-// LDS of a KT-tile workgroup: the transpose tiles, then with an adapter its
-// bf16 A rows and B columns and the f32 product tile.
-size_t expand_smem(int KT, int rank) {
-  const size_t rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
-  return kLdsT + (size_t)KT * kTBytes + (rank ? (size_t)kTile * KT * rp * 2 + kTile * rp * 2 + kTile * kCStride * 4 : 0);
+// LDS of a KT-tile workgroup: the transpose tiles, then with an adapter the
+// f32 product tile.
+size_t expand_smem(int KT, bool lora) {
+  return kLdsT + (size_t)KT * kTBytes + (lora ? (size_t)kTile * kCStride * 4 : 0);
+}
+
+// a16[k][r] = bf16(a[k][r]) and bt16[n][r] = bf16(b[r][n]), zero for r >= rank
+// (rp = 1 << rp_shift): blockIdx.y < rp transposes row r = blockIdx.y of b
+// (coalesced reads along n); blockIdx.y == rp copies a.
+__global__ void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b, int K, int N, int rank,
+                                 int rp_shift, uint16_t* __restrict__ a16, uint16_t* __restrict__ bt16) {
+  const int rp = 1 << rp_shift;
+  const int r = blockIdx.y;
+  if (r < rp) {
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < N; n += gridDim.x * blockDim.x)
+      bt16[((size_t)n << rp_shift) + r] = (uint16_t)(pack_bf16x2(r < rank ? b[(size_t)r * N + n] : 0.0f, 0.0f) & 0xffffu);
+    return;
+  }
+  const size_t total = (size_t)K << rp_shift;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int rr = (int)(i & (size_t)(rp - 1));
+    const size_t k = i >> rp_shift;
+    a16[i] = (uint16_t)(pack_bf16x2(rr < rank ? a[k * rank + rr] : 0.0f, 0.0f) & 0xffffu);
+  }
+}
 }
 
 template <bool DQ, bool STRIPED, bool LORA>
 hipError_t launch_t(const ExpandArgs& a, hipStream_t stream) {
   const long long band = a.N / kTile;
-  // without an adapter four (or two) tiles per workgroup where K allows:
-  // more loads in flight; with one, one tile (its LDS would otherwise limit
-  // the workgroups per CU, which measured slower)
-  if constexpr (!LORA) {
-    if (a.tiles_k % 4 == 0) {
-      expand_kernel<DQ, STRIPED, false, 4><<<(int)(band * (a.tiles_k / 4)), 256, expand_smem(4, 0), stream>>>(a);
-      return hipGetLastError();
-    }
-    if (a.tiles_k % 2 == 0) {
-      expand_kernel<DQ, STRIPED, false, 2><<<(int)(band * (a.tiles_k / 2)), 256, expand_smem(2, 0), stream>>>(a);
-      return hipGetLastError();
-    }
+  // four (or two) tiles per workgroup where K allows: more loads in flight
+  // (with an adapter of rank <= 16, whose fragments then fit the registers)
+  if (LORA && a.rp > 16) {
+    expand_kernel<DQ, STRIPED, LORA, 1><<<(int)(band * a.tiles_k), 256, expand_smem(1, LORA), stream>>>(a);
+    return hipGetLastError();
   }
-  expand_kernel<DQ, STRIPED, LORA, 1><<<(int)(band * a.tiles_k), 256, expand_smem(1, a.rank), stream>>>(a);
+  if (a.tiles_k % 4 == 0) {
+    expand_kernel<DQ, STRIPED, LORA, 4><<<(int)(band * (a.tiles_k / 4)), 256, expand_smem(4, LORA), stream>>>(a);
+    return hipGetLastError();
+  }
+  if (a.tiles_k % 2 == 0) {
+    expand_kernel<DQ, STRIPED, LORA, 2><<<(int)(band * (a.tiles_k / 2)), 256, expand_smem(2, LORA), stream>>>(a);
+    return hipGetLastError();
+  }
+  expand_kernel<DQ, STRIPED, LORA, 1><<<(int)(band * a.tiles_k), 256, expand_smem(1, LORA), stream>>>(a);
   return hipGetLastError();
 }
 
@@ -199,18 +222,36 @@ bool expand_supported(int K, int N, int rank) {
   return K > 0 && N > 0 && K % kTile == 0 && N % kTile == 0 && rank >= 0 && rank <= kMaxRank;
 }
 
+size_t expand_lora_scratch_bytes(int K, int N, int rank) {
+  if (rank <= 0) return 0;
+  const size_t rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
+  return ((size_t)K + N) * rp * sizeof(uint16_t);
+}
+
 hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
-                              const float* lora_a, const float* lora_b, int rank, float scaling, uint16_t* wt,
-                              hipStream_t stream) {
-  if (!expand_supported(K, N, rank) || (rank > 0 && (!lora_a || !lora_b))) return hipErrorInvalidValue;
+                              const float* lora_a, const float* lora_b, int rank, float scaling, void* lora_scratch,
+                              uint16_t* wt, hipStream_t stream) {
+  if (!expand_supported(K, N, rank) || (rank > 0 && (!lora_a || !lora_b || !lora_scratch)))
+    return hipErrorInvalidValue;
+  const int rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
+  uint16_t* a16 = static_cast<uint16_t*>(lora_scratch);
+  uint16_t* bt16 = a16 + (size_t)K * rp;
+  if (rank > 0) {
+    const int rp_shift = rp == 16 ? 4 : rp == 32 ? 5 : 6;
+    const unsigned bx = (unsigned)std::min<size_t>(((size_t)std::max(N, K) + 255) / 256, 1024);
+    lora_prep_kernel<<<dim3(bx, rp + 1), 256, 0, stream>>>(lora_a, lora_b, K, N, rank, rp_shift, a16, bt16);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   ExpandArgs a{};
   a.packed = packed;
   a.scales = scales;
   a.K = K;
   a.N = N;
-  a.lora_a = lora_a;
-  a.lora_b = lora_b;
+  a.a16 = a16;
+  a.bt16 = bt16;
   a.rank = rank;
+  a.rp = rp;
   a.scaling = scaling;
   a.wt = wt;
   a.tiles_k = K / kTile;

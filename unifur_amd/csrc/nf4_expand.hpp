@@ -10,10 +10,12 @@ namespace unifur {
 bool expand_supported(int K, int N, int rank);
 
 // Wt[N][K] bf16 = the dequantized weight (row-major or striped layout) plus
-// scaling * A B when rank > 0 (A f32 [K][rank], B f32 [rank][N]).
+// scaling * A B when rank > 0 (A f32 [K][rank], B f32 [rank][N]); the
+// adapter's bf16 operands go to lora_scratch (expand_lora_scratch_bytes).
+size_t expand_lora_scratch_bytes(int K, int N, int rank);
 hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
-                              const float* lora_a, const float* lora_b, int rank, float scaling, uint16_t* wt,
-                              hipStream_t stream);
+                              const float* lora_a, const float* lora_b, int rank, float scaling, void* lora_scratch,
+                              uint16_t* wt, hipStream_t stream);
 
 // Scratch the BLAS GEMM may use (its kernels' split-K partials and the like).
 constexpr size_t kBlasWorkspace = 32u << 20;
