@@ -435,13 +435,19 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
     L.u = L.path == MlpPath::kGemv ? c.take((size_t)rows * inter * sizeof(float)) : 0;
   } else if (mfma) {
     L.path = MlpPath::kMfma;
-    L.h = c.take((size_t)rows * inter * sizeof(float));
-    L.u = c.take((size_t)rows * inter * sizeof(float));
-    L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
-    L.expand = expand && expand_supported((int)hidden, (int)inter, 0) && expand_supported((int)inter, (int)hidden, 0);
+    L.expand = expand && expand_supported((int)hidden, (int)inter, 0) && expand_supported((int)inter, (int)hidden, 0) &&
+               2 * inter <= 0x7fffffffu;
     if (L.expand) {
-      L.wt = c.take(hidden * inter * sizeof(uint16_t));  // one weight at a time
+      // gate and up expanded side by side ([2 inter][hidden]: one GEMM with
+      // bf16 outputs [rows][2 inter]), then down into the same buffer
+      L.wt = c.take(2 * hidden * inter * sizeof(uint16_t));
       L.blas = c.take(kBlasWorkspace);
+      L.h = c.take((size_t)rows * 2 * inter * sizeof(uint16_t));
+      L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
+    } else {
+      L.h = c.take((size_t)rows * inter * sizeof(float));
+      L.u = c.take((size_t)rows * inter * sizeof(float));
+      L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
     }
   } else {
     L.path = MlpPath::kGeneric;
@@ -558,15 +564,15 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       uint16_t* hb = at<uint16_t>(ws, L.hb);
       if (L.expand) {
         uint16_t* wt = at<uint16_t>(ws, L.wt);
+        uint16_t* gu = at<uint16_t>(ws, L.h);
         void* bw = at<void>(ws, L.blas);
         const int hd = (int)hidden, in = (int)inter, m = (int)rows;
         UNIFUR_HIP(launch_expand_bf16(gate->packed, to_scales(gate->scales), hd, in, is_striped(gate), nullptr,
                                       nullptr, 0, 0.0f, nullptr, wt, stream));
-        UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, in, hd, h, false, bw, kBlasWorkspace, stream));
         UNIFUR_HIP(launch_expand_bf16(up->packed, to_scales(up->scales), hd, in, is_striped(up), nullptr, nullptr, 0,
-                                      0.0f, nullptr, wt, stream));
-        UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, in, hd, u, false, bw, kBlasWorkspace, stream));
-        UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
+                                      0.0f, nullptr, wt + (size_t)in * hd, stream));
+        UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, 2 * in, hd, gu, true, bw, kBlasWorkspace, stream));
+        UNIFUR_HIP(launch_silu_mul_rows_bf16(gu, (size_t)rows, (size_t)inter, hb, stream));
         UNIFUR_HIP(launch_expand_bf16(down->packed, to_scales(down->scales), in, hd, is_striped(down), nullptr,
                                       nullptr, 0, 0.0f, nullptr, wt, stream));
         UNIFUR_HIP(blas_gemm_xwt(hb, wt, nullptr, m, hd, in, y, ybf, bw, kBlasWorkspace, stream));

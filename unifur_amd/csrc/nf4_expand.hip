@@ -193,7 +193,6 @@ __global__ void lora_prep_kernel(const float* __restrict__ a, const float* __res
     a16[i] = (uint16_t)(pack_bf16x2(rr < rank ? a[k * rank + rr] : 0.0f, 0.0f) & 0xffffu);
   }
 }
-}
 
 template <bool DQ, bool STRIPED, bool LORA>
 hipError_t launch_t(const ExpandArgs& a, hipStream_t stream) {

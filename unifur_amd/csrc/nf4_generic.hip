@@ -129,6 +129,19 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
   }
 }
 
+// h[m][i] = bf16(silu(g) * u) with g = gu[m][i] and u = gu[m][inter + i],
+// both bf16 (the gate and up halves of one GEMM's output row).
+__global__ void silu_mul_rows_bf16_kernel(const uint16_t* __restrict__ gu, size_t rows, size_t inter,
+                                          uint16_t* __restrict__ h) {
+  const size_t n = rows * inter;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t m = i / inter, c = i % inter;
+    const float z = bf16_bits_to_f32(gu[m * 2 * inter + c]);
+    const float u = bf16_bits_to_f32(gu[m * 2 * inter + inter + c]);
+    h[i] = (uint16_t)(pack_bf16x2((z * (1.0f / (1.0f + __expf(-z)))) * u, 0.0f) & 0xffffu);
+  }
+}
+
 __global__ void silu_mul_bf16_kernel(const float* __restrict__ g, const float* __restrict__ u, size_t n,
                                      uint16_t* __restrict__ h) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
@@ -460,6 +473,15 @@ hipError_t launch_narrow_atb(const void* wide, bool wide_bf16, const float* nar,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return slab_sum(partials, slabs, (size_t)W * rank, scale, out, stream);
+}
+
+hipError_t launch_silu_mul_rows_bf16(const uint16_t* gu, size_t rows, size_t inter, uint16_t* h, hipStream_t stream) {
+  const size_t n = rows * inter;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks == 0) return hipSuccess;
+  silu_mul_rows_bf16_kernel<<<(unsigned)blocks, 256, 0, stream>>>(gu, rows, inter, h);
+  return hipGetLastError();
 }
 
 hipError_t launch_silu_mul(const float* g, const float* u, size_t n, float* h, hipStream_t stream) {

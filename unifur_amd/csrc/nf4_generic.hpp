@@ -48,5 +48,7 @@ hipError_t launch_lora_merge(const float* w, const float* a, const float* b, int
                              uint64_t N, float* out, hipStream_t stream);
 hipError_t launch_silu_mul(const float* g, const float* u, size_t n, float* h, hipStream_t stream);
 hipError_t launch_silu_mul_bf16(const float* g, const float* u, size_t n, uint16_t* h, hipStream_t stream);
+// h[m][:] = bf16(silu(gu[m][:inter]) * gu[m][inter:]), gu bf16 [rows][2 inter].
+hipError_t launch_silu_mul_rows_bf16(const uint16_t* gu, size_t rows, size_t inter, uint16_t* h, hipStream_t stream);
 
 }  // namespace unifur
