@@ -488,6 +488,45 @@ def cpu_baseline(sample_s: float) -> dict:
                       f"PackedNf4Tensor::dequantize + burn linear"}
 
 
+def cpu_beside() -> dict:
+    """The reference's CPU path (the oracle's restatement) beside the GPU
+    figures of configs 1 and 3, on this host: quantize and dequantize of the
+    4096 x 4096 config-1 tensor on one thread (the reference's loops are
+    serial), and the config-3 QLoRA layer as the reference runs it --
+    serial dequantize, then an all-core f32 matmul plus the adapter -- timed
+    on a 32-row sample of X and scaled to the 2048 rows."""
+    from oracle import oracle as O
+    threads = len(os.sched_getaffinity(0))
+    out = {"cores": threads}
+    n = 4096 * 4096
+    v = O.fill_normal(0x4E463458, 0.02, n)
+    t0 = time.perf_counter()
+    packed, absmax = O.quantize_packed(v)
+    tq = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    w = O.dequantize_packed(packed, n, absmax)
+    td = time.perf_counter() - t0
+    unit = 76_546_048  # config-1 bytes (read + write) of either direction
+    out["quantize_config1"] = {"s": round(tq, 4), "gbs": round(unit / tq / 1e9, 3), "threads": 1}
+    out["dequantize_config1"] = {"s": round(td, 4), "gbs": round(unit / td / 1e9, 3), "threads": 1}
+    M, K, N, r, rows = 2048, 4096, 4096, 16, 32
+    x = O.fill_normal(0x5A, 1.0, rows * K).reshape(rows, K)
+    a = O.fill_normal(0x41, 0.01, K * r).reshape(K, r)
+    b = O.fill_normal(0x42, 0.01, r * N).reshape(r, N)
+    t0 = time.perf_counter()
+    O.dequantize_packed(packed, n, absmax)                           # per forward, serial
+    t1 = time.perf_counter()
+    O.linear_f32(x, w, K, N, threads=threads)                        # base, all cores
+    xa = O.linear_f32(x, a, K, r, threads=threads)                   # adapter: (x A) B * scaling
+    O.linear_f32(xa, b, r, N, threads=threads)
+    t2 = time.perf_counter()
+    total = (t1 - t0) + (t2 - t1) * (M / rows)
+    flops = 2 * M * N * K + 2 * M * K * r + 2 * M * r * N
+    out["qlora_gemm_config3"] = {"s": round(total, 3), "tflops": round(flops / total / 1e12, 5),
+                                 "sample": f"{rows} of {M} rows timed, scaled", "threads": threads}
+    return out
+
+
 def read_traffic():
     """HBM bytes per GEMV launch from the committed rocprofv3 PMC summary."""
     try:
@@ -573,6 +612,8 @@ def main() -> int:
         secondary["embedding_qwen05b"] = bench_embedding(torch, Q, L)
         secondary["qlora_backward_config3"] = bench_backward(torch, Q, L)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample_s)
+    if not args.no_cpu and not args.quick:
+        secondary["cpu_port_beside"] = cpu_beside()
 
     achieved = gemv["bytes"] / gemv["kernel_cold_ms"] / 1e6
     line = {

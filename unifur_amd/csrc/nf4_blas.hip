@@ -212,7 +212,13 @@ hipError_t gemm_cm(const Shape& sh, const void* A, const void* B, const float* b
 
 hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
                          bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream) {
-  const Shape sh{true, false, N, M, K, K, K, N};
+  return blas_gemm_xwt_ld(x, wt, bias, M, N, K, y, N, y_bf16, ws, ws_bytes, stream);
+}
+
+hipError_t blas_gemm_xwt_ld(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
+                            int ldy, bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (ldy < N) return hipErrorInvalidValue;
+  const Shape sh{true, false, N, M, K, K, K, ldy};
   return gemm_cm(sh, wt, x, bias, y, y_bf16, ws, ws_bytes, stream);
 }
 

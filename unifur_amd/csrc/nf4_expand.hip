@@ -46,6 +46,7 @@ struct ExpandArgs {
   float scaling;
   uint16_t* wt;  // [N][K]
   int tiles_k;   // K / 64
+  int n_base;    // first column of the launch (a multiple of 64)
 };
 
 template <bool DQ, bool STRIPED, bool LORA, int KT>
@@ -57,7 +58,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   // column are adjacent
   const int groups_k = a.tiles_k / KT;
   const int k0 = (int)(blockIdx.x % (unsigned)groups_k) * (kTile * KT);
-  const int n0 = (int)(blockIdx.x / (unsigned)groups_k) * kTile;
+  const int n0 = a.n_base + (int)(blockIdx.x / (unsigned)groups_k) * kTile;
   const int kp = tid & 31, ng = tid >> 5;
   const int n = n0 + 8 * ng;
 
@@ -195,8 +196,8 @@ __global__ void lora_prep_kernel(const float* __restrict__ a, const float* __res
 }
 
 template <bool DQ, bool STRIPED, bool LORA>
-hipError_t launch_t(const ExpandArgs& a, hipStream_t stream) {
-  const long long band = a.N / kTile;
+hipError_t launch_t(const ExpandArgs& a, int n_count, hipStream_t stream) {
+  const long long band = n_count / kTile;
   // four (or two) tiles per workgroup where K allows: more loads in flight
   // (with an adapter of rank <= 16, whose fragments then fit the registers)
   if (LORA && a.rp > 16) {
@@ -230,18 +231,36 @@ size_t expand_lora_scratch_bytes(int K, int N, int rank) {
 hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
                               const float* lora_a, const float* lora_b, int rank, float scaling, void* lora_scratch,
                               uint16_t* wt, hipStream_t stream) {
-  if (!expand_supported(K, N, rank) || (rank > 0 && (!lora_a || !lora_b || !lora_scratch)))
-    return hipErrorInvalidValue;
+  if (rank > 0) {
+    const hipError_t e = launch_expand_prep(K, N, lora_a, lora_b, rank, lora_scratch, stream);
+    if (e != hipSuccess) return e;
+  }
+  return launch_expand_cols(packed, scales, K, N, striped, rank, scaling, lora_scratch, 0, N, wt, stream);
+}
+
+hipError_t launch_expand_prep(int K, int N, const float* lora_a, const float* lora_b, int rank, void* lora_scratch,
+                              hipStream_t stream) {
+  if (!expand_supported(K, N, rank) || rank <= 0 || !lora_a || !lora_b || !lora_scratch) return hipErrorInvalidValue;
   const int rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
   uint16_t* a16 = static_cast<uint16_t*>(lora_scratch);
   uint16_t* bt16 = a16 + (size_t)K * rp;
-  if (rank > 0) {
+  {
     const int rp_shift = rp == 16 ? 4 : rp == 32 ? 5 : 6;
     const unsigned bx = (unsigned)std::min<size_t>(((size_t)std::max(N, K) + 255) / 256, 1024);
     lora_prep_kernel<<<dim3(bx, rp + 1), 256, 0, stream>>>(lora_a, lora_b, K, N, rank, rp_shift, a16, bt16);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped, int rank,
+                              float scaling, const void* lora_scratch, int n_begin, int n_end, uint16_t* wt,
+                              hipStream_t stream) {
+  if (!expand_supported(K, N, rank) || (rank > 0 && !lora_scratch) || n_begin < 0 || n_end > N ||
+      n_begin % kTile != 0 || n_end % kTile != 0 || n_begin >= n_end)
+    return hipErrorInvalidValue;
+  const int rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
+  const uint16_t* a16 = static_cast<const uint16_t*>(lora_scratch);
+  const uint16_t* bt16 = a16 ? a16 + (size_t)K * rp : nullptr;
   ExpandArgs a{};
   a.packed = packed;
   a.scales = scales;
@@ -254,16 +273,18 @@ hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, in
   a.scaling = scaling;
   a.wt = wt;
   a.tiles_k = K / kTile;
-  const long long tiles = (long long)(K / kTile) * (N / kTile);
+  a.n_base = n_begin;
+  const int nc = n_end - n_begin;
+  const long long tiles = (long long)(K / kTile) * (nc / kTile);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const bool dq = scales.kind == kScalesDQ;
   const bool lora = rank > 0;
   if (dq) {
-    if (striped) return lora ? launch_t<true, true, true>(a, stream) : launch_t<true, true, false>(a, stream);
-    return lora ? launch_t<true, false, true>(a, stream) : launch_t<true, false, false>(a, stream);
+    if (striped) return lora ? launch_t<true, true, true>(a, nc, stream) : launch_t<true, true, false>(a, nc, stream);
+    return lora ? launch_t<true, false, true>(a, nc, stream) : launch_t<true, false, false>(a, nc, stream);
   }
-  if (striped) return lora ? launch_t<false, true, true>(a, stream) : launch_t<false, true, false>(a, stream);
-  return lora ? launch_t<false, false, true>(a, stream) : launch_t<false, false, false>(a, stream);
+  if (striped) return lora ? launch_t<false, true, true>(a, nc, stream) : launch_t<false, true, false>(a, nc, stream);
+  return lora ? launch_t<false, false, true>(a, nc, stream) : launch_t<false, false, false>(a, nc, stream);
 }
 
 }  // namespace unifur

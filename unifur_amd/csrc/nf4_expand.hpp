@@ -13,6 +13,13 @@ bool expand_supported(int K, int N, int rank);
 // scaling * A B when rank > 0 (A f32 [K][rank], B f32 [rank][N]); the
 // adapter's bf16 operands go to lora_scratch (expand_lora_scratch_bytes).
 size_t expand_lora_scratch_bytes(int K, int N, int rank);
+// The two halves of launch_expand_bf16: the adapter's bf16 operands into
+// lora_scratch, then the columns [n_begin, n_end) (multiples of 64) of Wt.
+hipError_t launch_expand_prep(int K, int N, const float* lora_a, const float* lora_b, int rank, void* lora_scratch,
+                              hipStream_t stream);
+hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped, int rank,
+                              float scaling, const void* lora_scratch, int n_begin, int n_end, uint16_t* wt,
+                              hipStream_t stream);
 hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
                               const float* lora_a, const float* lora_b, int rank, float scaling, void* lora_scratch,
                               uint16_t* wt, hipStream_t stream);
@@ -27,6 +34,9 @@ constexpr size_t kBlasWorkspace = 32u << 20;
 // library's first candidate without caching it.
 hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
                          bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream);
+// The same product into columns of a wider Y (row stride ldy >= N elements).
+hipError_t blas_gemm_xwt_ld(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
+                            int ldy, bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream);
 
 // dX[M][K] = dY[M][N] Wt[N][K] (the backward of the product above with
 // respect to X), bf16 operands, dX f32 or bf16; same kernel choice rule.
