@@ -407,13 +407,26 @@ def bench_backward(torch, Q, L) -> dict:
                                                gb.data_ptr(), ws.data_ptr(), ws_bytes,
                                                torch.cuda.current_stream().cuda_stream))
 
-    for i in range(3):
-        step(i)
-    graph = capture(torch, step, 4)
-    ms = graph_ms(torch, graph, 10) / 4 if graph is not None else event_ms(torch, step, 8)
+    def grads_only(i: int) -> None:
+        L.check(lib.unifur_nf4_linear_backward(dy.data_ptr(), L.BF16, M, ctypes.byref(w), ctypes.byref(lo),
+                                               x.data_ptr(), L.BF16, None, L.BF16, ga.data_ptr(),
+                                               gb.data_ptr(), ws.data_ptr(), ws_bytes,
+                                               torch.cuda.current_stream().cuda_stream))
+
+    res = {}
+    for name, fn in (("ms", step), ("grads_only_ms", grads_only)):
+        for i in range(3):
+            fn(i)
+        graph = capture(torch, fn, 4)
+        res[name] = graph_ms(torch, graph, 10) / 4 if graph is not None else event_ms(torch, fn, 8)
+    ms = res["ms"]
     flops = 2 * M * N * K + 2 * K * r * N + 4 * M * r * (K + N)
+    # the adapter gradients read x and dy twice each (bf16)
+    grads_bytes = 2 * 2 * M * (K + N)
     return {"ms": round(ms, 5), "tflops": round(flops / ms / 1e9, 1),
-            "frac": round(flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+            "frac": round(flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
+            "grads_only_ms": round(res["grads_only_ms"], 5),
+            "grads_only_gbs": round(grads_bytes / res["grads_only_ms"] / 1e6, 1)}
 
 
 # ------------------------------------------------------ next: embedding ----

@@ -63,6 +63,8 @@ def refs(x, dy, wdeq, a, b, s):
     (5, 1024, 128, 64, torch.bfloat16, torch.bfloat16, True, False),
     (129, 896, 4864, 16, torch.bfloat16, torch.bfloat16, True, True),
     (64, 100, 70, 3, torch.float32, torch.float32, False, True),  # ragged: generic path, d_out % 64 != 0
+    (257, 1024, 512, 32, torch.bfloat16, torch.float32, True, True),  # rank bucket 32, mixed input types
+    (16384, 256, 136, 16, torch.bfloat16, torch.bfloat16, False, True),  # unsplit row products, 32 row slabs
 ])
 def test_qlora_backward(device, oracle, case):
     M, K, N, r, dyt, xt_dtype, striped, dq = case

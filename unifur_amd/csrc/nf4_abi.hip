@@ -13,6 +13,7 @@
 #include <utility>
 
 #include "../../include/unifur_nf4.h"
+#include "nf4_adapter_grad.hpp"
 #include "nf4_codec.hpp"
 #include "nf4_embedding.hpp"
 #include "nf4_expand.hpp"
@@ -645,7 +646,7 @@ uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate,
 // x A, dY B^T and two row reductions.
 struct BackwardLayout {
   bool blas;
-  size_t wt, blas_ws, lora_ops, wf32, rm_codes, rm_scales, xa, u, partials, total;
+  size_t wt, blas_ws, lora_ops, wf32, rm_codes, rm_scales, grads, xa, u, partials, total;
 };
 
 BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t rank, int dy_dtype, bool want_dx,
@@ -668,13 +669,21 @@ BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint3
     }
   }
   if (want_grads && rank) {
-    L.xa = c.take((size_t)rows * rank * sizeof(float));
-    L.u = c.take((size_t)rows * rank * sizeof(float));
+    // one region for the MFMA kernels' scratch or, for operands they do not
+    // take, the narrow kernels' x A, dY B^T and slab partials
     const int m = (int)std::min<uint64_t>(rows, 0x7fffffffu);
     const int k = (int)std::min<uint64_t>(d_in, 0x7fffffffu), n = (int)std::min<uint64_t>(d_out, 0x7fffffffu);
+    Carver g;
+    g.off = 0;
+    L.xa = g.take((size_t)rows * rank * sizeof(float));
+    L.u = g.take((size_t)rows * rank * sizeof(float));
     const size_t p_mm = (size_t)std::max(narrow_mm_slabs(m, k), narrow_mm_slabs(m, n)) * rows * rank;
     const size_t p_atb = std::max((size_t)narrow_atb_slabs(m, n) * d_out, (size_t)narrow_atb_slabs(m, k) * d_in) * rank;
-    L.partials = c.take(std::max(p_mm, p_atb) * sizeof(float));
+    L.partials = g.take(std::max(p_mm, p_atb) * sizeof(float));
+    L.grads = c.take(std::max<size_t>(g.off, adapter_grads_scratch_bytes(m, k, n, (int)rank)));
+    L.xa += L.grads;
+    L.u += L.grads;
+    L.partials += L.grads;
   }
   L.total = c.off;
   return L;
@@ -729,7 +738,11 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       UNIFUR_HIP(launch_gemm_f32_wt(dy, dybf, wf, m, n, k, e, stream));
     }
   }
-  if (want_grads) {
+  if (want_grads && adapter_grads_supported(x, dy, lora->b, m, k, n, (int)rank)) {
+    UNIFUR_HIP(launch_adapter_grads(x, xbf, dy, dybf, lora->a, lora->b, m, k, n, (int)rank, lora->scaling, grad_a,
+                                    grad_b, at<void>(ws, L.grads), static_cast<unsigned*>(ws), kMaxCounters,
+                                    stream));
+  } else if (want_grads) {
     float* xa = at<float>(ws, L.xa);
     float* u = at<float>(ws, L.u);
     float* part = at<float>(ws, L.partials);

@@ -51,4 +51,22 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t a, uint32_t b, uint32_t se
   return __builtin_amdgcn_perm(a, b, sel);
 }
 
+// Split-K hand-off between workgroups.  Partial sums are written with
+// agent-scope atomic stores (coherent across the XCDs' L2s) and the writer
+// waits for them to complete before it counts itself in; the last arrival
+// reads them back with agent-scope atomic loads.  This is the release /
+// acquire sequence of the AMDGPU memory model for agent scope without its
+// L2 write-back and invalidate, which only non-atomic data would need.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_all_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt = expcnt = lgkmcnt = 0: every store acknowledged
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 }  // namespace unifur

@@ -68,24 +68,6 @@ typedef __attribute__((address_space(3))) const f32x2 lds_f32x2;
 
 __device__ __forceinline__ float silu_f32(float z) { return z * (1.0f / (1.0f + __expf(-z))); }
 
-// Split-K hand-off between workgroups.  Partial sums are written with
-// agent-scope atomic stores (coherent across the XCDs' L2s) and the writer
-// waits for them to complete before it counts itself in; the last arrival
-// reads them back with agent-scope atomic loads.  This is the release /
-// acquire sequence of the AMDGPU memory model for agent scope without its
-// L2 write-back and invalidate, which only non-atomic data would need.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_all_memory() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);  // vmcnt = expcnt = lgkmcnt = 0: every store acknowledged
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // One weight's loads for this thread: RT rows of 16 code bytes and a scale.
 template <int RT>
 struct RowLoads {

@@ -427,22 +427,6 @@ hipError_t dispatch_w(const StripedArgs& a, int grid, int waves, bool xbf16, boo
 typedef int v2i32 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i32 lds_v2i32;
 
-// Split-d_in hand-off: partial sums are written with agent-scope atomic
-// stores (coherent across the XCDs' L2s) and the writer waits for them to
-// complete before it counts itself in; the last arrival reads them back with
-// agent-scope atomic loads (release / acquire at agent scope without the L2
-// write-back and invalidate that only non-atomic data would need).
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_all_memory() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);  // vmcnt = expcnt = lgkmcnt = 0: every store acknowledged
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2_w;
 
 constexpr int kSkStageOffset = kStripedSmem;  // after the level and DQ LUTs
