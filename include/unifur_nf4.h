@@ -16,8 +16,15 @@
  *   - Return value: UNIFUR_NF4_OK (0) or a negative status; the message of the
  *     last failure on the calling thread is unifur_nf4_last_error().
  *   - The library holds no global mutable state except an optional internal
- *     workspace cache (used only when a call passes workspace == NULL),
- *     guarded by a mutex and keyed by (device, stream).
+ *     workspace cache (used only when a call passes workspace == NULL) and
+ *     the branch streams below, each guarded by a mutex and keyed by
+ *     (device, stream).
+ *   - A call may run part of its work on a library-owned branch stream
+ *     (default priority), forked from `stream` and joined back into it with
+ *     events before the call's last launch on `stream`: the call stays
+ *     ordered on `stream`, and a graph capture of `stream` records the fork
+ *     and the join.  The branch is created on the first such call outside
+ *     capture; under capture without one the work stays on `stream`.
  *   - Layout of a quantized tensor of `len` values (src/quantize.rs:221-257):
  *     ceil(len/64) blocks of 64 consecutive values; `packed` holds
  *     ceil(len/2) bytes, value 2i in the low nibble of byte i; scales are one
@@ -233,7 +240,8 @@ int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const un
  * src/quantize.rs:619-624) and of the base product.  bf16 dy goes through
  * the weight expanded to bf16 (with the adapter merged) and a BLAS GEMM;
  * f32 dy through the f32 dequantized weight.  The adapter gradients are
- * summed over the rows in a fixed order (deterministic). */
+ * summed over the rows in a fixed order (deterministic); when dx takes the
+ * BLAS path they run on the branch stream beside its GEMM. */
 uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
                                                    uint32_t lora_rank);
 int unifur_nf4_linear_backward(const void *dy, int dy_dtype, uint64_t rows, const unifur_nf4_weight *w,

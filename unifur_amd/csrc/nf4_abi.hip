@@ -639,6 +639,50 @@ uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate,
 }
 
 
+// -------------------------------------------------------- concurrent branch --
+
+// A second stream per (device, caller stream) for work that is independent of
+// the caller stream's next launches: forked from the caller stream and joined
+// back into it with events, which a graph capture records as a fork and a
+// join.  It is created on first use outside capture; a call under capture
+// that finds none runs everything on the caller stream.  Default priority,
+// like every stream here.
+struct Branch {
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+struct BranchCache {
+  std::mutex mu;
+  std::map<std::pair<int, hipStream_t>, Branch> branches;
+};
+
+BranchCache& branch_cache() {
+  static BranchCache* c = new BranchCache();  // never destroyed, like the workspaces
+  return *c;
+}
+
+Branch branch_for(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return {};
+  BranchCache& c = branch_cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  const auto it = c.branches.find({dev, stream});
+  if (it != c.branches.end()) return it->second;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return {};
+  Branch b;
+  if (hipStreamCreateWithFlags(&b.side, hipStreamNonBlocking) != hipSuccess) return {};
+  if (hipEventCreateWithFlags(&b.fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&b.join, hipEventDisableTiming) != hipSuccess) {
+    if (b.fork) (void)hipEventDestroy(b.fork);
+    (void)hipStreamDestroy(b.side);
+    return {};
+  }
+  c.branches[{dev, stream}] = b;
+  return b;
+}
+
 // ------------------------------------------------------------ backward -----
 
 // dX through the expanded bf16 weight and the BLAS GEMM (bf16 dY), or the
@@ -715,15 +759,43 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool dybf = dy_dtype == UNIFUR_NF4_BF16, xbf = x_dtype == UNIFUR_NF4_BF16;
   const int m = (int)rows, k = (int)K, n = (int)N;
+  const bool mfma_grads = want_grads && adapter_grads_supported(x, dy, lora->b, m, k, n, (int)rank);
+  const auto grads_on = [&](hipStream_t s) -> hipError_t {
+    return launch_adapter_grads(x, xbf, dy, dybf, lora->a, lora->b, m, k, n, (int)rank, lora->scaling, grad_a,
+                                grad_b, at<void>(ws, L.grads), static_cast<unsigned*>(ws), kMaxCounters, s);
+  };
+  // With both dX (expand + BLAS GEMM) and the MFMA adapter gradients to do,
+  // the gradients run on a branch stream beside the dX GEMM: they read x and
+  // dY and write their own scratch, counters and outputs, disjoint from dX's.
+  bool grads_done = false;
   if (want_dx && rows > 0) {
     // dX = dY (W + scaling A B)^T = dY W^T + ((dY scaling) B^T) A^T
     if (L.blas) {
       uint16_t* wt = at<uint16_t>(ws, L.wt);
-      UNIFUR_HIP(launch_expand_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w), lora ? lora->a : nullptr,
-                                    lora ? lora->b : nullptr, (int)rank, lora ? lora->scaling : 0.0f,
-                                    at<void>(ws, L.lora_ops), wt, stream));
-      UNIFUR_HIP(blas_gemm_dyw(static_cast<const uint16_t*>(dy), wt, m, n, k, dx, dx_dtype == UNIFUR_NF4_BF16,
-                               at<void>(ws, L.blas_ws), kBlasWorkspace, stream));
+      const Branch br = mfma_grads ? branch_for(stream) : Branch{};
+      bool forked = false;
+      const auto fork = [&]() -> hipError_t {
+        hipError_t e = hipEventRecord(br.fork, stream);
+        if (e != hipSuccess) return e;
+        if ((e = hipStreamWaitEvent(br.side, br.fork, 0)) != hipSuccess) return e;
+        forked = true;
+        e = grads_on(br.side);
+        const hipError_t j = hipEventRecord(br.join, br.side);  // recorded even when the launch failed
+        return e != hipSuccess ? e : j;
+      };
+      hipError_t e = launch_expand_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w),
+                                        lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
+                                        lora ? lora->scaling : 0.0f, at<void>(ws, L.lora_ops), wt, stream);
+      if (e == hipSuccess && br.side) e = fork();  // the gradients beside the GEMM, not the memory-bound expand
+      if (e == hipSuccess)
+        e = blas_gemm_dyw(static_cast<const uint16_t*>(dy), wt, m, n, k, dx, dx_dtype == UNIFUR_NF4_BF16,
+                          at<void>(ws, L.blas_ws), kBlasWorkspace, stream);
+      if (forked) {  // every exit after a fork joins it first
+        const hipError_t jn = hipStreamWaitEvent(stream, br.join, 0);
+        if (e == hipSuccess) e = jn;
+      }
+      grads_done = forked;
+      UNIFUR_HIP(e);
     } else {
       const uint8_t* packed = nullptr;
       ScalesArg scales{};
@@ -738,10 +810,8 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       UNIFUR_HIP(launch_gemm_f32_wt(dy, dybf, wf, m, n, k, e, stream));
     }
   }
-  if (want_grads && adapter_grads_supported(x, dy, lora->b, m, k, n, (int)rank)) {
-    UNIFUR_HIP(launch_adapter_grads(x, xbf, dy, dybf, lora->a, lora->b, m, k, n, (int)rank, lora->scaling, grad_a,
-                                    grad_b, at<void>(ws, L.grads), static_cast<unsigned*>(ws), kMaxCounters,
-                                    stream));
+  if (mfma_grads) {
+    if (!grads_done) UNIFUR_HIP(grads_on(stream));
   } else if (want_grads) {
     float* xa = at<float>(ws, L.xa);
     float* u = at<float>(ws, L.u);
