@@ -176,23 +176,28 @@ size_t expand_smem(int KT, bool lora) {
 }
 
 // a16[k][r] = bf16(a[k][r]) and bt16[n][r] = bf16(b[r][n]), zero for r >= rank
-// (rp = 1 << rp_shift): blockIdx.y < rp transposes row r = blockIdx.y of b
-// (coalesced reads along n); blockIdx.y == rp copies a.
-__global__ void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b, int K, int N, int rank,
-                                 int rp_shift, uint16_t* __restrict__ a16, uint16_t* __restrict__ bt16) {
-  const int rp = 1 << rp_shift;
-  const int r = blockIdx.y;
-  if (r < rp) {
-    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < N; n += gridDim.x * blockDim.x)
-      bt16[((size_t)n << rp_shift) + r] = (uint16_t)(pack_bf16x2(r < rank ? b[(size_t)r * N + n] : 0.0f, 0.0f) & 0xffffu);
-    return;
+// (rp = 1 << rp_shift).
+__global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                        int K, int N, int rank, int rp_shift,
+                                                        uint16_t* __restrict__ a16, uint16_t* __restrict__ bt16) {
+  // one thread per 8 consecutive entries of a row of a16 [K][rp] or
+  // bt16 [N][rp]: its eight loads are issued together and it stores 16 bytes
+  const int rp = 1 << rp_shift, oct = rp / 8;
+  const size_t na = (size_t)K * oct, nt = na + (size_t)N * oct;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nt) return;
+  const bool is_a = i < na;
+  const size_t row = is_a ? i / oct : (i - na) / oct;
+  const int r0 = (int)((is_a ? i : i - na) % oct) * 8;
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int r = r0 + e;
+    v[e] = r < rank ? (is_a ? a[row * rank + r] : b[(size_t)r * N + row]) : 0.0f;
   }
-  const size_t total = (size_t)K << rp_shift;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int rr = (int)(i & (size_t)(rp - 1));
-    const size_t k = i >> rp_shift;
-    a16[i] = (uint16_t)(pack_bf16x2(rr < rank ? a[k * rank + rr] : 0.0f, 0.0f) & 0xffffu);
-  }
+  uint16_t* dst = (is_a ? a16 : bt16) + (row << rp_shift) + r0;
+  *reinterpret_cast<u32x4*>(dst) =
+      u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
 }
 
 template <bool DQ, bool STRIPED, bool LORA>
@@ -246,8 +251,9 @@ hipError_t launch_expand_prep(int K, int N, const float* lora_a, const float* lo
   uint16_t* bt16 = a16 + (size_t)K * rp;
   {
     const int rp_shift = rp == 16 ? 4 : rp == 32 ? 5 : 6;
-    const unsigned bx = (unsigned)std::min<size_t>(((size_t)std::max(N, K) + 255) / 256, 1024);
-    lora_prep_kernel<<<dim3(bx, rp + 1), 256, 0, stream>>>(lora_a, lora_b, K, N, rank, rp_shift, a16, bt16);
+    const size_t threads = ((size_t)K + (size_t)N) * (size_t)(rp / 8);
+    lora_prep_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(lora_a, lora_b, K, N, rank, rp_shift,
+                                                                            a16, bt16);
   }
   return hipGetLastError();
 }
