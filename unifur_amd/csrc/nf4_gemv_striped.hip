@@ -676,22 +676,43 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
     __syncthreads();
     if (!*is_last) return;
     if (mine) {
+      // the partials of U slabs are all loaded before any of them is added
+      // (the sum keeps slab order), so the hand-off costs one memory latency
+      // per U slabs rather than one per slab
+      constexpr int kVals = NT * S * NW;
+      constexpr int U = kVals <= 8 ? 4 : kVals <= 16 ? 2 : 1;
+      const size_t stride = (size_t)a.rows * G.d_out;
 #pragma unroll
-      for (int tt = 0; tt < NT; ++tt) {
-        const int t = 16 * tt + t_l;
-        if (t >= a.rows) continue;
+      for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-        for (int i = 0; i < S; ++i) {
-          const size_t idx = (size_t)t * G.d_out + (s0 + i) * kStripeCols + cc;
-          const size_t stride = (size_t)a.rows * G.d_out;
+        for (int i = 0; i < S; ++i)
 #pragma unroll
-          for (int w = 0; w < NW; ++w) {
-            const float* part = a.w[PAIR ? w : wi].partials + idx;
-            float v = 0.0f;
-            for (int q = 0; q < P; ++q) v += load_coherent(part + q * stride);
-            sums[w][i][tt] = v;
-          }
-        }
+          for (int w = 0; w < NW; ++w) sums[w][i][tt] = 0.0f;
+      for (int q0 = 0; q0 < P; q0 += U) {
+        float pv[U][NT][S][NW];
+#pragma unroll
+        for (int dq = 0; dq < U; ++dq)
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int i = 0; i < S; ++i)
+#pragma unroll
+              for (int w = 0; w < NW; ++w) {
+                const int t = 16 * tt + t_l;
+                const size_t idx = (size_t)t * G.d_out + (s0 + i) * kStripeCols + cc;
+                pv[dq][tt][i][w] = (q0 + dq < P && t < a.rows)
+                                       ? load_coherent(a.w[PAIR ? w : wi].partials + idx + (q0 + dq) * stride)
+                                       : 0.0f;
+              }
+#pragma unroll
+        for (int dq = 0; dq < U; ++dq)
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int i = 0; i < S; ++i)
+#pragma unroll
+              for (int w = 0; w < NW; ++w)
+                if (q0 + dq < P) sums[w][i][tt] += pv[dq][tt][i][w];
       }
     }
     if (tid == 0) __hip_atomic_store(&G.counters[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
