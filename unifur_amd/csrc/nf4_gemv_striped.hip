@@ -847,6 +847,22 @@ StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool
   // microseconds of latency, which only a long d_in repays.
   const int g = (pair && tiles > 1) ? 2 : 4;
   int group = 1, splits = 1;
+  if (tiles == 1 && chunks >= 64) {
+    // one token tile over a long d_in: two stripes per wave and d_in slabs
+    // up to ~512 four-wave workgroups (measured on the 7B-shaped MLP at 16
+    // tokens: the gate/up pair 21.4 us against 24.1 us as 172 eight-wave
+    // workgroups of four stripes; the down projection 13.6 us either way)
+    group = 2;
+    while ((stripes / group) * splits < 512 && chunks / (splits * 2) >= 32) splits *= 2;
+    p.group = group;
+    p.waves = 4;
+    p.splits = splits;
+    const int cps = (chunks + splits - 1) / splits;
+    p.rows_per_wave = (cps + 3) / 4 * 64;
+    p.rows_per_split = p.rows_per_wave * 4;
+    p.stripes = stripes;
+    return p;
+  }
   if (stripes / g >= 160) {
     group = g;
   } else if (chunks >= 64) {
