@@ -182,7 +182,7 @@ struct LinearLayout {
   bool expand;  // kMfma: bf16 weight expanded in the workspace + BLAS GEMM (else the fused kernel)
   GemvPlan gemv;
   StripedPlan striped;
-  size_t partials, xa, lora_at, lora_bt, wt, blas, lora_ops, wf32, rm_codes, rm_scales, total;
+  size_t partials, xa, lora_at, lora_bt, wt, blas, wf32, rm_codes, rm_scales, total;
 };
 
 // Decode-sized batches (<= 4 rows) take a GEMV (the striped one for striped
@@ -224,7 +224,6 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
     if (L.expand) {
       L.wt = c.take(d_in * d_out * sizeof(uint16_t));
       L.blas = c.take(kBlasWorkspace);
-      L.lora_ops = c.take(expand_lora_scratch_bytes((int)d_in, (int)d_out, (int)lora_rank));
     }
   } else {
     L.path = LinearPath::kGeneric;
@@ -318,7 +317,7 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     uint16_t* wt = at<uint16_t>(ws, L.wt);
     UNIFUR_HIP(launch_expand_bf16(w->packed, to_scales(w->scales), (int)w->d_in, (int)w->d_out, is_striped(w),
                                   lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
-                                  lora ? lora->scaling : 0.0f, at<void>(ws, L.lora_ops), wt, stream));
+                                  lora ? lora->scaling : 0.0f, wt, stream));
     UNIFUR_HIP(blas_gemm_xwt(static_cast<const uint16_t*>(x), wt, bias, (int)rows, (int)w->d_out, (int)w->d_in, y,
                              ybf, at<void>(ws, L.blas), kBlasWorkspace, stream));
     return UNIFUR_NF4_OK;
@@ -569,13 +568,13 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
         void* bw = at<void>(ws, L.blas);
         const int hd = (int)hidden, in = (int)inter, m = (int)rows;
         UNIFUR_HIP(launch_expand_bf16(gate->packed, to_scales(gate->scales), hd, in, is_striped(gate), nullptr,
-                                      nullptr, 0, 0.0f, nullptr, wt, stream));
+                                      nullptr, 0, 0.0f, wt, stream));
         UNIFUR_HIP(launch_expand_bf16(up->packed, to_scales(up->scales), hd, in, is_striped(up), nullptr, nullptr, 0,
-                                      0.0f, nullptr, wt + (size_t)in * hd, stream));
+                                      0.0f, wt + (size_t)in * hd, stream));
         UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, 2 * in, hd, gu, true, bw, kBlasWorkspace, stream));
         UNIFUR_HIP(launch_silu_mul_rows_bf16(gu, (size_t)rows, (size_t)inter, hb, stream));
         UNIFUR_HIP(launch_expand_bf16(down->packed, to_scales(down->scales), in, hd, is_striped(down), nullptr,
-                                      nullptr, 0, 0.0f, nullptr, wt, stream));
+                                      nullptr, 0, 0.0f, wt, stream));
         UNIFUR_HIP(blas_gemm_xwt(hb, wt, nullptr, m, hd, in, y, ybf, bw, kBlasWorkspace, stream));
         return UNIFUR_NF4_OK;
       }
@@ -690,7 +689,7 @@ Branch branch_for(hipStream_t stream) {
 // x A, dY B^T and two row reductions.
 struct BackwardLayout {
   bool blas;
-  size_t wt, blas_ws, lora_ops, wf32, rm_codes, rm_scales, grads, xa, u, partials, total;
+  size_t wt, blas_ws, wf32, rm_codes, rm_scales, grads, xa, u, partials, total;
 };
 
 BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t rank, int dy_dtype, bool want_dx,
@@ -703,7 +702,6 @@ BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint3
     if (L.blas) {
       L.wt = c.take(d_in * d_out * sizeof(uint16_t));
       L.blas_ws = c.take(kBlasWorkspace);
-      L.lora_ops = c.take(expand_lora_scratch_bytes((int)d_in, (int)d_out, (int)rank));
     } else {
       L.wf32 = c.take(d_in * d_out * sizeof(float));
       if (striped) {
@@ -785,7 +783,7 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       };
       hipError_t e = launch_expand_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w),
                                         lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
-                                        lora ? lora->scaling : 0.0f, at<void>(ws, L.lora_ops), wt, stream);
+                                        lora ? lora->scaling : 0.0f, wt, stream);
       if (e == hipSuccess && br.side) e = fork();  // the gradients beside the GEMM, not the memory-bound expand
       if (e == hipSuccess)
         e = blas_gemm_dyw(static_cast<const uint16_t*>(dy), wt, m, n, k, dx, dx_dtype == UNIFUR_NF4_BF16,

@@ -40,8 +40,9 @@ struct ExpandArgs {
   const uint8_t* packed;
   ScalesArg scales;
   int K, N;
-  const uint16_t* a16;   // bf16 A [K][rp], zero past the rank (lora_prep_kernel)
-  const uint16_t* bt16;  // bf16 B transposed [N][rp]
+  const float* la;  // A f32 [K][rank]
+  const float* lb;  // B f32 [rank][N]
+  int la_vec;       // rank % 8 == 0 and A 16-byte aligned: fragments of A in two 16-byte loads
   int rank, rp;
   float scaling;
   uint16_t* wt;  // [N][K]
@@ -89,9 +90,10 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 
   float* lut = reinterpret_cast<float*>(smem + kLdsLut);
   if (tid < 16) lut[tid] = level(tid);
-  // LoRA: the MFMA fragments straight from the prepared bf16 operands (one
-  // 16-byte load each, issued with the code loads); the f32 product tile
-  // C [64][68] after the transpose tiles
+  // LoRA: the MFMA fragments straight from the f32 factors, issued with the
+  // code loads and rounded to bf16 in registers (A: eight consecutive values
+  // of a row; B^T: eight rows of a column, coalesced across the lanes); the
+  // f32 product tile C [64][68] after the transpose tiles
   const int lane = tid & 63, wv = tid >> 6, bi = wv >> 1, bj = wv & 1, h = lane >> 5;
   const int lds_c = kLdsT + KT * kTBytes;
   // adapter fragments per tile: up to rank 64 in the one-tile kernel, rank
@@ -104,11 +106,36 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 #pragma unroll
     for (int f = 0; f < kMaxFr; ++f) {
       if (f >= nf) break;
-      bfr[f] = *reinterpret_cast<const bf16x8_t*>(a.bt16 + (size_t)(n0 + 32 * bj + (lane & 31)) * a.rp + 16 * f + 8 * h);
+      const int r0 = 16 * f + 8 * h;  // this lane's eight adapter indices
+      const size_t col = (size_t)(n0 + 32 * bj + (lane & 31));
+      float bv[8];
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
-        afr[t][f] = *reinterpret_cast<const bf16x8_t*>(
-            a.a16 + (size_t)(k0 + kTile * t + 32 * bi + (lane & 31)) * a.rp + 16 * f + 8 * h);
+      for (int e = 0; e < 8; ++e) bv[e] = r0 + e < a.rank ? a.lb[(size_t)(r0 + e) * a.N + col] : 0.0f;
+      bfr[f] = __builtin_bit_cast(bf16x8_t, u32x4{pack_bf16x2(bv[0], bv[1]), pack_bf16x2(bv[2], bv[3]),
+                                                  pack_bf16x2(bv[4], bv[5]), pack_bf16x2(bv[6], bv[7])});
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const size_t row = (size_t)(k0 + kTile * t + 32 * bi + (lane & 31));
+        float av[8];
+        if (a.la_vec) {
+          f32x4 lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = lo;
+          if (r0 < a.rank) {
+            const f32x4* src = reinterpret_cast<const f32x4*>(a.la + row * a.rank + r0);
+            lo = src[0];
+            hi = src[1];
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            av[e] = lo[e];
+            av[4 + e] = hi[e];
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) av[e] = r0 + e < a.rank ? a.la[row * a.rank + r0 + e] : 0.0f;
+        }
+        afr[t][f] = __builtin_bit_cast(bf16x8_t, u32x4{pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]),
+                                                       pack_bf16x2(av[4], av[5]), pack_bf16x2(av[6], av[7])});
+      }
     }
   }
   __syncthreads();
@@ -175,31 +202,6 @@ size_t expand_smem(int KT, bool lora) {
   return kLdsT + (size_t)KT * kTBytes + (lora ? (size_t)kTile * kCStride * 4 : 0);
 }
 
-// a16[k][r] = bf16(a[k][r]) and bt16[n][r] = bf16(b[r][n]), zero for r >= rank
-// (rp = 1 << rp_shift).
-__global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b,
-                                                        int K, int N, int rank, int rp_shift,
-                                                        uint16_t* __restrict__ a16, uint16_t* __restrict__ bt16) {
-  // one thread per 8 consecutive entries of a row of a16 [K][rp] or
-  // bt16 [N][rp]: its eight loads are issued together and it stores 16 bytes
-  const int rp = 1 << rp_shift, oct = rp / 8;
-  const size_t na = (size_t)K * oct, nt = na + (size_t)N * oct;
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= nt) return;
-  const bool is_a = i < na;
-  const size_t row = is_a ? i / oct : (i - na) / oct;
-  const int r0 = (int)((is_a ? i : i - na) % oct) * 8;
-  float v[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int r = r0 + e;
-    v[e] = r < rank ? (is_a ? a[row * rank + r] : b[(size_t)r * N + row]) : 0.0f;
-  }
-  uint16_t* dst = (is_a ? a16 : bt16) + (row << rp_shift) + r0;
-  *reinterpret_cast<u32x4*>(dst) =
-      u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
-}
-
 template <bool DQ, bool STRIPED, bool LORA>
 hipError_t launch_t(const ExpandArgs& a, int n_count, hipStream_t stream) {
   const long long band = n_count / kTile;
@@ -227,53 +229,28 @@ bool expand_supported(int K, int N, int rank) {
   return K > 0 && N > 0 && K % kTile == 0 && N % kTile == 0 && rank >= 0 && rank <= kMaxRank;
 }
 
-size_t expand_lora_scratch_bytes(int K, int N, int rank) {
-  if (rank <= 0) return 0;
-  const size_t rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
-  return ((size_t)K + N) * rp * sizeof(uint16_t);
-}
 
 hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
-                              const float* lora_a, const float* lora_b, int rank, float scaling, void* lora_scratch,
+                              const float* lora_a, const float* lora_b, int rank, float scaling, uint16_t* wt,
+                              hipStream_t stream) {
+  return launch_expand_cols(packed, scales, K, N, striped, lora_a, lora_b, rank, scaling, 0, N, wt, stream);
+}
+
+hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
+                              const float* lora_a, const float* lora_b, int rank, float scaling, int n_begin, int n_end,
                               uint16_t* wt, hipStream_t stream) {
-  if (rank > 0) {
-    const hipError_t e = launch_expand_prep(K, N, lora_a, lora_b, rank, lora_scratch, stream);
-    if (e != hipSuccess) return e;
-  }
-  return launch_expand_cols(packed, scales, K, N, striped, rank, scaling, lora_scratch, 0, N, wt, stream);
-}
-
-hipError_t launch_expand_prep(int K, int N, const float* lora_a, const float* lora_b, int rank, void* lora_scratch,
-                              hipStream_t stream) {
-  if (!expand_supported(K, N, rank) || rank <= 0 || !lora_a || !lora_b || !lora_scratch) return hipErrorInvalidValue;
-  const int rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
-  uint16_t* a16 = static_cast<uint16_t*>(lora_scratch);
-  uint16_t* bt16 = a16 + (size_t)K * rp;
-  {
-    const int rp_shift = rp == 16 ? 4 : rp == 32 ? 5 : 6;
-    const size_t threads = ((size_t)K + (size_t)N) * (size_t)(rp / 8);
-    lora_prep_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(lora_a, lora_b, K, N, rank, rp_shift,
-                                                                            a16, bt16);
-  }
-  return hipGetLastError();
-}
-
-hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped, int rank,
-                              float scaling, const void* lora_scratch, int n_begin, int n_end, uint16_t* wt,
-                              hipStream_t stream) {
-  if (!expand_supported(K, N, rank) || (rank > 0 && !lora_scratch) || n_begin < 0 || n_end > N ||
+  if (!expand_supported(K, N, rank) || (rank > 0 && (!lora_a || !lora_b)) || n_begin < 0 || n_end > N ||
       n_begin % kTile != 0 || n_end % kTile != 0 || n_begin >= n_end)
     return hipErrorInvalidValue;
   const int rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
-  const uint16_t* a16 = static_cast<const uint16_t*>(lora_scratch);
-  const uint16_t* bt16 = a16 ? a16 + (size_t)K * rp : nullptr;
   ExpandArgs a{};
   a.packed = packed;
   a.scales = scales;
   a.K = K;
   a.N = N;
-  a.a16 = a16;
-  a.bt16 = bt16;
+  a.la = lora_a;
+  a.lb = lora_b;
+  a.la_vec = rank % 8 == 0 && (reinterpret_cast<uintptr_t>(lora_a) & 15u) == 0;
   a.rank = rank;
   a.rp = rp;
   a.scaling = scaling;

@@ -10,18 +10,14 @@ namespace unifur {
 bool expand_supported(int K, int N, int rank);
 
 // Wt[N][K] bf16 = the dequantized weight (row-major or striped layout) plus
-// scaling * A B when rank > 0 (A f32 [K][rank], B f32 [rank][N]); the
-// adapter's bf16 operands go to lora_scratch (expand_lora_scratch_bytes).
-size_t expand_lora_scratch_bytes(int K, int N, int rank);
-// The two halves of launch_expand_bf16: the adapter's bf16 operands into
-// lora_scratch, then the columns [n_begin, n_end) (multiples of 64) of Wt.
-hipError_t launch_expand_prep(int K, int N, const float* lora_a, const float* lora_b, int rank, void* lora_scratch,
-                              hipStream_t stream);
-hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped, int rank,
-                              float scaling, const void* lora_scratch, int n_begin, int n_end, uint16_t* wt,
-                              hipStream_t stream);
+// scaling * A B when rank > 0 (A f32 [K][rank], B f32 [rank][N], read by the
+// kernel itself and rounded to bf16 for its MFMAs).
 hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
-                              const float* lora_a, const float* lora_b, int rank, float scaling, void* lora_scratch,
+                              const float* lora_a, const float* lora_b, int rank, float scaling, uint16_t* wt,
+                              hipStream_t stream);
+// The columns [n_begin, n_end) (multiples of 64) of Wt only.
+hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
+                              const float* lora_a, const float* lora_b, int rank, float scaling, int n_begin, int n_end,
                               uint16_t* wt, hipStream_t stream);
 
 // Scratch the BLAS GEMM may use (its kernels' split-K partials and the like).
