@@ -322,24 +322,35 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
             for _ in range(layers) for (_, di, do) in QWEN_PROJ]
     torch.cuda.synchronize()
 
-    def quantize_all():
+    def quantize_all():  # the grouped pass: three launches per 48 weights
+        return Q.quantize_linears(vals)
+
+    def quantize_each():  # Nf4Linear::from_values per weight, as the reference's loop
         return [Q.Nf4Linear.from_values(v, di, do) for (v, di, do) in vals]
 
-    quantize_all()  # warm
-    # steady state: the best of three passes (the pass right after the
-    # warm-up one regrows the allocator's cache and runs several times slower)
-    q_s = float("inf")
-    for _ in range(3):
-        lins = None
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        lins = quantize_all()
-        torch.cuda.synchronize()
-        q_s = min(q_s, time.perf_counter() - t0)
+    def best_of_three(fn):
+        # steady state: the best of three passes (the pass right after the
+        # warm-up one regrows the allocator's cache and runs several times slower)
+        fn()  # warm
+        best, res = float("inf"), None
+        for _ in range(3):
+            res = None
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            res = fn()
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        return best, res
+
+    q_each_s, _ = best_of_three(quantize_each)
+    q_s, lins = best_of_three(quantize_all)
+    # the grouped pass's kernels alone: its launches timed with HIP events
+    q_kernel_ms = event_ms(torch, lambda i: Q.quantize_linears(vals), 3)
     params = sum(di * do for (_, di, do) in vals)
     q_bytes = 4 * params + params // 2 + 4 * (params // 64)  # f32 in, codes + f32 absmax out (config 5 unit)
     del vals
     out = {"quantize_pass_ms": round(q_s * 1e3, 3), "quantize_pass_gbs": round(q_bytes / q_s / 1e9, 1),
+           "quantize_pass_per_weight_ms": round(q_each_s * 1e3, 3), "quantize_pass_events_ms": round(q_kernel_ms, 3),
            "params": params}
     wbytes = sum(gemv_bytes(lin.d_input(), lin.d_output(), True, 0, 0) for lin in lins)
     for b in (1, 32):

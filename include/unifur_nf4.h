@@ -166,6 +166,24 @@ int unifur_nf4_embedding_forward(const uint8_t *packed, const unifur_nf4_scales 
 int unifur_nf4_quantize_transposed(const void *src, int src_dtype, uint64_t out_features, uint64_t in_features,
                                    uint8_t *packed, float *absmax, void *stream);
 
+/* The quantize pass over a model's linears (QwenTrunk::to_nf4,
+ * src/qwennet.rs:1185-1269, which runs Nf4Linear::from_values,
+ * src/qwennet.rs:196-205 -- PackedNf4Tensor::quantize then
+ * with_double_quantization, src/quantize.rs:259-309 -- on each weight in
+ * turn): n row-major f32 weights values[i] [d_in[i], d_out[i]] quantized with
+ * double quantization straight into the striped resident form, three
+ * launches per group of up to 48 weights.  packed[i] receives
+ * d_in*d_out/2 bytes of striped codes, dq_codes[i] the u8 scales
+ * [d_out/64][d_in], scale_of_scales[i] one f32 (device): byte for byte what
+ * unifur_nf4_quantize + unifur_nf4_double_quantize + unifur_nf4_stripe_weight
+ * write for that weight.  The pointer and shape arrays are host memory;
+ * d_out % 64 == 0, values 16-byte and packed 8-byte aligned.  Workspace:
+ * unifur_nf4_quantize_linears_workspace_size bytes (NULL: internal). */
+uint64_t unifur_nf4_quantize_linears_workspace_size(const uint64_t *d_in, const uint64_t *d_out, uint32_t n);
+int unifur_nf4_quantize_linears(const float *const *values, const uint64_t *d_in, const uint64_t *d_out, uint32_t n,
+                                uint8_t *const *packed, uint8_t *const *dq_codes, float *const *scale_of_scales,
+                                void *workspace, uint64_t workspace_bytes, void *stream);
+
 /* ---- device layout of a linear weight ------------------------------------------ */
 
 /* Row-major -> striped.  src->layout must be ROW_MAJOR, d_out % 64 == 0 and

@@ -1,0 +1,104 @@
+"""GPU parity of the grouped quantize pass (unifur_nf4_quantize_linears):
+QwenTrunk::to_nf4 (src/qwennet.rs:1185-1269) runs Nf4Linear::from_values
+(src/qwennet.rs:196-205) on every projection in turn; the grouped pass must
+write, for each weight, exactly the bytes of the per-weight path -- quantize
+(src/quantize.rs:259-279), double quantization (:281-309), then the striped
+layout -- whose codec is pinned bit-exact against the oracle by the codec
+tests.  Shapes cover the config-5 projections, spans that cross rows or end
+inside a 1024-value span, one-row weights, groups of more than 48 weights,
+and blocks of zeros, NaN, infinities and subnormals.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from unifur_amd import _lib as L
+from unifur_amd import quantize as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def per_weight(values, d_in, d_out):
+    return Q.Nf4Linear.from_values(values, d_in, d_out)
+
+
+def same_bytes(a: Q.Nf4Linear, b: Q.Nf4Linear):
+    assert a.is_striped() and b.is_striped()
+    assert torch.equal(a._codes, b._codes), "striped codes differ"
+    assert torch.equal(a._scales, b._scales), "u8 scales differ"
+    assert torch.equal(a._sos.view(torch.int32), b._sos.view(torch.int32)), "scale of scales differs"
+
+
+def weights(oracle, shapes, seed):
+    out = []
+    for i, (di, do) in enumerate(shapes):
+        v = torch.from_numpy(oracle.fill_normal(seed + i, 0.02, di * do)).cuda()
+        out.append((v, di, do))
+    return out
+
+
+def test_config5_projection_shapes(device, oracle):
+    shapes = [(896, 896), (896, 128), (896, 128), (896, 896), (896, 4864), (896, 4864), (4864, 896)]
+    ws = weights(oracle, shapes, 3000)
+    got = Q.quantize_linears(ws)
+    for (v, di, do), g in zip(ws, got):
+        same_bytes(g, per_weight(v, di, do))
+
+
+def test_partial_spans_tiny_and_many(device, oracle):
+    # 50 weights (two groups), spans crossing rows and ending mid-span
+    shapes = [(1, 64), (3, 128), (17, 192), (5, 64), (33, 320), (2, 1024), (7, 960)] * 7 + [(1, 64)]
+    ws = weights(oracle, shapes, 3100)
+    got = Q.quantize_linears(ws)
+    assert len(got) == len(shapes)
+    for (v, di, do), g in zip(ws, got):
+        same_bytes(g, per_weight(v, di, do))
+
+
+def test_special_values(device, oracle):
+    di, do = 9, 256
+    v = oracle.fill_normal(3200, 0.02, di * do).copy()
+    v[0:64] = 0.0                                     # zero block: codes 7, scale 0
+    v[64:128] = np.float32(1e-40)                     # subnormal block: exact division path
+    v[128] = np.nan                                   # NaN -> code 0, ignored by absmax
+    v[200] = np.inf                                   # Inf block
+    v[300:364] = np.nan                               # all-NaN block: absmax 0
+    v[400] = -0.0
+    v[500] = np.float32(3.0e38)                       # large absmax: exact path
+    t = torch.from_numpy(v).cuda()
+    got = Q.quantize_linears([(t, di, do)])[0]
+    same_bytes(got, per_weight(t, di, do))
+    # all-zero weight: max 0, every u8 scale 0, scale of scales 0
+    z = torch.zeros(4 * 128, device="cuda")
+    gz = Q.quantize_linears([(z, 4, 128)])[0]
+    same_bytes(gz, per_weight(z, 4, 128))
+    assert float(gz._sos) == 0.0 and not gz._scales.any()
+
+
+def test_forward_matches_and_argument_errors(device, oracle):
+    ws = weights(oracle, [(256, 384)], 3300)
+    got = Q.quantize_linears(ws)[0]
+    ref = per_weight(*ws[0])
+    x = torch.from_numpy(oracle.fill_normal(3301, 1.0, 3 * 256)).cuda().view(3, 256)
+    assert torch.equal(got.forward(x), ref.forward(x))
+    assert torch.equal(got.dequantized_weight(), ref.dequantized_weight())
+    with pytest.raises(ValueError):
+        Q.quantize_linears([(torch.zeros(8 * 100, device="cuda"), 8, 100)])  # d_out % 64 != 0
+    lib = L.lib()
+    P = ctypes.c_void_p * 1
+    U = ctypes.c_uint64 * 1
+    buf = torch.zeros(1024, dtype=torch.uint8, device="cuda")
+    vals = torch.zeros(64, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    # misaligned values
+    assert lib.unifur_nf4_quantize_linears(P(vals.data_ptr() + 4), U(1), U(64), 1, P(buf.data_ptr()),
+                                           P(buf.data_ptr() + 256), P(buf.data_ptr() + 512), None, 0,
+                                           st) == L.ERR_INVALID
+    # a NULL array
+    assert lib.unifur_nf4_quantize_linears(None, U(1), U(64), 1, P(buf.data_ptr()), P(buf.data_ptr() + 256),
+                                           P(buf.data_ptr() + 512), None, 0, st) == L.ERR_INVALID
+    assert lib.unifur_nf4_quantize_linears(None, None, None, 0, None, None, None, None, 0, st) == 0

@@ -1102,6 +1102,35 @@ int unifur_nf4_quantize_transposed(const void* src, int src_dtype, uint64_t out_
   return UNIFUR_NF4_OK;
 }
 
+uint64_t unifur_nf4_quantize_linears_workspace_size(const uint64_t* d_in, const uint64_t* d_out, uint32_t n) {
+  if (n == 0 || !d_in || !d_out) return 0;
+  Carver c;
+  c.take(quantize_linears_scratch_bytes(d_in, d_out, n));
+  return c.off;
+}
+
+int unifur_nf4_quantize_linears(const float* const* values, const uint64_t* d_in, const uint64_t* d_out, uint32_t n,
+                                uint8_t* const* packed, uint8_t* const* dq_codes, float* const* scale_of_scales,
+                                void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (n == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(values && d_in && d_out && packed && dq_codes && scale_of_scales, "an argument array is NULL");
+  for (uint32_t i = 0; i < n; ++i) {
+    UNIFUR_ARG(d_in[i] > 0 && d_out[i] > 0 && d_out[i] % 64 == 0, "quantize_linears needs d_out % 64 == 0");
+    UNIFUR_ARG(d_in[i] <= 0x7fffffffu && d_out[i] <= 0x7fffffffu, "quantize_linears: weight too large");
+    UNIFUR_ARG(values[i] && packed[i] && dq_codes[i] && scale_of_scales[i], "a tensor pointer is NULL");
+    UNIFUR_ARG(aligned_to(values[i], 16) && aligned_to(packed[i], 8) && aligned_to(scale_of_scales[i], 4),
+               "values must be 16-byte, packed 8-byte aligned");
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t need = quantize_linears_scratch_bytes(d_in, d_out, n);
+  void* ws = nullptr;
+  Carver c;
+  const size_t off = c.take(need);
+  if (int r = resolve_workspace(workspace, workspace_bytes, c.off, st, &ws)) return r;
+  UNIFUR_HIP(launch_quantize_linears(values, d_in, d_out, n, packed, dq_codes, scale_of_scales, at<void>(ws, off), st));
+  return UNIFUR_NF4_OK;
+}
+
 uint64_t unifur_nf4_dense_linear_workspace_size(uint64_t rows, uint32_t lora_rank) {
   if (rows == 0 || lora_rank == 0) return 0;
   Carver c;

@@ -376,6 +376,143 @@ int grid_for(size_t work_items, int threads, int max_blocks) {
   return g < 1 ? 1 : (int)g;
 }
 
+// ------------------------------------------------- grouped linear quantize --
+// The quantize pass of a model's linears in three launches per group of up
+// to kQGroupMax tensors instead of ~6 per tensor: each tensor is a
+// row-major f32 [K, N] weight (N % 64 == 0) quantized with double
+// quantization straight into the striped resident form.  The arithmetic is
+// quantize_full_kernel's and dq_encode_kernel's, so codes, DQ codes and the
+// scale of scales equal quantize + double quantize + stripe of the tensor.
+//   1. a wave per span of 16 rows x one 64-column block: codes of block
+//      (k, b) go to the stripes 4b .. 4b+3 at row k -- 8 bytes each, stripe s
+//      holding K rows of 8 bytes, so a span writes 128 contiguous bytes per
+//      stripe -- and its f32 absmax to absmax_tmp[b K + k], the striped
+//      scale order
+//   2. the max of each tensor's block scales (one workgroup per tensor; an
+//      atomic max per wave instead serialises on one address per tensor)
+//   3. encode absmax_tmp against the max into the u8 scales, same order
+constexpr int kQGroupMax = 48;
+
+struct QGroupTensor {
+  const float* values;  // [K][N] f32, 16-byte aligned
+  uint8_t* packed;      // striped codes, K N / 2 bytes, 8-byte aligned
+  uint8_t* dq;          // u8 scales [N / 64][K]
+  float* absmax;        // workspace f32 [N / 64][K]
+  uint32_t* max_bits;   // the scale of scales (device f32), written as its bits
+  uint32_t K, N;
+  uint32_t span_begin;  // first span of this tensor in the group
+};
+
+struct QGroupArgs {
+  int n;
+  uint32_t spans;  // over the group
+  QGroupTensor t[kQGroupMax];
+};
+
+__global__ __launch_bounds__(kQuantThreads) void qgroup_quantize_kernel(QGroupArgs a) {
+  __shared__ BucketEntry tab[33];
+  build_bucket_table(tab);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const uint32_t nwaves = gridDim.x * kQuantWaves;
+  for (uint32_t span = blockIdx.x * kQuantWaves + (threadIdx.x >> 6); span < a.spans; span += nwaves) {
+    int lo = 0, hi = a.n - 1;  // the tensor holding this span (wave-uniform binary search)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (span >= a.t[mid].span_begin) lo = mid;
+      else hi = mid - 1;
+    }
+    const QGroupTensor& T = a.t[lo];
+    // span = (16-row group rg, block column b): block q * 4 + lane / 16 of
+    // the wave is row 16 rg + 4 q + lane / 16, columns 64 b .. 64 b + 63, so
+    // each stripe of the block gets 16 consecutive rows = 128 contiguous
+    // bytes from this wave, and the block scales 16 consecutive entries
+    const uint32_t bpr = T.N / kBlock;
+    const uint32_t local = span - T.span_begin;
+    const uint32_t rg = local / bpr, b = local - rg * bpr;
+    const uint32_t c = lane & 15;  // values 4c .. 4c + 3 of the block: columns 64 b + 4 c ..
+    f32x4 v[4];
+    bool live[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t k = 16 * rg + 4 * q + lane / 16;
+      live[q] = k < T.K;
+      v[q] = live[q] ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(T.values + (size_t)k * T.N +
+                                                                                   64 * b) + c)
+                     : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    float m[4];
+    uint32_t nib[4];
+    bool exact = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // absmax = fold(0, max(acc, |v|)) (src/quantize.rs:103), as quantize_full_kernel
+      m[q] = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v[q].x)), fmaxf(fabsf(v[q].y), fabsf(v[q].z))), fabsf(v[q].w));
+      m[q] = max16(m[q]);
+      exact = exact || !(m[q] >= 1.1754943508222875e-38f && m[q] <= 8.507059173023462e+37f);
+      const float r = __builtin_amdgcn_rcpf(m[q]);
+      nib[q] = code_fast(v[q].x, r, tab, exact) | (code_fast(v[q].y, r, tab, exact) << 4) |
+               (code_fast(v[q].z, r, tab, exact) << 8) | (code_fast(v[q].w, r, tab, exact) << 12);
+    }
+    if (exact) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        nib[q] = code_exact(v[q].x, m[q], tab) | (code_exact(v[q].y, m[q], tab) << 4) |
+                 (code_exact(v[q].z, m[q], tab) << 8) | (code_exact(v[q].w, m[q], tab) << 12);
+    }
+    const uint64_t stripe = 4ull * b + c / 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (!live[q]) continue;
+      const uint32_t k = 16 * rg + 4 * q + lane / 16;
+      reinterpret_cast<uint16_t*>(T.packed)[(stripe * T.K + k) * 4 + (c & 3)] = (uint16_t)nib[q];
+      if (c == 0) T.absmax[(uint64_t)b * T.K + k] = m[q];
+    }
+  }
+}
+
+// The scale of scales of tensor blockIdx.x: the max of its block scales
+// (src/quantize.rs:285-290), one workgroup per tensor.  The values are >= 0
+// and never NaN, so the order of the max does not matter.
+__global__ __launch_bounds__(1024) void qgroup_max_kernel(QGroupArgs a) {
+  __shared__ float wm[16];
+  const QGroupTensor& T = a.t[blockIdx.x];
+  const uint64_t nb = (uint64_t)T.K * (T.N / kBlock);
+  float m = 0.0f;
+  const uint64_t step = blockDim.x;
+  for (uint64_t i0 = threadIdx.x; i0 < nb; i0 += 8 * step) {  // eight loads in flight per thread
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = i0 + u * step < nb ? T.absmax[i0 + u * step] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m = fmaxf(m, v[u]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, wm[w]);
+    *T.max_bits = __float_as_uint(r);
+  }
+}
+
+__global__ void qgroup_encode_kernel(QGroupArgs a) {
+  const QGroupTensor& T = a.t[blockIdx.y];
+  const float M = __uint_as_float(*T.max_bits);
+  const uint64_t nb = (uint64_t)T.K * (T.N / kBlock);
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nb; i += (uint64_t)gridDim.x * blockDim.x) {
+    uint8_t c = 0;
+    if (M != 0.0f) {
+      // (s / max_scale * 255.0).round().clamp(0.0, 255.0) as u8 (src/quantize.rs:285-303)
+      const float r = roundf((T.absmax[i] / M) * 255.0f);  // half away from zero
+      c = (r == r) ? (uint8_t)fminf(fmaxf(r, 0.0f), 255.0f) : (uint8_t)0;
+    }
+    T.dq[i] = c;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_quantize(const float* values, size_t n, uint8_t* packed, float* absmax, bool aligned,
@@ -453,6 +590,51 @@ hipError_t launch_quantize_transposed(const void* src, bool bf16_in, uint64_t ou
     quantize_transposed_kernel<false><<<dim3((unsigned)gx, (unsigned)gy), 256, 0, stream>>>(src, out_f, in_f, packed,
                                                                                             absmax);
   return hipGetLastError();
+}
+
+
+size_t quantize_linears_scratch_bytes(const uint64_t* d_in, const uint64_t* d_out, uint32_t n) {
+  size_t total = 0;
+  for (uint32_t i = 0; i < n; ++i) total += ((size_t)(d_in[i] * (d_out[i] / kBlock) * 4) + 255) & ~size_t{255};
+  return total;
+}
+
+hipError_t launch_quantize_linears(const float* const* values, const uint64_t* d_in, const uint64_t* d_out,
+                                   uint32_t n, uint8_t* const* packed, uint8_t* const* dq, float* const* sos,
+                                   void* scratch, hipStream_t stream) {
+  char* tmp = static_cast<char*>(scratch);
+  for (uint32_t g0 = 0; g0 < n; g0 += kQGroupMax) {
+    QGroupArgs a{};
+    a.n = (int)std::min<uint32_t>(kQGroupMax, n - g0);
+    uint64_t spans = 0, max_nb = 0;
+    for (int i = 0; i < a.n; ++i) {
+      const uint32_t j = g0 + i;
+      QGroupTensor& T = a.t[i];
+      T.values = values[j];
+      T.packed = packed[j];
+      T.dq = dq[j];
+      T.absmax = reinterpret_cast<float*>(tmp);
+      T.max_bits = reinterpret_cast<uint32_t*>(sos[j]);
+      T.K = (uint32_t)d_in[j];
+      T.N = (uint32_t)d_out[j];
+      T.span_begin = (uint32_t)spans;
+      const uint64_t nb = d_in[j] * (d_out[j] / kBlock);
+      tmp += ((size_t)nb * 4 + 255) & ~size_t{255};
+      spans += (d_in[j] + 15) / 16 * (d_out[j] / kBlock);  // 16-row groups x block columns
+      max_nb = std::max(max_nb, nb);
+    }
+    if (spans > 0xffffffffull) return hipErrorInvalidValue;
+    a.spans = (uint32_t)spans;
+    if (spans) qgroup_quantize_kernel<<<grid_for(spans, kQuantWaves, 8192), kQuantThreads, 0, stream>>>(a);
+    qgroup_max_kernel<<<(unsigned)a.n, 1024, 0, stream>>>(a);
+    if (max_nb) {
+      const unsigned gx = (unsigned)std::min<uint64_t>((max_nb + 255) / 256, 256);
+      qgroup_encode_kernel<<<dim3(gx, (unsigned)a.n), 256, 0, stream>>>(a);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace unifur

@@ -25,5 +25,15 @@ hipError_t launch_quantize_transposed(const void* src, bool bf16_in, uint64_t ou
                                       float* absmax, hipStream_t stream);
 hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, size_t n, void* out, bool bf16_out,
                              bool aligned, hipStream_t stream);
+// The quantize pass of n linears: row-major f32 values[i] [d_in[i], d_out[i]]
+// (d_out % 64 == 0, values 16-byte and packed 8-byte aligned) quantized with
+// double quantization into the striped resident form (packed[i] striped
+// codes, dq[i] u8 scales [d_out / 64][d_in], sos[i] the scale of scales),
+// three launches per group of up to 48 tensors; scratch holds the f32 block
+// scales (quantize_linears_scratch_bytes).
+size_t quantize_linears_scratch_bytes(const uint64_t* d_in, const uint64_t* d_out, uint32_t n);
+hipError_t launch_quantize_linears(const float* const* values, const uint64_t* d_in, const uint64_t* d_out,
+                                   uint32_t n, uint8_t* const* packed, uint8_t* const* dq, float* const* sos,
+                                   void* scratch, hipStream_t stream);
 
 }  // namespace unifur

@@ -323,6 +323,22 @@ class Nf4Linear:
         return Nf4Linear(PackedNf4Tensor.quantize(values.contiguous().view(-1)).with_double_quantization(),
                          d_input, d_output, striped=striped)
 
+    @classmethod
+    def _from_striped(cls, codes: torch.Tensor, dq_codes: torch.Tensor, scale_of_scales: torch.Tensor, d_input: int,
+                      d_output: int) -> "Nf4Linear":
+        """A layer over already-striped, double-quantized device buffers."""
+        self = cls.__new__(cls)
+        self._d_in, self._d_out = int(d_input), int(d_output)
+        self.bias = None
+        self._striped = True
+        self._len = self._d_in * self._d_out
+        self._dq = True
+        self._sos = scale_of_scales
+        self._codes = codes
+        self._scales = dq_codes
+        self._packed = None
+        return self
+
     def d_input(self) -> int:
         return self._d_in
 
@@ -418,6 +434,44 @@ class Nf4Linear:
         takes through the detached dequantized weight (src/qwennet.rs:238-241
         under src/qwentrain.rs:421-470); the frozen weight gets none."""
         return self._backward(dy, None, None, True, dx_dtype)[0]
+
+
+def quantize_linears(weights) -> list:
+    """Nf4Linear.from_values on every (values, d_input, d_output) of
+    ``weights`` -- the quantize pass of QwenTrunk::to_nf4
+    (src/qwennet.rs:1185-1269) -- in one grouped pass (three launches per 48
+    weights): values are f32 [d_input * d_output] row-major on the device,
+    d_output % 64 == 0; the layers come back striped and double quantized,
+    their buffers slices of one allocation each for codes, scales and scales
+    of scales."""
+    ws = [(v.contiguous().view(-1), int(di), int(do)) for (v, di, do) in weights]
+    n = len(ws)
+    if n == 0:
+        return []
+    for v, di, do in ws:
+        _require_cuda(v, "values")
+        if v.dtype != torch.float32 or v.numel() != di * do:
+            raise ValueError(f"values must be float32 with {di} x {do} elements")
+        if do % 64 != 0:
+            raise ValueError("quantize_linears needs d_output % 64 == 0")
+    dev = ws[0][0].device
+    # back to back: code sizes are multiples of 32 bytes (d_output % 64 == 0),
+    # so every slice stays 8-byte aligned; u8 scales need no alignment
+    c_sizes = [di * do // 2 for (_, di, do) in ws]
+    s_sizes = [di * do // 64 for (_, di, do) in ws]
+    codes = torch.empty(sum(c_sizes), dtype=torch.uint8, device=dev)
+    dq = torch.empty(sum(s_sizes), dtype=torch.uint8, device=dev)
+    sos = torch.empty(n, dtype=torch.float32, device=dev)
+    code_views, dq_views, sos_views = torch.split(codes, c_sizes), torch.split(dq, s_sizes), torch.split(sos, 1)
+    P = ctypes.c_void_p * n
+    U = ctypes.c_uint64 * n
+    vals = [v if v.data_ptr() % 16 == 0 else v.clone() for (v, _, _) in ws]
+    L.check(L.lib().unifur_nf4_quantize_linears(
+        P(*[v.data_ptr() for v in vals]), U(*[di for (_, di, _) in ws]), U(*[do for (_, _, do) in ws]), n,
+        P(*[c.data_ptr() for c in code_views]), P(*[d.data_ptr() for d in dq_views]),
+        P(*[o.data_ptr() for o in sos_views]), None, 0, _stream()))
+    return [Nf4Linear._from_striped(code_views[i], dq_views[i], sos_views[i], di, do)
+            for i, (_, di, do) in enumerate(ws)]
 
 
 def forward_shared_input(x: torch.Tensor, layers, out_dtype: Optional[torch.dtype] = None) -> list:
