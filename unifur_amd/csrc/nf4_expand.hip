@@ -29,11 +29,10 @@ namespace {
 
 constexpr int kTile = 64;
 constexpr int kTStride = 36;                      // dwords per transposed column (32 + 4 pad)
-constexpr int kLdsLut = 0;                        // NF4_LEVELS, 16 x f32
-constexpr int kLdsT = 64;                         // KT transpose tiles of 64 x 36 dwords
+constexpr int kLdsLut = 0;                        // NF4_LEVELS, 16 x f32 per wave
+constexpr int kLdsT = 256;                        // KT transpose tiles of 64 x 36 dwords
 constexpr int kTBytes = kTile * kTStride * 4;
 constexpr int kMaxRank = 64;
-constexpr int kCStride = 68;  // f32 per row of the LoRA product tile
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct ExpandArgs {
@@ -50,7 +49,42 @@ struct ExpandArgs {
   int n_base;    // first column of the launch (a multiple of 64)
 };
 
-template <bool DQ, bool STRIPED, bool LORA, int KT>
+// Codes of rows k, k + 1 of a 64 x 64 tile for columns n .. n + 7 and the
+// rows' scales of block n0 / 64.
+template <bool DQ, bool STRIPED>
+__device__ __forceinline__ void load_row_codes(const ExpandArgs& a, size_t row, int n, int ng, int blk, uint32_t& code,
+                                               float& s) {
+  size_t sidx;
+  if constexpr (STRIPED) {
+    // stripe n / 16 holds 8 bytes per row; these 8 columns are its half (n % 16) / 8
+    code = *reinterpret_cast<const uint32_t*>(a.packed + ((size_t)(n / 16) * a.K + row) * 8 + (size_t)(ng & 1) * 4);
+    sidx = (size_t)blk * a.K + row;
+  } else {
+    code = *reinterpret_cast<const uint32_t*>(a.packed + row * (size_t)(a.N / 2) + n / 2);
+    sidx = row * (size_t)(a.N / kBlock) + blk;
+  }
+  if constexpr (DQ)
+    s = ((float)a.scales.dq_codes[sidx] / 255.0f) * (*a.scales.scale_of_scales);  // src/quantize.rs:349
+  else
+    s = a.scales.absmax[sidx];
+}
+
+// The bf16 (k, k + 1) pairs of each tile's columns, left in the transpose
+// tiles T, leave as 128-byte column segments: column c = tid / 4, quarter
+// q = tid % 4 stores 16 k values of each tile (two 16-byte stores).
+template <int KT>
+__device__ __forceinline__ void store_tiles(const ExpandArgs& a, const uint32_t* T, int tid, int k0, int n0) {
+  const int c = tid >> 2, q = tid & 3;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(T + t * (kTile * kTStride) + c * kTStride + 8 * q);
+    u32x4* dst = reinterpret_cast<u32x4*>(a.wt + (size_t)(n0 + c) * a.K + k0 + kTile * t + 16 * q);
+    dst[0] = src[0];
+    dst[1] = src[1];
+  }
+}
+
+template <bool DQ, bool STRIPED, int KT>
 __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
@@ -71,156 +105,187 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 #pragma unroll
   for (int t = 0; t < KT; ++t)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const size_t row = (size_t)(k0 + kTile * t + 2 * kp + i);
-      size_t sidx;
-      if constexpr (STRIPED) {
-        // stripe n / 16 holds 8 bytes per row; these 8 columns are its half (n % 16) / 8
-        code[t][i] = *reinterpret_cast<const uint32_t*>(a.packed + ((size_t)(n / 16) * a.K + row) * 8 + (size_t)(ng & 1) * 4);
-        sidx = (size_t)blk * a.K + row;
-      } else {
-        code[t][i] = *reinterpret_cast<const uint32_t*>(a.packed + row * (size_t)(a.N / 2) + n / 2);
-        sidx = row * (size_t)(a.N / kBlock) + blk;
-      }
-      if constexpr (DQ)
-        s[t][i] = ((float)a.scales.dq_codes[sidx] / 255.0f) * (*a.scales.scale_of_scales);  // src/quantize.rs:349
-      else
-        s[t][i] = a.scales.absmax[sidx];
-    }
+    for (int i = 0; i < 2; ++i)
+      load_row_codes<DQ, STRIPED>(a, (size_t)(k0 + kTile * t + 2 * kp + i), n, ng, blk, code[t][i], s[t][i]);
 
   float* lut = reinterpret_cast<float*>(smem + kLdsLut);
   if (tid < 16) lut[tid] = level(tid);
-  // LoRA: the MFMA fragments straight from the f32 factors, issued with the
-  // code loads and rounded to bf16 in registers (A: eight consecutive values
-  // of a row; B^T: eight rows of a column, coalesced across the lanes); the
-  // f32 product tile C [64][68] after the transpose tiles
-  const int lane = tid & 63, wv = tid >> 6, bi = wv >> 1, bj = wv & 1, h = lane >> 5;
-  const int lds_c = kLdsT + KT * kTBytes;
-  // adapter fragments per tile: up to rank 64 in the one-tile kernel, rank
-  // 16 (one fragment) when a workgroup takes several tiles
-  constexpr int kMaxFr = (LORA && KT == 1) ? kMaxRank / 16 : 1;
-  bf16x8_t bfr[kMaxFr];
-  bf16x8_t afr[KT][kMaxFr];
-  if constexpr (LORA) {
-    const int nf = a.rp / 16;
-#pragma unroll
-    for (int f = 0; f < kMaxFr; ++f) {
-      if (f >= nf) break;
-      const int r0 = 16 * f + 8 * h;  // this lane's eight adapter indices
-      const size_t col = (size_t)(n0 + 32 * bj + (lane & 31));
-      float bv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bv[e] = r0 + e < a.rank ? a.lb[(size_t)(r0 + e) * a.N + col] : 0.0f;
-      bfr[f] = __builtin_bit_cast(bf16x8_t, u32x4{pack_bf16x2(bv[0], bv[1]), pack_bf16x2(bv[2], bv[3]),
-                                                  pack_bf16x2(bv[4], bv[5]), pack_bf16x2(bv[6], bv[7])});
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const size_t row = (size_t)(k0 + kTile * t + 32 * bi + (lane & 31));
-        float av[8];
-        if (a.la_vec) {
-          f32x4 lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = lo;
-          if (r0 < a.rank) {
-            const f32x4* src = reinterpret_cast<const f32x4*>(a.la + row * a.rank + r0);
-            lo = src[0];
-            hi = src[1];
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            av[e] = lo[e];
-            av[4 + e] = hi[e];
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) av[e] = r0 + e < a.rank ? a.la[row * a.rank + r0 + e] : 0.0f;
-        }
-        afr[t][f] = __builtin_bit_cast(bf16x8_t, u32x4{pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]),
-                                                       pack_bf16x2(av[4], av[5]), pack_bf16x2(av[6], av[7])});
-      }
-    }
-  }
   __syncthreads();
 
   uint32_t* T = reinterpret_cast<uint32_t*>(smem + kLdsT);
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
-    // v[i][j]: row k0 + 64 t + 2 kp + i, column n + j
-    float v[2][8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[i][j] = lut[(code[t][i] >> (4 * j)) & 15u] * s[t][i];  // NF4_LEVELS[c] * scale
-    if constexpr (LORA) {
-      // C = A_t B for this tile: wave w computes the 32 x 32 block
-      // (w / 2, w % 2) with rp / 16 v_mfma_f32_32x32x16_bf16 (bf16 factors,
-      // f32 sums); C passes through LDS to the (k, k + 1) x 8-column layout
-      float* C = reinterpret_cast<float*>(smem + lds_c);
-      f32x16 acc = {};
-#pragma unroll
-      for (int f = 0; f < kMaxFr; ++f) {
-        if (f >= a.rp / 16) break;
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[t][f], bfr[f], acc, 0, 0, 0);
-      }
-      if (t > 0) __syncthreads();  // the previous tile's C has been read
-      // acc[4 q + e] = C[8 q + 4 h + e][lane % 32] of the block
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) C[(32 * bi + 8 * q + 4 * h + e) * kCStride + 32 * bj + (lane & 31)] = acc[4 * q + e];
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const f32x4* cr = reinterpret_cast<const f32x4*>(C + (2 * kp + i) * kCStride + 8 * ng);
-        const f32x4 c0 = cr[0], c1 = cr[1];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[i][j] += a.scaling * c0[j];
-          v[i][j + 4] += a.scaling * c1[j];
-        }
-      }
-    }
     // transpose through tile buffer t: column 8 ng + j, dword kp = bf16 pair (k, k + 1)
     uint32_t* Tt = T + t * (kTile * kTStride);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) Tt[(8 * ng + j) * kTStride + kp] = pack_bf16x2(v[0][j], v[1][j]);
+    for (int j = 0; j < 8; ++j) {
+      const float v0 = lut[(code[t][0] >> (4 * j)) & 15u] * s[t][0];  // NF4_LEVELS[c] * scale
+      const float v1 = lut[(code[t][1] >> (4 * j)) & 15u] * s[t][1];
+      Tt[(8 * ng + j) * kTStride + kp] = pack_bf16x2(v0, v1);
+    }
   }
   __syncthreads();
-  // column c = t / 4, quarter q = t % 4: 16 k values of each tile = two
-  // 16-byte stores per tile
-  const int c = tid >> 2, q = tid & 3;
+  store_tiles<KT>(a, T, tid, k0, n0);
+}
+
+// With an adapter.  Wave w of a tile computes the 32 (k) x 32 (n) block
+// (w / 2, w % 2) of the adapter product as (B^T A^T) with
+// v_mfma_f32_32x32x16_bf16 (bf16 factors, f32 sums): with B^T as the first
+// operand, lane l ends up holding row k = 32 (w / 2) + l % 32 and the 16
+// columns 8 q + 4 (l / 32) + e (acc[4 q + e]) of the block, so each lane
+// loads the codes of exactly those 16 (row, column) entries and adds the
+// product in registers.  Adjacent lanes (rows k, k + 1) then swap half of
+// their columns by DPP so that each holds whole (k, k + 1) pairs for the
+// transpose tiles.  The factors' MFMA fragments are read straight from the
+// f32 A [K][rank] and B [rank][N] and rounded to bf16 in registers.
+template <bool DQ, bool STRIPED, int KT, int NFR>
+__global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x;
+  const int groups_k = a.tiles_k / KT;
+  const int k0 = (int)(blockIdx.x % (unsigned)groups_k) * (kTile * KT);
+  const int n0 = a.n_base + (int)(blockIdx.x / (unsigned)groups_k) * kTile;
+  const int lane = tid & 63, wv = tid >> 6, bi = wv >> 1, bj = wv & 1, h = lane >> 5, lr = lane & 31;
+  const int cb = n0 + 32 * bj;  // first column of this wave's block
+  const int blk = n0 / kBlock;
+  const int nf = a.rp / 16;
+
+  // codes: dword q holds columns cb + 8 q .. + 7 of the lane's row (this
+  // lane uses nibbles 4 h .. 4 h + 3 of each), and the row's scale
+  uint32_t cw[KT][4];
+  float s[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(T + t * (kTile * kTStride) + c * kTStride + 8 * q);
-    u32x4* dst = reinterpret_cast<u32x4*>(a.wt + (size_t)(n0 + c) * a.K + k0 + kTile * t + 16 * q);
-    dst[0] = src[0];
-    dst[1] = src[1];
+    const size_t row = (size_t)(k0 + kTile * t + 32 * bi + lr);
+    size_t sidx;
+    if constexpr (STRIPED) {
+      const u32x2* p = reinterpret_cast<const u32x2*>(a.packed + ((size_t)(cb / 16) * a.K + row) * 8);
+      const u32x2 c0 = p[0];
+      const u32x2 c1 = p[a.K];  // the next stripe, same row
+      cw[t][0] = c0[0];
+      cw[t][1] = c0[1];
+      cw[t][2] = c1[0];
+      cw[t][3] = c1[1];
+      sidx = (size_t)blk * a.K + row;
+    } else {
+      const u32x4 c = *reinterpret_cast<const u32x4*>(a.packed + row * (size_t)(a.N / 2) + cb / 2);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) cw[t][q] = c[q];
+      sidx = row * (size_t)(a.N / kBlock) + blk;
+    }
+    if constexpr (DQ)
+      s[t] = ((float)a.scales.dq_codes[sidx] / 255.0f) * (*a.scales.scale_of_scales);  // src/quantize.rs:349
+    else
+      s[t] = a.scales.absmax[sidx];
   }
+
+  // fragments: B^T rows = columns cb + l % 32 of B, A^T columns = rows of A;
+  // lane l carries adapter indices 16 f + 8 (l / 32) .. + 7
+  bf16x8_t bfr[NFR];
+  bf16x8_t afr[KT][NFR];
+#pragma unroll
+  for (int f = 0; f < NFR; ++f) {
+    if (f >= nf) break;
+    const int r0 = 16 * f + 8 * h;
+    const size_t col = (size_t)(cb + lr);
+    float bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bv[e] = r0 + e < a.rank ? a.lb[(size_t)(r0 + e) * a.N + col] : 0.0f;
+    bfr[f] = __builtin_bit_cast(bf16x8_t, u32x4{pack_bf16x2(bv[0], bv[1]), pack_bf16x2(bv[2], bv[3]),
+                                                pack_bf16x2(bv[4], bv[5]), pack_bf16x2(bv[6], bv[7])});
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const size_t row = (size_t)(k0 + kTile * t + 32 * bi + lr);
+      float av[8];
+      if (a.la_vec) {
+        f32x4 lo = {0.0f, 0.0f, 0.0f, 0.0f}, hi = lo;
+        if (r0 < a.rank) {
+          const f32x4* src = reinterpret_cast<const f32x4*>(a.la + row * a.rank + r0);
+          lo = src[0];
+          hi = src[1];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          av[e] = lo[e];
+          av[4 + e] = hi[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) av[e] = r0 + e < a.rank ? a.la[row * a.rank + r0 + e] : 0.0f;
+      }
+      afr[t][f] = __builtin_bit_cast(bf16x8_t, u32x4{pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3]),
+                                                     pack_bf16x2(av[4], av[5]), pack_bf16x2(av[6], av[7])});
+    }
+  }
+
+  // one LUT copy per wave: no workgroup barrier before the decode
+  float* lut = reinterpret_cast<float*>(smem + kLdsLut) + 16 * wv;
+  if (lane < 16) lut[lane] = level(lane);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  uint32_t* T = reinterpret_cast<uint32_t*>(smem + kLdsT);
+  const bool odd = (lr & 1) != 0;
+  const int kpair = 16 * bi + (lr >> 1);
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    f32x16 acc = {};
+#pragma unroll
+    for (int f = 0; f < NFR; ++f) {
+      if (f >= nf) break;
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[f], afr[t][f], acc, 0, 0, 0);
+    }
+    // v[4 q + e]: row k, column cb + 8 q + 4 h + e
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float w = lut[(cw[t][q] >> (16 * h + 4 * e)) & 15u] * s[t];  // NF4_LEVELS[c] * scale
+        v[4 * q + e] = w + a.scaling * acc[4 * q + e];
+      }
+    // the even lane keeps columns q = 0, 1 and receives row k + 1 of them;
+    // the odd lane keeps q = 2, 3 and receives row k - 1 of them
+    uint32_t* Tt = T + t * (kTile * kTStride);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float send = odd ? v[j] : v[8 + j];
+      const float keep = odd ? v[8 + j] : v[j];
+      const float got = __uint_as_float(
+          __builtin_amdgcn_update_dpp(0u, __float_as_uint(send), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+      const int q = (odd ? 2 : 0) + (j >> 2), e = j & 3;
+      const int col = 32 * bj + 8 * q + 4 * h + e;
+      Tt[col * kTStride + kpair] = odd ? pack_bf16x2(got, keep) : pack_bf16x2(keep, got);
+    }
+  }
+  __syncthreads();
+  store_tiles<KT>(a, T, tid, k0, n0);
 }
 
-// LDS of a KT-tile workgroup: the transpose tiles, then with an adapter the
-// f32 product tile.
-size_t expand_smem(int KT, bool lora) {
-  return kLdsT + (size_t)KT * kTBytes + (lora ? (size_t)kTile * kCStride * 4 : 0);
+// LDS of a KT-tile workgroup: the LUT (one copy per wave), then the transpose tiles.
+size_t expand_smem(int KT) { return kLdsT + (size_t)KT * kTBytes; }
+
+template <bool DQ, bool STRIPED, int KT>
+hipError_t launch_kt(const ExpandArgs& a, int n_count, hipStream_t stream) {
+  const unsigned grid = (unsigned)((long long)(n_count / kTile) * (a.tiles_k / KT));
+  if (a.rank == 0)
+    expand_kernel<DQ, STRIPED, KT><<<grid, 256, expand_smem(KT), stream>>>(a);
+  else if (a.rp == 16)
+    expand_lora_kernel<DQ, STRIPED, KT, 1><<<grid, 256, expand_smem(KT), stream>>>(a);
+  else
+    expand_lora_kernel<DQ, STRIPED, 1, kMaxRank / 16><<<grid, 256, expand_smem(1), stream>>>(a);
+  return hipGetLastError();
 }
 
-template <bool DQ, bool STRIPED, bool LORA>
+template <bool DQ, bool STRIPED>
 hipError_t launch_t(const ExpandArgs& a, int n_count, hipStream_t stream) {
-  const long long band = n_count / kTile;
   // four (or two) tiles per workgroup where K allows: more loads in flight
   // (with an adapter of rank <= 16, whose fragments then fit the registers)
-  if (LORA && a.rp > 16) {
-    expand_kernel<DQ, STRIPED, LORA, 1><<<(int)(band * a.tiles_k), 256, expand_smem(1, LORA), stream>>>(a);
-    return hipGetLastError();
-  }
-  if (a.tiles_k % 4 == 0) {
-    expand_kernel<DQ, STRIPED, LORA, 4><<<(int)(band * (a.tiles_k / 4)), 256, expand_smem(4, LORA), stream>>>(a);
-    return hipGetLastError();
-  }
-  if (a.tiles_k % 2 == 0) {
-    expand_kernel<DQ, STRIPED, LORA, 2><<<(int)(band * (a.tiles_k / 2)), 256, expand_smem(2, LORA), stream>>>(a);
-    return hipGetLastError();
-  }
-  expand_kernel<DQ, STRIPED, LORA, 1><<<(int)(band * a.tiles_k), 256, expand_smem(1, LORA), stream>>>(a);
-  return hipGetLastError();
+  if (a.rank > 0 && a.rp > 16) return launch_kt<DQ, STRIPED, 1>(a, n_count, stream);
+  if (a.tiles_k % 4 == 0) return launch_kt<DQ, STRIPED, 4>(a, n_count, stream);
+  if (a.tiles_k % 2 == 0) return launch_kt<DQ, STRIPED, 2>(a, n_count, stream);
+  return launch_kt<DQ, STRIPED, 1>(a, n_count, stream);
 }
 
 }  // namespace
@@ -261,13 +326,8 @@ hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, in
   const long long tiles = (long long)(K / kTile) * (nc / kTile);
   if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
   const bool dq = scales.kind == kScalesDQ;
-  const bool lora = rank > 0;
-  if (dq) {
-    if (striped) return lora ? launch_t<true, true, true>(a, nc, stream) : launch_t<true, true, false>(a, nc, stream);
-    return lora ? launch_t<true, false, true>(a, nc, stream) : launch_t<true, false, false>(a, nc, stream);
-  }
-  if (striped) return lora ? launch_t<false, true, true>(a, nc, stream) : launch_t<false, true, false>(a, nc, stream);
-  return lora ? launch_t<false, false, true>(a, nc, stream) : launch_t<false, false, false>(a, nc, stream);
+  if (dq) return striped ? launch_t<true, true>(a, nc, stream) : launch_t<true, false>(a, nc, stream);
+  return striped ? launch_t<false, true>(a, nc, stream) : launch_t<false, false>(a, nc, stream);
 }
 
 }  // namespace unifur
