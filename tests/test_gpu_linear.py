@@ -190,6 +190,36 @@ def test_swiglu_prefill_expanded_and_fused(device, oracle, striped):
         check(y, ref, h, wd, TOL_BF16, f"swiglu T={T} workspace {need}")
 
 
+def test_swiglu_decode_repeated_on_one_workspace(device, oracle):
+    # Decode SwiGLU calls of two shapes and both pair row counts, one after
+    # another on one zero-filled caller workspace: each matches the oracle
+    # and leaves the workspace's counter region zero (its contract).
+    from unifur_amd import _lib as L
+    import ctypes
+    shapes = [(896, 4864, 71), (256, 512, 75)]
+    mlps = []
+    for hidden, inter, seed in shapes:
+        g, wg = make_linear(oracle, hidden, inter, seed, device, striped=True)
+        u, wu = make_linear(oracle, hidden, inter, seed + 1, device, striped=True)
+        d, wd = make_linear(oracle, inter, hidden, seed + 2, device, striped=True)
+        mlps.append((hidden, inter, (g, u, d), (wg, wu, wd)))
+    need = max(L.lib().unifur_nf4_swiglu_workspace_size(2, h_, i_, L.F32) for h_, i_, _ in shapes)
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    for call, (k, rows) in enumerate([(0, 1), (1, 2), (0, 2), (1, 1), (0, 1)]):
+        hidden, inter, (g, u, d), (wg, wu, wd) = mlps[k]
+        x, xt = acts(oracle, rows, hidden, 80 + call, torch.float32, device)
+        gs, us, ds = g.weight_struct(), u.weight_struct(), d.weight_struct()
+        y = torch.empty(rows, hidden, device=device)
+        L.check(L.lib().unifur_nf4_swiglu_forward(xt.data_ptr(), L.F32, rows, ctypes.byref(gs), ctypes.byref(us),
+                                                  ctypes.byref(ds), y.data_ptr(), L.F32, ws.data_ptr(), need,
+                                                  stream))
+        ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+        h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+        check(y, ref, h, wd, TOL_F32, f"swiglu call {call} shape {hidden}x{inter} rows={rows}")
+        assert int(ws[:64 << 10].count_nonzero()) == 0, f"counter region not left zero after call {call}"
+
+
 def test_workspace_shared_by_generic_then_gemv_calls(device, oracle):
     # A generic-path call writes an f32 weight copy into the workspace; the
     # GEMV's split-K arrival counters live in a region nothing else touches,
