@@ -14,12 +14,12 @@
 // Y = X Wt^T product, which the BLAS GEMM then streams with 16-byte loads.
 //
 // One 256-thread workgroup expands a 64 (k) x 64 (n) tile -- one NF4 block
-// wide.  Thread t owns rows 2 (t % 32) and 2 (t % 32) + 1 and the 8 columns
-// 8 (t / 32) .. + 7: one code dword per row, one scale per row.  The bf16
-// (k, k + 1) pairs of each column go through an LDS transpose (row stride
-// 36 dwords: the two column groups of a wave land on opposite bank halves)
-// and leave as 128-byte column segments.  A workgroup takes up to four tiles
-// along K, their loads all issued first.
+// wide -- or up to four of them along K, their loads all issued first.
+// Without an adapter thread t owns rows 2 (t % 32) and 2 (t % 32) + 1 and
+// the 8 columns 8 (t / 32) .. + 7: one code dword per row, one scale per
+// row, and each column's bf16 (k, k + 1) pair is one dword of Wt; for one
+// column the 32 lanes of a half-wave write 32 consecutive pairs, a 128-byte
+// segment, so the output needs no LDS transpose.
 #include "nf4_expand.hpp"
 
 #include <algorithm>
@@ -28,10 +28,8 @@ namespace unifur {
 namespace {
 
 constexpr int kTile = 64;
-constexpr int kTStride = 36;                      // dwords per transposed column (32 + 4 pad)
 constexpr int kLdsLut = 0;                        // NF4_LEVELS, 16 x f32 per wave
-constexpr int kLdsT = 256;                        // KT transpose tiles of 64 x 36 dwords
-constexpr int kTBytes = kTile * kTStride * 4;
+constexpr int kLdsBytes = 256;                        // LDS bytes: the four waves' LUTs
 constexpr int kMaxRank = 64;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -69,21 +67,6 @@ __device__ __forceinline__ void load_row_codes(const ExpandArgs& a, size_t row, 
     s = a.scales.absmax[sidx];
 }
 
-// The bf16 (k, k + 1) pairs of each tile's columns, left in the transpose
-// tiles T, leave as 128-byte column segments: column c = tid / 4, quarter
-// q = tid % 4 stores 16 k values of each tile (two 16-byte stores).
-template <int KT>
-__device__ __forceinline__ void store_tiles(const ExpandArgs& a, const uint32_t* T, int tid, int k0, int n0) {
-  const int c = tid >> 2, q = tid & 3;
-#pragma unroll
-  for (int t = 0; t < KT; ++t) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(T + t * (kTile * kTStride) + c * kTStride + 8 * q);
-    u32x4* dst = reinterpret_cast<u32x4*>(a.wt + (size_t)(n0 + c) * a.K + k0 + kTile * t + 16 * q);
-    dst[0] = src[0];
-    dst[1] = src[1];
-  }
-}
-
 template <bool DQ, bool STRIPED, int KT>
 __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -108,24 +91,27 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     for (int i = 0; i < 2; ++i)
       load_row_codes<DQ, STRIPED>(a, (size_t)(k0 + kTile * t + 2 * kp + i), n, ng, blk, code[t][i], s[t][i]);
 
-  float* lut = reinterpret_cast<float*>(smem + kLdsLut);
-  if (tid < 16) lut[tid] = level(tid);
-  __syncthreads();
+  // one LUT copy per wave: no workgroup barrier
+  const int lane = tid & 63, wv = tid >> 6;
+  float* lut = reinterpret_cast<float*>(smem + kLdsLut) + 16 * wv;
+  if (lane < 16) lut[lane] = level(lane);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  uint32_t* T = reinterpret_cast<uint32_t*>(smem + kLdsT);
+  // the bf16 (k, k + 1) pair of column n + j goes straight to Wt: for one
+  // j the 32 lanes of a half-wave write 32 consecutive pairs of that
+  // column, one 128-byte segment
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
-    // transpose through tile buffer t: column 8 ng + j, dword kp = bf16 pair (k, k + 1)
-    uint32_t* Tt = T + t * (kTile * kTStride);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(a.wt + (size_t)n * a.K + k0 + kTile * t) + kp;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float v0 = lut[(code[t][0] >> (4 * j)) & 15u] * s[t][0];  // NF4_LEVELS[c] * scale
       const float v1 = lut[(code[t][1] >> (4 * j)) & 15u] * s[t][1];
-      Tt[(8 * ng + j) * kTStride + kp] = pack_bf16x2(v0, v1);
+      dst[(size_t)j * (a.K / 2)] = pack_bf16x2(v0, v1);
     }
   }
-  __syncthreads();
-  store_tiles<KT>(a, T, tid, k0, n0);
 }
 
 // With an adapter.  Wave w of a tile computes the 32 (k) x 32 (n) block
@@ -225,7 +211,6 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  uint32_t* T = reinterpret_cast<uint32_t*>(smem + kLdsT);
   const bool odd = (lr & 1) != 0;
   const int kpair = 16 * bi + (lr >> 1);
 #pragma unroll
@@ -246,8 +231,10 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
         v[4 * q + e] = w + a.scaling * acc[4 * q + e];
       }
     // the even lane keeps columns q = 0, 1 and receives row k + 1 of them;
-    // the odd lane keeps q = 2, 3 and receives row k - 1 of them
-    uint32_t* Tt = T + t * (kTile * kTStride);
+    // the odd lane keeps q = 2, 3 and receives row k - 1 of them; each
+    // (k, k + 1) pair goes straight to Wt (for one j, 16 lanes write 64
+    // consecutive bytes of one column)
+    uint32_t* dst = reinterpret_cast<uint32_t*>(a.wt + (size_t)n0 * a.K + k0 + kTile * t) + kpair;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float send = odd ? v[j] : v[8 + j];
@@ -256,25 +243,20 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
           __builtin_amdgcn_update_dpp(0u, __float_as_uint(send), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
       const int q = (odd ? 2 : 0) + (j >> 2), e = j & 3;
       const int col = 32 * bj + 8 * q + 4 * h + e;
-      Tt[col * kTStride + kpair] = odd ? pack_bf16x2(got, keep) : pack_bf16x2(keep, got);
+      dst[(size_t)col * (a.K / 2)] = odd ? pack_bf16x2(got, keep) : pack_bf16x2(keep, got);
     }
   }
-  __syncthreads();
-  store_tiles<KT>(a, T, tid, k0, n0);
 }
-
-// LDS of a KT-tile workgroup: the LUT (one copy per wave), then the transpose tiles.
-size_t expand_smem(int KT) { return kLdsT + (size_t)KT * kTBytes; }
 
 template <bool DQ, bool STRIPED, int KT>
 hipError_t launch_kt(const ExpandArgs& a, int n_count, hipStream_t stream) {
   const unsigned grid = (unsigned)((long long)(n_count / kTile) * (a.tiles_k / KT));
   if (a.rank == 0)
-    expand_kernel<DQ, STRIPED, KT><<<grid, 256, expand_smem(KT), stream>>>(a);
+    expand_kernel<DQ, STRIPED, KT><<<grid, 256, kLdsBytes, stream>>>(a);
   else if (a.rp == 16)
-    expand_lora_kernel<DQ, STRIPED, KT, 1><<<grid, 256, expand_smem(KT), stream>>>(a);
+    expand_lora_kernel<DQ, STRIPED, KT, 1><<<grid, 256, kLdsBytes, stream>>>(a);
   else
-    expand_lora_kernel<DQ, STRIPED, 1, kMaxRank / 16><<<grid, 256, expand_smem(1), stream>>>(a);
+    expand_lora_kernel<DQ, STRIPED, 1, kMaxRank / 16><<<grid, 256, kLdsBytes, stream>>>(a);
   return hipGetLastError();
 }
 
