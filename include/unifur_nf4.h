@@ -144,6 +144,16 @@ int unifur_nf4_double_quantize(const float *absmax, uint64_t num_blocks, uint8_t
 int unifur_nf4_dequantize(const uint8_t *packed, const unifur_nf4_scales *scales, uint64_t len, void *out,
                           int out_dtype, void *stream);
 
+/* The simulated form's storage, Nf4Block::codes (src/quantize.rs:68-77): one
+ * code per byte.  unpack_codes writes codes[len] from packed[ceil(len/2)]
+ * (value i from nibble i % 2 of byte i / 2, src/quantize.rs:329-337), the
+ * codes Nf4Tensor::quantize (src/quantize.rs:99-124) holds; pack_codes is
+ * the pairing loop of PackedNf4Tensor::quantize (src/quantize.rs:266-273),
+ * low nibble first, a zero high nibble after an odd length's last code.
+ * Codes are taken modulo 16. */
+int unifur_nf4_unpack_codes(const uint8_t *packed, uint64_t len, uint8_t *codes, void *stream);
+int unifur_nf4_pack_codes(const uint8_t *codes, uint64_t len, uint8_t *packed, void *stream);
+
 /* Nf4Embedding::forward (src/qwennet.rs:288-290): out[t][:] = row ids[t] of
  * the dequantized [n_embedding, d_model] table, held as one packed tensor
  * with its scales (Nf4Embedding::from_values, src/qwennet.rs:265-271); f32

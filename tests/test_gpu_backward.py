@@ -9,8 +9,9 @@ src/qwentrain.rs:421-470, the base weight frozen:
     grad_a = x^T ((dy s) B^T)
 
 Each is checked against the float64 evaluation of those formulas with the
-oracle's dequantized weight (bit-identical to the reference's), normwise
-(max |got - ref| over the sum of absolute products): f32 dy through the f32
+oracle's dequantized weight (bit-identical to the reference's), by the larger of the
+per-element normwise error (max_i |got_i - ref_i| over that element's sum of
+absolute products) and the literal max|got - ref| / max|ref|: f32 dy through the f32
 dequantized weight within 1e-5; bf16 dy through the bf16-expanded weight
 within 1e-2 (the forward GEMM's bar); the adapter gradients, summed in f32,
 within 1e-5 whatever the input types.  A transposed factor, a dropped
@@ -34,8 +35,15 @@ pytestmark = pytest.mark.gpu
 
 
 def normwise(got, ref, bound):
+    """max over elements of |got_i - ref_i| / bound_i (the per-element
+    normwise error of test_gpu_linear.check), or the BASELINE-literal
+    max|got - ref| / max|ref| when that is larger: both are held to the
+    tolerance."""
     got = np.asarray(got, np.float64)
-    return float(np.max(np.abs(got - ref)) / max(float(np.max(bound)), 1e-30))
+    ref = np.asarray(ref, np.float64)
+    per_elem = float(np.max(np.abs(got - ref) / np.maximum(np.asarray(bound, np.float64), 1e-30)))
+    literal = float(np.max(np.abs(got - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
+    return max(per_elem, literal)
 
 
 def refs(x, dy, wdeq, a, b, s):

@@ -108,3 +108,96 @@ def test_skinny_split_and_gemv_replay(device, oracle):
         y1.copy_(lin.forward(x1))
 
     replay_matches(run, lambda: [y16, y1])
+
+
+def _hip():
+    import ctypes
+    h = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch and the library already share
+    P = ctypes.c_void_p
+    h.hipStreamCreateWithFlags.argtypes = [ctypes.POINTER(P), ctypes.c_uint]
+    h.hipStreamBeginCapture.argtypes = [P, ctypes.c_int]
+    h.hipStreamEndCapture.argtypes = [P, ctypes.POINTER(P)]
+    h.hipGraphGetNodes.argtypes = [P, P, ctypes.POINTER(ctypes.c_size_t)]
+    h.hipGraphInstantiate.argtypes = [ctypes.POINTER(P), P, P, P, ctypes.c_size_t]
+    h.hipGraphLaunch.argtypes = [P, P]
+    h.hipStreamSynchronize.argtypes = [P]
+    for f in ("hipGraphDestroy", "hipGraphExecDestroy", "hipStreamDestroy"):
+        getattr(h, f).argtypes = [P]
+    return h
+
+
+def test_internal_workspace_under_capture(device, oracle):
+    # The internal workspace (workspace == NULL) of a stream: a call under
+    # capture that would have to create or grow it is refused with
+    # UNIFUR_NF4_ERR_WORKSPACE and records nothing; a graph captured from a
+    # small call keeps replaying correctly after eager calls on the same
+    # stream have grown the workspace past it (outgrown buffers stay alive).
+    import ctypes
+    from unifur_amd import _lib as L
+    h = _hip()
+    lib = L.lib()
+    P = ctypes.c_void_p
+    relaxed = 2  # hipStreamCaptureModeRelaxed
+    s = P()
+    assert h.hipStreamCreateWithFlags(ctypes.byref(s), 1) == 0  # a new stream: no workspace yet
+    try:
+        lin, _ = make_linear(oracle, 1024, 512, 2040, device)
+        _, x1 = acts(oracle, 2, 1024, 2041, torch.float32, device)
+        _, xb = acts(oracle, 300, 1024, 2042, torch.bfloat16, device)
+        w = lin.weight_struct()
+        y1 = torch.empty(2, 512, device=device)
+        yb = torch.empty(300, 512, device=device)
+        torch.cuda.synchronize()
+
+        def small():
+            return lib.unifur_nf4_linear_forward(x1.data_ptr(), L.F32, 2, ctypes.byref(w), None, None,
+                                                 y1.data_ptr(), L.F32, None, 0, s)
+
+        def large():
+            return lib.unifur_nf4_linear_forward(xb.data_ptr(), L.BF16, 300, ctypes.byref(w), None, None,
+                                                 yb.data_ptr(), L.F32, None, 0, s)
+
+        graph = P()
+        assert h.hipStreamBeginCapture(s, relaxed) == 0
+        st = small()
+        assert h.hipStreamEndCapture(s, ctypes.byref(graph)) == 0
+        n = ctypes.c_size_t(0)
+        assert h.hipGraphGetNodes(graph, None, ctypes.byref(n)) == 0
+        h.hipGraphDestroy(graph)
+        assert st == L.ERR_WORKSPACE and b"capturing" in lib.unifur_nf4_last_error()
+        assert n.value == 0, "a refused call recorded graph nodes"
+
+        # eager call sizes the workspace, then capture the small call
+        assert small() == 0
+        assert h.hipStreamSynchronize(s) == 0
+        want = y1.clone()
+        assert h.hipStreamBeginCapture(s, relaxed) == 0
+        assert small() == 0
+        assert h.hipStreamEndCapture(s, ctypes.byref(graph)) == 0
+        ex = P()
+        assert h.hipGraphInstantiate(ctypes.byref(ex), graph, None, None, 0) == 0
+        # a larger call of the same stream under capture is refused too
+        assert h.hipStreamBeginCapture(s, relaxed) == 0
+        st = large()
+        g2 = P()
+        assert h.hipStreamEndCapture(s, ctypes.byref(g2)) == 0
+        h.hipGraphDestroy(g2)
+        assert st == L.ERR_WORKSPACE
+        # eagerly it grows the workspace; the captured graph still replays
+        assert large() == 0
+        assert h.hipStreamSynchronize(s) == 0
+        want_b = yb.clone()
+        for _ in range(3):
+            y1.fill_(float("nan"))
+            torch.cuda.synchronize()
+            assert h.hipGraphLaunch(ex, s) == 0
+            assert h.hipStreamSynchronize(s) == 0
+            assert torch.equal(y1, want), "replay after the workspace grew differs"
+            assert large() == 0
+            assert h.hipStreamSynchronize(s) == 0
+            assert torch.equal(yb, want_b)
+        h.hipGraphExecDestroy(ex)
+        h.hipGraphDestroy(graph)
+    finally:
+        assert h.hipStreamSynchronize(s) == 0
+        h.hipStreamDestroy(s)

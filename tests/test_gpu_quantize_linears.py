@@ -49,6 +49,34 @@ def test_config5_projection_shapes(device, oracle):
         same_bytes(g, per_weight(v, di, do))
 
 
+def test_config5_all_weights_against_the_oracle(device, oracle):
+    # QwenTrunk::to_nf4 over the config-5 projection set (src/qwennet.rs:1196-1269):
+    # 24 layers x {q, k, v, o, gate, up, down}, 168 weights ~ N(0, 0.02^2), in
+    # ONE grouped call; every weight's striped codes, u8 scales and scale of
+    # scales equal the oracle's PackedNf4Tensor::quantize +
+    # with_double_quantization (src/quantize.rs:259-309) in the documented
+    # striped permutation, byte for byte.
+    from test_gpu_layout import striped_codes_np, striped_scales_np
+    per_layer = [(896, 896), (896, 128), (896, 128), (896, 896), (896, 4864), (896, 4864), (4864, 896)]
+    shapes = per_layer * 24
+    host, dev = [], []
+    for i, (di, do) in enumerate(shapes):
+        v = oracle.fill_normal(0x4E463457 + 5 + 0x10000 * i, 0.02, di * do)
+        host.append(v)
+        dev.append((torch.from_numpy(v).to(device), di, do))
+    got = Q.quantize_linears(dev)
+    torch.cuda.synchronize()
+    assert len(got) == 168
+    for i, ((di, do), v, g) in enumerate(zip(shapes, host, got)):
+        packed, absmax = oracle.quantize_packed(v)
+        q, sos = oracle.double_quantize(absmax)
+        assert g.is_striped()
+        assert np.array_equal(g._codes.cpu().numpy(), striped_codes_np(packed, di, do)), f"weight {i}: codes"
+        assert np.array_equal(g._scales.cpu().numpy(), striped_scales_np(q, di, do)), f"weight {i}: u8 scales"
+        assert g._sos.cpu().numpy().view(np.uint32)[0] == np.float32(sos).view(np.uint32), f"weight {i}: sos"
+    print(f"config 5: {sum(a * b for a, b in shapes)} values in 168 weights byte-exact", flush=True)
+
+
 def test_partial_spans_tiny_and_many(device, oracle):
     # 50 weights (two groups), spans crossing rows and ending mid-span
     shapes = [(1, 64), (3, 128), (17, 192), (5, 64), (33, 320), (2, 1024), (7, 960)] * 7 + [(1, 64)]

@@ -74,6 +74,8 @@ SIGNATURES = {
     "unifur_nf4_quantize": (_I, [_P, _U64, _P, _P, _P]),
     "unifur_nf4_double_quantize": (_I, [_P, _U64, _P, _P, _P]),
     "unifur_nf4_dequantize": (_I, [_P, ctypes.POINTER(Scales), _U64, _P, _I, _P]),
+    "unifur_nf4_unpack_codes": (_I, [_P, _U64, _P, _P]),
+    "unifur_nf4_pack_codes": (_I, [_P, _U64, _P, _P]),
     "unifur_nf4_quantize_transposed": (_I, [_P, _I, _U64, _U64, _P, _P, _P]),
     "unifur_nf4_quantize_linears_workspace_size": (_U64, [_P, _P, ctypes.c_uint32]),
     "unifur_nf4_quantize_linears": (_I, [_P, _P, _P, ctypes.c_uint32, _P, _P, _P, _P, _U64, _P]),

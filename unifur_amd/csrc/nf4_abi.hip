@@ -112,6 +112,12 @@ WsCache& ws_cache() {
 }
 
 // Internal workspace for (current device, stream), zero-filled when created.
+// It only grows, and a buffer it outgrows is never freed: a graph captured
+// from an earlier call may still hold its address, and a later replay must
+// find it alive.  Under stream capture nothing is allocated, synchronized or
+// filled: a call that would have to create or grow the buffer there fails
+// with UNIFUR_NF4_ERR_WORKSPACE (make one eager call of the largest shape
+// first, or pass a workspace).
 int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
   int dev = 0;
   UNIFUR_HIP(hipGetDevice(&dev));
@@ -119,16 +125,20 @@ int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
   std::lock_guard<std::mutex> lock(c.mu);
   auto& slot = c.buffers[{dev, stream}];
   if (slot.second < bytes) {
-    if (slot.first) {
-      UNIFUR_HIP(hipStreamSynchronize(stream));
-      UNIFUR_HIP(hipFree(slot.first));
-      slot = {nullptr, 0};
-    }
-    const size_t sz = align_up(bytes < (1u << 20) ? (1u << 20) : bytes);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    UNIFUR_HIP(hipStreamIsCapturing(stream, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(UNIFUR_NF4_ERR_WORKSPACE,
+                  "the internal workspace of this stream holds " + std::to_string(slot.second) + " bytes, " +
+                      std::to_string(bytes) + " needed, and the stream is capturing: make one eager call of "
+                      "this shape first or pass a workspace");
+    // grow at least twofold, so a rising sequence of shapes retires few buffers
+    const size_t want = std::max<size_t>({bytes, size_t{1} << 20, 2 * slot.second});
+    const size_t sz = align_up(want);
     void* p = nullptr;
     UNIFUR_HIP(hipMalloc(&p, sz));
     UNIFUR_HIP(hipMemsetAsync(p, 0, sz, stream));
-    slot = {p, sz};
+    slot = {p, sz};  // the outgrown buffer stays allocated until the process ends
   }
   *out = slot.first;
   return UNIFUR_NF4_OK;
@@ -977,6 +987,20 @@ int unifur_nf4_dequantize(const uint8_t* packed, const unifur_nf4_scales* scales
                        (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
   UNIFUR_HIP(launch_dequantize(packed, to_scales(*scales), len, out, out_dtype == UNIFUR_NF4_BF16, aligned,
                                static_cast<hipStream_t>(stream)));
+  return UNIFUR_NF4_OK;
+}
+
+int unifur_nf4_unpack_codes(const uint8_t* packed, uint64_t len, uint8_t* codes, void* stream) {
+  if (len == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(packed && codes, "packed or codes is NULL");
+  UNIFUR_HIP(launch_unpack_codes(packed, len, codes, static_cast<hipStream_t>(stream)));
+  return UNIFUR_NF4_OK;
+}
+
+int unifur_nf4_pack_codes(const uint8_t* codes, uint64_t len, uint8_t* packed, void* stream) {
+  if (len == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(packed && codes, "packed or codes is NULL");
+  UNIFUR_HIP(launch_pack_codes(codes, len, packed, static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
 }
 

@@ -593,6 +593,44 @@ hipError_t launch_quantize_transposed(const void* src, bool bf16_in, uint64_t ou
 }
 
 
+// The simulated form's storage (src/quantize.rs:68-95): one code per byte.
+// Thread i owns packed byte i, i.e. values 2i and 2i + 1 (low nibble first,
+// src/quantize.rs:329-337).  Unpack writes both codes (only the first when
+// 2i + 1 is past the end); pack joins them, with a zero high nibble for an
+// odd length's last byte, as PackedNf4Tensor::quantize does
+// (src/quantize.rs:266-273).
+__global__ __launch_bounds__(256) void unpack_codes_kernel(const uint8_t* __restrict__ packed, size_t len,
+                                                           uint8_t* __restrict__ codes) {
+  const size_t bytes = (len + 1) / 2;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes; i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t b = packed[i];
+    codes[2 * i] = (uint8_t)(b & 15u);
+    if (2 * i + 1 < len) codes[2 * i + 1] = (uint8_t)(b >> 4);
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_codes_kernel(const uint8_t* __restrict__ codes, size_t len,
+                                                         uint8_t* __restrict__ packed) {
+  const size_t bytes = (len + 1) / 2;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes; i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t lo = codes[2 * i] & 15u;
+    const uint32_t hi = 2 * i + 1 < len ? (codes[2 * i + 1] & 15u) : 0u;
+    packed[i] = (uint8_t)(lo | (hi << 4));
+  }
+}
+
+hipError_t launch_unpack_codes(const uint8_t* packed, size_t len, uint8_t* codes, hipStream_t stream) {
+  if (len == 0) return hipSuccess;
+  unpack_codes_kernel<<<grid_for((len + 1) / 2, 256, 8192), 256, 0, stream>>>(packed, len, codes);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_codes(const uint8_t* codes, size_t len, uint8_t* packed, hipStream_t stream) {
+  if (len == 0) return hipSuccess;
+  pack_codes_kernel<<<grid_for((len + 1) / 2, 256, 8192), 256, 0, stream>>>(codes, len, packed);
+  return hipGetLastError();
+}
+
 size_t quantize_linears_scratch_bytes(const uint64_t* d_in, const uint64_t* d_out, uint32_t n) {
   size_t total = 0;
   for (uint32_t i = 0; i < n; ++i) total += ((size_t)(d_in[i] * (d_out[i] / kBlock) * 4) + 255) & ~size_t{255};

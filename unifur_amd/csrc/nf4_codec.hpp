@@ -25,6 +25,9 @@ hipError_t launch_quantize_transposed(const void* src, bool bf16_in, uint64_t ou
                                       float* absmax, hipStream_t stream);
 hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, size_t n, void* out, bool bf16_out,
                              bool aligned, hipStream_t stream);
+// One code per byte (the simulated Nf4Tensor's storage) <-> two per byte.
+hipError_t launch_unpack_codes(const uint8_t* packed, size_t len, uint8_t* codes, hipStream_t stream);
+hipError_t launch_pack_codes(const uint8_t* codes, size_t len, uint8_t* packed, hipStream_t stream);
 // The quantize pass of n linears: row-major f32 values[i] [d_in[i], d_out[i]]
 // (d_out % 64 == 0, values 16-byte and packed 8-byte aligned) quantized with
 // double quantization into the striped resident form (packed[i] striped

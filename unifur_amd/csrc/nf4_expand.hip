@@ -121,9 +121,11 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 // columns 8 q + 4 (l / 32) + e (acc[4 q + e]) of the block, so each lane
 // loads the codes of exactly those 16 (row, column) entries and adds the
 // product in registers.  Adjacent lanes (rows k, k + 1) then swap half of
-// their columns by DPP so that each holds whole (k, k + 1) pairs for the
-// transpose tiles.  The factors' MFMA fragments are read straight from the
-// f32 A [K][rank] and B [rank][N] and rounded to bf16 in registers.
+// their columns by DPP so that each holds whole (k, k + 1) bf16 pairs, and
+// stores every pair as one dword of Wt[n][k] straight from registers (a
+// half-wave writes 128 or 64 contiguous bytes of a column; no LDS tile).
+// The factors' MFMA fragments are read straight from the f32 A [K][rank]
+// and B [rank][N] and rounded to bf16 in registers.
 template <bool DQ, bool STRIPED, int KT, int NFR>
 __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];

@@ -143,46 +143,73 @@ class PackedNf4Tensor:
 
 
 class Nf4Tensor:
-    """The reference's simulated form (one code per byte, src/quantize.rs:79-201).
+    """The reference's simulated form (src/quantize.rs:79-201): one code per
+    byte (``codes``, u8[len], the concatenated ``Nf4Block::codes``), the f32
+    absmax of every block (kept after double quantization, as the
+    reference's blocks keep theirs), and with double quantization the u8
+    scale codes and the scale of scales.
 
-    It is numerically identical to the packed form (src/quantize.rs:240-247),
-    so it is held packed on the device; only its accounting differs."""
+    Its codes are those of the packed codec (PackedNf4Tensor::quantize takes
+    them from Nf4Tensor::quantize, src/quantize.rs:262-265), unpacked on the
+    device; its dequantize packs them back and runs the packed dequantize,
+    which is bit-identical to Nf4Tensor::dequantize (src/quantize.rs:353-354)."""
 
-    def __init__(self, packed: PackedNf4Tensor):
-        self._packed = packed
+    def __init__(self, codes: torch.Tensor, absmax: torch.Tensor, dq_codes: Optional[torch.Tensor] = None,
+                 scale_of_scales: Optional[torch.Tensor] = None):
+        self.codes = codes
+        self.absmax = absmax
+        self.dq_codes = dq_codes
+        self.scale_of_scales = scale_of_scales
 
     @staticmethod
     def quantize(values: torch.Tensor) -> "Nf4Tensor":
-        return Nf4Tensor(PackedNf4Tensor.quantize(values))
+        """Nf4Tensor::quantize (src/quantize.rs:99-124)."""
+        p = PackedNf4Tensor.quantize(values)
+        codes = torch.empty(len(p), dtype=torch.uint8, device=values.device)
+        L.check(L.lib().unifur_nf4_unpack_codes(p.codes.data_ptr(), len(p), codes.data_ptr(), _stream()))
+        return Nf4Tensor(codes, p.absmax)
 
     def with_double_quantization(self) -> "Nf4Tensor":
-        return Nf4Tensor(self._packed.with_double_quantization())
+        """src/quantize.rs:128-149: recomputed from the kept absmax values,
+        so applying it twice gives the same codes."""
+        nb = self.num_blocks()
+        dq = torch.empty(nb, dtype=torch.uint8, device=self.codes.device)
+        sos = torch.empty(1, dtype=torch.float32, device=self.codes.device)
+        L.check(L.lib().unifur_nf4_double_quantize(self.absmax.data_ptr(), nb, dq.data_ptr(), sos.data_ptr(),
+                                                   _stream()))
+        return Nf4Tensor(self.codes, self.absmax, dq_codes=dq, scale_of_scales=sos)
 
     def is_double_quantized(self) -> bool:
-        return self._packed.is_double_quantized()
+        return self.dq_codes is not None
 
     def len(self) -> int:
-        return len(self._packed)
+        return self.codes.numel()
 
     def __len__(self) -> int:
-        return len(self._packed)
+        return self.codes.numel()
 
     def is_empty(self) -> bool:
-        return self._packed.is_empty()
+        return self.codes.numel() == 0
 
     def num_blocks(self) -> int:
-        return self._packed.num_blocks()
+        return self.absmax.numel()
+
+    def packed(self) -> PackedNf4Tensor:
+        """The same codes two per byte, with this tensor's scales."""
+        n = self.len()
+        bytes_ = torch.empty((n + 1) // 2, dtype=torch.uint8, device=self.codes.device)
+        L.check(L.lib().unifur_nf4_pack_codes(self.codes.data_ptr(), n, bytes_.data_ptr(), _stream()))
+        if self.is_double_quantized():
+            return PackedNf4Tensor(bytes_, n, dq_codes=self.dq_codes, scale_of_scales=self.scale_of_scales)
+        return PackedNf4Tensor(bytes_, n, absmax=self.absmax)
 
     def dequantize(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
-        return self._packed.dequantize(dtype)
+        """Nf4Tensor::dequantize (src/quantize.rs:177-185)."""
+        return self.packed().dequantize(dtype)
 
     def bits_per_value(self) -> float:
         """src/quantize.rs:190-200: quotes a 4-bit payload it does not pack."""
-        return float(L.lib().unifur_nf4_simulated_bits_per_value(len(self._packed),
-                                                                 int(self.is_double_quantized())))
-
-    def packed(self) -> PackedNf4Tensor:
-        return self._packed
+        return float(L.lib().unifur_nf4_simulated_bits_per_value(self.len(), int(self.is_double_quantized())))
 
 
 def quantize_dequantize_tensor(tensor: torch.Tensor, double_quantization: bool) -> torch.Tensor:
