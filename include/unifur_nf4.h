@@ -250,6 +250,21 @@ int unifur_nf4_linear_forward_multi(const void *x, int x_dtype, uint64_t rows, c
                                     const float *const *bias, void *const *y, int y_dtype, uint32_t n,
                                     void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): unifur_nf4_linear_forward without a workspace argument.
+ * It allocates nothing -- no hipMalloc / hipFree, no allocating library
+ * call -- and uses a static device scratch of 16 MiB per GPU (held until the
+ * process ends).  Batches of more than 64 bf16 rows take the fused MFMA
+ * kernel (the unifur_nf4_linear_min_workspace_size path), never the expanded
+ * weight.  A call whose scratch need exceeds 16 MiB fails with
+ * UNIFUR_NF4_ERR_WORKSPACE and a message naming the size.  All calls on one
+ * GPU share that scratch: calls that overlap on one GPU (concurrent streams
+ * or threads) race and must be serialized by the caller. */
+int unifur_nf4_linear_forward_noalloc(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,
+                                      const float *bias, const unifur_nf4_lora *lora, void *y, int y_dtype,
+                                      void *stream);
+
 /* QloraLinear::forward (src/qwennet.rs:325-345); identical to
  * unifur_nf4_linear_forward with a non-NULL lora. */
 int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,

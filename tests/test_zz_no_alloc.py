@@ -1,0 +1,110 @@
+"""The allocation-free linear entry point (unifur_nf4_linear_forward_noalloc).
+
+It has no counterpart in the reference: it is unifur_nf4_linear_forward for
+callers that cannot allocate, running on a static per-GPU scratch.  Each case
+calls it through the C ABI twice in a row -- the second call with a smaller
+input, so that it runs on the scratch the first call left behind -- and
+compares every output bit for bit with unifur_nf4_linear_forward given its
+least workspace (unifur_nf4_linear_min_workspace_size: the same kernels), and
+the prefill case also against the float64 product within the bf16 bar.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from unifur_amd import _lib as L
+from unifur_amd import quantize as Q
+
+from test_gpu_gemm import lora_parts
+from test_gpu_linear import TOL_BF16, acts, check, make_linear
+
+pytestmark = pytest.mark.gpu
+
+
+def _dt(t: torch.dtype) -> int:
+    return L.BF16 if t == torch.bfloat16 else L.F32
+
+
+def existing(lin, x, lora, y_dtype, bias=None):
+    """unifur_nf4_linear_forward with the least workspace it accepts."""
+    lib = L.lib()
+    w = lin.weight_struct()
+    rows, d_in = x.shape
+    rank = lora.rank if lora is not None else 0
+    need = lib.unifur_nf4_linear_min_workspace_size(rows, d_in, lin.d_output(), _dt(x.dtype), rank)
+    ws = torch.zeros(max(int(need), 1), dtype=torch.uint8, device=x.device)
+    y = torch.empty(rows, lin.d_output(), dtype=y_dtype, device=x.device)
+    L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), _dt(x.dtype), rows, ctypes.byref(w),
+                                          bias.data_ptr() if bias is not None else None,
+                                          ctypes.byref(lora) if lora is not None else None, y.data_ptr(),
+                                          _dt(y_dtype), ws.data_ptr(), int(need),
+                                          torch.cuda.current_stream().cuda_stream))
+    return y
+
+
+def noalloc(lin, x, lora, y_dtype, bias=None):
+    lib = L.lib()
+    w = lin.weight_struct()
+    rows = x.shape[0]
+    y = torch.empty(rows, lin.d_output(), dtype=y_dtype, device=x.device)
+    L.check(lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), _dt(x.dtype), rows, ctypes.byref(w),
+                                                  bias.data_ptr() if bias is not None else None,
+                                                  ctypes.byref(lora) if lora is not None else None, y.data_ptr(),
+                                                  _dt(y_dtype), torch.cuda.current_stream().cuda_stream))
+    return y
+
+
+@pytest.mark.parametrize("case", [
+    # (rows of the first call, rows of the second, d_in, d_out, x dtype, y dtype, lora rank, striped)
+    (4, 1, 4096, 11008, torch.float32, torch.float32, 0, True),      # config-2 GEMV
+    (3, 1, 1024, 512, torch.bfloat16, torch.float32, 8, False),      # row-major GEMV with an adapter
+    (48, 16, 4096, 11008, torch.bfloat16, torch.bfloat16, 0, True),  # skinny MFMA, split d_in
+    (300, 100, 1024, 768, torch.bfloat16, torch.bfloat16, 16, True),  # fused prefill GEMM with LoRA
+    (2048, 256, 4096, 4096, torch.bfloat16, torch.bfloat16, 16, True),  # config 3, then a smaller batch
+    (20, 7, 512, 384, torch.float32, torch.float32, 4, False),      # generic dequantize + f32 GEMM
+])
+def test_noalloc_matches_linear_forward_twice(device, oracle, case):
+    m1, m2, k, n, xt, yt, r, striped = case
+    print(f"noalloc case {case}", flush=True)
+    lin, wdeq = make_linear(oracle, k, n, 5000 + k + n, device, dq=True, striped=striped)
+    lora = None
+    if r:
+        a, b, ad = lora_parts(oracle, k, n, r, 5001 + r, device)
+        lora = ad.struct()
+    bias = torch.from_numpy(oracle.fill_normal(5002, 0.1, n)).to(device)
+    for m, seed in ((m1, 5003), (m2, 5004)):
+        x, xd = acts(oracle, m, k, seed, xt, device)
+        want = existing(lin, xd, lora, yt, bias)
+        got = noalloc(lin, xd, lora, yt, bias)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"rows {m}: noalloc output differs from linear_forward"
+        if m == m1 and m >= 300:
+            ref = oracle.linear_ref_f64(x, wdeq, oracle.fill_normal(5002, 0.1, n))
+            if r:
+                ref = ref + oracle.lora_ref_f64(x, a, b, ad.scaling())
+            check(got, ref, x, wdeq, TOL_BF16, f"noalloc rows {m}")
+
+
+def test_noalloc_refuses_what_does_not_fit(device, oracle):
+    # f32 activations over 4 rows take the generic path: the whole weight
+    # dequantized to f32 (4096 * 11008 * 4 bytes) does not fit the scratch
+    lin, _ = make_linear(oracle, 4096, 11008, 5100, device)
+    _, x = acts(oracle, 8, 4096, 5101, torch.float32, device)
+    w = lin.weight_struct()
+    y = torch.empty(8, 11008, device=device)
+    lib = L.lib()
+    st = lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), L.F32, 8, ctypes.byref(w), None, None, y.data_ptr(),
+                                               L.F32, torch.cuda.current_stream().cuda_stream)
+    assert st == L.ERR_WORKSPACE and b"16777216" in lib.unifur_nf4_last_error()
+    # and bad arguments are refused like the existing entry point's
+    assert lib.unifur_nf4_linear_forward_noalloc(None, L.F32, 1, ctypes.byref(w), None, None, y.data_ptr(), L.F32,
+                                                 None) == L.ERR_INVALID
+    assert lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), 7, 1, ctypes.byref(w), None, None, y.data_ptr(),
+                                                 L.F32, None) == L.ERR_INVALID
+    # an empty batch does nothing
+    assert lib.unifur_nf4_linear_forward_noalloc(None, L.F32, 0, ctypes.byref(w), None, None, None, L.F32,
+                                                 None) == L.OK

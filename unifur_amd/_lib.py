@@ -96,6 +96,8 @@ SIGNATURES = {
     "unifur_nf4_linear_min_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
     "unifur_nf4_linear_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), _P, ctypes.POINTER(Lora), _P, _I,
                                        _P, _U64, _P]),
+    "unifur_nf4_linear_forward_noalloc": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), _P, ctypes.POINTER(Lora), _P,
+                                               _I, _P]),
     "unifur_nf4_qlora_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Lora), _P, _I, _P,
                                       _U64, _P]),
     "unifur_nf4_swiglu_workspace_size": (_U64, [_U64, _U64, _U64, _I]),

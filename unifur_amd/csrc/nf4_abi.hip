@@ -296,9 +296,11 @@ GemvWeight gemv_weight(const unifur_nf4_weight* w, void* y, bool y_bf16, unsigne
   return g;
 }
 
+// allow_expand == false keeps prefill batches on the fused MFMA kernel (no
+// weight-sized scratch, no BLAS call), whatever the workspace size.
 int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w, const float* bias,
                const unifur_nf4_lora* lora, void* y, int y_dtype, void* workspace, uint64_t workspace_bytes,
-               hipStream_t stream) {
+               hipStream_t stream, bool allow_expand = true) {
   UNIFUR_ARG(valid_dtype(x_dtype) && valid_dtype(y_dtype), "dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
   if (int r = check_weight(w, "linear")) return r;
   if (rows == 0) return UNIFUR_NF4_OK;
@@ -309,7 +311,8 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     UNIFUR_ARG(lora->a != nullptr && lora->b != nullptr, "lora factors are NULL");
     UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
   }
-  LinearLayout L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind);
+  LinearLayout L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind,
+                               allow_expand);
   if (L.path == LinearPath::kMfma && L.expand &&
       ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
     // a workspace too small for the expanded weight (or an output the BLAS
@@ -920,6 +923,78 @@ int run_linear_multi(const void* x, int x_dtype, uint64_t rows, const unifur_nf4
   return UNIFUR_NF4_OK;
 }
 
+// ------------------------------------------------- allocation-free entry --
+
+// The scratch of unifur_nf4_linear_forward_noalloc: a file-scope device array,
+// one copy per GPU the library runs on, held until the process ends.  In host
+// code its name is only a symbol: kernels and fills get the per-device address
+// that hipGetSymbolAddress returns, kept in static_scratch().
+constexpr size_t kStaticScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+__global__ void zero_words_kernel(uint32_t* p, size_t words) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+struct StaticScratch {
+  std::mutex mu;
+  std::map<int, void*> ptr;  // device -> address of its copy of `scratch`
+};
+
+StaticScratch& static_scratch() {
+  static StaticScratch* s = new StaticScratch();  // never destroyed, like the workspaces
+  return *s;
+}
+
+// Set-up on the first call on a device, with that device current: look up
+// this device's address of `scratch` and clear its arrival-counter region
+// (the only part a call expects to find zero; every call leaves it zero) with
+// a fill kernel on the caller's stream, ahead of the call's own launches.  A
+// first call under stream capture records that fill in the graph and sets up
+// again on the next call.
+int static_scratch_address(hipStream_t stream, void** out) {
+  int dev = 0;
+  UNIFUR_HIP(hipGetDevice(&dev));
+  StaticScratch& s = static_scratch();
+  std::lock_guard<std::mutex> lock(s.mu);
+  const auto it = s.ptr.find(dev);
+  if (it != s.ptr.end()) {
+    *out = it->second;
+    return UNIFUR_NF4_OK;
+  }
+  void* p = nullptr;
+  UNIFUR_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  if (p == nullptr) return fail(UNIFUR_NF4_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch");
+  zero_words_kernel<<<16, 256, 0, stream>>>(static_cast<uint32_t*>(p), kCounterRegion / sizeof(uint32_t));
+  UNIFUR_HIP(hipGetLastError());
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  UNIFUR_HIP(hipStreamIsCapturing(stream, &cap));
+  if (cap == hipStreamCaptureStatusNone) s.ptr[dev] = p;
+  *out = p;
+  return UNIFUR_NF4_OK;
+}
+
+int run_linear_noalloc(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w, const float* bias,
+                       const unifur_nf4_lora* lora, void* y, int y_dtype, hipStream_t stream) {
+  UNIFUR_ARG(valid_dtype(x_dtype) && valid_dtype(y_dtype), "dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  if (int r = check_weight(w, "linear")) return r;
+  if (rows == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(x != nullptr && y != nullptr, "x or y is NULL");
+  UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  const uint32_t rank = lora ? lora->rank : 0;
+  if (lora) UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
+  const LinearLayout L =
+      plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false);
+  if (L.total > kStaticScratchBytes)
+    return fail(UNIFUR_NF4_ERR_WORKSPACE, "linear_forward_noalloc: this call needs " + std::to_string(L.total) +
+                                              " bytes of scratch, the allocation-free entry point holds " +
+                                              std::to_string(kStaticScratchBytes));
+  void* p = nullptr;
+  if (int r = static_scratch_address(stream, &p)) return r;
+  return run_linear(x, x_dtype, rows, w, bias, lora, y, y_dtype, p, kStaticScratchBytes, stream, false);
+}
+
 }  // namespace
 }  // namespace unifur
 
@@ -1099,6 +1174,12 @@ int unifur_nf4_linear_forward(const void* x, int x_dtype, uint64_t rows, const u
                               uint64_t workspace_bytes, void* stream) {
   return run_linear(x, x_dtype, rows, w, bias, lora, y, y_dtype, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream));
+}
+
+int unifur_nf4_linear_forward_noalloc(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w,
+                                      const float* bias, const unifur_nf4_lora* lora, void* y, int y_dtype,
+                                      void* stream) {
+  return run_linear_noalloc(x, x_dtype, rows, w, bias, lora, y, y_dtype, static_cast<hipStream_t>(stream));
 }
 
 int unifur_nf4_qlora_forward(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w,
