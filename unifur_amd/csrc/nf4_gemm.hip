@@ -10,20 +10,23 @@
 //
 // Tiling.  A 512-thread workgroup computes a 256 x 128 output tile, K in
 // steps of 64.  It is warp-specialised: four MFMA waves (one per SIMD) each
-// own 64 rows x 128 columns (2 x 4 MFMA 32x32x16 tiles, f32 accumulators)
-// and only read LDS and issue MFMAs; four producer waves (one per SIMD
-// beside an MFMA wave) copy X into LDS with coalesced buffer_load ... lds
-// copies (three stages, two steps ahead) and expand the NF4 codes (byte LUT
-// -> level pair, x block scale, -> bf16) into a double-buffered W tile
+// own 64 rows x 128 columns (2 x 4 MFMA 32x32x16 tiles, f32 accumulators),
+// copy their own X rows into LDS with coalesced buffer_load ... lds copies
+// (three stages, two steps ahead), read operand fragments one k16 slice
+// ahead of the MFMAs and issue the MFMAs; four producer waves (one per SIMD
+// beside an MFMA wave) expand the NF4 codes (byte LUT -> level pair, x
+// block scale, -> bf16) two steps ahead into a three-buffer W tile ring
 // stored [n][k], so that every MFMA operand fetch is one 16-byte ds_read.
-// Their VALU / LDS / memory work overlaps the MFMAs on the same SIMD; one
-// workgroup barrier per step hands the buffers over.  Both tiles use a
-// 16-byte-chunk XOR swizzle, chunk ^ ((row % 8) ^ (row / 8 % 8)), which
-// makes the operand reads (8 consecutive rows, one chunk) conflict-free.
+// Their VALU / LDS work overlaps the MFMAs on the same SIMD; one workgroup
+// barrier per step (an LDS-only barrier: no wait for outstanding global
+// loads) hands the W buffers over.  Both tiles use a 16-byte-chunk XOR
+// swizzle, chunk ^ ((row % 8) ^ (row / 8 % 8)), which makes the operand
+// reads (8 consecutive rows, one chunk) conflict-free.
 #include "nf4_gemm.hpp"
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 namespace unifur {
 namespace {
@@ -34,15 +37,17 @@ constexpr int kBTileBytes = kBN * kBK * 2;       // dequantized bf16 W tile: 16 
 constexpr int kATileBytes = kBM * kBK * 2;       // X tile: 32 KiB (8 KiB per wave)
 constexpr int kAStages = 3;
 constexpr int kLdsA = 0;                         // kAStages buffers
-constexpr int kLdsB = kAStages * kATileBytes;    // 2 buffers
-constexpr int kLdsLut = kLdsB + 2 * kBTileBytes; // byte LUT, 256 x f32x2
+constexpr int kBStages = 3;
+constexpr int kLdsB = kAStages * kATileBytes;    // kBStages buffers
+constexpr int kLdsLut = kLdsB + kBStages * kBTileBytes;  // byte LUT, 256 x f32x2
 constexpr int kLdsDq = kLdsLut + 256 * 8;        // DQ scale LUT, 256 x f32
-constexpr size_t kGemmSmem = kLdsDq + 256 * 4;   // 131 KiB: one workgroup per CU
+constexpr size_t kGemmSmem = kLdsDq + 256 * 4;   // 147 KiB: one workgroup per CU
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
 typedef __attribute__((address_space(3))) const f32x2 lds_f32x2_c;
 
 struct GemmArgs {
@@ -83,85 +88,104 @@ __device__ __forceinline__ void load_a(__amdgpu_buffer_rsrc_t xr, int K, int row
   }
 }
 
-// NF4 codes and block scales of one K step: thread t covers rows 4 (t / 16)
-// .. + 3 and columns 8 (t % 16) .. + 7 of the 64 x 128 W tile.
+// NF4 codes and block scales of one K step for producer thread d (0..255):
+// stripe st = d / 32 of the tile (columns n0 + 16 st .. + 15) at rows
+// k0 + 2 (d % 32) and the next -- 8 code bytes of each row.  The 256 threads
+// cover the 64 x 128 W tile once.
 struct BStep {
-  uint32_t code[4];
-  uint32_t scale[4];
+  uint32_t code[4];   // row 0 bytes 0-3, 4-7, then row 1
+  uint32_t scale[2];  // f32 bits, or u8 DQ codes (striped DQ: both rows in scale[0])
 };
 
-// The producer's vmcnt arithmetic counts these: the B loads of one step (4
-// code dwords, and 4 scale loads row-major or 1 striped).
-template <bool STRIPED>
-constexpr int kStepLoads = 4 + (STRIPED ? 1 : 4);
-
 template <bool DQ, bool STRIPED>
-__device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int k0, int tid) {
-  const int c = tid & 15, g4 = tid >> 4;
-  const int n = n0 + 8 * c, k = k0 + 4 * g4;  // first column and row of this thread's 4 x 8 codes
+__device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int k0, int d) {
+  const int n = n0 + 16 * (d >> 5), k = k0 + 2 * (d & 31);
   if constexpr (STRIPED) {
-    // stripe n / 16 holds 8 bytes per row; these 8 columns are its half (n % 16) / 8
-    const uint8_t* cp = g.packed + ((size_t)(n / 16) * g.K + k) * 8 + (size_t)(c & 1) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) B.code[i] = *reinterpret_cast<const uint32_t*>(cp + (size_t)i * 8);
-    // block-major scales: rows k .. k + 3 of block n / 64 are consecutive (k % 4 == 0, K % 64 == 0)
+    // stripe n / 16 holds 8 bytes per row, rows consecutive
+    const uint8_t* cp = g.packed + ((size_t)(n / 16) * g.K + k) * 8;
+    const u32x2 r0 = *reinterpret_cast<const u32x2*>(cp);
+    const u32x2 r1 = *reinterpret_cast<const u32x2*>(cp + 8);
+    B.code[0] = r0.x;
+    B.code[1] = r0.y;
+    B.code[2] = r1.x;
+    B.code[3] = r1.y;
+    // block-major scales: rows k, k + 1 of block n / 64 are consecutive (k even)
     const size_t blk = (size_t)(n / kBlock) * g.K + k;
     if constexpr (DQ) {
-      B.scale[0] = *reinterpret_cast<const uint32_t*>(g.scales.dq_codes + blk);  // 4 codes, split in store_b
+      // the aligned dword holding both rows' u8 codes (bytes 2 (d % 2), + 1:
+      // blk % 4 == k % 4 == 2 (d % 2)); a dword load leaves no zero-extension
+      // for the compiler to place away from the decode
+      B.scale[0] = *reinterpret_cast<const uint32_t*>(g.scales.dq_codes + (blk & ~size_t{3}));
+      B.scale[1] = 0u;
     } else {
-      const u32x4 s4 = *reinterpret_cast<const u32x4*>(g.scales.absmax + blk);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) B.scale[i] = s4[i];
+      const u32x2 s2 = *reinterpret_cast<const u32x2*>(g.scales.absmax + blk);
+      B.scale[0] = s2.x;
+      B.scale[1] = s2.y;
     }
   } else {
-    const uint32_t row_bytes = (uint32_t)g.N / 2, bpr = (uint32_t)g.N / kBlock;
+    const size_t row_bytes = (size_t)g.N / 2, bpr = (size_t)g.N / kBlock;
     const uint8_t* cp = g.packed + (size_t)k * row_bytes + n / 2;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) B.code[i] = *reinterpret_cast<const uint32_t*>(cp + (size_t)i * row_bytes);
+    const u32x2 r0 = *reinterpret_cast<const u32x2*>(cp);
+    const u32x2 r1 = *reinterpret_cast<const u32x2*>(cp + row_bytes);
+    B.code[0] = r0.x;
+    B.code[1] = r0.y;
+    B.code[2] = r1.x;
+    B.code[3] = r1.y;
     const size_t blk = (size_t)k * bpr + n / kBlock;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (DQ)
-        B.scale[i] = g.scales.dq_codes[blk + (size_t)i * bpr];
-      else
-        B.scale[i] = __float_as_uint(g.scales.absmax[blk + (size_t)i * bpr]);
+    if constexpr (DQ) {
+      B.scale[0] = g.scales.dq_codes[blk];
+      B.scale[1] = g.scales.dq_codes[blk + bpr];
+    } else {
+      B.scale[0] = __float_as_uint(g.scales.absmax[blk]);
+      B.scale[1] = __float_as_uint(g.scales.absmax[blk + bpr]);
     }
   }
 }
 
-// Codes -> dequantized bf16 W tile [n][k] in LDS buffer buf.
+// Codes -> dequantized bf16 W tile [n][k] in LDS buffer buf: byte j of a row
+// holds columns 2j (low nibble) and 2j + 1; one byte-LUT lookup gives both
+// levels, each times its row's block scale (one f32 multiply, as the
+// reference's dequantize), rounded to bf16, and the (k, k + 1) pair of a
+// column is one 4-byte LDS store.
 template <bool DQ, bool STRIPED>
-__device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int tid) {
-  const int c = tid & 15, g4 = tid >> 4;
+__device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int d) {
+  const int st = d >> 5, rp = d & 31;
   const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq);
-  float s[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if constexpr (DQ && STRIPED)
-      s[i] = dq_lut[(B.scale[0] >> (8 * i)) & 0xffu];
-    else
-      s[i] = DQ ? dq_lut[B.scale[i] & 0xffu] : __uint_as_float(B.scale[i]);
+  float s0, s1;
+  if constexpr (DQ && STRIPED) {
+    const int sh = 16 * (d & 1);
+    s0 = dq_lut[(B.scale[0] >> sh) & 0xffu];
+    s1 = dq_lut[(B.scale[0] >> (sh + 8)) & 0xffu];
+  } else if constexpr (DQ) {
+    s0 = dq_lut[B.scale[0] & 0xffu];
+    s1 = dq_lut[B.scale[1] & 0xffu];
+  } else {
+    s0 = __uint_as_float(B.scale[0]);
+    s1 = __uint_as_float(B.scale[1]);
   }
-  // v[i][j]: row k0 + 4 g4 + i, column n0 + 8 c + j; value level[code] * scale
-  // (one f32 multiply, as the reference's dequantize), then bf16.
-  float v[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const uint32_t byte = (B.code[i] >> (8 * b)) & 0xffu;
-      const f32x2 lv = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + byte * 8));
-      v[i][2 * b] = lv.x * s[i];
-      v[i][2 * b + 1] = lv.y * s[i];
-    }
-  }
-  // column 8c + j gets k = 4 g4 .. 4 g4 + 3: half (g4 & 1) of chunk g4 / 2
+  const int base = kLdsB + buf * kBTileBytes;
+  const int chunk = rp >> 2;                   // k = 2 rp lies in 16-byte chunk rp / 4 of a row
+  const uint32_t within = (uint32_t)(rp & 3) * 4u;
+  // all 16 lookups first, so that one LDS latency covers them (a producer
+  // wave has its SIMD to itself beside an MFMA wave: nothing else hides it)
+  f32x2 l[2][8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int n = 8 * c + j;
-    const u32x2 w = {pack_bf16x2(v[0][j], v[1][j]), pack_bf16x2(v[2][j], v[3][j])};
-    const uint32_t addr = lds_addr(kLdsB + buf * kBTileBytes, n, g4 >> 1) + (uint32_t)(g4 & 1) * 8u;
-    *reinterpret_cast<lds_u32x2*>((size_t)addr) = w;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t byte = (B.code[2 * r + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+      l[r][j] = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + byte * 8));
+    }
+  }
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // the 16 LUT reads
+  __builtin_amdgcn_sched_group_barrier(0x002, 64, 1);  // then VALU
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t even = pack_bf16x2(l[0][j].x * s0, l[1][j].x * s1);  // column 2j, rows k and k + 1
+    const uint32_t odd = pack_bf16x2(l[0][j].y * s0, l[1][j].y * s1);   // column 2j + 1
+    const int n = 16 * st + 2 * j;
+    *reinterpret_cast<lds_u32*>((size_t)(lds_addr(base, n, chunk) + within)) = even;
+    *reinterpret_cast<lds_u32*>((size_t)(lds_addr(base, n + 1, chunk) + within)) = odd;
   }
 }
 
@@ -186,35 +210,51 @@ __device__ __forceinline__ void read_frags(Frags& F, int abase, int bbase, int k
   for (int j = 0; j < 4; ++j) F.b[j] = read_frag(bbase, 32 * j + (lane & 31), ch);
 }
 
+// The 8 MFMAs of one k16 slice.  The scheduling groups put the fragment
+// reads the caller issued just before (6 ds_read_b128, the next slice's)
+// ahead of these MFMAs, so that their LDS latency hides behind them.
 __device__ __forceinline__ void mma_frags(f32x16 (&acc)[2][4], const Frags& F) {
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.a[i], F.b[j], acc[i][j], 0, 0, 0);
-}
-
-__device__ __forceinline__ void mma_step(f32x16 (&acc)[2][4], int abase, int bbase, int lane) {
-  Frags F0, F1;
-  read_frags(F0, abase, bbase, 0, lane);
-  read_frags(F1, abase, bbase, 1, lane);
-  mma_frags(acc, F0);
-  read_frags(F0, abase, bbase, 2, lane);
-  mma_frags(acc, F1);
-  read_frags(F1, abase, bbase, 3, lane);
-  mma_frags(acc, F0);
-  mma_frags(acc, F1);
+  __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // DS reads first
+  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // then the MFMAs
 }
 
 // vmcnt(n): wait until at most n vector-memory loads of this wave are in
 // flight (they complete in issue order).
 #define UNIFUR_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
+// Workgroup barrier for LDS hand-offs only: this wave's LDS operations
+// complete (lgkmcnt(0)), then s_barrier.  Unlike __syncthreads() it does not
+// wait for the wave's vector-memory loads, so the X copies and code loads
+// issued steps ahead stay in flight across it.  The signal fences keep the
+// compiler from moving memory operations across the barrier, the scheduling
+// barriers any instruction (a later step's code decoding hoisted above it
+// would wait for that step's loads here).
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Workgroup tile 256 x 128, warp-specialised: waves 0-3 ("MFMA waves") own
-// rows 64 w .. + 63 and all 128 columns and only read LDS and issue MFMAs;
-// waves 4-7 ("producer waves", one per SIMD beside an MFMA wave) copy the X
-// tiles into LDS and dequantize the W tiles, one step ahead, so that their
-// VALU / LDS / memory work overlaps the MFMAs on the same SIMD.  One
-// workgroup barrier per K step hands the buffers over.
+// rows 64 w .. + 63 and all 128 columns; each copies its own X rows into its
+// LDS region (buffer_load ... lds, two steps ahead, three stages), reads
+// fragments and issues MFMAs, the next slice's fragments read while the
+// current slice's MFMAs run (across steps too: the next step's first slice
+// is read during the current step's last).  Waves 4-7 ("producer waves", one
+// per SIMD beside an MFMA wave) dequantize the W tile two steps ahead into a
+// three-buffer ring, from codes loaded four steps ahead in registers, so
+// that their VALU / LDS work overlaps the MFMAs on the same SIMD.  One
+// workgroup barrier per K step hands the W buffers over: barrier s + 1 comes
+// after the producers wrote step s + 2 and the MFMA waves read the last of
+// step s; X needs none (each MFMA wave reads only the rows it copied itself,
+// after waiting for its own copies).
 template <bool DQ, bool YBF16, bool LORA, bool STRIPED>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -238,102 +278,101 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     if constexpr (DQ)
       reinterpret_cast<float*>(smem + kLdsDq)[tid] = ((float)tid / 255.0f) * (*g.scales.scale_of_scales);
   }
+  const int nk = g.K / kBK;
+
+  // Every role passes the same nk + 1 workgroup barriers: the LUTs, steps 0
+  // and 1 ready, then one per further step.
+  if (wave >= 4) {
+    constexpr int kBRing = 4;
+    const int d = tid - 256;
+    BStep Br[kBRing];
+#pragma unroll
+    for (int r = 0; r < kBRing; ++r) load_b<DQ, STRIPED>(Br[r], g, n0, min(r, nk - 1) * kBK, d);
+    lds_barrier();  // LUTs visible
+    store_b<DQ, STRIPED>(Br[0], smem, 0, d);
+    load_b<DQ, STRIPED>(Br[0], g, n0, min(kBRing, nk - 1) * kBK, d);
+    if (nk > 1) {
+      store_b<DQ, STRIPED>(Br[1], smem, 1, d);
+      load_b<DQ, STRIPED>(Br[1], g, n0, min(kBRing + 1, nk - 1) * kBK, d);
+    }
+    lds_barrier();  // steps 0 and 1 ready
+    // step t2 (from 2 on) into W buffer t2 % 3 from ring slot t2 % kBRing,
+    // then the barrier that publishes it
+    auto produce = [&](int t2, int slot) {
+      store_b<DQ, STRIPED>(Br[slot], smem, t2 % kBStages, d);
+      load_b<DQ, STRIPED>(Br[slot], g, n0, min(t2 + kBRing, nk - 1) * kBK, d);
+      lds_barrier();
+    };
+    int t2 = 2;
+    for (; t2 + kBRing <= nk; t2 += kBRing) {
+#pragma unroll
+      for (int u = 0; u < kBRing; ++u) produce(t2 + u, (2 + u) % kBRing);
+    }
+    for (int u = 0; t2 < nk; ++t2, ++u) {
+      if (u == 0) produce(t2, 2);
+      else if (u == 1) produce(t2, 3);
+      else produce(t2, 0);
+    }
+    if (nk >= 2) lds_barrier();  // the last step's barrier: nothing left to produce
+    UNIFUR_WAIT_VMCNT(0);        // drain the clamped reloads before the wave exits
+    return;
+  }
 
   // rows past M read as zero (buffer bound)
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(g.x), (short)0, (int)((uint32_t)g.M * (uint32_t)g.K * 2u), 0x00020000);
-  const int nk = g.K / kBK;
   const int awave = kLdsA + w4 * (kATileBytes / 4);
-
-  // Every role passes the same workgroup barriers: 2 before the K loop, one
-  // per step handed over (nk - 1), and one more when nk is even (the MFMA
-  // waves' loop runs steps in pairs and ends with a barrier).
-  if (wave == 4 || wave == 5) {
-    // Copy waves: X tiles of MFMA waves 2 (wave - 4) and 2 (wave - 4) + 1,
-    // two steps ahead in three LDS stages.  These waves issue nothing but
-    // the LDS copies, so the only waits on them are the explicit ones.
-    const int c0 = 2 * (wave - 4);
-    const int base0 = kLdsA + c0 * (kATileBytes / 4), base1 = base0 + kATileBytes / 4;
-    const int r0 = m0 + 64 * c0, r1 = r0 + 64;
-    auto copy = [&](int step, int stage) {
-      load_a(xr, g.K, r0, min(step, nk - 1) * kBK, base0 + stage * kATileBytes, lane);
-      load_a(xr, g.K, r1, min(step, nk - 1) * kBK, base1 + stage * kATileBytes, lane);
-    };
-    copy(0, 0);
-    copy(1, 1);
-    __syncthreads();  // LUTs visible
-    UNIFUR_WAIT_VMCNT(16);  // step 0 landed (step 1's 16 copies may fly)
-    __syncthreads();
-    int stage = 2;  // stage of step s1 + 1
-    for (int s1 = 1; s1 < nk; ++s1) {
-      copy(s1 + 1, stage);  // clamped past the last step: a harmless reload into a free stage
-      UNIFUR_WAIT_VMCNT(16);  // step s1 landed
-      __syncthreads();
-      stage = stage == 2 ? 0 : stage + 1;
-    }
-    if ((nk & 1) == 0) __syncthreads();
-    UNIFUR_WAIT_VMCNT(0);
-    return;
-  }
-  if (wave >= 6) {
-    // Dequantizing waves: thread d expands the W-tile parts of producer
-    // indices d and d + 128, from codes loaded kBRing steps ahead.
-    constexpr int kBRing = 4;
-    const int d = tid - 384;
-    BStep Br[2][kBRing];
-#pragma unroll
-    for (int r = 0; r < kBRing; ++r)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) load_b<DQ, STRIPED>(Br[h][r], g, n0, min(r, nk - 1) * kBK, d + 128 * h);
-    __syncthreads();  // LUTs visible
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      store_b<DQ, STRIPED>(Br[h][0], smem, 0, d + 128 * h);
-      load_b<DQ, STRIPED>(Br[h][0], g, n0, min(kBRing, nk - 1) * kBK, d + 128 * h);
-    }
-    __syncthreads();  // step 0 ready
-    auto handoff = [&](int s1, int slot) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        store_b<DQ, STRIPED>(Br[h][slot], smem, s1 & 1, d + 128 * h);
-        load_b<DQ, STRIPED>(Br[h][slot], g, n0, min(s1 + kBRing, nk - 1) * kBK, d + 128 * h);
-      }
-      __syncthreads();
-    };
-    // whole rounds of kBRing handoffs (static ring slots), then the rest
-    int s1 = 1;
-    for (; s1 + kBRing <= nk; s1 += kBRing) {
-#pragma unroll
-      for (int u = 0; u < kBRing; ++u) handoff(s1 + u, (u + 1) % kBRing);
-    }
-    for (int u = 0; s1 < nk; ++s1, ++u) {  // slot of step s1 = (u + 1) % kBRing
-      if (u == 0) handoff(s1, 1);
-      else if (u == 1) handoff(s1, 2);
-      else handoff(s1, 3);
-    }
-    if ((nk & 1) == 0) __syncthreads();
-    UNIFUR_WAIT_VMCNT(0);  // drain the clamped reloads before the wave exits
-    return;
-  }
-
   f32x16 acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  __syncthreads();  // LUTs visible
-  __syncthreads();  // step 0 ready
-  int sa = 0;
-  int kt = 0;
-  for (; kt + 1 < nk; kt += 2) {
-    mma_step(acc, awave + sa * kATileBytes, kLdsB, lane);
-    __syncthreads();
-    sa = sa == 2 ? 0 : sa + 1;
-    mma_step(acc, awave + sa * kATileBytes, kLdsB + kBTileBytes, lane);
-    __syncthreads();
-    sa = sa == 2 ? 0 : sa + 1;
-  }
-  if (kt < nk) mma_step(acc, awave + sa * kATileBytes, kLdsB, lane);  // odd step count: last W in buffer 0
+  load_a(xr, g.K, row0, 0, awave, lane);
+  if (nk > 1) load_a(xr, g.K, row0, kBK, awave + kATileBytes, lane);
+  lds_barrier();  // LUTs visible
+  lds_barrier();  // steps 0 and 1 ready
+  if (nk > 1) UNIFUR_WAIT_VMCNT(8);  // this wave's X copies of step 0 landed
+  else UNIFUR_WAIT_VMCNT(0);
+  Frags Fa, Fb;
+  read_frags(Fa, awave, kLdsB, 0, lane);
+  int sa = 0, sb = 0;  // X stage and W buffer of step s
+  // One K step; COPY2: copy step s + 2's X, NEXT: read step s + 1's first
+  // slice at the end.  The main loop takes both, the last two steps are
+  // peeled, so that the LDS wait counts stay exact (no branch merges them).
+  auto step = [&](int s, auto copy2, auto next) {
+    constexpr bool kCopy2 = decltype(copy2)::value, kNext = decltype(next)::value;
+    const int ab = awave + sa * kATileBytes, bb = kLdsB + sb * kBTileBytes;
+    const int sa1 = sa == 2 ? 0 : sa + 1, sb1 = sb == kBStages - 1 ? 0 : sb + 1;
+    // the first slice's fragments were read during the previous step (and
+    // waited for by its barrier): nothing is in flight on LDS here
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    // step s + 2 goes to the stage step s - 1 used: all its reads completed
+    // before that step's last MFMAs issued
+    if constexpr (kCopy2) load_a(xr, g.K, row0, (s + 2) * kBK, awave + (sa == 0 ? 2 : sa - 1) * kATileBytes, lane);
+    read_frags(Fb, ab, bb, 1, lane);
+    mma_frags(acc, Fa);
+    read_frags(Fa, ab, bb, 2, lane);
+    mma_frags(acc, Fb);
+    read_frags(Fb, ab, bb, 3, lane);
+    mma_frags(acc, Fa);
+    if constexpr (kNext) {
+      // step s + 1's W tile was published by the previous barrier; its X
+      // copies are the older of the (up to) two groups in flight
+      if constexpr (kCopy2) UNIFUR_WAIT_VMCNT(8);
+      else UNIFUR_WAIT_VMCNT(0);
+      read_frags(Fa, awave + sa1 * kATileBytes, kLdsB + sb1 * kBTileBytes, 0, lane);
+    }
+    mma_frags(acc, Fb);
+    if constexpr (kNext) lds_barrier();
+    sa = sa1;
+    sb = sb1;
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
+  int s = 0;
+  for (; s + 2 < nk; ++s) step(s, yes{}, yes{});
+  if (s + 1 < nk) step(s++, no{}, yes{});
+  step(s, no{}, no{});
 
   if constexpr (LORA) {
     // acc += xa[rows, r] . B[r, cols] (xa already scaled), one 32x32x16 MFMA
