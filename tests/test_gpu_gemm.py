@@ -157,3 +157,36 @@ def test_fused_prefill_kernel_config3_shapes(device, oracle, M):
     K, N, r = 4096, 4096, 16
     lean = L.lib().unifur_nf4_linear_min_workspace_size(M, K, N, L.BF16, r)
     _qlora_with_workspace(device, oracle, M, K, N, r, lean, 700 + M)
+
+
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shift", [0, 1, 2])
+def test_fused_prefill_output_alignment(device, oracle, ydt, shift):
+    # The fused kernel stores four outputs at once when y is 16-byte aligned
+    # and one at a time otherwise; an output offset by `shift` elements (and
+    # rows past a 256-row tile) must give the aligned result bit for bit.
+    M, K, N, r = 300, 512, 384, 8
+    lin, wdeq = make_linear(oracle, K, N, 800 + shift, device)
+    x, xt = acts(oracle, M, K, 801, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 802, device)
+    bias = oracle.fill_normal(803, 0.1, N)
+    bt = torch.from_numpy(bias).to(device)
+    need = L.lib().unifur_nf4_linear_min_workspace_size(M, K, N, L.BF16, r)
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    w, lo = lin.weight_struct(), ad.struct()
+    st = torch.cuda.current_stream().cuda_stream
+    code = L.BF16 if ydt == torch.bfloat16 else L.F32
+
+    def run(y_ptr):
+        L.check(L.lib().unifur_nf4_linear_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w), bt.data_ptr(),
+                                                  ctypes.byref(lo), y_ptr, code, ws.data_ptr(), need, st))
+
+    y0 = torch.empty(M, N, dtype=ydt, device=device)
+    run(y0.data_ptr())
+    buf = torch.full((M * N + 8,), float("nan"), dtype=ydt, device=device)
+    run(buf[shift:].data_ptr())
+    y1 = buf[shift:shift + M * N].view(M, N)
+    assert torch.equal(y0, y1)
+    assert torch.isnan(buf[:shift]).all() and torch.isnan(buf[shift + M * N:]).all()
+    ref = oracle.linear_ref_f64(x, wdeq, bias) + oracle.lora_ref_f64(x, a, b, ad.scaling())
+    check(y0, ref, x, wdeq, TOL_BF16, f"fused prefill y {ydt} shift {shift}")

@@ -61,6 +61,7 @@ struct GemmArgs {
   int lora_rank, lora_pad;
   void* y;  // [M, N] f32 or bf16
   int y_bf16;
+  int y_aligned;  // y 16-byte aligned: the epilogue stores 4 outputs at once
   int tiles_n;  // N / kBN
 };
 
@@ -399,27 +400,72 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  // Epilogue: acc[i][j][4 a + e] = C[row 8 a + 4 (lane / 32) + e][col lane % 32].
+  // Epilogue, through this wave's own X-stage chunks of stages 0 and 1 (its
+  // copies all landed and its reads completed in the last step; no other
+  // wave touches them).  acc[i][j][4 a + e] is C[row 32 i + 8 a + 4 (lane /
+  // 32) + e][col 32 j + lane % 32]; each half i (32 rows) of the wave's tile
+  // is staged as f32 -- row r at chunk r / 16, byte (r % 16) * 512 +
+  // (4 c ^ 128 * (r / 4 % 2)), so that the two row groups of a store land in
+  // different bank halves -- then read back row-contiguous: lane l takes
+  // columns 4 (l % 32) .. + 3 of row 2 q + l / 32 and writes them as one
+  // 16-byte (f32) or 8-byte (bf16) store, the bias added.
+  {
+    const int cq = 4 * (lane & 31);
+    float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (g.bias) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + 32 * j + (lane & 31);
-    const float bias = g.bias ? g.bias[n] : 0.0f;
+      for (int t2 = 0; t2 < 4; ++t2) bias4[t2] = g.bias[n0 + cq + t2];
+    }
+    auto stage_off = [&](int r, int c) -> uint32_t {
+      return (uint32_t)(awave + (r >> 4) * kATileBytes + (r & 15) * 512) +
+             (((uint32_t)c * 4u) ^ ((uint32_t)((r >> 2) & 1) << 7));
+    };
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = row0 + 32 * i + 8 * a4 + 4 * (lane >> 5) + e;
-          if (m >= g.M) continue;
-          const float yv = acc[i][j][4 * a4 + e] + bias;
-          const size_t idx = (size_t)m * g.N + n;
-          if constexpr (YBF16)
-            reinterpret_cast<uint16_t*>(g.y)[idx] = (uint16_t)(pack_bf16x2(yv, 0.0f) & 0xffffu);
-          else
-            reinterpret_cast<float*>(g.y)[idx] = yv;
+        for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            *reinterpret_cast<__attribute__((address_space(3))) float*>(
+                (size_t)stage_off(8 * a4 + 4 * (lane >> 5) + e, 32 * j + (lane & 31))) = acc[i][j][4 * a4 + e];
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // a wave's LDS operations complete in order; be explicit
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int r = 2 * q + (lane >> 5);
+        const int m = row0 + 32 * i + r;
+        const f32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>((size_t)stage_off(r, cq));
+        if (m < g.M) {
+          const size_t idx = (size_t)m * g.N + n0 + cq;
+          const float y0 = v.x + bias4[0], y1 = v.y + bias4[1], y2 = v.z + bias4[2], y3 = v.w + bias4[3];
+          if constexpr (YBF16) {
+            const u32x2 o = {pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+            if (g.y_aligned) {
+              *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(g.y) + idx) = o;
+            } else {
+              uint16_t* p = reinterpret_cast<uint16_t*>(g.y) + idx;
+              p[0] = (uint16_t)(o.x & 0xffffu);
+              p[1] = (uint16_t)(o.x >> 16);
+              p[2] = (uint16_t)(o.y & 0xffffu);
+              p[3] = (uint16_t)(o.y >> 16);
+            }
+          } else {
+            float* p = reinterpret_cast<float*>(g.y) + idx;
+            if (g.y_aligned) {
+              *reinterpret_cast<f32x4*>(p) = f32x4{y0, y1, y2, y3};
+            } else {
+              p[0] = y0;
+              p[1] = y1;
+              p[2] = y2;
+              p[3] = y3;
+            }
+          }
         }
       }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();  // the next half reuses the chunks
     }
   }
 }
@@ -547,6 +593,7 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
   g.lora_pad = lora_pad(lora_rank);
   g.y = y;
   g.y_bf16 = y_bf16;
+  g.y_aligned = (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
   g.tiles_n = N / kBN;
   const bool dq = scales.kind == kScalesDQ;
   const bool lora = lora_xa != nullptr;
