@@ -491,42 +491,60 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
 // ------------------------------------------------------------ LoRA x A ------
 // The adapter operands of the fused epilogue, in bf16 layouts whose MFMA
 // fragments are single 16-byte loads (pad = rank rounded up to 16, zero past
-// the rank): at[pad][K] = A transposed and bt[N][pad] = B transposed (one
-// small prep kernel), then xa[M][pad] = bf16(scaling * (X A)) -- the first
-// factor of LoraAdapter::forward (src/quantize.rs:619-624) with the scaling
-// folded in -- by a kernel of 16-row x 16-column tiles whose four waves split
-// K into quarters (v_mfma_f32_16x16x32_bf16, X and at straight from memory,
-// eight steps of loads in flight) and add their quarters through LDS.
+// the rank):
+//   * lora_prep_kernel: at[pad][K] = A transposed and bt[N][pad] = B
+//     transposed, one row k of A or one column n of B per thread (each
+//     thread reads a row of A / writes a row of bt contiguously, and the
+//     threads of a wave write at / read B at consecutive addresses);
+//   * lora_xa_kernel: xa[M][pad] = bf16(scaling * (X A)) -- the first factor
+//     of LoraAdapter::forward (src/quantize.rs:619-624) with the scaling
+//     folded in -- 16 rows x 16 columns per workgroup; eight waves split K
+//     (v_mfma_f32_16x16x32_bf16, X and at straight from memory, eight steps
+//     of 16-byte loads in flight) and add their slices through LDS in wave
+//     order.
 
-__global__ void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b, int K, int N, int rank,
-                                 int pad, uint16_t* __restrict__ at, uint16_t* __restrict__ bt) {
-  const size_t na = (size_t)pad * K, total = na + (size_t)N * pad;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    if (i < na) {
-      const int j = (int)(i / K), k = (int)(i % K);  // at[j][k] = a[k][j]
-      at[i] = j < rank ? (uint16_t)(pack_bf16x2(a[(size_t)k * rank + j], 0.0f) & 0xffffu) : (uint16_t)0;
-    } else {
-      const size_t q = i - na;
-      const int n = (int)(q / pad), j = (int)(q % pad);  // bt[n][j] = b[j][n]
-      bt[q] = j < rank ? (uint16_t)(pack_bf16x2(b[(size_t)j * N + n], 0.0f) & 0xffffu) : (uint16_t)0;
+__global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                        int K, int N, int rank, int pad, uint16_t* __restrict__ at,
+                                                        uint16_t* __restrict__ bt) {
+  const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (t < K) {
+    const float* row = a + (size_t)t * rank;  // A[t][0 .. rank)
+    for (int j = 0; j < pad; ++j) at[(size_t)j * K + t] = j < rank ? (uint16_t)(pack_bf16x2(row[j], 0.0f) & 0xffffu) : 0;
+  } else if (t < K + N) {
+    const int n = t - K;
+    for (int c0 = 0; c0 < pad; c0 += 16) {
+      uint32_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r0 = c0 + 2 * j, r1 = r0 + 1;
+        w[j] = pack_bf16x2(r0 < rank ? b[(size_t)r0 * N + n] : 0.0f, r1 < rank ? b[(size_t)r1 * N + n] : 0.0f);
+      }
+      u32x4* dst = reinterpret_cast<u32x4*>(bt + (size_t)n * pad + c0);
+      dst[0] = u32x4{w[0], w[1], w[2], w[3]};
+      dst[1] = u32x4{w[4], w[5], w[6], w[7]};
     }
   }
 }
 
+constexpr int kXaWaves = 8;
 constexpr int kXaBatch = 8;  // k32 steps whose loads are in flight together
 
-__global__ __launch_bounds__(256) void lora_xa_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ at,
-                                                      int M, int K, int pad, float scaling, uint16_t* __restrict__ xa) {
-  __shared__ float red[4][256];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+__global__ __launch_bounds__(64 * kXaWaves) void lora_xa_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ at, int M, int K,
+                                                                int pad, float scaling, uint16_t* __restrict__ xa) {
+  __shared__ float red[kXaWaves][256];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m0 = blockIdx.x * 16, c0 = blockIdx.y * 16;
-  const int kq = K / 4;  // a multiple of 16 (K % 64 == 0)
-  const int kbeg = w * kq, kend = kbeg + kq;
-  // rows past M read as zero (buffer bound)
+  const int kq = K / kXaWaves;  // a multiple of 8 (K % 64 == 0)
+  const int kbeg = wv * kq, kend = kbeg + kq;
+  // rows past M read as zero (buffer bound), and so does a step past the
+  // wave's slice (an offset past the end): no load sits behind a branch
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(at), (short)0, (int)((uint32_t)pad * (uint32_t)K * 2u), 0x00020000);
   const uint32_t xrow = (uint32_t)(m0 + (lane & 15)) * (uint32_t)K * 2u;
-  const uint16_t* arow = at + (size_t)(c0 + (lane & 15)) * K;
+  const uint32_t arow = (uint32_t)(c0 + (lane & 15)) * (uint32_t)K * 2u;
   const int kl = 8 * (lane >> 4);  // this lane's 8 k of each 32
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int k0 = kbeg; k0 < kend; k0 += 32 * kXaBatch) {
@@ -534,22 +552,29 @@ __global__ __launch_bounds__(256) void lora_xa_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int q = 0; q < kXaBatch; ++q) {
       const int k = k0 + 32 * q + kl;
-      const bool ok = k < kend;  // K / 4 may be an odd multiple of 16: mask per 8-k group
-      xv[q] = ok ? __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, xrow + (uint32_t)k * 2u, 0, 0))
-                 : bf16x8{};
-      av[q] = ok ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(arow + k)) : bf16x8{};
+      const bool ok = k < kend;  // K / 8 may end inside a 32-k step: mask per 8-k group
+      xv[q] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xrow + (uint32_t)k * 2u : 0xffffffffu, 0, 0));
+      av[q] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ar, ok ? arow + (uint32_t)k * 2u : 0xffffffffu, 0, 0));
     }
+    __builtin_amdgcn_sched_barrier(0);  // the whole batch's loads are in flight before the first MFMA
 #pragma unroll
     for (int q = 0; q < kXaBatch; ++q) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[q], av[q], acc, 0, 0, 0);
   }
-  // acc[e] = C[row 4 (lane / 16) + e][col lane % 16]; add the four K quarters
+  // acc[e] = C[row 4 (lane / 16) + e][col lane % 16]; add the K slices in order
 #pragma unroll
-  for (int e = 0; e < 4; ++e) red[w][(4 * (lane >> 4) + e) * 16 + (lane & 15)] = acc[e];
+  for (int e = 0; e < 4; ++e) red[wv][(4 * (lane >> 4) + e) * 16 + (lane & 15)] = acc[e];
   __syncthreads();
-  const int t = threadIdx.x, m = m0 + t / 16;
-  if (m < M) {
-    const float v = (red[0][t] + red[1][t] + red[2][t] + red[3][t]) * scaling;
-    xa[(size_t)m * pad + c0 + (t & 15)] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+  const int t = threadIdx.x;
+  if (t < 256) {
+    const int m = m0 + t / 16;
+    if (m < M) {
+      float v = red[0][t];
+#pragma unroll
+      for (int w = 1; w < kXaWaves; ++w) v += red[w][t];
+      xa[(size_t)m * pad + c0 + (t & 15)] = (uint16_t)(pack_bf16x2(v * scaling, 0.0f) & 0xffffu);
+    }
   }
 }
 
@@ -567,12 +592,11 @@ hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* 
                                 float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa, hipStream_t stream) {
   if (rank < 1 || rank > 64 || K % 64 != 0) return hipErrorInvalidValue;
   const int pad = lora_pad(rank);
-  const size_t total = (size_t)pad * K + (size_t)N * pad;
-  lora_prep_kernel<<<(unsigned)std::min<size_t>((total + 255) / 256, 2048), 256, 0, stream>>>(a, b, K, N, rank, pad,
-                                                                                             at, bt);
+  lora_prep_kernel<<<(unsigned)((K + N + 255) / 256), 256, 0, stream>>>(a, b, K, N, rank, pad, at, bt);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  lora_xa_kernel<<<dim3((M + 15) / 16, pad / 16), 256, 0, stream>>>(x, at, M, K, pad, scaling, xa);
+  lora_xa_kernel<<<dim3((unsigned)((M + 15) / 16), (unsigned)(pad / 16)), 64 * kXaWaves, 0, stream>>>(x, at, M, K, pad,
+                                                                                                    scaling, xa);
   return hipGetLastError();
 }
 

@@ -15,9 +15,9 @@ bool gemm_supported(int M, int K, int N, const void* x);
 // operand buffers below).
 int lora_pad(int rank);
 
-// The fused LoRA epilogue's operands, bf16: at[pad][K] (A transposed),
-// bt[N][pad] (B transposed) and xa[M][pad] = scaling * (X A), zero past the
-// rank; rank <= 64, K a multiple of 64.
+// The fused LoRA epilogue's operands, bf16: at[pad][K] (A transposed, a
+// scratch operand), bt[N][pad] (B transposed) and xa[M][pad] =
+// scaling * (X A), zero past the rank; rank <= 64, K a multiple of 64.
 hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* b, int M, int K, int N, int rank,
                                 float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa, hipStream_t stream);
 
