@@ -123,6 +123,12 @@ def rand_weights(torch, Q, d_in, d_out, gen, dq=True, striped=True):
     return Q.Nf4Linear.from_packed(p, d_in, d_out, striped=striped)
 
 
+def clone_linear(Q, lin):
+    """A second device copy of a striped double-quantized layer (same bytes)."""
+    return Q.Nf4Linear._from_striped(lin._codes.clone(), lin._scales.clone(), lin._sos.clone(), lin.d_input(),
+                                     lin.d_output())
+
+
 # --------------------------------------------------------------- config 2 --
 
 def bench_gemv(torch, Q, L, args) -> dict:
@@ -157,14 +163,16 @@ def bench_gemv(torch, Q, L, args) -> dict:
     graph = capture(torch, launch, copies)
     steps = args.steps
     torch.cuda.synchronize()
-    if graph is not None:
-        reps = -(-steps // copies)
-        steps = reps * copies
+    # exactly `steps` launches, rotating over the copies: one graph of them
+    timed = capture(torch, launch, steps) if graph is not None else None
+    if timed is not None:
+        timed.replay()  # once untimed (graph upload)
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(reps):
-            graph.replay()
+        timed.replay()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
+        del timed
     else:
         t0 = time.perf_counter()
         for i in range(steps):
@@ -194,6 +202,47 @@ def bench_gemv(torch, Q, L, args) -> dict:
     gb = capture(torch, launch_b, copies)
     out["kernel_cold_ms_bf16x"] = replay_event_ms(torch, gb, copies) if gb is not None else event_ms(
         torch, launch_b, 4 * copies)
+    return out
+
+
+# ----------------------------------------------------------- HBM ceiling --
+
+def bench_ceiling(torch, L, nbytes: int) -> dict:
+    """What this part streams for buffers of the GEMV's size, timed as the
+    GEMV is (graph replay over copies rotated past the Infinity Cache, one
+    event pair around the replays): the library's streaming probe
+    (unifur_nf4_stream_probe, 16-byte accesses, grid-stride) as a plain read
+    of nbytes and as a copy of nbytes / 2 (nbytes moved), the best over a few
+    grid sizes."""
+    dev = torch.device("cuda:0")
+    nbytes = nbytes // 64 * 64
+    copies = max(2, -(-(2 * MALL_BYTES) // nbytes))
+    bufs = [torch.ones(nbytes // 4, device=dev) for _ in range(copies)]
+    dsts = [torch.empty(nbytes // 8, device=dev) for _ in range(copies)]
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    lib = L.lib()
+    out = {"bytes": nbytes, "copies": copies, "kernel": "unifur_nf4_stream_probe"}
+    for name, moved in (("read", nbytes), ("copy", nbytes)):
+        best = None
+        for grid in (256, 512, 1024, 2048, 4096):
+            def fn(i: int, grid=grid, name=name) -> None:
+                if name == "read":
+                    L.check(lib.unifur_nf4_stream_probe(bufs[i % copies].data_ptr(), nbytes, None, sink.data_ptr(),
+                                                        grid, torch.cuda.current_stream().cuda_stream))
+                else:
+                    L.check(lib.unifur_nf4_stream_probe(bufs[i % copies].data_ptr(), nbytes // 2,
+                                                        dsts[i % copies].data_ptr(), sink.data_ptr(), grid,
+                                                        torch.cuda.current_stream().cuda_stream))
+            gr = capture(torch, fn, copies)
+            ms = replay_event_ms(torch, gr, copies) if gr is not None else event_ms(torch, fn, 2 * copies)
+            if best is None or ms < best[0]:
+                best = (ms, grid)
+        out[f"{name}_us"] = round(best[0] * 1e3, 2)
+        out[f"{name}_gbs"] = round(moved / best[0] / 1e6, 1)
+        out[f"{name}_workgroups"] = best[1]
+    if int(sink.count_nonzero()) != 0:
+        raise RuntimeError("stream probe sink written: the read was not of the expected data")
+    del bufs, dsts
     return out
 
 
@@ -274,8 +323,33 @@ def bench_gemm(torch, Q, L) -> dict:
     gbase = capture(torch, base, 8)
     base_ms = replay_event_ms(torch, gbase, 8, reps=10) if gbase is not None else event_ms(torch, base, 16)
     base_flops = 2 * M * N * K
+    # the fused kernel (NF4 tiles dequantized on chip, LoRA in the epilogue):
+    # what the least workspace selects, with the adapter and without
+    fused = {}
+    for name, lo_ in (("qlora", lo), ("base", None)):
+        rank = r if lo_ is not None else 0
+        lean = lib.unifur_nf4_linear_min_workspace_size(M, K, N, L.BF16, rank)
+        wl = torch.zeros(lean, dtype=torch.uint8, device=dev)
+        yf = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+        def fused_launch(i: int, lo_=lo_, wl=wl, lean=lean, yf=yf) -> None:
+            L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), L.BF16, M, ctypes.byref(w), None,
+                                                  ctypes.byref(lo_) if lo_ is not None else None, yf.data_ptr(),
+                                                  L.BF16, wl.data_ptr(), lean, torch.cuda.current_stream().cuda_stream))
+        fused_launch(0)
+        torch.cuda.synchronize()
+        if name == "qlora":
+            ferr = float((yf.float() - ref).abs().max() / ref.abs().max())
+            if not ferr < 1e-2:
+                raise RuntimeError(f"fused GEMM sanity check failed: {ferr:.3e}")
+        gf = capture(torch, fused_launch, 8)
+        f_ms = graph_ms(torch, gf, 10) / 8 if gf is not None else event_ms(torch, fused_launch, 16)
+        f_flops = flops if name == "qlora" else base_flops
+        fused[name] = {"ms": round(f_ms, 5), "tflops": round(f_flops / f_ms / 1e9, 1),
+                       "frac": round(f_flops / f_ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
     return {"ms": ms, "tflops": flops / ms / 1e9, "frac": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
-            "base_kernel_ms": base_ms, "base_tflops": base_flops / base_ms / 1e9, "max_rel_err": err}
+            "base_kernel_ms": base_ms, "base_tflops": base_flops / base_ms / 1e9, "max_rel_err": err,
+            "fused": fused}
 
 
 # --------------------------------------------------------------- config 4 --
@@ -285,10 +359,13 @@ def bench_swiglu(torch, Q, L, tokens) -> dict:
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(0x4E463457 + 4)
-    copies = 3  # 3 x 38 MB of packed weights per block: > the Infinity Cache
-    blocks = [Q.QwenMlp(rand_weights(torch, Q, hidden, inter, g), rand_weights(torch, Q, hidden, inter, g),
-                        rand_weights(torch, Q, inter, hidden, g)) for _ in range(copies)]
     wbytes = 2 * gemv_bytes(hidden, inter, True, 0, 0) + gemv_bytes(inter, hidden, True, 0, 0)
+    # rotate >= 512 MiB of packed weights (twice the 256 MiB Infinity Cache):
+    # 8 blocks of 69.7 MB, so every step streams its weights from HBM
+    copies = max(2, -(-(2 * MALL_BYTES) // wbytes))
+    base = [rand_weights(torch, Q, hidden, inter, g), rand_weights(torch, Q, hidden, inter, g),
+            rand_weights(torch, Q, inter, hidden, g)]
+    blocks = [Q.QwenMlp(*base)] + [Q.QwenMlp(*[clone_linear(Q, w) for w in base]) for _ in range(copies - 1)]
     out = {}
     for T in tokens:
         x = torch.randn(T, hidden, device=dev, generator=g).to(torch.bfloat16)
@@ -299,11 +376,33 @@ def bench_swiglu(torch, Q, L, tokens) -> dict:
 
         for i in range(copies):
             run(i)
-        graph = capture(torch, run, copies * 2)
-        ms = graph_ms(torch, graph, 20) / (copies * 2) if graph is not None else event_ms(torch, run, 12)
+        graph = capture(torch, run, copies)
+        ms = graph_ms(torch, graph, 10) / copies if graph is not None else event_ms(torch, run, 2 * copies)
         flops = T * 270_532_608
         out[f"T{T}"] = {"ms": round(ms, 5), "weight_gbs": round(wbytes / ms / 1e6, 1),
                         "tflops": round(flops / ms / 1e9, 2)}
+    # T = 512 with the least workspace: the fused MFMA kernels (no expanded
+    # weight copies), silu(g) * u between them
+    T = 512
+    x = torch.randn(T, hidden, device=dev, generator=g).to(torch.bfloat16)
+    lib = L.lib()
+    lean = lib.unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)
+    wsl = torch.zeros(lean, dtype=torch.uint8, device=dev)
+    yl = torch.empty(T, hidden, dtype=torch.bfloat16, device=dev)
+    structs = [[m.gate_proj.weight_struct(), m.up_proj.weight_struct(), m.down_proj.weight_struct()] for m in blocks]
+
+    def run_fused(i: int) -> None:
+        gw, uw, dw = structs[i % copies]
+        L.check(lib.unifur_nf4_swiglu_forward(x.data_ptr(), L.BF16, T, ctypes.byref(gw), ctypes.byref(uw),
+                                              ctypes.byref(dw), yl.data_ptr(), L.BF16, wsl.data_ptr(), lean,
+                                              torch.cuda.current_stream().cuda_stream))
+    for i in range(copies):
+        run_fused(i)
+    graph = capture(torch, run_fused, copies)
+    ms = graph_ms(torch, graph, 10) / copies if graph is not None else event_ms(torch, run_fused, 2 * copies)
+    out["T512_fused"] = {"ms": round(ms, 5), "weight_gbs": round(wbytes / ms / 1e6, 1),
+                         "tflops": round(T * 270_532_608 / ms / 1e9, 2), "workspace_bytes": lean}
+    out["rotation"] = f"{copies} blocks of {wbytes} B rotated (cold HBM)"
     return out
 
 
@@ -353,38 +452,43 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
            "quantize_pass_per_weight_ms": round(q_each_s * 1e3, 3), "quantize_pass_events_ms": round(q_kernel_ms, 3),
            "params": params}
     wbytes = sum(gemv_bytes(lin.d_input(), lin.d_output(), True, 0, 0) for lin in lins)
+    # the 184.5 MB model fits the 256 MiB Infinity Cache: rotate model copies
+    # (>= 512 MiB in all) so that every token step reads its weights from HBM
+    mcopies = max(2, -(-(2 * MALL_BYTES) // wbytes))
+    models = [lins] + [[clone_linear(Q, lin) for lin in lins] for _ in range(mcopies - 1)]
     for b in (1, 32):
         xs = {di: torch.randn(b, di, device=dev, generator=g).to(torch.bfloat16 if b > 4 else torch.float32)
               for (_, di, _) in QWEN_PROJ}
 
         def step(i: int) -> None:
-            for lin in lins:
+            for lin in models[i % mcopies]:
                 lin.forward(xs[lin.d_input()])
 
         step(0)
-        graph = capture(torch, step, 1)
-        ms = graph_ms(torch, graph, 20) if graph is not None else event_ms(torch, step, 5)
+        graph = capture(torch, step, mcopies)
+        ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, step, 2 * mcopies)
         out[f"decode_b{b}"] = {"ms_per_token_step": round(ms, 4), "weight_gbs": round(wbytes / ms / 1e6, 1),
                                "tokens_per_s": round(b / ms * 1e3, 1)}
 
         # the same weights as a decoder layer drives them: q, k, v in one
         # shared-input launch, o, and the SwiGLU block (gate/up pair + down)
-        layers_ = [(lins[7 * l:7 * l + 3], lins[7 * l + 3], Q.QwenMlp(*lins[7 * l + 4:7 * l + 7]))
-                   for l in range(layers)]
+        layer_sets = [[(m[7 * l:7 * l + 3], m[7 * l + 3], Q.QwenMlp(*m[7 * l + 4:7 * l + 7])) for l in range(layers)]
+                      for m in models]
 
         def layer_step(i: int) -> None:
-            for qkv, o, mlp in layers_:
+            for qkv, o, mlp in layer_sets[i % mcopies]:
                 Q.forward_shared_input(xs[896], qkv)
                 o.forward(xs[896])
                 mlp.forward(xs[896])
 
         layer_step(0)
-        graph = capture(torch, layer_step, 1)
-        ms = graph_ms(torch, graph, 20) if graph is not None else event_ms(torch, layer_step, 5)
+        graph = capture(torch, layer_step, mcopies)
+        ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, layer_step, 2 * mcopies)
         out[f"decode_b{b}_layer_launches"] = {"ms_per_token_step": round(ms, 4),
                                               "weight_gbs": round(wbytes / ms / 1e6, 1),
                                               "tokens_per_s": round(b / ms * 1e3, 1), "launches": 4 * layers}
     out["weight_bytes"] = wbytes
+    out["rotation"] = f"{mcopies} model copies of {wbytes} B rotated (cold HBM)"
     return out
 
 
@@ -506,10 +610,21 @@ def cpu_baseline(sample_s: float) -> dict:
             break
     dt = (time.perf_counter() - t0) / iters
     return {"value": round(gemv_bytes(d_in, d_out, dq=True) / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"{iters} x config-2 GEMV (1-thread dequantize of the 4096x11008 DQ weight + {threads}-thread "
                       f"f32 GEMV), {dt * 1e3:.1f} ms each; oracle/nf4_oracle.c restatement of "
                       f"PackedNf4Tensor::dequantize + burn linear"}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_beside() -> dict:
@@ -521,7 +636,7 @@ def cpu_beside() -> dict:
     on a 32-row sample of X and scaled to the 2048 rows."""
     from oracle import oracle as O
     threads = len(os.sched_getaffinity(0))
-    out = {"cores": threads}
+    out = {"cores": threads, "cpu_model": cpu_model()}
     n = 4096 * 4096
     v = O.fill_normal(0x4E463458, 0.02, n)
     t0 = time.perf_counter()
@@ -569,6 +684,7 @@ PARTS = {
     "qwen": lambda torch, Q, L: bench_qwen(torch, Q, L),
     "embedding": lambda torch, Q, L: bench_embedding(torch, Q, L),
     "backward": lambda torch, Q, L: bench_backward(torch, Q, L),
+    "ceiling": lambda torch, Q, L: {f"{mib}MiB": bench_ceiling(torch, L, mib << 20) for mib in (22, 69, 256)},
 }
 
 
@@ -613,8 +729,11 @@ def main() -> int:
         print(json.dumps({name: PARTS[name](torch, Q, L) for name in args.parts}))
         return 0
     gemv = bench_gemv(torch, Q, L, args)
+    ceiling = bench_ceiling(torch, L, gemv["bytes"])
     codec = bench_codec(torch, Q, L)
     secondary = {
+        "hbm_ceiling_gemv_size": ceiling,
+        "hbm_ceiling_config1_size": bench_ceiling(torch, L, codec["bytes"]),
         "gemv_warm": {"kernel_ms": round(gemv["kernel_warm_ms"], 5),
                       "gbs": round(gemv["bytes"] / gemv["kernel_warm_ms"] / 1e6, 1)},
         "gemv_bf16_activations_cold": {
@@ -628,9 +747,13 @@ def main() -> int:
     if not args.quick:
         gemm = bench_gemm(torch, Q, L)
         secondary["prefill_qlora_gemm_config3"] = {
+            "path": "default workspace: W (+ s A B) expanded to bf16, then hipBLASLt",
             "ms": round(gemm["ms"], 5), "tflops": round(gemm["tflops"], 1), "frac": round(gemm["frac"], 4),
             "base_gemm_kernel_ms": round(gemm["base_kernel_ms"], 5), "base_tflops": round(gemm["base_tflops"], 1),
             "max_rel_err": gemm["max_rel_err"]}
+        secondary["prefill_fused_gemm_config3"] = dict(
+            path="least workspace: the fused MFMA kernel (NF4 tiles dequantized in LDS, LoRA in the epilogue)",
+            **gemm["fused"])
         secondary["swiglu_config4"] = bench_swiglu(torch, Q, L, (1, 16, 512))
         secondary["qwen05b_config5"] = bench_qwen(torch, Q, L)
         secondary["embedding_qwen05b"] = bench_embedding(torch, Q, L)
@@ -646,6 +769,7 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": gemv["steps"],
+        "steps_requested": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(gemv["ms_per_step"], 5),
         "higher_is_better": True,
@@ -669,6 +793,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": read_traffic(),
+            "frac_of_measured_read": round(achieved / ceiling["read_gbs"], 4),
+            "measured_read_gbs": ceiling["read_gbs"],
         },
         "cpu_baseline": cpu,
         "secondary": secondary,

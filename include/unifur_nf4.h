@@ -321,6 +321,16 @@ int unifur_nf4_swiglu_forward(const void *x, int x_dtype, uint64_t rows, const u
                               const unifur_nf4_weight *up, const unifur_nf4_weight *down, void *y, int y_dtype,
                               void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* ---- measurement --------------------------------------------------------- */
+
+/* No counterpart in the reference: the ceiling the decode GEMV's roofline
+ * fraction is compared with.  Streams `bytes` (a multiple of 16) from src with
+ * 16-byte loads over `workgroups` workgroups: a read only (dst == NULL;
+ * sink, 64 u32, is written only if the data XOR to a fixed odd value) or a
+ * copy to dst.  16-byte aligned buffers. */
+int unifur_nf4_stream_probe(const void *src, uint64_t bytes, void *dst, uint32_t *sink, uint32_t workgroups,
+                            void *stream);
+
 #ifdef __cplusplus
 }
 #endif

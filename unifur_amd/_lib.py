@@ -100,6 +100,7 @@ SIGNATURES = {
                                                _I, _P]),
     "unifur_nf4_qlora_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Lora), _P, _I, _P,
                                       _U64, _P]),
+    "unifur_nf4_stream_probe": (_I, [_P, _U64, _P, _P, ctypes.c_uint32, _P]),
     "unifur_nf4_swiglu_workspace_size": (_U64, [_U64, _U64, _U64, _I]),
     "unifur_nf4_swiglu_min_workspace_size": (_U64, [_U64, _U64, _U64, _I]),
     "unifur_nf4_swiglu_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Weight),

@@ -21,6 +21,7 @@
 #include "nf4_generic.hpp"
 #include "nf4_gemv.hpp"
 #include "nf4_layout.hpp"
+#include "nf4_probe.hpp"
 
 namespace unifur {
 namespace {
@@ -1309,6 +1310,17 @@ int unifur_nf4_unstripe_weight(const unifur_nf4_weight* src, uint8_t* dst_packed
   UNIFUR_HIP(launch_stripe_codes(src->packed, dst_packed, src->d_in, src->d_out, false, st));
   UNIFUR_HIP(launch_stripe_scales(dq ? (const void*)src->scales.dq_codes : (const void*)src->scales.absmax,
                                   dst_scales, src->d_in, src->d_out, dq, false, st));
+  return UNIFUR_NF4_OK;
+}
+
+int unifur_nf4_stream_probe(const void* src, uint64_t bytes, void* dst, uint32_t* sink, uint32_t workgroups,
+                            void* stream) {
+  if (bytes == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(src && sink, "src or sink is NULL");
+  UNIFUR_ARG(bytes % 16 == 0 && aligned_to(src, 16) && aligned_to(dst, 16), "bytes and buffers must be 16-byte multiples");
+  UNIFUR_ARG(workgroups >= 1 && workgroups <= 65536, "workgroups must be in [1, 65536]");
+  UNIFUR_HIP(launch_stream_probe(src, bytes / 16, dst, 0x9e3779b9u, sink, (int)workgroups,
+                                 static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
 }
 
