@@ -487,6 +487,33 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
         out[f"decode_b{b}_layer_launches"] = {"ms_per_token_step": round(ms, 4),
                                               "weight_gbs": round(wbytes / ms / 1e6, 1),
                                               "tokens_per_s": round(b / ms * 1e3, 1), "launches": 4 * layers}
+
+        # QwenDecoderLayer::step's NF4 chain through the two stage entry
+        # points per layer (input norm + q/k/v; o + residual, post norm +
+        # SwiGLU + residual), each layer's output feeding the next; q stands
+        # in for the attention output (the attention itself is not on the NF4
+        # path and is not timed)
+        norms = [(torch.randn(896, device=dev, generator=g) * 0.1, torch.randn(896, device=dev, generator=g) * 0.1)
+                 for _ in range(layers)]
+        from unifur_amd import qwennet as N
+        dec_sets = [[N.QwenDecoderLayer(*m[7 * l:7 * l + 4], Q.QwenMlp(*m[7 * l + 4:7 * l + 7]), *norms[l], 1e-6)
+                     for l in range(layers)] for m in models]
+        x0 = xs[896]
+
+        def decoder_step(i: int) -> None:
+            h = x0
+            for lay in dec_sets[i % mcopies]:
+                q, _, _ = lay.project(h)
+                h = lay.attn_out_mlp(h, q)
+
+        decoder_step(0)
+        graph = capture(torch, decoder_step, mcopies)
+        ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, decoder_step, 2 * mcopies)
+        out[f"decode_b{b}_decoder_stages"] = {"ms_per_token_step": round(ms, 4),
+                                              "weight_gbs": round(wbytes / ms / 1e6, 1),
+                                              "tokens_per_s": round(b / ms * 1e3, 1),
+                                              "calls_per_layer": 2,
+                                              "activations": "f32" if b <= 4 else "bf16"}
     out["weight_bytes"] = wbytes
     out["rotation"] = f"{mcopies} model copies of {wbytes} B rotated (cold HBM)"
     return out

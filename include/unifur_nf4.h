@@ -321,6 +321,46 @@ int unifur_nf4_swiglu_forward(const void *x, int x_dtype, uint64_t rows, const u
                               const unifur_nf4_weight *up, const unifur_nf4_weight *down, void *y, int y_dtype,
                               void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* ---- decoder-layer decode ------------------------------------------------ */
+
+/* The NF4 projections and norms of one decoder layer with a full-attention
+ * mixer: QwenDecoderLayer (src/qwennet.rs:1064-1129) whose QwenFullAttention
+ * (src/qwennet.rs:856-956, attn_output_gate = false) and QwenMlp
+ * (src/qwennet.rs:786-820) hold Nf4Linear projections.  q, k, v, gate and up
+ * are [hidden, *], o is [q.d_out, hidden], down [gate.d_out, hidden].
+ * input_norm and post_norm are the QwenRmsNorm weights [hidden] (f32, applied
+ * as w + 1, src/qwennet.rs:104-109) with epsilon eps. */
+typedef struct unifur_nf4_decoder_layer {
+  unifur_nf4_weight q, k, v, o;
+  unifur_nf4_weight gate, up, down;
+  const float *input_norm;
+  const float *post_norm;
+  float eps;
+} unifur_nf4_decoder_layer;
+
+/* QwenDecoderLayer::step up to the attention (src/qwennet.rs:1112-1121 with
+ * QwenFullAttention::project, :927-951): n = input_norm(x), then
+ * q = n Wq, k = n Wk, v = n Wv -- before the per-head norms, rotary and the
+ * attention itself, which stay with the caller.  x [rows, hidden]; q, k, v
+ * [rows, d_out of their weight]; all of dtype.  Decode batches (<= 4 rows)
+ * over striped weights of one scale kind take one launch with the norm
+ * folded in; other calls norm x into the workspace first. */
+uint64_t unifur_nf4_decoder_attn_in_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer *layer, int dtype);
+int unifur_nf4_decoder_attn_in(const void *x, int dtype, uint64_t rows, const unifur_nf4_decoder_layer *layer,
+                               void *q, void *k, void *v, void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* QwenDecoderLayer::step after the attention (src/qwennet.rs:1122-1128):
+ * x1 = x + ctx Wo, then y = x1 + down(silu(gate(n)) * up(n)) with
+ * n = post_norm(x1).  x, y [rows, hidden]; ctx [rows, o.d_in] (the merged
+ * attention heads); all of dtype; y may be x.  Decode batches over striped
+ * weights add the residuals in the projections' epilogues and fold the norm
+ * into the gate/up launch (<= 2 rows) or norm x1 once (3..64 bf16 rows). */
+uint64_t unifur_nf4_decoder_attn_out_mlp_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer *layer,
+                                                        int dtype);
+int unifur_nf4_decoder_attn_out_mlp(const void *x, const void *ctx, int dtype, uint64_t rows,
+                                    const unifur_nf4_decoder_layer *layer, void *y, void *workspace,
+                                    uint64_t workspace_bytes, void *stream);
+
 /* ---- measurement --------------------------------------------------------- */
 
 /* No counterpart in the reference: the ceiling the decode GEMV's roofline

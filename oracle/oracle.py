@@ -217,6 +217,29 @@ def swiglu_ref_f64(x, wg, wu, wd) -> np.ndarray:
     return h @ np.asarray(wd, np.float64)
 
 
+def rms_norm_f64(x, w, eps) -> np.ndarray:
+    """QwenRmsNorm::forward (src/qwennet.rs:104-109) over the last dim:
+    x * (mean(x^2) + eps)^(-1/2) * (w + 1), in float64."""
+    x64 = np.asarray(x, np.float64)
+    ms = np.mean(x64 * x64, axis=-1, keepdims=True)
+    return x64 * (ms + float(eps)) ** -0.5 * (np.asarray(w, np.float64) + 1.0)
+
+
+def decoder_attn_in_ref_f64(x, input_norm, eps, wq, wk, wv):
+    """QwenDecoderLayer::step up to the attention (src/qwennet.rs:1112-1121,
+    QwenFullAttention::project :927-951 before the QK norms): q, k, v of
+    input_norm(x), each with its dequantized weight [hidden, d_out]."""
+    n = rms_norm_f64(x, input_norm, eps)
+    return linear_ref_f64(n, wq), linear_ref_f64(n, wk), linear_ref_f64(n, wv)
+
+
+def decoder_attn_out_mlp_ref_f64(x, ctx, post_norm, eps, wo, wg, wu, wd):
+    """QwenDecoderLayer::step after the attention (src/qwennet.rs:1122-1128):
+    x1 = x + ctx Wo; x1 + QwenMlp(post_norm(x1)).  Returns (x1, y)."""
+    x1 = np.asarray(x, np.float64) + linear_ref_f64(ctx, wo)
+    return x1, x1 + swiglu_ref_f64(rms_norm_f64(x1, post_norm, eps), wg, wu, wd)
+
+
 def normwise_error(y, ref, x, w_abs_bound) -> float:
     """max_n |y_n - r_n| / max(sum_k |x_k| |W_kn|, tiny), per output row.
 

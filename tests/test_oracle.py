@@ -303,6 +303,49 @@ def test_silu_closed_forms(oracle):
     assert np.all(np.abs(s - ref) <= 4 * np.spacing(np.abs(ref).astype(np.float32)) + 1e-12)
 
 
+def test_rms_norm_closed_forms(oracle):
+    """QwenRmsNorm (src/qwennet.rs:104-109): known answers that catch a sum
+    taken for the mean, eps added outside the root, or w used for w + 1."""
+    x = np.array([[3.0, 4.0]])
+    np.testing.assert_allclose(oracle.rms_norm_f64(x, [0.0, 0.0], 0.0), x / np.sqrt(12.5), rtol=1e-15)
+    # eps inside the root: mean 1, eps 3 -> 1 / sqrt(4)
+    np.testing.assert_allclose(oracle.rms_norm_f64([[1.0, 1.0]], [0.0, 0.0], 3.0), [[0.5, 0.5]], rtol=1e-15)
+    # the weight enters as w + 1: a constant row normalises to sign * (w + 1)
+    w = np.array([0.5, -0.25, 2.0])
+    np.testing.assert_allclose(oracle.rms_norm_f64([[-7.0, -7.0, -7.0]], w, 0.0), [-(w + 1.0)], rtol=1e-15)
+    # unit mean square with w = 0, eps = 0, for any row; scale invariant
+    r = np.random.default_rng(5).normal(size=(4, 37))
+    n = oracle.rms_norm_f64(r, np.zeros(37), 0.0)
+    np.testing.assert_allclose(np.mean(n * n, axis=-1), 1.0, rtol=1e-12)
+    np.testing.assert_allclose(oracle.rms_norm_f64(9.0 * r, np.zeros(37), 0.0), n, rtol=1e-12)
+    assert np.all(oracle.rms_norm_f64(np.zeros((1, 5)), np.zeros(5), 1e-6) == 0.0)
+
+
+def test_decoder_stage_references_compose(oracle):
+    """The decoder-step references: residuals are identities when the
+    projections are zero, and the attention-input stage is the norm followed
+    by the three products."""
+    rng = np.random.default_rng(11)
+    h, inter, qd = 8, 12, 6
+    x = rng.normal(size=(2, h))
+    ctx = rng.normal(size=(2, qd))
+    g = rng.normal(size=h)
+    z = lambda a, b: np.zeros((a, b))
+    x1, y = oracle.decoder_attn_out_mlp_ref_f64(x, ctx, g, 1e-6, z(qd, h), z(h, inter), z(h, inter), z(inter, h))
+    np.testing.assert_array_equal(x1, x)
+    np.testing.assert_array_equal(y, x)
+    wo = rng.normal(size=(qd, h))
+    x1, y = oracle.decoder_attn_out_mlp_ref_f64(x, ctx, g, 1e-6, wo, rng.normal(size=(h, inter)),
+                                                rng.normal(size=(h, inter)), z(inter, h))
+    np.testing.assert_allclose(x1, x + ctx @ wo, rtol=1e-14)
+    np.testing.assert_array_equal(y, x1)
+    wq, wk, wv = (rng.normal(size=(h, d)) for d in (4, 2, 2))
+    q, k, v = oracle.decoder_attn_in_ref_f64(x, g, 1e-6, wq, wk, wv)
+    n = oracle.rms_norm_f64(x, g, 1e-6)
+    for got, w in ((q, wq), (k, wk), (v, wv)):
+        np.testing.assert_allclose(got, n @ w, rtol=1e-14)
+
+
 def test_transpose_is_an_involution_with_index_identity(oracle):
     a = np.arange(130 * 67, dtype=np.float32)
     t = oracle.transpose(a, 130, 67)

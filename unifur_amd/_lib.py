@@ -50,6 +50,21 @@ class Weight(ctypes.Structure):
     ]
 
 
+class DecoderLayer(ctypes.Structure):
+    _fields_ = [
+        ("q", Weight),
+        ("k", Weight),
+        ("v", Weight),
+        ("o", Weight),
+        ("gate", Weight),
+        ("up", Weight),
+        ("down", Weight),
+        ("input_norm", ctypes.c_void_p),
+        ("post_norm", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+    ]
+
+
 class Lora(ctypes.Structure):
     _fields_ = [
         ("a", ctypes.c_void_p),
@@ -101,6 +116,10 @@ SIGNATURES = {
     "unifur_nf4_qlora_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Lora), _P, _I, _P,
                                       _U64, _P]),
     "unifur_nf4_stream_probe": (_I, [_P, _U64, _P, _P, ctypes.c_uint32, _P]),
+    "unifur_nf4_decoder_attn_in_workspace_size": (_U64, [_U64, ctypes.POINTER(DecoderLayer), _I]),
+    "unifur_nf4_decoder_attn_in": (_I, [_P, _I, _U64, ctypes.POINTER(DecoderLayer), _P, _P, _P, _P, _U64, _P]),
+    "unifur_nf4_decoder_attn_out_mlp_workspace_size": (_U64, [_U64, ctypes.POINTER(DecoderLayer), _I]),
+    "unifur_nf4_decoder_attn_out_mlp": (_I, [_P, _P, _I, _U64, ctypes.POINTER(DecoderLayer), _P, _P, _U64, _P]),
     "unifur_nf4_swiglu_workspace_size": (_U64, [_U64, _U64, _U64, _I]),
     "unifur_nf4_swiglu_min_workspace_size": (_U64, [_U64, _U64, _U64, _I]),
     "unifur_nf4_swiglu_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Weight),

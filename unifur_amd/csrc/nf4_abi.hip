@@ -924,6 +924,229 @@ int run_linear_multi(const void* x, int x_dtype, uint64_t rows, const unifur_nf4
   return UNIFUR_NF4_OK;
 }
 
+// ------------------------------------------------ decoder-layer decode --
+//
+// The two halves of QwenDecoderLayer::step around the attention
+// (src/qwennet.rs:1112-1129).  Workspace: the region a general-path call of
+// run_linear / run_linear_multi / run_swiglu needs (it starts with the shared
+// counter region), then this stage's own buffers.
+
+size_t dtype_bytes(int dtype) { return dtype == UNIFUR_NF4_BF16 ? 2 : 4; }
+
+int check_layer(const unifur_nf4_decoder_layer* l) {
+  UNIFUR_ARG(l != nullptr, "decoder layer is NULL");
+  if (int r = check_weight(&l->q, "q")) return r;
+  if (int r = check_weight(&l->k, "k")) return r;
+  if (int r = check_weight(&l->v, "v")) return r;
+  if (int r = check_weight(&l->o, "o")) return r;
+  if (int r = check_weight(&l->gate, "gate")) return r;
+  if (int r = check_weight(&l->up, "up")) return r;
+  if (int r = check_weight(&l->down, "down")) return r;
+  const uint64_t h = l->q.d_in;
+  UNIFUR_ARG(l->k.d_in == h && l->v.d_in == h, "q, k and v must share d_in (hidden)");
+  UNIFUR_ARG(l->o.d_out == h, "o must map back to hidden");
+  UNIFUR_ARG(l->gate.d_in == h && l->up.d_in == h && l->up.d_out == l->gate.d_out,
+             "gate and up must be [hidden, intermediate]");
+  UNIFUR_ARG(l->down.d_in == l->gate.d_out && l->down.d_out == h, "down must be [intermediate, hidden]");
+  UNIFUR_ARG(l->input_norm != nullptr && l->post_norm != nullptr, "the norm weights are NULL");
+  UNIFUR_ARG(h <= 0x7fffffffu && l->gate.d_out <= 0x7fffffffu, "dimension exceeds 2^31-1");
+  return UNIFUR_NF4_OK;
+}
+
+// q, k, v in one striped GEMV launch with the input norm folded in
+bool attn_in_fused(uint64_t rows, const unifur_nf4_decoder_layer* l) {
+  const unifur_nf4_weight* w[3] = {&l->q, &l->k, &l->v};
+  for (const auto* x : w)
+    if (!is_striped(x) || x->scales.kind != l->q.scales.kind) return false;
+  return rows >= 1 && rows <= (uint64_t)kGemvMaxRows;
+}
+
+struct AttnInLayout {
+  size_t inner, normed, total;
+};
+
+AttnInLayout plan_attn_in(uint64_t rows, const unifur_nf4_decoder_layer* l, int dtype) {
+  AttnInLayout L{};
+  const uint64_t dn[3] = {l->q.d_out, l->k.d_out, l->v.d_out};
+  L.inner = align_up(std::max<uint64_t>(kCounterRegion,
+                                        unifur_nf4_linear_multi_workspace_size(rows, l->q.d_in, dn, 3, dtype)));
+  L.normed = L.inner;
+  L.total = L.normed + align_up((size_t)rows * l->q.d_in * dtype_bytes(dtype));
+  return L;
+}
+
+int run_attn_in(const void* x, int dtype, uint64_t rows, const unifur_nf4_decoder_layer* l, void* q, void* k,
+                void* v, void* workspace, uint64_t workspace_bytes, hipStream_t stream) {
+  UNIFUR_ARG(valid_dtype(dtype), "dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  if (int r = check_layer(l)) return r;
+  if (rows == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(x != nullptr && q != nullptr && k != nullptr && v != nullptr, "x, q, k or v is NULL");
+  UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  const bool bf = dtype == UNIFUR_NF4_BF16;
+  const unifur_nf4_weight w[3] = {l->q, l->k, l->v};
+  void* const outs[3] = {q, k, v};
+  if (attn_in_fused(rows, l)) {
+    int dn[3];
+    GemvWeight gw[3];
+    for (int i = 0; i < 3; ++i) {
+      dn[i] = (int)w[i].d_out;
+      gw[i] = gemv_weight(&w[i], outs[i], bf, nullptr, nullptr);
+    }
+    const StripedPlan plan = plan_gemv_striped((int)rows, (int)l->q.d_in, dn, 3, false);
+    UNIFUR_HIP(launch_gemv_striped(plan, x, bf, (int)rows, (int)l->q.d_in, gw, 3, false, stream, l->input_norm,
+                                   l->eps));
+    return UNIFUR_NF4_OK;
+  }
+  const AttnInLayout L = plan_attn_in(rows, l, dtype);
+  void* ws = nullptr;
+  if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
+  void* n = at<void>(ws, L.normed);
+  UNIFUR_HIP(launch_rms_norm(x, bf, (int)rows, (int)l->q.d_in, l->input_norm, l->eps, n, bf, stream));
+  return run_linear_multi(n, dtype, rows, w, nullptr, outs, dtype, 3, ws, L.inner, stream);
+}
+
+enum class OutPath { kGemv, kSkinny, kGeneral };
+enum class MlpStage { kPairNorm, kMultiNorm, kSkinny, kGeneral };
+
+struct AttnOutLayout {
+  OutPath o_path;
+  MlpStage mlp;
+  StripedPlan o_plan, up_plan, down_plan;
+  size_t inner, x1, nrm, tmp, h, u, hb, part0, part1, total;
+};
+
+AttnOutLayout plan_attn_out(uint64_t rows, const unifur_nf4_decoder_layer* l, int dtype, const void* ctx,
+                            const void* x1_probe) {
+  AttnOutLayout L{};
+  const uint64_t hid = l->o.d_out, inter = l->gate.d_out, ctx_dim = l->o.d_in;
+  const bool bf = dtype == UNIFUR_NF4_BF16;
+  const int hd = (int)hid, gi[2] = {(int)inter, (int)inter};
+  const bool mlp_striped = is_striped(&l->gate) && is_striped(&l->up) && is_striped(&l->down) &&
+                           l->gate.scales.kind == l->up.scales.kind;
+  // o with the residual in its epilogue
+  if (is_striped(&l->o) && rows <= (uint64_t)kGemvMaxRows) {
+    L.o_path = OutPath::kGemv;
+    L.o_plan = plan_gemv_striped((int)rows, (int)ctx_dim, &hd, 1, false);
+  } else if (is_striped(&l->o) && bf && rows <= (uint64_t)kSkinnyMaxRows && ctx_dim <= 0x7fffffffu &&
+             skinny_supported((int)rows, (int)ctx_dim, ctx) && hid / 64 <= (uint64_t)kMaxCounters) {
+    L.o_path = OutPath::kSkinny;
+    L.o_plan = plan_skinny((int)rows, (int)ctx_dim, &hd, 1, false);
+  } else {
+    L.o_path = OutPath::kGeneral;
+  }
+  // gate/up (+ norm) then down with the residual in its epilogue
+  if (mlp_striped && rows <= (uint64_t)kGemvPairMaxRows) {
+    L.mlp = MlpStage::kPairNorm;
+    L.up_plan = plan_gemv_striped((int)rows, (int)hid, gi, 2, true);
+    L.down_plan = plan_gemv_striped((int)rows, (int)inter, &hd, 1, false);
+  } else if (mlp_striped && rows <= (uint64_t)kGemvMaxRows) {
+    L.mlp = MlpStage::kMultiNorm;
+    L.up_plan = plan_gemv_striped((int)rows, (int)hid, gi, 2, false);
+    L.down_plan = plan_gemv_striped((int)rows, (int)inter, &hd, 1, false);
+  } else if (mlp_striped && bf && rows <= (uint64_t)kSkinnyMaxRows && skinny_supported((int)rows, (int)hid, x1_probe) &&
+             skinny_supported((int)rows, (int)inter, x1_probe) && std::max(hid, inter) / 64 <= (uint64_t)kMaxCounters) {
+    L.mlp = MlpStage::kSkinny;
+    L.up_plan = plan_skinny((int)rows, (int)hid, gi, 2, true);
+    L.down_plan = plan_skinny((int)rows, (int)inter, &hd, 1, false);
+  } else {
+    L.mlp = MlpStage::kGeneral;
+  }
+  uint64_t inner = kCounterRegion;
+  if (L.o_path == OutPath::kGeneral)
+    inner = std::max<uint64_t>(inner, unifur_nf4_linear_workspace_size(rows, ctx_dim, hid, dtype, 0));
+  if (L.mlp == MlpStage::kGeneral)
+    inner = std::max<uint64_t>(inner, swiglu_workspace(rows, hid, inter, dtype, true));
+  Carver c;
+  c.off = align_up(inner);
+  L.inner = c.off;
+  const size_t act = (size_t)rows * hid * dtype_bytes(dtype);
+  L.x1 = c.take(act);
+  L.nrm = c.take(act);
+  L.tmp = c.take(act);
+  L.h = c.take((size_t)rows * inter * 4);
+  L.u = c.take((size_t)rows * inter * 4);
+  L.hb = c.take((size_t)rows * inter * 2);
+  size_t p0 = 0, p1 = 0;
+  if (L.o_path == OutPath::kSkinny) p0 = skinny_partial_floats(L.o_plan, (int)rows, hd);
+  if (L.mlp == MlpStage::kSkinny) {
+    p0 = std::max(p0, std::max(skinny_partial_floats(L.up_plan, (int)rows, (int)inter),
+                               skinny_partial_floats(L.down_plan, (int)rows, hd)));
+    p1 = skinny_partial_floats(L.up_plan, (int)rows, (int)inter);
+  }
+  L.part0 = c.take(p0 * sizeof(float));
+  L.part1 = c.take(p1 * sizeof(float));
+  L.total = c.off;
+  return L;
+}
+
+int run_attn_out_mlp(const void* x, const void* ctx, int dtype, uint64_t rows, const unifur_nf4_decoder_layer* l,
+                     void* y, void* workspace, uint64_t workspace_bytes, hipStream_t stream) {
+  UNIFUR_ARG(valid_dtype(dtype), "dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  if (int r = check_layer(l)) return r;
+  if (rows == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(x != nullptr && ctx != nullptr && y != nullptr, "x, ctx or y is NULL");
+  UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  const bool bf = dtype == UNIFUR_NF4_BF16;
+  const uint64_t hid = l->o.d_out, inter = l->gate.d_out;
+  const AttnOutLayout L = plan_attn_out(rows, l, dtype, ctx, reinterpret_cast<const void*>(uintptr_t{256}));
+  void* ws = nullptr;
+  if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
+  unsigned* cnt = at<unsigned>(ws, 0);
+  void* x1 = at<void>(ws, L.x1);
+  // x1 = x + ctx Wo
+  if (L.o_path == OutPath::kGeneral) {
+    void* t = at<void>(ws, L.tmp);
+    if (int r = run_linear(ctx, dtype, rows, &l->o, nullptr, nullptr, t, dtype, ws, L.inner, stream)) return r;
+    UNIFUR_HIP(launch_add(x, t, bf, (size_t)rows * hid, x1, stream));
+  } else {
+    GemvWeight ow = gemv_weight(&l->o, x1, bf, cnt, at<float>(ws, L.part0));
+    ow.residual = x;
+    if (L.o_path == OutPath::kGemv)
+      UNIFUR_HIP(launch_gemv_striped(L.o_plan, ctx, bf, (int)rows, (int)l->o.d_in, &ow, 1, false, stream));
+    else
+      UNIFUR_HIP(launch_skinny(L.o_plan, static_cast<const uint16_t*>(ctx), (int)rows, (int)l->o.d_in, &ow, 1, false,
+                               stream));
+  }
+  // y = x1 + down(silu(gate n) * up n), n = post_norm(x1)
+  float* h = at<float>(ws, L.h);
+  switch (L.mlp) {
+    case MlpStage::kPairNorm:
+    case MlpStage::kMultiNorm: {
+      const bool pair = L.mlp == MlpStage::kPairNorm;
+      GemvWeight gw[2] = {gemv_weight(&l->gate, h, false, cnt, nullptr),
+                          gemv_weight(&l->up, pair ? nullptr : at<float>(ws, L.u), false, cnt, nullptr)};
+      UNIFUR_HIP(launch_gemv_striped(L.up_plan, x1, bf, (int)rows, (int)hid, gw, 2, pair, stream, l->post_norm,
+                                     l->eps));
+      if (!pair) UNIFUR_HIP(launch_silu_mul(h, at<float>(ws, L.u), (size_t)rows * inter, h, stream));
+      GemvWeight dw = gemv_weight(&l->down, y, bf, cnt, nullptr);
+      dw.residual = x1;
+      UNIFUR_HIP(launch_gemv_striped(L.down_plan, h, false, (int)rows, (int)inter, &dw, 1, false, stream));
+      return UNIFUR_NF4_OK;
+    }
+    case MlpStage::kSkinny: {
+      uint16_t* n = at<uint16_t>(ws, L.nrm);
+      uint16_t* hb = at<uint16_t>(ws, L.hb);
+      float* p0 = at<float>(ws, L.part0);
+      UNIFUR_HIP(launch_rms_norm(x1, true, (int)rows, (int)hid, l->post_norm, l->eps, n, true, stream));
+      GemvWeight gw[2] = {gemv_weight(&l->gate, hb, true, cnt, p0),
+                          gemv_weight(&l->up, nullptr, true, cnt, at<float>(ws, L.part1))};
+      UNIFUR_HIP(launch_skinny(L.up_plan, n, (int)rows, (int)hid, gw, 2, true, stream));
+      GemvWeight dw = gemv_weight(&l->down, y, true, cnt, p0);
+      dw.residual = x1;
+      UNIFUR_HIP(launch_skinny(L.down_plan, hb, (int)rows, (int)inter, &dw, 1, false, stream));
+      return UNIFUR_NF4_OK;
+    }
+    case MlpStage::kGeneral:
+      break;
+  }
+  void* n = at<void>(ws, L.nrm);
+  void* t = at<void>(ws, L.tmp);
+  UNIFUR_HIP(launch_rms_norm(x1, bf, (int)rows, (int)hid, l->post_norm, l->eps, n, bf, stream));
+  if (int r = run_swiglu(n, dtype, rows, &l->gate, &l->up, &l->down, t, dtype, ws, L.inner, stream)) return r;
+  UNIFUR_HIP(launch_add(x1, t, bf, (size_t)rows * hid, y, stream));
+  return UNIFUR_NF4_OK;
+}
+
 // ------------------------------------------------- allocation-free entry --
 
 // The scratch of unifur_nf4_linear_forward_noalloc: a file-scope device array,
@@ -1078,6 +1301,30 @@ int unifur_nf4_pack_codes(const uint8_t* codes, uint64_t len, uint8_t* packed, v
   UNIFUR_ARG(packed && codes, "packed or codes is NULL");
   UNIFUR_HIP(launch_pack_codes(codes, len, packed, static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
+}
+
+uint64_t unifur_nf4_decoder_attn_in_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer* layer, int dtype) {
+  if (rows == 0 || check_layer(layer) != UNIFUR_NF4_OK || !valid_dtype(dtype)) return 0;
+  if (attn_in_fused(rows, layer)) return 0;
+  return plan_attn_in(rows, layer, dtype).total;
+}
+
+int unifur_nf4_decoder_attn_in(const void* x, int dtype, uint64_t rows, const unifur_nf4_decoder_layer* layer,
+                               void* q, void* k, void* v, void* workspace, uint64_t workspace_bytes, void* stream) {
+  return run_attn_in(x, dtype, rows, layer, q, k, v, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+uint64_t unifur_nf4_decoder_attn_out_mlp_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer* layer,
+                                                        int dtype) {
+  if (rows == 0 || check_layer(layer) != UNIFUR_NF4_OK || !valid_dtype(dtype)) return 0;
+  const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
+  return plan_attn_out(rows, layer, dtype, aligned, aligned).total;
+}
+
+int unifur_nf4_decoder_attn_out_mlp(const void* x, const void* ctx, int dtype, uint64_t rows,
+                                    const unifur_nf4_decoder_layer* layer, void* y, void* workspace,
+                                    uint64_t workspace_bytes, void* stream) {
+  return run_attn_out_mlp(x, ctx, dtype, rows, layer, y, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 uint64_t unifur_nf4_linear_multi_workspace_size(uint64_t rows, uint64_t d_in, const uint64_t* d_out, uint32_t n,

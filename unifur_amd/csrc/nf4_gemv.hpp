@@ -21,6 +21,7 @@ struct GemvWeight {
   float lora_scaling;
   unsigned* counters;  // workspace: one zeroed u32 per 256-column tile
   float* partials;     // workspace: splits * rows * d_out floats (split-K)
+  const void* residual;  // striped GEMV / skinny: [rows, d_out] in y's dtype added last, or null
 };
 
 struct GemvPlan {
@@ -67,12 +68,20 @@ struct StripedArgs {
   int nweights;
   GemvWeight w[kMaxGemvWeights];
   int stripe_begin[kMaxGemvWeights + 1];  // prefix sums of stripes per weight
+  // GEMV only (null for the skinny kernel): QwenRmsNorm folded into the
+  // launch, x -> x * rsqrt(mean(x^2) + norm_eps) * (norm_w + 1) per row
+  const float* norm_w;  // [d_in] or null
+  float norm_eps;
 };
 
 StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights, bool pair);
 
+// norm_w != null folds QwenRmsNorm (weight norm_w, epsilon norm_eps) over x
+// into the launch: each workgroup sums x^2 over all of d_in beside the
+// products and scales its results by the row's 1 / sqrt(mean + eps).
 hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16, int rows, int d_in,
-                               const GemvWeight* weights, int nweights, bool pair, hipStream_t stream);
+                               const GemvWeight* weights, int nweights, bool pair, hipStream_t stream,
+                               const float* norm_w = nullptr, float norm_eps = 0.0f);
 
 // ---- 5..64 bf16 rows over striped weights, on MFMA ----
 // Same decomposition (a workgroup per stripe over all of d_in, waves split

@@ -84,6 +84,7 @@ template <int T, int NW, bool XBF16, bool DQ>
 struct Chunk {
   ChunkW<DQ> w[NW];
   std::conditional_t<XBF16, uint16_t, uint32_t> x[T];  // bf16 or f32 bits
+  uint32_t g;  // with a folded norm: the norm weight of this row (f32 bits)
 };
 
 // Wave-uniform resources of one weight, bounded to this wave's rows so that
@@ -94,8 +95,10 @@ struct WaveW {
 
 template <int T, int NW, bool XBF16, bool DQ>
 __device__ __forceinline__ void issue_chunk(Chunk<T, NW, XBF16, DQ>& c, const WaveW (&ww)[NW],
-                                            const __amdgpu_buffer_rsrc_t (&xr)[T], int chunk, int lane) {
+                                            const __amdgpu_buffer_rsrc_t (&xr)[T], __amdgpu_buffer_rsrc_t gr,
+                                            bool norm, int chunk, int lane) {
   const uint32_t row = (uint32_t)(chunk * 64 + lane);
+  if (norm) c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     c.w[w].code = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
@@ -182,6 +185,13 @@ __device__ __forceinline__ int wave_column_index(int lane) {
   return ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
 }
 
+// Sum of v over the 64 lanes, in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
 __device__ __forceinline__ float epilogue_value(const GemvWeight& W, float base, int t, int gcol) {
   float y = base;
   if (W.bias) y += W.bias[gcol];
@@ -195,7 +205,12 @@ __device__ __forceinline__ float epilogue_value(const GemvWeight& W, float base,
   return y;
 }
 
+// y (+ residual[idx], the residual stream a decoder layer adds its
+// projection to: src/qwennet.rs:1124-1128), stored in y's dtype.
 __device__ __forceinline__ void store_y(const GemvWeight& W, size_t idx, float y) {
+  if (W.residual)
+    y += W.y_bf16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(W.residual)[idx])
+                  : reinterpret_cast<const float*>(W.residual)[idx];
   if (W.y_bf16)
     reinterpret_cast<uint16_t*>(W.y)[idx] = (uint16_t)(pack_bf16x2(y, 0.0f) & 0xffffu);
   else
@@ -245,6 +260,11 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
     xr[t] = XBF16 ? make_rsrc(static_cast<const uint16_t*>(a.x) + off, (uint32_t)nrows * 2u)
                   : make_rsrc(static_cast<const float*>(a.x) + off, (uint32_t)nrows * 4u);
   }
+  // folded QwenRmsNorm (src/qwennet.rs:104-109): the products take
+  // x * (w + 1), each lane sums x^2 over its rows, and the column sums are
+  // scaled by the row's 1 / sqrt(mean(x^2) + eps) at the end
+  const bool norm = a.norm_w != nullptr;
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : a.norm_w, norm ? (uint32_t)nrows * 4u : 0u);
 
   // LUTs first: their barrier must not wait for the issue of the chunk
   // loads, which the memory system back-pressures when every workgroup
@@ -275,7 +295,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   Chunk<T, NW, XBF16, DQ> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
-    issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, j, lane);
+    issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, norm, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -288,6 +308,9 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[w][t][i] = 0.0f;
+  float xsq[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) xsq[t] = 0.0f;
 
   Looked<NW> lk[2];
   lookup<T, NW, XBF16, DQ>(lk[0], ring[0], dq_lut, lane_off);
@@ -301,13 +324,16 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
       lookup<T, NW, XBF16, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, lane_off);
       float xs[NW][T];
 #pragma unroll
-      for (int w = 0; w < NW; ++w)
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-          const float xv = XBF16 ? bf16_bits_to_f32((uint32_t)ring[j].x[t]) : as_f((uint32_t)ring[j].x[t]);
-          xs[w][t] = xv * lk[j & 1].scale[w];  // x * block scale, once per row
+      for (int t = 0; t < T; ++t) {
+        float xv = XBF16 ? bf16_bits_to_f32((uint32_t)ring[j].x[t]) : as_f((uint32_t)ring[j].x[t]);
+        if (norm) {
+          xsq[t] = __builtin_fmaf(xv, xv, xsq[t]);
+          xv = xv * (as_f(ring[j].g) + 1.0f);
         }
-      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, c0 + j + D, lane);
+#pragma unroll
+        for (int w = 0; w < NW; ++w) xs[w][t] = xv * lk[j & 1].scale[w];  // x * block scale, once per row
+      }
+      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, norm, c0 + j + D, lane);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
@@ -337,6 +363,14 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #pragma unroll
       for (int t = 0; t < T; ++t) red[((w * T + t) * W + wave) * 16 + ci] = col[w][t];
   }
+  float* red_sq = red + NW * T * W * 16;  // the waves' sums of x^2, per row
+  if (norm) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float v = wave_sum(xsq[t]);
+      if (lane == 0) red_sq[t * W + wave] = v;
+    }
+  }
   __syncthreads();
   if (tid >= T * 16) return;
   const int t = tid / 16, cc = tid % 16;
@@ -349,6 +383,15 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #pragma unroll
     for (int q = 0; q < W; ++q) v += red[((w * T + t) * W + q) * 16 + cc];
     sum[w] = v;
+  }
+  if (norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < W; ++q) ss += red_sq[t * W + q];
+    // (mean(x^2) + eps)^(-1/2), the factor every normed x of this row carries
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)K + a.norm_eps);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum[w] *= inv;
   }
   float y = epilogue_value(G, sum[0], t, gcol);
   if constexpr (PAIR) y = silu_f32(y) * epilogue_value(a.w[1], sum[1], t, gcol);  // silu(gate x) * up x
@@ -799,9 +842,12 @@ StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights
 }
 
 hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16, int rows, int d_in,
-                               const GemvWeight* weights, int nweights, bool pair, hipStream_t stream) {
+                               const GemvWeight* weights, int nweights, bool pair, hipStream_t stream,
+                               const float* norm_w, float norm_eps) {
   StripedArgs a{};
   a.x = x;
+  a.norm_w = norm_w;
+  a.norm_eps = norm_eps;
   a.rows = rows;
   a.d_in = d_in;
   a.rows_per_wave = p.rows_per_wave;

@@ -532,4 +532,65 @@ hipError_t launch_silu_mul_bf16(const float* g, const float* u, size_t n, uint16
   return hipGetLastError();
 }
 
+// One workgroup per row: the sum of squares over the row in f32 (threads
+// stride the row, then a fixed-order tree), then every element scaled.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ x, int x_bf16, int h,
+                                                       const float* __restrict__ w, float eps, void* __restrict__ out,
+                                                       int out_bf16) {
+  __shared__ float part[256];
+  const size_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  auto load = [&](int i) -> float {
+    return x_bf16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(x)[row * h + i])
+                  : static_cast<const float*>(x)[row * h + i];
+  };
+  float ss = 0.0f;
+  for (int i = t; i < h; i += 256) {
+    const float v = load(i);
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  part[t] = ss;
+  __syncthreads();
+  for (int m = 128; m > 0; m >>= 1) {
+    if (t < m) part[t] += part[t + m];
+    __syncthreads();
+  }
+  const float inv = 1.0f / __builtin_sqrtf(part[0] / (float)h + eps);
+  for (int i = t; i < h; i += 256) {
+    const float v = (load(i) * inv) * (w[i] + 1.0f);
+    if (out_bf16)
+      static_cast<uint16_t*>(out)[row * h + i] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+    else
+      static_cast<float*>(out)[row * h + i] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void add_kernel(const void* __restrict__ a, const void* __restrict__ b, int bf16,
+                                                  size_t n, void* __restrict__ y) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    if (bf16) {
+      const float v = bf16_bits_to_f32(static_cast<const uint16_t*>(a)[i]) +
+                      bf16_bits_to_f32(static_cast<const uint16_t*>(b)[i]);
+      static_cast<uint16_t*>(y)[i] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+    } else {
+      static_cast<float*>(y)[i] = static_cast<const float*>(a)[i] + static_cast<const float*>(b)[i];
+    }
+  }
+}
+
+hipError_t launch_rms_norm(const void* x, bool x_bf16, int rows, int h, const float* w, float eps, void* out,
+                           bool out_bf16, hipStream_t stream) {
+  if (rows <= 0 || h <= 0) return hipSuccess;
+  rms_norm_kernel<<<(unsigned)rows, 256, 0, stream>>>(x, x_bf16, h, w, eps, out, out_bf16);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(const void* a, const void* b, bool bf16, size_t n, void* y, hipStream_t stream) {
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks == 0) return hipSuccess;
+  add_kernel<<<(unsigned)blocks, 256, 0, stream>>>(a, b, bf16, n, y);
+  return hipGetLastError();
+}
+
 }  // namespace unifur

@@ -50,5 +50,13 @@ hipError_t launch_silu_mul(const float* g, const float* u, size_t n, float* h, h
 hipError_t launch_silu_mul_bf16(const float* g, const float* u, size_t n, uint16_t* h, hipStream_t stream);
 // h[m][:] = bf16(silu(gu[m][:inter]) * gu[m][inter:]), gu bf16 [rows][2 inter].
 hipError_t launch_silu_mul_rows_bf16(const uint16_t* gu, size_t rows, size_t inter, uint16_t* h, hipStream_t stream);
+// QwenRmsNorm::forward (src/qwennet.rs:104-109) over the rows of x [rows, h]:
+// out = (x * (mean(x^2) + eps)^(-1/2)) * (w + 1), f32 arithmetic, x and out
+// f32 or bf16 (out rounded to nearest even).
+hipError_t launch_rms_norm(const void* x, bool x_bf16, int rows, int h, const float* w, float eps, void* out,
+                           bool out_bf16, hipStream_t stream);
+// y = a + b elementwise over n values, each f32 or bf16 (the residual adds of
+// QwenDecoderLayer::step, src/qwennet.rs:1124-1128).
+hipError_t launch_add(const void* a, const void* b, bool bf16, size_t n, void* y, hipStream_t stream);
 
 }  // namespace unifur

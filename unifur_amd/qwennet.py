@@ -10,6 +10,8 @@ this module                            reference (s-b-repo/unifur)
 ``Nf4ResidencyReport``                 ``Nf4ResidencyReport`` (src/qwennet.rs:1609-1681)
 ``qwen_linear``                        ``qwen_linear`` (src/qwennet.rs:1683-1726)
 ``projections_to_nf4``                 ``QwenTrunk::to_nf4`` (src/qwennet.rs:1185-1269), projections only
+``QwenDecoderLayer``                   ``QwenDecoderLayer::step`` (src/qwennet.rs:1112-1129), the NF4
+                                       projections and norms around a caller-supplied attention
 =====================================  ==========================================
 
 Every computation is a call into ``libunifur_nf4.so`` (through
@@ -241,3 +243,84 @@ def projections_to_nf4(projections: dict, report: Optional[Nf4ResidencyReport] =
             report.record(name.split(".")[-1], conv.resident_bytes(), WeightStore.NF4)
         out[name] = conv
     return out
+
+
+# ------------------------------------------------------- decoder-layer decode --
+
+class QwenDecoderLayer:
+    """The NF4 projection chain of one full-attention decoder layer's decode
+    step, ``QwenDecoderLayer::step`` (src/qwennet.rs:1112-1129):
+
+        n = input_norm(x); q, k, v = n Wq, n Wk, n Wv      (project, :927-951)
+        ctx = attend(q, k, v)                               (the caller's attention)
+        x1 = x + ctx Wo
+        y = x1 + down(silu(gate(post_norm(x1))) * up(post_norm(x1)))
+
+    ``input_norm`` / ``post_norm`` are QwenRmsNorm weights [hidden] applied as
+    ``w + 1`` with epsilon ``eps`` (src/qwennet.rs:104-109).  The per-head QK
+    norms, rotary and the attention itself belong to ``attend``: they are not
+    on the NF4 path.  Two library calls per step:
+    ``unifur_nf4_decoder_attn_in`` and ``unifur_nf4_decoder_attn_out_mlp``."""
+
+    def __init__(self, q_proj: "Q.Nf4Linear", k_proj: "Q.Nf4Linear", v_proj: "Q.Nf4Linear",
+                 o_proj: "Q.Nf4Linear", mlp: "Q.QwenMlp", input_norm: torch.Tensor, post_norm: torch.Tensor,
+                 eps: float = 1e-6):
+        hidden = q_proj.d_input()
+        if k_proj.d_input() != hidden or v_proj.d_input() != hidden:
+            raise ValueError("q, k and v must share d_input (hidden)")
+        if o_proj.d_output() != hidden or mlp.gate_proj.d_input() != hidden:
+            raise ValueError("o and the MLP must map hidden back to hidden")
+        for name, t in (("input_norm", input_norm), ("post_norm", post_norm)):
+            Q._require_cuda(t, name)
+            if t.dtype != torch.float32 or t.numel() != hidden:
+                raise ValueError(f"{name} must be float32 [hidden]")
+        self.q_proj, self.k_proj, self.v_proj, self.o_proj = q_proj, k_proj, v_proj, o_proj
+        self.mlp = mlp
+        self.input_norm, self.post_norm, self.eps = input_norm, post_norm, float(eps)
+
+    def hidden(self) -> int:
+        return self.q_proj.d_input()
+
+    def layer_struct(self) -> L.DecoderLayer:
+        m = self.mlp
+        return L.DecoderLayer(self.q_proj.weight_struct(), self.k_proj.weight_struct(), self.v_proj.weight_struct(),
+                              self.o_proj.weight_struct(), m.gate_proj.weight_struct(), m.up_proj.weight_struct(),
+                              m.down_proj.weight_struct(), self.input_norm.data_ptr(), self.post_norm.data_ptr(),
+                              self.eps)
+
+    def _rows(self, x: torch.Tensor, width: int, name: str) -> int:
+        Q._require_cuda(x, name)
+        if x.shape[-1] != width:
+            raise ValueError(f"{name} has last dim {x.shape[-1]}, expected {width}")
+        return x.numel() // width
+
+    def project(self, x: torch.Tensor):
+        """q, k, v of input_norm(x) (before the per-head QK norms)."""
+        rows = self._rows(x, self.hidden(), "x")
+        lead = x.shape[:-1]
+        q = torch.empty(*lead, self.q_proj.d_output(), dtype=x.dtype, device=x.device)
+        k = torch.empty(*lead, self.k_proj.d_output(), dtype=x.dtype, device=x.device)
+        v = torch.empty(*lead, self.v_proj.d_output(), dtype=x.dtype, device=x.device)
+        layer = self.layer_struct()
+        L.check(L.lib().unifur_nf4_decoder_attn_in(x.data_ptr(), Q._dtype_code(x.dtype), rows, ctypes.byref(layer),
+                                                    q.data_ptr(), k.data_ptr(), v.data_ptr(), None, 0,
+                                                    Q._stream()))
+        return q, k, v
+
+    def attn_out_mlp(self, x: torch.Tensor, ctx: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x + ctx Wo, then its MLP residual: the step's output."""
+        rows = self._rows(x, self.hidden(), "x")
+        if self._rows(ctx, self.o_proj.d_input(), "ctx") != rows or ctx.dtype != x.dtype:
+            raise ValueError("ctx must hold one row per row of x, in x's dtype")
+        y = torch.empty_like(x) if out is None else out
+        if y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous():
+            raise ValueError("out must be a contiguous tensor shaped and typed like x")
+        layer = self.layer_struct()
+        L.check(L.lib().unifur_nf4_decoder_attn_out_mlp(x.data_ptr(), ctx.data_ptr(), Q._dtype_code(x.dtype), rows,
+                                                         ctypes.byref(layer), y.data_ptr(), None, 0, Q._stream()))
+        return y
+
+    def step(self, x: torch.Tensor, attend) -> torch.Tensor:
+        """One decode step: ``attend(q, k, v) -> ctx`` supplies the attention."""
+        q, k, v = self.project(x)
+        return self.attn_out_mlp(x, attend(q, k, v))
