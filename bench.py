@@ -456,9 +456,9 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
     # (>= 512 MiB in all) so that every token step reads its weights from HBM
     mcopies = max(2, -(-(2 * MALL_BYTES) // wbytes))
     models = [lins] + [[clone_linear(Q, lin) for lin in lins] for _ in range(mcopies - 1)]
-    for b in (1, 32):
-        xs = {di: torch.randn(b, di, device=dev, generator=g).to(torch.bfloat16 if b > 4 else torch.float32)
-              for (_, di, _) in QWEN_PROJ}
+    # batch 1 in f32 (the reference's precision), batch 32 in bf16 and in f32
+    for b, xdt, tag in ((1, torch.float32, "b1"), (32, torch.bfloat16, "b32"), (32, torch.float32, "b32_f32")):
+        xs = {di: torch.randn(b, di, device=dev, generator=g).to(xdt) for (_, di, _) in QWEN_PROJ}
 
         def step(i: int) -> None:
             for lin in models[i % mcopies]:
@@ -467,8 +467,8 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
         step(0)
         graph = capture(torch, step, mcopies)
         ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, step, 2 * mcopies)
-        out[f"decode_b{b}"] = {"ms_per_token_step": round(ms, 4), "weight_gbs": round(wbytes / ms / 1e6, 1),
-                               "tokens_per_s": round(b / ms * 1e3, 1)}
+        out[f"decode_{tag}"] = {"ms_per_token_step": round(ms, 4), "weight_gbs": round(wbytes / ms / 1e6, 1),
+                                "tokens_per_s": round(b / ms * 1e3, 1)}
 
         # the same weights as a decoder layer drives them: q, k, v in one
         # shared-input launch, o, and the SwiGLU block (gate/up pair + down)
@@ -484,7 +484,7 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
         layer_step(0)
         graph = capture(torch, layer_step, mcopies)
         ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, layer_step, 2 * mcopies)
-        out[f"decode_b{b}_layer_launches"] = {"ms_per_token_step": round(ms, 4),
+        out[f"decode_{tag}_layer_launches"] = {"ms_per_token_step": round(ms, 4),
                                               "weight_gbs": round(wbytes / ms / 1e6, 1),
                                               "tokens_per_s": round(b / ms * 1e3, 1), "launches": 4 * layers}
 
@@ -509,11 +509,11 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
         decoder_step(0)
         graph = capture(torch, decoder_step, mcopies)
         ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, decoder_step, 2 * mcopies)
-        out[f"decode_b{b}_decoder_stages"] = {"ms_per_token_step": round(ms, 4),
+        out[f"decode_{tag}_decoder_stages"] = {"ms_per_token_step": round(ms, 4),
                                               "weight_gbs": round(wbytes / ms / 1e6, 1),
                                               "tokens_per_s": round(b / ms * 1e3, 1),
                                               "calls_per_layer": 2,
-                                              "activations": "f32" if b <= 4 else "bf16"}
+                                              "activations": "f32" if xdt == torch.float32 else "bf16"}
     out["weight_bytes"] = wbytes
     out["rotation"] = f"{mcopies} model copies of {wbytes} B rotated (cold HBM)"
     return out

@@ -26,9 +26,10 @@ from test_gpu_linear import TOL_BF16, acts, check, make_linear
 pytestmark = pytest.mark.gpu
 
 
-def lora_parts(oracle, d_in, d_out, r, seed, device, scaling=2.0):
-    a = oracle.fill_normal(seed, 0.02, d_in * r).reshape(d_in, r)
-    b = oracle.fill_normal(seed + 1, 0.02, r * d_out).reshape(r, d_out)
+def lora_parts(oracle, d_in, d_out, r, seed, device, scaling=2.0, sigma=0.01):
+    # config 3's adapters: A, B ~ N(0, 0.01^2)
+    a = oracle.fill_normal(seed, sigma, d_in * r).reshape(d_in, r)
+    b = oracle.fill_normal(seed + 1, sigma, r * d_out).reshape(r, d_out)
     ad = Q.LoraAdapter.from_parts(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device), scaling)
     return a, b, ad
 

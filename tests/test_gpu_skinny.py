@@ -21,7 +21,7 @@ from unifur_amd import _lib as L
 from unifur_amd import quantize as Q
 
 from test_gpu_gemm import lora_parts
-from test_gpu_linear import TOL_BF16, acts, check, make_linear
+from test_gpu_linear import TOL_BF16, TOL_F32, acts, check, make_linear
 
 pytestmark = pytest.mark.gpu
 
@@ -151,3 +151,66 @@ def test_split_d_in_hand_off_with_user_workspace(device, oracle, T):
         assert int(ws[:65536].count_nonzero()) == 0
         outs.append(y)
     assert torch.equal(outs[0], outs[1])  # slabs added in a fixed order
+
+
+# ---- f32 activations (v_mfma_f32_16x16x4_f32, exact f32 weight operand) ----
+# The reference's own precision: the f32 bar (1e-5) of BASELINE.json's north
+# star.  33..64 rows run as launches of at most 32 rows.
+
+@pytest.mark.parametrize("T", [5, 8, 16, 17, 31, 32, 33, 48, 64])
+@pytest.mark.parametrize("dq", [True, False])
+def test_f32_token_counts_and_scale_kinds(device, oracle, T, dq):
+    K, N = 1024, 512
+    lin, wdeq = make_linear(oracle, K, N, 2700 + T, device, dq=dq, striped=True)
+    x, xt = acts(oracle, T, K, 2701 + T, torch.float32, device)
+    ref = oracle.linear_ref_f64(x, wdeq)
+    check(lin.forward(xt), ref, x, wdeq, TOL_F32, f"skinny f32 T={T} dq={dq}")
+    check(lin.forward(xt, out_dtype=torch.bfloat16), ref, x, wdeq, TOL_BF16, f"skinny f32 T={T} bf16-out")
+
+
+@pytest.mark.parametrize("shape", [(904, 192), (40, 64), (896, 896), (896, 128), (896, 4864), (4864, 896),
+                                   (904, 11008)])
+@pytest.mark.parametrize("T", [7, 32, 64])
+def test_f32_ragged_d_in_and_qwen_shapes(device, oracle, shape, T):
+    K, N = shape
+    lin, wdeq = make_linear(oracle, K, N, 2800 + K + N + T, device, striped=True)
+    x, xt = acts(oracle, T, K, 2801 + T, torch.float32, device)
+    y = lin.forward(xt)
+    check(y, oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_F32, f"skinny f32 {shape} T={T}")
+    assert torch.equal(lin.forward(xt), y)  # slabs added in a fixed order
+
+
+@pytest.mark.parametrize("T", [12, 40])
+def test_f32_bias_and_lora(device, oracle, T):
+    K, N, r = 512, 256, 16
+    lin, wdeq = make_linear(oracle, K, N, 2900, device, striped=True)
+    bias = oracle.fill_normal(2901, 0.1, N)
+    lin.bias = torch.from_numpy(bias).to(device)
+    x, xt = acts(oracle, T, K, 2902 + T, torch.float32, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 2903, device, scaling=2.0)
+    ref = oracle.linear_ref_f64(x, wdeq, bias) + oracle.lora_ref_f64(x, a, b, 2.0)
+    y = Q.QloraLinear(lin, ad).forward(xt)
+    bound_x = np.abs(x) @ np.abs(wdeq) + np.abs(x) @ np.abs(a) @ np.abs(b) * 2.0
+    from oracle import oracle as O
+    nw = O.normwise_error(y.cpu().numpy(), ref, x, bound_x)
+    assert nw <= TOL_F32 and O.max_rel_error(y.cpu().numpy(), ref) <= TOL_F32, nw
+
+
+@pytest.mark.parametrize("T", [5, 16, 32])
+@pytest.mark.parametrize("kinds", [(True, True, True), (True, False, True)])
+def test_f32_swiglu_keeps_an_f32_middle(device, oracle, T, kinds):
+    hidden, inter = 896, 4864  # config 5's MLP
+    (g, u, d), (wg, wu, wd) = _swiglu_parts(oracle, hidden, inter, 3000 + T, device, kinds)
+    x, xt = acts(oracle, T, hidden, 3010 + T, torch.float32, device)
+    y = Q.QwenMlp(g, u, d).forward(xt)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    check(y, oracle.swiglu_ref_f64(x, wg, wu, wd), h, wd, TOL_F32, f"skinny f32 swiglu T={T} kinds={kinds}")
+
+
+@pytest.mark.parametrize("T", [6, 32])
+def test_f32_shared_input_qkv(device, oracle, T):
+    lins = [make_linear(oracle, 896, n, 3100 + n, device, striped=True) for n in (896, 128, 128)]
+    x, xt = acts(oracle, T, 896, 3101 + T, torch.float32, device)
+    ys = Q.forward_shared_input(xt, [l for l, _ in lins])
+    for (lin, wdeq), y in zip(lins, ys):
+        check(y, oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_F32, f"skinny f32 qkv T={T} d_out={lin.d_output()}")

@@ -192,7 +192,7 @@ struct LinearLayout {
   LinearPath path;
   bool expand;  // kMfma: bf16 weight expanded in the workspace + BLAS GEMM (else the fused kernel)
   GemvPlan gemv;
-  StripedPlan striped;
+  StripedPlan striped, striped_tail;  // skinny: the plan of each launch (the last of several f32 launches)
   size_t partials, xa, lora_at, lora_bt, wt, blas, wf32, rm_codes, rm_scales, total;
 };
 
@@ -212,9 +212,11 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
   const bool layout_ok = striped || gemv_layout_ok(d_in, d_out, packed);
   const bool mfma = !small && x_dtype == UNIFUR_NF4_BF16 && layout_ok && rows <= 0x7fffffffu &&
                     gemm_supported((int)rows, (int)d_in, (int)d_out, x);
-  const bool skinny = !small && striped && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
-                      d_in <= 0x7fffffffu && skinny_supported((int)rows, (int)d_in, x) &&
-                      d_out / 64 <= (uint64_t)kMaxCounters;
+  // f32 activations: skinny launches of at most kSkinnyMaxRowsF32 rows each
+  const bool xf32 = x_dtype == UNIFUR_NF4_F32;
+  const uint64_t sk_rows = xf32 ? std::min<uint64_t>(rows, kSkinnyMaxRowsF32) : rows;
+  const bool skinny = !small && striped && rows <= (uint64_t)kSkinnyMaxRows && d_in <= 0x7fffffffu &&
+                      skinny_supported((int)sk_rows, (int)d_in, x, xf32) && d_out / 64 <= (uint64_t)kMaxCounters;
   if (small && striped) {
     L.path = LinearPath::kGemvStriped;
     const int n = (int)d_out;
@@ -222,8 +224,14 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
   } else if (skinny) {
     L.path = LinearPath::kSkinny;
     const int n = (int)d_out;
-    L.striped = plan_skinny((int)rows, (int)d_in, &n, 1, false);
-    L.partials = c.take(skinny_partial_floats(L.striped, (int)rows, n) * sizeof(float));
+    L.striped = plan_skinny((int)sk_rows, (int)d_in, &n, 1, false);
+    size_t part = skinny_partial_floats(L.striped, (int)sk_rows, n);
+    if (rows > sk_rows) {  // the last f32 launch's own plan
+      const int tail = (int)((rows - 1) % sk_rows + 1);
+      L.striped_tail = plan_skinny(tail, (int)d_in, &n, 1, false);
+      part = std::max(part, skinny_partial_floats(L.striped_tail, tail, n));
+    }
+    L.partials = c.take(part * sizeof(float));
   } else if (small && layout_ok && ceil_div_u64(d_out, 256) <= (uint64_t)kMaxCounters) {
     L.path = LinearPath::kGemv;
     const int n = (int)d_out;
@@ -360,13 +368,25 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     gw.lora_b = lora ? lora->b : nullptr;
     gw.lora_rank = (int)rank;
     gw.lora_scaling = lora ? lora->scaling : 0.0f;
-    if (L.path == LinearPath::kGemvStriped)
+    if (L.path == LinearPath::kGemvStriped) {
       UNIFUR_HIP(launch_gemv_striped(L.striped, x, xbf, (int)rows, (int)w->d_in, &gw, 1, false, stream));
-    else if (L.path == LinearPath::kSkinny)
-      UNIFUR_HIP(launch_skinny(L.striped, static_cast<const uint16_t*>(x), (int)rows, (int)w->d_in, &gw, 1, false,
-                               stream));
-    else
+    } else if (L.path == LinearPath::kSkinny) {
+      // bf16: one launch; f32: launches of up to kSkinnyMaxRowsF32 rows in
+      // stream order (they take turns on the partials)
+      const uint64_t step = xbf ? rows : (uint64_t)kSkinnyMaxRowsF32;
+      const size_t xe = xbf ? 2 : 4, ye = ybf ? 2 : 4;
+      for (uint64_t r0 = 0; r0 < rows; r0 += step) {
+        const int n = (int)std::min<uint64_t>(step, rows - r0);
+        GemvWeight g = gw;
+        g.y = static_cast<char*>(y) + r0 * w->d_out * ye;
+        if (xa) g.lora_xa = xa + r0 * rank;
+        const StripedPlan& p = (r0 + step >= rows && r0 > 0) ? L.striped_tail : L.striped;
+        UNIFUR_HIP(launch_skinny(p, static_cast<const char*>(x) + r0 * w->d_in * xe, !xbf, n, (int)w->d_in, &g, 1,
+                                 false, stream));
+      }
+    } else {
       UNIFUR_HIP(launch_gemv(L.gemv, x, xbf, (int)rows, (int)w->d_in, &gw, 1, stream));
+    }
     return UNIFUR_NF4_OK;
   }
   // Generic: the reference's own sequence -- dequantize the whole weight to
@@ -411,11 +431,12 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
                     gemm_supported((int)rows, (int)inter, (int)hidden, reinterpret_cast<const void*>(uintptr_t{256}));
   const int gi[2] = {(int)inter, (int)inter};
   const int hd = (int)hidden;
-  // the skinny kernel for up to 64 bf16 rows; h lives 256-byte aligned in the workspace
-  const bool skinny = !small && all_striped && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
-                      hidden <= 0x7fffffffu && inter <= 0x7fffffffu &&
-                      skinny_supported((int)rows, (int)hidden, x) &&
-                      skinny_supported((int)rows, (int)inter, reinterpret_cast<const void*>(uintptr_t{256})) &&
+  // the skinny kernel for up to 64 bf16 (32 f32) rows; h lives 256-byte
+  // aligned in the workspace
+  const bool xf32 = x_dtype == UNIFUR_NF4_F32;
+  const bool skinny = !small && all_striped && rows <= (uint64_t)kSkinnyMaxRows && hidden <= 0x7fffffffu &&
+                      inter <= 0x7fffffffu && skinny_supported((int)rows, (int)hidden, x, xf32) &&
+                      skinny_supported((int)rows, (int)inter, reinterpret_cast<const void*>(uintptr_t{256}), xf32) &&
                       std::max(inter, hidden) / 64 <= (uint64_t)kMaxCounters;
   if (skinny) {
     L.path = MlpPath::kSkinny;
@@ -429,10 +450,8 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
     L.partials0 = c.take(std::max(up_part, skinny_partial_floats(L.s_down, (int)rows, (int)hidden)) * sizeof(float));
     L.partials1 = c.take(up_part * sizeof(float));
     L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
-    if (!same_kind) {
-      L.h = c.take((size_t)rows * inter * sizeof(float));
-      L.u = c.take((size_t)rows * inter * sizeof(float));
-    }
+    if (!same_kind || xf32) L.h = c.take((size_t)rows * inter * sizeof(float));  // f32 x: the middle stays f32
+    if (!same_kind) L.u = c.take((size_t)rows * inter * sizeof(float));
   } else if (small && all_striped) {
     L.path = rows <= (uint64_t)kGemvPairMaxRows && same_kind ? MlpPath::kPairStriped : MlpPath::kStriped;
     L.s_up = plan_gemv_striped((int)rows, (int)hidden, gi, 2, L.path == MlpPath::kPairStriped);
@@ -550,24 +569,29 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       return UNIFUR_NF4_OK;
     }
     case MlpPath::kSkinny: {
-      // gate and up in one pass storing silu(g) * u as bf16 (two passes and
-      // the elementwise kernel when their scales differ in kind), then down
-      const uint16_t* xb = static_cast<const uint16_t*>(x);
+      // gate and up in one pass storing silu(g) * u -- bf16 for bf16 x, f32
+      // for f32 x -- (two passes and the elementwise kernel when their scales
+      // differ in kind), then down over that middle
+      const bool xf = !xbf;
       uint16_t* hb = at<uint16_t>(ws, L.hb);
+      void* mid = xf ? static_cast<void*>(h) : static_cast<void*>(hb);
       float* p0 = at<float>(ws, L.partials0);
       float* p1 = at<float>(ws, L.partials1);
       if (gate->scales.kind == up->scales.kind) {
-        GemvWeight gw[2] = {gemv_weight(gate, hb, true, cnt, p0), gemv_weight(up, nullptr, true, cnt, p1)};
-        UNIFUR_HIP(launch_skinny(L.s_up, xb, (int)rows, (int)hidden, gw, 2, true, stream));
+        GemvWeight gw[2] = {gemv_weight(gate, mid, !xf, cnt, p0), gemv_weight(up, nullptr, !xf, cnt, p1)};
+        UNIFUR_HIP(launch_skinny(L.s_up, x, xf, (int)rows, (int)hidden, gw, 2, true, stream));
       } else {
         float* u = at<float>(ws, L.u);
         GemvWeight gw[2] = {gemv_weight(gate, h, false, cnt, p0), gemv_weight(up, u, false, cnt, p0)};
-        UNIFUR_HIP(launch_skinny(L.s_up, xb, (int)rows, (int)hidden, &gw[0], 1, false, stream));
-        UNIFUR_HIP(launch_skinny(L.s_up, xb, (int)rows, (int)hidden, &gw[1], 1, false, stream));
-        UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
+        UNIFUR_HIP(launch_skinny(L.s_up, x, xf, (int)rows, (int)hidden, &gw[0], 1, false, stream));
+        UNIFUR_HIP(launch_skinny(L.s_up, x, xf, (int)rows, (int)hidden, &gw[1], 1, false, stream));
+        if (xf)
+          UNIFUR_HIP(launch_silu_mul(h, u, (size_t)rows * inter, h, stream));
+        else
+          UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
       }
       GemvWeight dw = gemv_weight(down, y, ybf, cnt, p0);
-      UNIFUR_HIP(launch_skinny(L.s_down, hb, (int)rows, (int)inter, &dw, 1, false, stream));
+      UNIFUR_HIP(launch_skinny(L.s_down, mid, xf, (int)rows, (int)inter, &dw, 1, false, stream));
       return UNIFUR_NF4_OK;
     }
     case MlpPath::kMfma: {
@@ -874,8 +898,8 @@ MultiLayout plan_multi(uint64_t rows, uint64_t d_in, const uint64_t* d_out, cons
   if (ok && rows <= (uint64_t)kGemvMaxRows) {
     L.fused = true;
     L.plan = plan_gemv_striped((int)rows, (int)d_in, dn, (int)n, false);
-  } else if (ok && x_dtype == UNIFUR_NF4_BF16 && rows <= (uint64_t)kSkinnyMaxRows &&
-             skinny_supported((int)rows, (int)d_in, x)) {
+  } else if (ok && rows <= (uint64_t)kSkinnyMaxRows &&
+             skinny_supported((int)rows, (int)d_in, x, x_dtype == UNIFUR_NF4_F32)) {
     L.fused = L.skinny = true;
     L.plan = plan_skinny((int)rows, (int)d_in, dn, (int)n, false);
     for (uint32_t i = 0; i < n; ++i)
@@ -916,7 +940,7 @@ int run_linear_multi(const void* x, int x_dtype, uint64_t rows, const unifur_nf4
     gw[i].bias = bias ? bias[i] : nullptr;
   }
   if (L.skinny)
-    UNIFUR_HIP(launch_skinny(L.plan, static_cast<const uint16_t*>(x), (int)rows, (int)w[0].d_in, gw, (int)n, false,
+    UNIFUR_HIP(launch_skinny(L.plan, x, x_dtype == UNIFUR_NF4_F32, (int)rows, (int)w[0].d_in, gw, (int)n, false,
                              stream));
   else
     UNIFUR_HIP(launch_gemv_striped(L.plan, x, x_dtype == UNIFUR_NF4_BF16, (int)rows, (int)w[0].d_in, gw, (int)n,
@@ -1027,8 +1051,8 @@ AttnOutLayout plan_attn_out(uint64_t rows, const unifur_nf4_decoder_layer* l, in
   if (is_striped(&l->o) && rows <= (uint64_t)kGemvMaxRows) {
     L.o_path = OutPath::kGemv;
     L.o_plan = plan_gemv_striped((int)rows, (int)ctx_dim, &hd, 1, false);
-  } else if (is_striped(&l->o) && bf && rows <= (uint64_t)kSkinnyMaxRows && ctx_dim <= 0x7fffffffu &&
-             skinny_supported((int)rows, (int)ctx_dim, ctx) && hid / 64 <= (uint64_t)kMaxCounters) {
+  } else if (is_striped(&l->o) && rows <= (uint64_t)kSkinnyMaxRows && ctx_dim <= 0x7fffffffu &&
+             skinny_supported((int)rows, (int)ctx_dim, ctx, !bf) && hid / 64 <= (uint64_t)kMaxCounters) {
     L.o_path = OutPath::kSkinny;
     L.o_plan = plan_skinny((int)rows, (int)ctx_dim, &hd, 1, false);
   } else {
@@ -1043,8 +1067,9 @@ AttnOutLayout plan_attn_out(uint64_t rows, const unifur_nf4_decoder_layer* l, in
     L.mlp = MlpStage::kMultiNorm;
     L.up_plan = plan_gemv_striped((int)rows, (int)hid, gi, 2, false);
     L.down_plan = plan_gemv_striped((int)rows, (int)inter, &hd, 1, false);
-  } else if (mlp_striped && bf && rows <= (uint64_t)kSkinnyMaxRows && skinny_supported((int)rows, (int)hid, x1_probe) &&
-             skinny_supported((int)rows, (int)inter, x1_probe) && std::max(hid, inter) / 64 <= (uint64_t)kMaxCounters) {
+  } else if (mlp_striped && rows <= (uint64_t)kSkinnyMaxRows && skinny_supported((int)rows, (int)hid, x1_probe, !bf) &&
+             skinny_supported((int)rows, (int)inter, x1_probe, !bf) &&
+             std::max(hid, inter) / 64 <= (uint64_t)kMaxCounters) {
     L.mlp = MlpStage::kSkinny;
     L.up_plan = plan_skinny((int)rows, (int)hid, gi, 2, true);
     L.down_plan = plan_skinny((int)rows, (int)inter, &hd, 1, false);
@@ -1104,8 +1129,7 @@ int run_attn_out_mlp(const void* x, const void* ctx, int dtype, uint64_t rows, c
     if (L.o_path == OutPath::kGemv)
       UNIFUR_HIP(launch_gemv_striped(L.o_plan, ctx, bf, (int)rows, (int)l->o.d_in, &ow, 1, false, stream));
     else
-      UNIFUR_HIP(launch_skinny(L.o_plan, static_cast<const uint16_t*>(ctx), (int)rows, (int)l->o.d_in, &ow, 1, false,
-                               stream));
+      UNIFUR_HIP(launch_skinny(L.o_plan, ctx, !bf, (int)rows, (int)l->o.d_in, &ow, 1, false, stream));
   }
   // y = x1 + down(silu(gate n) * up n), n = post_norm(x1)
   float* h = at<float>(ws, L.h);
@@ -1124,16 +1148,17 @@ int run_attn_out_mlp(const void* x, const void* ctx, int dtype, uint64_t rows, c
       return UNIFUR_NF4_OK;
     }
     case MlpStage::kSkinny: {
-      uint16_t* n = at<uint16_t>(ws, L.nrm);
-      uint16_t* hb = at<uint16_t>(ws, L.hb);
+      // n = post_norm(x1) and the SwiGLU middle in the stage's dtype
+      void* n = at<void>(ws, L.nrm);
+      void* mid = bf ? at<void>(ws, L.hb) : static_cast<void*>(h);
       float* p0 = at<float>(ws, L.part0);
-      UNIFUR_HIP(launch_rms_norm(x1, true, (int)rows, (int)hid, l->post_norm, l->eps, n, true, stream));
-      GemvWeight gw[2] = {gemv_weight(&l->gate, hb, true, cnt, p0),
-                          gemv_weight(&l->up, nullptr, true, cnt, at<float>(ws, L.part1))};
-      UNIFUR_HIP(launch_skinny(L.up_plan, n, (int)rows, (int)hid, gw, 2, true, stream));
-      GemvWeight dw = gemv_weight(&l->down, y, true, cnt, p0);
+      UNIFUR_HIP(launch_rms_norm(x1, bf, (int)rows, (int)hid, l->post_norm, l->eps, n, bf, stream));
+      GemvWeight gw[2] = {gemv_weight(&l->gate, mid, bf, cnt, p0),
+                          gemv_weight(&l->up, nullptr, bf, cnt, at<float>(ws, L.part1))};
+      UNIFUR_HIP(launch_skinny(L.up_plan, n, !bf, (int)rows, (int)hid, gw, 2, true, stream));
+      GemvWeight dw = gemv_weight(&l->down, y, bf, cnt, p0);
       dw.residual = x1;
-      UNIFUR_HIP(launch_skinny(L.down_plan, hb, (int)rows, (int)inter, &dw, 1, false, stream));
+      UNIFUR_HIP(launch_skinny(L.down_plan, mid, !bf, (int)rows, (int)inter, &dw, 1, false, stream));
       return UNIFUR_NF4_OK;
     }
     case MlpStage::kGeneral:

@@ -39,8 +39,18 @@ constexpr int kAStages = 3;
 constexpr int kLdsA = 0;                         // kAStages buffers
 constexpr int kBStages = 3;
 constexpr int kLdsB = kAStages * kATileBytes;    // kBStages buffers
-constexpr int kLdsLut = kLdsB + kBStages * kBTileBytes;  // byte LUT, 256 x f32x2
-constexpr int kLdsDq = kLdsLut + 256 * 8;        // DQ scale LUT, 256 x f32
+// Level lookup of the W-dequantizing waves (UNIFUR_GEMM_LUT): 0 = one byte
+// LUT (256 x {level lo, level hi}), 1 = four copies of it (lane % 4 picks
+// one, fewer bank conflicts), 2 = a 16-entry level table read per nibble
+// (64 lanes meet at most 16 addresses in 16 banks: broadcast, no conflicts).
+#ifndef UNIFUR_GEMM_LUT
+#define UNIFUR_GEMM_LUT 0
+#endif
+constexpr int kLutMode = UNIFUR_GEMM_LUT;
+static_assert(kLutMode >= 0 && kLutMode <= 2, "UNIFUR_GEMM_LUT");
+constexpr int kLutBytes = kLutMode == 1 ? 4 * 256 * 8 : kLutMode == 2 ? 16 * 4 : 256 * 8;
+constexpr int kLdsLut = kLdsB + kBStages * kBTileBytes;  // level LUT
+constexpr int kLdsDq = kLdsLut + kLutBytes;      // DQ scale LUT, 256 x f32
 constexpr size_t kGemmSmem = kLdsDq + 256 * 4;   // 147 KiB: one workgroup per CU
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -170,15 +180,31 @@ __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int
   // all 16 lookups first, so that one LDS latency covers them (a producer
   // wave has its SIMD to itself beside an MFMA wave: nothing else hides it)
   f32x2 l[2][8];
+  if constexpr (kLutMode == 2) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < 8; ++j) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const uint32_t byte = (B.code[2 * r + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
-      l[r][j] = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + byte * 8));
+      for (int r = 0; r < 2; ++r) {
+        const uint32_t w = B.code[2 * r + (j >> 2)], sh = 8 * (j & 3);
+        l[r][j].x = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+            (size_t)(kLdsLut + (((w >> sh) & 0xfu) << 2)));
+        l[r][j].y = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+            (size_t)(kLdsLut + (((w >> (sh + 4)) & 0xfu) << 2)));
+      }
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 32, 1);  // the 32 level reads
+  } else {
+    const uint32_t copy = kLutMode == 1 ? (uint32_t)(d & 3) * 2048u : 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const uint32_t byte = (B.code[2 * r + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+        l[r][j] = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + copy + byte * 8));
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // the 16 LUT reads
   }
-  __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // the 16 LUT reads
   __builtin_amdgcn_sched_group_barrier(0x002, 64, 1);  // then VALU
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -274,8 +300,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
 
   if (tid < 256) {
     float* lut = reinterpret_cast<float*>(smem + kLdsLut);
-    lut[2 * tid] = level(tid & 15);
-    lut[2 * tid + 1] = level(tid >> 4);
+    if constexpr (kLutMode == 2) {
+      if (tid < 16) lut[tid] = level(tid);
+    } else {
+#pragma unroll
+      for (int c = 0; c < (kLutMode == 1 ? 4 : 1); ++c) {
+        lut[c * 512 + 2 * tid] = level(tid & 15);
+        lut[c * 512 + 2 * tid + 1] = level(tid >> 4);
+      }
+    }
     if constexpr (DQ)
       reinterpret_cast<float*>(smem + kLdsDq)[tid] = ((float)tid / 255.0f) * (*g.scales.scale_of_scales);
   }

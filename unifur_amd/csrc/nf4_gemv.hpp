@@ -72,6 +72,7 @@ struct StripedArgs {
   // launch, x -> x * rsqrt(mean(x^2) + norm_eps) * (norm_w + 1) per row
   const float* norm_w;  // [d_in] or null
   float norm_eps;
+  int early;  // GEMV: issue the first chunk loads before the LUT build
 };
 
 StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights, bool pair);
@@ -83,24 +84,27 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
                                const GemvWeight* weights, int nweights, bool pair, hipStream_t stream,
                                const float* norm_w = nullptr, float norm_eps = 0.0f);
 
-// ---- 5..64 bf16 rows over striped weights, on MFMA ----
+// ---- 5..64 bf16 rows (5..32 f32 rows) over striped weights, on MFMA ----
 // Same decomposition (a workgroup per stripe over all of d_in, waves split
-// d_in) with the products on v_mfma_f32_16x16x32_bf16: the weight operand is
-// bf16(level * scale) (the rounding of the MFMA GEMM path), x is used as it
-// is.  Needs bf16 x with d_in % 8 == 0, 16-byte aligned, rows * d_in * 2 under
+// d_in) with the products on MFMA: for bf16 x v_mfma_f32_16x16x32_bf16 with
+// the weight operand bf16(level * scale) (the rounding of the MFMA GEMM
+// path); for f32 x v_mfma_f32_16x16x4_f32 with the weight operand the exact
+// f32 level * scale (the reference's dequantized value).  x is used as it
+// is.  Needs d_in % 8 == 0, x 16-byte aligned, rows * d_in * sizeof(x) under
 // 2^31; the SwiGLU pair mode stores silu(gate x) * (up x).  With
 // plan.splits > 1 the workgroups of a stripe group split d_in and hand their
 // partial sums over through the GemvWeight fields partials (splits * rows *
 // d_out floats per weight) and counters (one zeroed u32 per stripe group,
 // left zeroed): the last to arrive adds them in slab order.
 constexpr int kSkinnyMaxRows = 64;
+constexpr int kSkinnyMaxRowsF32 = 32;
 
-bool skinny_supported(int rows, int d_in, const void* x);
+bool skinny_supported(int rows, int d_in, const void* x, bool x_f32 = false);
 
 StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool pair);
 
-hipError_t launch_skinny(const StripedPlan& p, const uint16_t* x, int rows, int d_in, const GemvWeight* weights,
-                         int nweights, bool pair, hipStream_t stream);
+hipError_t launch_skinny(const StripedPlan& p, const void* x, bool x_f32, int rows, int d_in,
+                         const GemvWeight* weights, int nweights, bool pair, hipStream_t stream);
 
 // floats of GemvWeight::partials one weight of a skinny launch needs (0 without splits)
 size_t skinny_partial_floats(const StripedPlan& p, int rows, int d_out);

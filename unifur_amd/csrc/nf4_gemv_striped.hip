@@ -50,6 +50,10 @@ static_assert(kLutCopies == 8 || kLutCopies == 16 || kLutCopies == 32, "LUT copi
 constexpr int kLutBytes = 256 * kLutCopies * 8;  // at LDS address 0
 constexpr int kDqLutOffset = kLutBytes;          // one 256-entry DQ scale table per weight
 constexpr int kStripedSmem = kDqLutOffset + 2 * 256 * 4;
+// the GEMV's reduction space after the LUTs: (NW * T * W * 16 + T * W)
+// floats, at most 2 * 2 * 8 * 16 + 64 (pair), 4 * 8 * 16 + 32, 2 * 16 * 16 + 32
+constexpr int kGemvRedOffset = kStripedSmem;
+constexpr int kGemvSmem = kGemvRedOffset + (512 + 64) * 4;
 
 typedef const __attribute__((address_space(4))) float const_f32;
 typedef __attribute__((address_space(3))) const f32x2 lds_f32x2;
@@ -125,14 +129,16 @@ struct Looked {
 
 template <int T, int NW, bool XBF16, bool DQ>
 __device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW, XBF16, DQ>& c, const float* dq_lut,
-                                       uint32_t lane_off) {
+                                       const float (&sos)[NW], uint32_t lane_off) {
   // lane_off is (copy * 8) << (8 - log2(kLutCopies * 8 / 32)): the v_perm
   // puts the code byte in bits 8-15, and a shift brings the entry stride down
   // to kLutCopies * 8 bytes when that is under 256.
   constexpr int kShift = kLutCopies == 32 ? 0 : (kLutCopies == 16 ? 1 : 2);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    o.scale[w] = DQ ? dq_lut[w * 256 + (uint32_t)c.w[w].scale] : as_f((uint32_t)c.w[w].scale);
+    // DQ: ((float)q / 255.0f) * scale_of_scales (src/quantize.rs:349), the
+    // quotient from the table and the product here (the same two roundings)
+    o.scale[w] = DQ ? dq_lut[(uint32_t)c.w[w].scale] * sos[w] : as_f((uint32_t)c.w[w].scale);
 #pragma unroll
     for (int d = 0; d < 2; ++d)
 #pragma unroll
@@ -266,38 +272,40 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   const bool norm = a.norm_w != nullptr;
   const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : a.norm_w, norm ? (uint32_t)nrows * 4u : 0u);
 
-  // LUTs first: their barrier must not wait for the issue of the chunk
+  // The prologue issues the first D chunks in chunk order like the steady
+  // state (a load of chunk 0 issued last would make every pass through the
+  // loop head wait for the newest loads).  Launches that fill the GPU build
+  // the LUTs first: their barrier must not wait for the issue of the chunk
   // loads, which the memory system back-pressures when every workgroup
-  // starts at once.  The scale of scales is read through the scalar cache.
+  // starts at once.  Smaller launches (a.early) issue the chunks first, so
+  // that their memory latency overlaps the LUT build and its barrier.  The
+  // DQ table holds q / 255 and the scale of scales (read through the scalar
+  // cache) is applied per row, so the table does not wait for that load.
+  Chunk<T, NW, XBF16, DQ> ring[D];
+  auto prologue = [&]() {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, norm, j, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const bool early = a.early != 0;
+  if (early) prologue();
+  float sos[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) sos[w] = DQ ? *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
   if (tid < 256) {
     const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
     const f32x4 v = {lo, hi, lo, hi};
     f32x4* dst = reinterpret_cast<f32x4*>(smem + tid * (kLutCopies * 8));
 #pragma unroll
     for (int j = 0; j < kLutCopies / 2; ++j) dst[(j + tid) & (kLutCopies / 2 - 1)] = v;
-    if constexpr (DQ) {
-      float* dq_lut = reinterpret_cast<float*>(smem + kDqLutOffset);
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        // ((float)q / 255.0f) * scale_of_scales (src/quantize.rs:349)
-        const float sos = *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales);
-        dq_lut[w * 256 + tid] = ((float)tid / 255.0f) * sos;
-      }
-    }
+    if constexpr (DQ) reinterpret_cast<float*>(smem + kDqLutOffset)[tid] = (float)tid / 255.0f;
   }
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
-
-  // prologue: the first D chunks, issued in chunk order like the steady
-  // state (a load of chunk 0 issued last would make every pass through the
-  // loop head wait for the newest loads)
-  Chunk<T, NW, XBF16, DQ> ring[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j) {
-    issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, norm, j, lane);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  if (!early) prologue();
 
   const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
   const uint32_t lane_off = ((uint32_t)(lane & (kLutCopies - 1)) * 8u) << (kLutCopies == 32 ? 0 : kLutCopies == 16 ? 1 : 2);
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   for (int t = 0; t < T; ++t) xsq[t] = 0.0f;
 
   Looked<NW> lk[2];
-  lookup<T, NW, XBF16, DQ>(lk[0], ring[0], dq_lut, lane_off);
+  lookup<T, NW, XBF16, DQ>(lk[0], ring[0], dq_lut, sos, lane_off);
   for (int c0 = 0; c0 < nchunks; c0 += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
@@ -321,7 +329,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
       // chunk c0 + j + 1 is in ring[(j + 1) % D] (refilled at step 0 when
       // j + 1 == D).  Chunks past this wave's rows read as zero: x = 0.
       __builtin_amdgcn_sched_barrier(0);
-      lookup<T, NW, XBF16, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, lane_off);
+      lookup<T, NW, XBF16, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, sos, lane_off);
       float xs[NW][T];
 #pragma unroll
       for (int t = 0; t < T; ++t) {
@@ -354,8 +362,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   for (int w = 0; w < NW; ++w)
 #pragma unroll
     for (int t = 0; t < T; ++t) col[w][t] = wave_column_sum(acc[w][t], lane);
-  __syncthreads();  // every wave is done with the LUT
-  float* red = reinterpret_cast<float*>(smem);
+  float* red = reinterpret_cast<float*>(smem + kGemvRedOffset);  // past the LUTs: no barrier before writing it
   if ((lane & 3) == 0) {
     const int ci = wave_column_index(lane);
 #pragma unroll
@@ -405,6 +412,9 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #endif
 constexpr int kDepth = UNIFUR_GEMV_DEPTH;
 
+template <bool PAIR>
+constexpr int NWof() { return PAIR ? 2 : 1; }
+
 template <int T, int W, bool XBF16, bool DQ, bool PAIR>
 hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
   auto* fn = &gemv_striped_kernel<T, W, kDepth, XBF16, DQ, PAIR>;
@@ -415,11 +425,12 @@ hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
   const uint64_t bit = 1ull << (dev & 63);
   if (!(done.load(std::memory_order_acquire) & bit)) {
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kStripedSmem);
+                            kGemvSmem);
     if (e != hipSuccess) return e;
     done.fetch_or(bit, std::memory_order_acq_rel);
   }
-  fn<<<grid, W * 64, kStripedSmem, stream>>>(a);
+  static_assert(NWof<PAIR>() * T * W * 16 + T * W <= 512 + 64, "GEMV reduction space");
+  fn<<<grid, W * 64, kGemvSmem, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -485,11 +496,11 @@ __device__ __forceinline__ void row_bcast_all(float v, float (&o)[16]) {
   if constexpr (J + 1 < 16) row_bcast_all<J + 1>(v, o);
 }
 
-template <int NT, int NW, int S, bool DQ>
+template <int NT, int NW, int S, bool DQ, bool XF32>
 struct SkChunk {
   u32x2 code[NW][S];
   std::conditional_t<DQ, uint8_t, uint32_t> scale[NW];  // narrow, as in the GEMV ring
-  u32x4 x[NT][2];
+  u32x4 x[NT][XF32 ? 4 : 2];  // 16 activations of one token: bf16, or f32
 };
 
 // Loads of chunk `chunk` of this wave: codes of row 64 chunk + lane of each
@@ -499,9 +510,9 @@ struct SkChunk {
 // next rows of their stripe, which meet zero scales and zero activations);
 // activation offsets past the wave's rows are sent out of the buffer (zero),
 // tokens past `rows` fall out of it by themselves.
-template <int NT, int NW, int S, bool DQ>
-__device__ __forceinline__ void sk_issue(SkChunk<NT, NW, S, DQ>& c, const WaveW (&ww)[NW], __amdgpu_buffer_rsrc_t xr,
-                                         int K, int kw, int kend, int chunk, int lane) {
+template <int NT, int NW, int S, bool DQ, bool XF32>
+__device__ __forceinline__ void sk_issue(SkChunk<NT, NW, S, DQ, XF32>& c, const WaveW (&ww)[NW],
+                                         __amdgpu_buffer_rsrc_t xr, int K, int kw, int kend, int chunk, int lane) {
   const uint32_t row = (uint32_t)(chunk * 64 + lane);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
@@ -515,14 +526,17 @@ __device__ __forceinline__ void sk_issue(SkChunk<NT, NW, S, DQ>& c, const WaveW 
       c.scale[w] = __builtin_amdgcn_raw_buffer_load_b32(ww[w].scales, row * 4u, 0, 0);
   }
   const int k0 = kw + chunk * 64 + 16 * (lane >> 4);
-  const uint32_t off = (uint32_t)((lane & 15) * K + k0) * 2u;
+  constexpr uint32_t kEl = XF32 ? 4u : 2u;  // bytes per activation
+  constexpr int kPer = XF32 ? 4 : 8;        // activations per 16-byte load
+  const uint32_t off = (uint32_t)((lane & 15) * K + k0) * kEl;
   const uint32_t out = 0x80000000u;  // beyond num_records: reads zero
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
-    const uint32_t o = off + (uint32_t)(16 * tt * K) * 2u;
-    c.x[tt][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, k0 + 8 <= kend ? o : out, 0, 0));
-    c.x[tt][1] =
-        __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, k0 + 16 <= kend ? o + 16u : out, 0, 0));
+    const uint32_t o = off + (uint32_t)(16 * tt * K) * kEl;
+#pragma unroll
+    for (int q = 0; q < (XF32 ? 4 : 2); ++q)
+      c.x[tt][q] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, k0 + kPer * (q + 1) <= kend ? o + 16u * q : out, 0, 0));
   }
 }
 
@@ -541,7 +555,7 @@ __device__ __forceinline__ void sk_lookup(f32x2 (&lv)[8], u32x2 code, uint32_t s
     }
 }
 
-template <int NT, int W, int D, int S, bool DQ, bool PAIR>
+template <int NT, int W, int D, int S, bool DQ, bool PAIR, bool XF32>
 __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   constexpr int NW = PAIR ? 2 : 1;
   constexpr int U = NW * S;  // units per chunk
@@ -577,7 +591,7 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
     ww[w].scales = DQ ? make_rsrc(G.scales.dq_codes + srow, (uint32_t)nrows)
                       : make_rsrc(G.scales.absmax + srow, (uint32_t)nrows * 4u);
   }
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.rows * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.rows * (uint32_t)K * (XF32 ? 4u : 2u));
 
   if (tid < 256) {  // level-pair LUT and DQ scale table, as in the GEMV
     const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
@@ -598,10 +612,10 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
 
-  SkChunk<NT, NW, S, DQ> ring[D];
+  SkChunk<NT, NW, S, DQ, XF32> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {  // in chunk order, as in the GEMV
-    sk_issue<NT, NW, S, DQ>(ring[j], ww, xr, K, kw, kw + nrows, j, lane);
+    sk_issue<NT, NW, S, DQ, XF32>(ring[j], ww, xr, K, kw, kw + nrows, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -617,7 +631,7 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) acc[w][i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto decode_scale = [&](const SkChunk<NT, NW, S, DQ>& c, int w) {
+  auto decode_scale = [&](const SkChunk<NT, NW, S, DQ, XF32>& c, int w) {
     return DQ ? dq_lut[w * 256 + (uint32_t)c.scale[w]] : as_f((uint32_t)c.scale[w]);
   };
   float sdec[2][NW];  // this lane's row scale, per chunk parity
@@ -644,22 +658,36 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
           sk_lookup(lk[(q + 1) & 1], ring[(j + 1) % D].code[0][0], stage, lane_off);
         }
         const f32x2(&L)[8] = lk[q & 1];
-        u32x4 b0, b1;
+        if constexpr (XF32) {
+          // f32 operands: B = level * scale exactly as the reference's
+          // dequantized f32 value (src/quantize.rs:362), 16 MFMAs of 4 k
+          // (lane group G supplies k = 16 G + m of MFMA m, for both operands)
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          b0[m] = pack_bf16x2(L[m].x * sc[w][2 * m], L[m].y * sc[w][2 * m + 1]);
-          b1[m] = pack_bf16x2(L[4 + m].x * sc[w][8 + 2 * m], L[4 + m].y * sc[w][9 + 2 * m]);
-        }
-        const bf16x8_t B0 = __builtin_bit_cast(bf16x8_t, b0), B1 = __builtin_bit_cast(bf16x8_t, b1);
+          for (int m = 0; m < 16; ++m) {
+            const float bm = ((m & 1) ? L[m >> 1].y : L[m >> 1].x) * sc[w][m];
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-          acc[w][i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][0]), B0,
-                                                                  acc[w][i][tt], 0, 0, 0);
-          acc[w][i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][1]), B1,
-                                                                  acc[w][i][tt], 0, 0, 0);
+            for (int tt = 0; tt < NT; ++tt)
+              acc[w][i][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f(ring[j].x[tt][m >> 2][m & 3]), bm,
+                                                                   acc[w][i][tt], 0, 0, 0);
+          }
+        } else {
+          u32x4 b0, b1;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            b0[m] = pack_bf16x2(L[m].x * sc[w][2 * m], L[m].y * sc[w][2 * m + 1]);
+            b1[m] = pack_bf16x2(L[4 + m].x * sc[w][8 + 2 * m], L[4 + m].y * sc[w][9 + 2 * m]);
+          }
+          const bf16x8_t B0 = __builtin_bit_cast(bf16x8_t, b0), B1 = __builtin_bit_cast(bf16x8_t, b1);
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt) {
+            acc[w][i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][0]),
+                                                                    B0, acc[w][i][tt], 0, 0, 0);
+            acc[w][i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ring[j].x[tt][1]),
+                                                                    B1, acc[w][i][tt], 0, 0, 0);
+          }
         }
       }
-      sk_issue<NT, NW, S, DQ>(ring[j], ww, xr, K, kw, kw + nrows, c0 + j + D, lane);
+      sk_issue<NT, NW, S, DQ, XF32>(ring[j], ww, xr, K, kw, kw + nrows, c0 + j + D, lane);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -775,35 +803,35 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   }
 }
 
-template <int NT, int W, int S, bool DQ, bool PAIR>
+template <int NT, int W, int S, bool DQ, bool PAIR, bool XF32>
 hipError_t sk_launch_t(const StripedArgs& a, int grid, int splits, hipStream_t stream) {
   constexpr int NW = PAIR ? 2 : 1;
   constexpr int D = (NT == 1 && S == 1) ? 4 : 2;
   constexpr int smem = kSkStageOffset + W * 512;
   static_assert(smem <= 65536, "skinny LDS");
   static_assert(W * NW * 1024 <= kLutBytes, "the reduction reuses the LUT space");
-  skinny_kernel<NT, W, D, S, DQ, PAIR><<<dim3(grid, splits), W * 64, smem, stream>>>(a);
+  skinny_kernel<NT, W, D, S, DQ, PAIR, XF32><<<dim3(grid, splits), W * 64, smem, stream>>>(a);
   return hipGetLastError();
 }
 
-template <int NT, int S, bool PAIR>
+template <int NT, int S, bool PAIR, bool XF32>
 hipError_t sk_dispatch_w(const StripedArgs& a, int grid, int splits, int waves, bool dq, hipStream_t stream) {
   if (waves == 4)
-    return dq ? sk_launch_t<NT, 4, S, true, PAIR>(a, grid, splits, stream)
-              : sk_launch_t<NT, 4, S, false, PAIR>(a, grid, splits, stream);
+    return dq ? sk_launch_t<NT, 4, S, true, PAIR, XF32>(a, grid, splits, stream)
+              : sk_launch_t<NT, 4, S, false, PAIR, XF32>(a, grid, splits, stream);
   if (waves == 8)
-    return dq ? sk_launch_t<NT, 8, S, true, PAIR>(a, grid, splits, stream)
-              : sk_launch_t<NT, 8, S, false, PAIR>(a, grid, splits, stream);
+    return dq ? sk_launch_t<NT, 8, S, true, PAIR, XF32>(a, grid, splits, stream)
+              : sk_launch_t<NT, 8, S, false, PAIR, XF32>(a, grid, splits, stream);
   return hipErrorInvalidValue;
 }
 
-template <int NT, bool PAIR>
+template <int NT, bool PAIR, bool XF32>
 hipError_t sk_dispatch_s(const StripedArgs& a, int grid, int splits, int waves, int group, bool dq,
                          hipStream_t stream) {
-  if (group == 1) return sk_dispatch_w<NT, 1, PAIR>(a, grid, splits, waves, dq, stream);
-  if (group == 2) return sk_dispatch_w<NT, 2, PAIR>(a, grid, splits, waves, dq, stream);
+  if (group == 1) return sk_dispatch_w<NT, 1, PAIR, XF32>(a, grid, splits, waves, dq, stream);
+  if (group == 2) return sk_dispatch_w<NT, 2, PAIR, XF32>(a, grid, splits, waves, dq, stream);
   if constexpr (!PAIR || NT == 1) {
-    if (group == 4) return sk_dispatch_w<NT, 4, PAIR>(a, grid, splits, waves, dq, stream);
+    if (group == 4) return sk_dispatch_w<NT, 4, PAIR, XF32>(a, grid, splits, waves, dq, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -811,13 +839,17 @@ hipError_t sk_dispatch_s(const StripedArgs& a, int grid, int splits, int waves, 
 // token tiles of 16: 1, 2 or 4 (33..48 tokens run as four tiles)
 int skinny_tiles(int rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : 4; }
 
-template <bool PAIR>
+// f32 activations take at most two token tiles (their 16 values per lane and
+// tile fill the registers four tiles of bf16 take)
+template <bool PAIR, bool XF32>
 hipError_t sk_dispatch_rows(const StripedArgs& a, int grid, int splits, int waves, int group, bool dq,
                             hipStream_t stream) {
   switch (skinny_tiles(a.rows)) {
-    case 1: return sk_dispatch_s<1, PAIR>(a, grid, splits, waves, group, dq, stream);
-    case 2: return sk_dispatch_s<2, PAIR>(a, grid, splits, waves, group, dq, stream);
-    case 4: return sk_dispatch_s<4, PAIR>(a, grid, splits, waves, group, dq, stream);
+    case 1: return sk_dispatch_s<1, PAIR, XF32>(a, grid, splits, waves, group, dq, stream);
+    case 2: return sk_dispatch_s<2, PAIR, XF32>(a, grid, splits, waves, group, dq, stream);
+    case 4:
+      if constexpr (!XF32) return sk_dispatch_s<4, PAIR, XF32>(a, grid, splits, waves, group, dq, stream);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -832,7 +864,10 @@ StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights
   // About 4096 waves over the GPU (16 per CU): waves per workgroup = the
   // power of two at most 4096 / stripes, within [4, 16] (8 for the pair or
   // more than two rows, for registers) and no more than the 64-row chunks.
-  const int max_waves = (pair || rows > 2) ? 8 : 16;
+  // The pair's kernel takes ~240 VGPRs (two waves per SIMD): one 8-wave
+  // workgroup per CU, so it keeps 4 waves (two workgroups per CU) once its
+  // stripes pass 256, where 8 would run the grid in two rounds.
+  const int max_waves = pair ? (stripes > 256 ? 4 : 8) : rows > 2 ? 8 : 16;
   int waves = 4;
   while (waves < max_waves && (long)stripes * waves * 2 <= 4096 && waves * 2 <= chunks) waves *= 2;
   p.waves = waves;
@@ -848,6 +883,10 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
   a.x = x;
   a.norm_w = norm_w;
   a.norm_eps = norm_eps;
+  // chunk loads ahead of the LUT build when the grid leaves the GPU room
+  // (two workgroups per CU or fewer), where latency rather than the memory
+  // system's back-pressure bounds the launch
+  a.early = p.stripes <= 512;
   a.rows = rows;
   a.d_in = d_in;
   a.rows_per_wave = p.rows_per_wave;
@@ -874,9 +913,10 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
   }
 }
 
-bool skinny_supported(int rows, int d_in, const void* x) {
-  return rows >= 1 && rows <= kSkinnyMaxRows && d_in > 0 && d_in % 8 == 0 &&
-         (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (uint64_t)rows * (uint64_t)d_in * 2u < (1ull << 31);
+bool skinny_supported(int rows, int d_in, const void* x, bool x_f32) {
+  return rows >= 1 && rows <= (x_f32 ? kSkinnyMaxRowsF32 : kSkinnyMaxRows) && d_in > 0 && d_in % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+         (uint64_t)rows * (uint64_t)d_in * (x_f32 ? 4u : 2u) < (1ull << 31);
 }
 
 StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool pair) {
@@ -912,8 +952,11 @@ StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool
   if (stripes / g >= 160) {
     group = g;
   } else if (chunks >= 64) {
-    group = g;
-    while ((stripes / group) * splits < 256 && chunks / (splits * 2) >= 32) splits *= 2;
+    // few stripes over a long d_in (the down projection of a decode batch):
+    // fewer stripes per wave and slabs of >= 16 chunks, up to ~256
+    // workgroups (Qwen2-0.5B down at 32 tokens: 28 -> 224 workgroups)
+    group = stripes / g >= 64 ? g : stripes / 2 >= 64 ? 2 : 1;
+    while ((stripes / group) * splits < 256 && chunks / (splits * 2) >= 16) splits *= 2;
   } else if (stripes / 2 >= 160) {
     group = 2;
   }
@@ -928,9 +971,9 @@ StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool
   return p;
 }
 
-hipError_t launch_skinny(const StripedPlan& p, const uint16_t* x, int rows, int d_in, const GemvWeight* weights,
-                         int nweights, bool pair, hipStream_t stream) {
-  if (!skinny_supported(rows, d_in, x) || nweights < 1 || nweights > kMaxGemvWeights || (pair && nweights != 2))
+hipError_t launch_skinny(const StripedPlan& p, const void* x, bool x_f32, int rows, int d_in,
+                         const GemvWeight* weights, int nweights, bool pair, hipStream_t stream) {
+  if (!skinny_supported(rows, d_in, x, x_f32) || nweights < 1 || nweights > kMaxGemvWeights || (pair && nweights != 2))
     return hipErrorInvalidValue;
   if ((p.group != 1 && p.group != 2 && p.group != 4) || p.splits < 1 || p.splits > 65535 ||
       (long)p.rows_per_split * p.splits < d_in || p.rows_per_split != p.rows_per_wave * p.waves)
@@ -952,8 +995,11 @@ hipError_t launch_skinny(const StripedPlan& p, const uint16_t* x, int rows, int 
   for (int i = nweights; i <= kMaxGemvWeights; ++i) a.stripe_begin[i] = s;
   const bool dq = weights[0].scales.kind == kScalesDQ;
   const int grid = s / p.group;
-  return pair ? sk_dispatch_rows<true>(a, grid, p.splits, p.waves, p.group, dq, stream)
-              : sk_dispatch_rows<false>(a, grid, p.splits, p.waves, p.group, dq, stream);
+  if (x_f32)
+    return pair ? sk_dispatch_rows<true, true>(a, grid, p.splits, p.waves, p.group, dq, stream)
+                : sk_dispatch_rows<false, true>(a, grid, p.splits, p.waves, p.group, dq, stream);
+  return pair ? sk_dispatch_rows<true, false>(a, grid, p.splits, p.waves, p.group, dq, stream)
+              : sk_dispatch_rows<false, false>(a, grid, p.splits, p.waves, p.group, dq, stream);
 }
 
 size_t skinny_partial_floats(const StripedPlan& p, int rows, int d_out) {
