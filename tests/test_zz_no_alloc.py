@@ -90,16 +90,26 @@ def test_noalloc_matches_linear_forward_twice(device, oracle, case):
 
 
 def test_noalloc_refuses_what_does_not_fit(device, oracle):
-    # f32 activations over 4 rows take the generic path: the whole weight
+    # f32 activations over 64 rows take the generic path: the whole weight
     # dequantized to f32 (4096 * 11008 * 4 bytes) does not fit the scratch
     lin, _ = make_linear(oracle, 4096, 11008, 5100, device)
-    _, x = acts(oracle, 8, 4096, 5101, torch.float32, device)
+    _, x = acts(oracle, 100, 4096, 5101, torch.float32, device)
     w = lin.weight_struct()
-    y = torch.empty(8, 11008, device=device)
+    y = torch.empty(100, 11008, device=device)
     lib = L.lib()
-    st = lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), L.F32, 8, ctypes.byref(w), None, None, y.data_ptr(),
-                                               L.F32, torch.cuda.current_stream().cuda_stream)
+    stream = torch.cuda.current_stream().cuda_stream
+    st = lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), L.F32, 100, ctypes.byref(w), None, None, y.data_ptr(),
+                                               L.F32, stream)
     assert st == L.ERR_WORKSPACE and b"16777216" in lib.unifur_nf4_last_error()
+    # 5..64 f32 rows run on MFMA over the striped weight and fit: the same
+    # result as the entry point with a workspace
+    y8 = torch.empty(8, 11008, device=device)
+    L.check(lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), L.F32, 8, ctypes.byref(w), None, None, y8.data_ptr(),
+                                                  L.F32, stream))
+    ref8 = torch.empty_like(y8)
+    L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), L.F32, 8, ctypes.byref(w), None, None, ref8.data_ptr(), L.F32,
+                                          None, 0, stream))
+    assert torch.equal(y8, ref8)
     # and bad arguments are refused like the existing entry point's
     assert lib.unifur_nf4_linear_forward_noalloc(None, L.F32, 1, ctypes.byref(w), None, None, y.data_ptr(), L.F32,
                                                  None) == L.ERR_INVALID

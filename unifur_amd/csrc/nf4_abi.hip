@@ -472,10 +472,11 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
                2 * inter <= 0x7fffffffu;
     if (L.expand) {
       // gate and up expanded side by side ([2 inter][hidden]: one GEMM with
-      // bf16 outputs [rows][2 inter]), then down into the same buffer
+      // f32 outputs [rows][2 inter], so silu(g) * u is rounded to bf16 once,
+      // as on the fused path), then down into the same buffer
       L.wt = c.take(2 * hidden * inter * sizeof(uint16_t));
       L.blas = c.take(kBlasWorkspace);
-      L.h = c.take((size_t)rows * 2 * inter * sizeof(uint16_t));
+      L.h = c.take((size_t)rows * 2 * inter * sizeof(float));
       L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
     } else {
       L.h = c.take((size_t)rows * inter * sizeof(float));
@@ -595,22 +596,23 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       return UNIFUR_NF4_OK;
     }
     case MlpPath::kMfma: {
-      // gate and up (f32 out), silu(g) * u rounded to bf16, then down: each
-      // weight expanded to bf16 in turn and a BLAS GEMM, or the fused kernel.
+      // gate and up (f32 out), silu(g) * u rounded to bf16 once, then down:
+      // each weight expanded to bf16 in turn and a BLAS GEMM, or the fused
+      // kernel -- both paths round the same intermediates.
       const uint16_t* xb = static_cast<const uint16_t*>(x);
       float* u = at<float>(ws, L.u);
       uint16_t* hb = at<uint16_t>(ws, L.hb);
       if (L.expand) {
         uint16_t* wt = at<uint16_t>(ws, L.wt);
-        uint16_t* gu = at<uint16_t>(ws, L.h);
+        float* gu = at<float>(ws, L.h);
         void* bw = at<void>(ws, L.blas);
         const int hd = (int)hidden, in = (int)inter, m = (int)rows;
         UNIFUR_HIP(launch_expand_bf16(gate->packed, to_scales(gate->scales), hd, in, is_striped(gate), nullptr,
                                       nullptr, 0, 0.0f, wt, stream));
         UNIFUR_HIP(launch_expand_bf16(up->packed, to_scales(up->scales), hd, in, is_striped(up), nullptr, nullptr, 0,
                                       0.0f, wt + (size_t)in * hd, stream));
-        UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, 2 * in, hd, gu, true, bw, kBlasWorkspace, stream));
-        UNIFUR_HIP(launch_silu_mul_rows_bf16(gu, (size_t)rows, (size_t)inter, hb, stream));
+        UNIFUR_HIP(blas_gemm_xwt(xb, wt, nullptr, m, 2 * in, hd, gu, false, bw, kBlasWorkspace, stream));
+        UNIFUR_HIP(launch_silu_mul_rows_bf16(gu, true, (size_t)rows, (size_t)inter, hb, stream));
         UNIFUR_HIP(launch_expand_bf16(down->packed, to_scales(down->scales), in, hd, is_striped(down), nullptr,
                                       nullptr, 0, 0.0f, wt, stream));
         UNIFUR_HIP(blas_gemm_xwt(hb, wt, nullptr, m, hd, in, y, ybf, bw, kBlasWorkspace, stream));
@@ -822,7 +824,10 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       hipError_t e = launch_expand_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w),
                                         lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
                                         lora ? lora->scaling : 0.0f, wt, stream);
-      if (e == hipSuccess && br.side) e = fork();  // the gradients beside the GEMM, not the memory-bound expand
+      // the gradients beside the GEMM, not the memory-bound expand; on a
+      // shape's first call the GEMM's kernel is chosen by timing candidates,
+      // so the gradients wait and run after it instead of contending
+      if (e == hipSuccess && br.side && blas_gemm_dyw_tuned(m, n, k, dx_dtype == UNIFUR_NF4_BF16)) e = fork();
       if (e == hipSuccess)
         e = blas_gemm_dyw(static_cast<const uint16_t*>(dy), wt, m, n, k, dx, dx_dtype == UNIFUR_NF4_BF16,
                           at<void>(ws, L.blas_ws), kBlasWorkspace, stream);

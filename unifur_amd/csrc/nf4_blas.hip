@@ -222,6 +222,15 @@ hipError_t blas_gemm_xwt_ld(const uint16_t* x, const uint16_t* wt, const float* 
   return gemm_cm(sh, wt, x, bias, y, y_bf16, ws, ws_bytes, stream);
 }
 
+bool blas_gemm_dyw_tuned(int M, int N, int K, bool dx_bf16) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  const Shape sh{false, false, K, M, N, K, N, K};
+  State& st = state();
+  std::lock_guard<std::mutex> lock(st.mu);
+  return st.tuned.count(Key{dev, sh, dx_bf16, false}) != 0;
+}
+
 hipError_t blas_gemm_dyw(const uint16_t* dy, const uint16_t* wt, int M, int N, int K, void* dx, bool dx_bf16,
                          void* ws, size_t ws_bytes, hipStream_t stream) {
   const Shape sh{false, false, K, M, N, K, N, K};

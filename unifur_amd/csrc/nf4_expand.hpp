@@ -38,5 +38,8 @@ hipError_t blas_gemm_xwt_ld(const uint16_t* x, const uint16_t* wt, const float* 
 // respect to X), bf16 operands, dX f32 or bf16; same kernel choice rule.
 hipError_t blas_gemm_dyw(const uint16_t* dy, const uint16_t* wt, int M, int N, int K, void* dx, bool dx_bf16,
                          void* ws, size_t ws_bytes, hipStream_t stream);
+// Whether this device has chosen its blas_gemm_dyw kernel for the shape (a
+// call before that times the candidates, which wants the GPU to itself).
+bool blas_gemm_dyw_tuned(int M, int N, int K, bool dx_bf16);
 
 }  // namespace unifur

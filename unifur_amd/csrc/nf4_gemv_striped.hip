@@ -100,9 +100,9 @@ struct WaveW {
 template <int T, int NW, bool XBF16, bool DQ>
 __device__ __forceinline__ void issue_chunk(Chunk<T, NW, XBF16, DQ>& c, const WaveW (&ww)[NW],
                                             const __amdgpu_buffer_rsrc_t (&xr)[T], __amdgpu_buffer_rsrc_t gr,
-                                            bool norm, int chunk, int lane) {
+                                            int chunk, int lane) {
   const uint32_t row = (uint32_t)(chunk * 64 + lane);
-  if (norm) c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);
+  c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);  // 0 without a norm
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     c.w[w].code = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
@@ -268,9 +268,12 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   }
   // folded QwenRmsNorm (src/qwennet.rs:104-109): the products take
   // x * (w + 1), each lane sums x^2 over its rows, and the column sums are
-  // scaled by the row's 1 / sqrt(mean(x^2) + eps) at the end
+  // scaled by the row's 1 / sqrt(mean(x^2) + eps) at the end.  Without a norm
+  // the weight buffer has no records: its loads read 0, so x is multiplied
+  // by exactly 1 -- the loop has no branch on the norm (a branch there made
+  // the compiler keep two versions of the loop and double the registers).
   const bool norm = a.norm_w != nullptr;
-  const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : a.norm_w, norm ? (uint32_t)nrows * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : a.x, norm ? (uint32_t)nrows * 4u : 0u);
 
   // The prologue issues the first D chunks in chunk order like the steady
   // state (a load of chunk 0 issued last would make every pass through the
@@ -285,7 +288,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   auto prologue = [&]() {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, norm, j, lane);
+      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, j, lane);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -334,14 +337,12 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         float xv = XBF16 ? bf16_bits_to_f32((uint32_t)ring[j].x[t]) : as_f((uint32_t)ring[j].x[t]);
-        if (norm) {
-          xsq[t] = __builtin_fmaf(xv, xv, xsq[t]);
-          xv = xv * (as_f(ring[j].g) + 1.0f);
-        }
+        xsq[t] = __builtin_fmaf(xv, xv, xsq[t]);
+        xv = xv * (as_f(ring[j].g) + 1.0f);
 #pragma unroll
         for (int w = 0; w < NW; ++w) xs[w][t] = xv * lk[j & 1].scale[w];  // x * block scale, once per row
       }
-      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, norm, c0 + j + D, lane);
+      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, c0 + j + D, lane);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
@@ -864,9 +865,10 @@ StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights
   // About 4096 waves over the GPU (16 per CU): waves per workgroup = the
   // power of two at most 4096 / stripes, within [4, 16] (8 for the pair or
   // more than two rows, for registers) and no more than the 64-row chunks.
-  // The pair's kernel takes ~240 VGPRs (two waves per SIMD): one 8-wave
-  // workgroup per CU, so it keeps 4 waves (two workgroups per CU) once its
-  // stripes pass 256, where 8 would run the grid in two rounds.
+  // The pair's kernel takes ~140 VGPRs (three waves per SIMD): one 8-wave
+  // workgroup per CU, so it keeps 4 waves (three workgroups per CU) once its
+  // stripes pass 256, where 8 would run the grid in two rounds (Qwen2-0.5B
+  // gate/up at one token: 9.9 -> 6.8 us).
   const int max_waves = pair ? (stripes > 256 ? 4 : 8) : rows > 2 ? 8 : 16;
   int waves = 4;
   while (waves < max_waves && (long)stripes * waves * 2 <= 4096 && waves * 2 <= chunks) waves *= 2;
@@ -883,10 +885,12 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
   a.x = x;
   a.norm_w = norm_w;
   a.norm_eps = norm_eps;
-  // chunk loads ahead of the LUT build when the grid leaves the GPU room
-  // (two workgroups per CU or fewer), where latency rather than the memory
-  // system's back-pressure bounds the launch
-  a.early = p.stripes <= 512;
+  // chunk loads ahead of the LUT build when every chunk of a wave fits the
+  // prologue (the small decode weights), where one memory latency rather
+  // than the memory system's back-pressure bounds the launch; longer d_in
+  // build the LUTs first (7B-shaped down projection at one token: 30 us
+  // with the loads first against 23.5 us)
+  a.early = p.rows_per_wave <= kDepth * 64;
   a.rows = rows;
   a.d_in = d_in;
   a.rows_per_wave = p.rows_per_wave;

@@ -129,22 +129,26 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
   }
 }
 
-// h[m][i] = bf16(silu(g) * u) with g = gu[m][i] and u = gu[m][inter + i],
-// both bf16 (the gate and up halves of one GEMM's output row).
-__global__ void silu_mul_rows_bf16_kernel(const uint16_t* __restrict__ gu, size_t rows, size_t inter,
+// h[m][i] = bf16(silu(g) * u) with g = gu[m][i] and u = gu[m][inter + i]
+// (the gate and up halves of one GEMM's output row), gu f32 or bf16.
+__device__ __forceinline__ float gu_value(const uint16_t* p, size_t i) { return bf16_bits_to_f32(p[i]); }
+__device__ __forceinline__ float gu_value(const float* p, size_t i) { return p[i]; }
+
+template <typename TIn>
+__global__ void silu_mul_rows_bf16_kernel(const TIn* __restrict__ gu, size_t rows, size_t inter,
                                           uint16_t* __restrict__ h) {
   const size_t n = rows * inter;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     const size_t m = i / inter, c = i % inter;
-    const float z = bf16_bits_to_f32(gu[m * 2 * inter + c]);
-    const float u = bf16_bits_to_f32(gu[m * 2 * inter + inter + c]);
+    const float z = gu_value(gu, m * 2 * inter + c);
+    const float u = gu_value(gu, m * 2 * inter + inter + c);
     h[i] = (uint16_t)(pack_bf16x2((z * (1.0f / (1.0f + __expf(-z)))) * u, 0.0f) & 0xffffu);
   }
 }
 
-// The same for inter % 8 == 0 and 16-byte aligned buffers: eight values per
-// thread, two 16-byte loads and one 16-byte store; n8 = rows * inter / 8 and
-// the row arithmetic fit 32 bits.
+// The same for bf16 gu, inter % 8 == 0 and 16-byte aligned buffers: eight
+// values per thread, two 16-byte loads and one 16-byte store; n8 = rows *
+// inter / 8 and the row arithmetic fit 32 bits.
 __global__ __launch_bounds__(256) void silu_mul_rows_bf16_v8_kernel(const uint16_t* __restrict__ gu, uint32_t inter8,
                                                                     uint32_t n8, uint16_t* __restrict__ h) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += gridDim.x * blockDim.x) {
@@ -501,18 +505,49 @@ hipError_t launch_narrow_atb(const void* wide, bool wide_bf16, const float* nar,
   return slab_sum(partials, slabs, (size_t)W * rank, scale, out, stream);
 }
 
-hipError_t launch_silu_mul_rows_bf16(const uint16_t* gu, size_t rows, size_t inter, uint16_t* h, hipStream_t stream) {
+// f32 gu with inter % 4 == 0 and 16-byte aligned buffers: four values per
+// thread, two 16-byte loads and one 8-byte store; n4 fits 32 bits.
+__global__ __launch_bounds__(256) void silu_mul_rows_f32_v4_kernel(const float* __restrict__ gu, uint32_t inter4,
+                                                                   uint32_t n4, uint16_t* __restrict__ h) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+    const uint32_t m = i / inter4, c4 = i - m * inter4;
+    const size_t row = (size_t)m * inter4 * 8;  // 2 inter values per gu row
+    const f32x4 z4 = *reinterpret_cast<const f32x4*>(gu + row + (size_t)c4 * 4);
+    const f32x4 u4 = *reinterpret_cast<const f32x4*>(gu + row + (size_t)inter4 * 4 + (size_t)c4 * 4);
+    float r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = (z4[e] * (1.0f / (1.0f + __expf(-z4[e])))) * u4[e];
+    *reinterpret_cast<u32x2*>(h + (size_t)i * 4) = u32x2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+  }
+}
+
+hipError_t launch_silu_mul_rows_bf16(const void* gu, bool gu_f32, size_t rows, size_t inter, uint16_t* h,
+                                     hipStream_t stream) {
   const size_t n = rows * inter;
   size_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   if (blocks == 0) return hipSuccess;
-  const size_t n8 = n / 8;
-  if (inter % 8 == 0 && n8 <= 0xffffffffu && ((reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(h)) & 15u) == 0) {
-    const size_t b8 = std::min<size_t>((n8 + 255) / 256, 16384);
-    silu_mul_rows_bf16_v8_kernel<<<(unsigned)b8, 256, 0, stream>>>(gu, (uint32_t)(inter / 8), (uint32_t)n8, h);
+  if (gu_f32 && inter % 4 == 0 && n / 4 <= 0xffffffffu &&
+      ((reinterpret_cast<uintptr_t>(gu) | reinterpret_cast<uintptr_t>(h)) & 15u) == 0) {
+    const size_t n4 = n / 4;
+    const size_t b4 = std::min<size_t>((n4 + 255) / 256, 16384);
+    silu_mul_rows_f32_v4_kernel<<<(unsigned)b4, 256, 0, stream>>>(static_cast<const float*>(gu),
+                                                                  (uint32_t)(inter / 4), (uint32_t)n4, h);
     return hipGetLastError();
   }
-  silu_mul_rows_bf16_kernel<<<(unsigned)blocks, 256, 0, stream>>>(gu, rows, inter, h);
+  if (gu_f32) {
+    silu_mul_rows_bf16_kernel<float><<<(unsigned)blocks, 256, 0, stream>>>(static_cast<const float*>(gu), rows, inter,
+                                                                           h);
+    return hipGetLastError();
+  }
+  const uint16_t* gb = static_cast<const uint16_t*>(gu);
+  const size_t n8 = n / 8;
+  if (inter % 8 == 0 && n8 <= 0xffffffffu && ((reinterpret_cast<uintptr_t>(gb) | reinterpret_cast<uintptr_t>(h)) & 15u) == 0) {
+    const size_t b8 = std::min<size_t>((n8 + 255) / 256, 16384);
+    silu_mul_rows_bf16_v8_kernel<<<(unsigned)b8, 256, 0, stream>>>(gb, (uint32_t)(inter / 8), (uint32_t)n8, h);
+    return hipGetLastError();
+  }
+  silu_mul_rows_bf16_kernel<uint16_t><<<(unsigned)blocks, 256, 0, stream>>>(gb, rows, inter, h);
   return hipGetLastError();
 }
 

@@ -48,8 +48,9 @@ hipError_t launch_lora_merge(const float* w, const float* a, const float* b, int
                              uint64_t N, float* out, hipStream_t stream);
 hipError_t launch_silu_mul(const float* g, const float* u, size_t n, float* h, hipStream_t stream);
 hipError_t launch_silu_mul_bf16(const float* g, const float* u, size_t n, uint16_t* h, hipStream_t stream);
-// h[m][:] = bf16(silu(gu[m][:inter]) * gu[m][inter:]), gu bf16 [rows][2 inter].
-hipError_t launch_silu_mul_rows_bf16(const uint16_t* gu, size_t rows, size_t inter, uint16_t* h, hipStream_t stream);
+// h[m][:] = bf16(silu(gu[m][:inter]) * gu[m][inter:]), gu [rows][2 inter] f32 or bf16.
+hipError_t launch_silu_mul_rows_bf16(const void* gu, bool gu_f32, size_t rows, size_t inter, uint16_t* h,
+                                     hipStream_t stream);
 // QwenRmsNorm::forward (src/qwennet.rs:104-109) over the rows of x [rows, h]:
 // out = (x * (mean(x^2) + eps)^(-1/2)) * (w + 1), f32 arithmetic, x and out
 // f32 or bf16 (out rounded to nearest even).
