@@ -164,21 +164,29 @@ def bench_gemv(torch, Q, L, args) -> dict:
     steps = args.steps
     torch.cuda.synchronize()
     # exactly `steps` launches, rotating over the copies: one graph of them
+    # Each measurement times exactly `steps` launches between two
+    # synchronizations; it is repeated (at least 5 times and ~0.2 s in all)
+    # and the median taken, so that a short run (the driver's --steps 20 is
+    # ~0.2 ms of GPU work) is not one sample of host and graph-launch jitter.
     timed = capture(torch, launch, steps) if graph is not None else None
+    samples = []
     if timed is not None:
         timed.replay()  # once untimed (graph upload)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        timed.replay()
+    while len(samples) < 5 or (sum(samples) < 0.2 and len(samples) < 1000):
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        if timed is not None:
+            timed.replay()
+        else:
+            for i in range(steps):
+                launch(i)
+        torch.cuda.synchronize()
+        samples.append(time.perf_counter() - t0)
+    if timed is not None:
         del timed
-    else:
-        t0 = time.perf_counter()
-        for i in range(steps):
-            launch(i)
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    samples.sort()
+    elapsed = samples[len(samples) // 2]
     # per-launch kernel time: HIP events on the launch stream around graph
     # replays of the rotating launches (cold), and of one weight (warm)
     cold_ms = replay_event_ms(torch, graph, copies) if graph is not None else event_ms(
@@ -189,7 +197,7 @@ def bench_gemv(torch, Q, L, args) -> dict:
     torch.cuda.synchronize()
     if not float((y - ref).abs().max() / ref.abs().max()) < 1e-4:
         raise RuntimeError("GEMV result drifted during timing")
-    out = {"steps": steps, "elapsed_s": elapsed, "bytes": nbytes, "copies": copies,
+    out = {"steps": steps, "elapsed_s": elapsed, "bytes": nbytes, "copies": copies, "repeats": len(samples),
            "value_gbs": nbytes * steps / elapsed / 1e9, "ms_per_step": elapsed * 1e3 / steps,
            "kernel_cold_ms": cold_ms, "kernel_warm_ms": warm_ms, "graph": graph is not None}
     # bf16 activations (same weight bytes, x half the size)
@@ -808,7 +816,8 @@ def main() -> int:
             "workload": "config 2: NF4 decode GEMV x[1x4096] f32 . W[4096x11008] (Wt of the logical 11008x4096), "
                         "block 64, double-quantized scales, y f32; weight held striped; "
                         f"{gemv['copies']} weight copies rotated (cold HBM)",
-            "timing": "HIP-graph replay of the launches" if gemv["graph"] else "eager launches",
+            "timing": ("HIP-graph replay of the launches" if gemv["graph"] else "eager launches") +
+                      f"; median of {gemv['repeats']} timed runs of exactly {gemv['steps']} steps",
             "d_in": 4096, "d_out": 11008, "rows": 1, "block_size": 64, "double_quantized": True,
             "bytes_per_step": gemv["bytes"],
         },
