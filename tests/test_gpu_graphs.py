@@ -201,3 +201,32 @@ def test_internal_workspace_under_capture(device, oracle):
     finally:
         assert h.hipStreamSynchronize(s) == 0
         h.hipStreamDestroy(s)
+
+
+@pytest.mark.parametrize("rows,dt", [(1, torch.float32), (2, torch.bfloat16), (32, torch.bfloat16),
+                                     (12, torch.float32)])
+def test_decoder_stages_replay(device, oracle, rows, dt):
+    """QwenDecoderLayer::step's two stages (src/qwennet.rs:1112-1129) at a
+    reduced shape, captured together as a decode loop would capture them:
+    the folded norms, residual epilogues, the norm kernel and the skinny
+    splits' arrival counters all replay to the eager bits."""
+    from unifur_amd import qwennet as N
+    hid, qd, kvd, inter = 256, 256, 64, 704
+    lins = {}
+    for i, (name, di, do) in enumerate((("q", hid, qd), ("k", hid, kvd), ("v", hid, kvd), ("o", qd, hid),
+                                        ("gate", hid, inter), ("up", hid, inter), ("down", inter, hid))):
+        lins[name], _ = make_linear(oracle, di, do, 2400 + i, device)
+    g_in = torch.from_numpy(oracle.fill_normal(2410, 0.1, hid)).to(device)
+    g_post = torch.from_numpy(oracle.fill_normal(2411, 0.1, hid)).to(device)
+    lay = N.QwenDecoderLayer(lins["q"], lins["k"], lins["v"], lins["o"],
+                             Q.QwenMlp(lins["gate"], lins["up"], lins["down"]), g_in, g_post, 1e-6)
+    _, xt = acts(oracle, rows, hid, 2412 + rows, dt, device)
+    q = torch.empty(rows, qd, dtype=dt, device=device)
+    y = torch.empty(rows, hid, dtype=dt, device=device)
+
+    def run():
+        qq, _, _ = lay.project(xt)
+        q.copy_(qq)
+        y.copy_(lay.attn_out_mlp(xt, q))  # q stands in for the attention output
+
+    replay_matches(run, lambda: [q, y])

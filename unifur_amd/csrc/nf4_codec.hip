@@ -238,7 +238,7 @@ __device__ __forceinline__ float block_scale(const ScalesArg& s, size_t blk) {
 // code bytes each), so each store is a contiguous 1 KiB across the wave and
 // each code load a contiguous 128 bytes; 16 lanes share a 64-value block.
 // All loads of a step are issued before its lookups and stores.
-constexpr int kDeqTiles = 4;
+constexpr int kDeqTiles = 8;
 
 template <bool kBf16Out, bool kDQ>
 __global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* __restrict__ packed, ScalesArg scales,

@@ -72,7 +72,6 @@ struct StripedArgs {
   // launch, x -> x * rsqrt(mean(x^2) + norm_eps) * (norm_w + 1) per row
   const float* norm_w;  // [d_in] or null
   float norm_eps;
-  int early;  // GEMV: issue the first chunk loads before the LUT build
 };
 
 StripedPlan plan_gemv_striped(int rows, int d_in, const int* d_out, int nweights, bool pair);

@@ -275,25 +275,19 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   const bool norm = a.norm_w != nullptr;
   const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : a.x, norm ? (uint32_t)nrows * 4u : 0u);
 
-  // The prologue issues the first D chunks in chunk order like the steady
+  // The prologue issues the first D chunks, in chunk order like the steady
   // state (a load of chunk 0 issued last would make every pass through the
-  // loop head wait for the newest loads).  Launches that fill the GPU build
-  // the LUTs first: their barrier must not wait for the issue of the chunk
-  // loads, which the memory system back-pressures when every workgroup
-  // starts at once.  Smaller launches (a.early) issue the chunks first, so
-  // that their memory latency overlaps the LUT build and its barrier.  The
-  // DQ table holds q / 255 and the scale of scales (read through the scalar
-  // cache) is applied per row, so the table does not wait for that load.
+  // loop head wait for the newest loads), before the LUT build, so that
+  // their memory latency overlaps the build and its barrier (config 2:
+  // 8.85 -> 8.65 us per launch).  The DQ table holds q / 255 and the scale
+  // of scales (read through the scalar cache) is applied per row, so the
+  // table does not wait for that load.
   Chunk<T, NW, XBF16, DQ> ring[D];
-  auto prologue = [&]() {
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, j, lane);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  const bool early = a.early != 0;
-  if (early) prologue();
+  for (int j = 0; j < D; ++j) {
+    issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, j, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float sos[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) sos[w] = DQ ? *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
@@ -308,7 +302,6 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
-  if (!early) prologue();
 
   const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
   const uint32_t lane_off = ((uint32_t)(lane & (kLutCopies - 1)) * 8u) << (kLutCopies == 32 ? 0 : kLutCopies == 16 ? 1 : 2);
@@ -594,31 +587,28 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   }
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.rows * (uint32_t)K * (XF32 ? 4u : 2u));
 
-  if (tid < 256) {  // level-pair LUT and DQ scale table, as in the GEMV
-    const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
-    const f32x4 v = {lo, hi, lo, hi};
-    f32x4* dst = reinterpret_cast<f32x4*>(smem + tid * (kLutCopies * 8));
-#pragma unroll
-    for (int j = 0; j < kLutCopies / 2; ++j) dst[(j + tid) & (kLutCopies / 2 - 1)] = v;
-    if constexpr (DQ) {
-      float* dq_lut = reinterpret_cast<float*>(smem + kDqLutOffset);
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float sos = *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales);
-        dq_lut[w * 256 + tid] = ((float)tid / 255.0f) * sos;  // src/quantize.rs:349
-      }
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();
-  __builtin_amdgcn_sched_barrier(0);
-
+  // as in the GEMV: the first chunks in flight before the LUT build, and the
+  // scale of scales applied per row (the DQ table holds q / 255)
   SkChunk<NT, NW, S, DQ, XF32> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {  // in chunk order, as in the GEMV
     sk_issue<NT, NW, S, DQ, XF32>(ring[j], ww, xr, K, kw, kw + nrows, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
+  float sos[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) sos[w] = DQ ? *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
+  if (tid < 256) {  // level-pair LUT and DQ scale table, as in the GEMV
+    const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
+    const f32x4 v = {lo, hi, lo, hi};
+    f32x4* dst = reinterpret_cast<f32x4*>(smem + tid * (kLutCopies * 8));
+#pragma unroll
+    for (int j = 0; j < kLutCopies / 2; ++j) dst[(j + tid) & (kLutCopies / 2 - 1)] = v;
+    if constexpr (DQ) reinterpret_cast<float*>(smem + kDqLutOffset)[tid] = (float)tid / 255.0f;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
 
   const float* dq_lut = reinterpret_cast<const float*>(smem + kDqLutOffset);
   const uint32_t lane_off = ((uint32_t)(lane & (kLutCopies - 1)) * 8u)
@@ -633,7 +623,8 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
       for (int tt = 0; tt < NT; ++tt) acc[w][i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto decode_scale = [&](const SkChunk<NT, NW, S, DQ, XF32>& c, int w) {
-    return DQ ? dq_lut[w * 256 + (uint32_t)c.scale[w]] : as_f((uint32_t)c.scale[w]);
+    // ((float)q / 255.0f) * scale_of_scales (src/quantize.rs:349)
+    return DQ ? dq_lut[(uint32_t)c.scale[w]] * sos[w] : as_f((uint32_t)c.scale[w]);
   };
   float sdec[2][NW];  // this lane's row scale, per chunk parity
   f32x2 lk[2][8];     // level pairs, per unit parity
@@ -885,12 +876,6 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
   a.x = x;
   a.norm_w = norm_w;
   a.norm_eps = norm_eps;
-  // chunk loads ahead of the LUT build when every chunk of a wave fits the
-  // prologue (the small decode weights), where one memory latency rather
-  // than the memory system's back-pressure bounds the launch; longer d_in
-  // build the LUTs first (7B-shaped down projection at one token: 30 us
-  // with the loads first against 23.5 us)
-  a.early = p.rows_per_wave <= kDepth * 64;
   a.rows = rows;
   a.d_in = d_in;
   a.rows_per_wave = p.rows_per_wave;
