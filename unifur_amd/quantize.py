@@ -23,6 +23,7 @@ fallback: without the built library, or without a GPU, calls raise.
 from __future__ import annotations
 
 import ctypes
+import itertools
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -471,34 +472,44 @@ def quantize_linears(weights) -> list:
     d_output % 64 == 0; the layers come back striped and double quantized,
     their buffers slices of one allocation each for codes, scales and scales
     of scales."""
-    ws = [(v.contiguous().view(-1), int(di), int(do)) for (v, di, do) in weights]
-    n = len(ws)
+    n = len(weights)
     if n == 0:
         return []
-    for v, di, do in ws:
-        _require_cuda(v, "values")
+    vals, dims, v_ptrs = [], [], []
+    for (v, di, do) in weights:
+        di, do = int(di), int(do)
+        if not v.is_cuda:
+            raise ValueError("values must be a CUDA (HIP) device tensor")
         if v.dtype != torch.float32 or v.numel() != di * do:
             raise ValueError(f"values must be float32 with {di} x {do} elements")
         if do % 64 != 0:
             raise ValueError("quantize_linears needs d_output % 64 == 0")
-    dev = ws[0][0].device
+        if not v.is_contiguous() or v.data_ptr() % 16 != 0:
+            v = v.contiguous().clone()
+        vals.append(v)
+        dims.append((di, do))
+        v_ptrs.append(v.data_ptr())
+    dev = vals[0].device
     # back to back: code sizes are multiples of 32 bytes (d_output % 64 == 0),
-    # so every slice stays 8-byte aligned; u8 scales need no alignment
-    c_sizes = [di * do // 2 for (_, di, do) in ws]
-    s_sizes = [di * do // 64 for (_, di, do) in ws]
+    # so every slice stays 8-byte aligned; u8 scales need no alignment.  The
+    # slices' addresses are computed before the launch and their views made
+    # after it (the host work then overlaps the kernels).
+    c_sizes = [di * do // 2 for (di, do) in dims]
+    s_sizes = [di * do // 64 for (di, do) in dims]
     codes = torch.empty(sum(c_sizes), dtype=torch.uint8, device=dev)
     dq = torch.empty(sum(s_sizes), dtype=torch.uint8, device=dev)
     sos = torch.empty(n, dtype=torch.float32, device=dev)
-    code_views, dq_views, sos_views = torch.split(codes, c_sizes), torch.split(dq, s_sizes), torch.split(sos, 1)
+    c_off = list(itertools.accumulate(c_sizes, initial=0))
+    s_off = list(itertools.accumulate(s_sizes, initial=0))
+    cb, db, sb = codes.data_ptr(), dq.data_ptr(), sos.data_ptr()
     P = ctypes.c_void_p * n
     U = ctypes.c_uint64 * n
-    vals = [v if v.data_ptr() % 16 == 0 else v.clone() for (v, _, _) in ws]
     L.check(L.lib().unifur_nf4_quantize_linears(
-        P(*[v.data_ptr() for v in vals]), U(*[di for (_, di, _) in ws]), U(*[do for (_, _, do) in ws]), n,
-        P(*[c.data_ptr() for c in code_views]), P(*[d.data_ptr() for d in dq_views]),
-        P(*[o.data_ptr() for o in sos_views]), None, 0, _stream()))
-    return [Nf4Linear._from_striped(code_views[i], dq_views[i], sos_views[i], di, do)
-            for i, (_, di, do) in enumerate(ws)]
+        P(*v_ptrs), U(*[di for (di, _) in dims]), U(*[do for (_, do) in dims]), n,
+        P(*[cb + o for o in c_off[:n]]), P(*[db + o for o in s_off[:n]]), P(*[sb + 4 * i for i in range(n)]),
+        None, 0, _stream()))
+    return [Nf4Linear._from_striped(codes[c_off[i]:c_off[i + 1]], dq[s_off[i]:s_off[i + 1]], sos[i:i + 1], di, do)
+            for i, (di, do) in enumerate(dims)]
 
 
 def forward_shared_input(x: torch.Tensor, layers, out_dtype: Optional[torch.dtype] = None) -> list:
