@@ -191,3 +191,71 @@ def test_fused_prefill_output_alignment(device, oracle, ydt, shift):
     assert torch.isnan(buf[:shift]).all() and torch.isnan(buf[shift + M * N:]).all()
     ref = oracle.linear_ref_f64(x, wdeq, bias) + oracle.lora_ref_f64(x, a, b, ad.scaling())
     check(y0, ref, x, wdeq, TOL_BF16, f"fused prefill y {ydt} shift {shift}")
+
+
+# ---- split-K of the fused kernel (no adapter; a workspace with room for the
+# f32 partials but not for the expanded weight) ----
+
+@pytest.mark.parametrize("M,K,N", [(300, 4096, 512), (512, 11008, 1024), (130, 2048, 256), (64 + 8, 4096, 128)])
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
+def test_fused_split_k(device, oracle, M, K, N, ydt):
+    lin, wdeq = make_linear(oracle, K, N, 3300 + M, device)
+    bias = oracle.fill_normal(3301, 0.1, N)
+    bt = torch.from_numpy(bias).to(device)
+    x, xt = acts(oracle, M, K, 3302 + M, torch.bfloat16, device)
+    lean = L.lib().unifur_nf4_linear_min_workspace_size(M, K, N, L.BF16, 0)
+    full = L.lib().unifur_nf4_linear_workspace_size(M, K, N, L.BF16, 0)
+    split_room = lean + 8 * M * N * 4 + 4096  # partials of up to 8 slabs
+    assert split_room < full
+    w = lin.weight_struct()
+    st = torch.cuda.current_stream().cuda_stream
+    code = L.BF16 if ydt == torch.bfloat16 else L.F32
+    ref = oracle.linear_ref_f64(x, wdeq, bias)
+    outs = {}
+    for name, need in (("split", split_room), ("whole", lean)):
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        y = torch.empty(M, N, dtype=ydt, device=device)
+        L.check(L.lib().unifur_nf4_linear_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w), bt.data_ptr(), None,
+                                                  y.data_ptr(), code, ws.data_ptr(), need, st))
+        check(y, ref, x, wdeq, TOL_BF16, f"fused {name} M={M} K={K} N={N}")
+        y2 = torch.empty_like(y)
+        L.check(L.lib().unifur_nf4_linear_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w), bt.data_ptr(), None,
+                                                  y2.data_ptr(), code, ws.data_ptr(), need, st))
+        assert torch.equal(y, y2)  # slabs added in a fixed order
+        assert int(ws[:65536].count_nonzero()) == 0
+        outs[name] = y.float()
+    # both sum the same products, in another order: within f32 rounding (plus
+    # one bf16 rounding of the output)
+    tol = 1e-2 if ydt == torch.bfloat16 else 1e-4
+    assert float((outs["split"] - outs["whole"]).abs().max() / outs["whole"].abs().max()) < tol
+
+
+@pytest.mark.parametrize("T", [256, 512])
+def test_fused_swiglu_split_k(device, oracle, T):
+    # a 7B-shaped MLP at reduced width: down (inter -> hidden) has few tiles
+    # and splits d_in; gate/up may too
+    hidden, inter = 1024, 2816
+    ws_, deqs = [], []
+    for i, (din, dout) in enumerate([(hidden, inter), (hidden, inter), (inter, hidden)]):
+        lin, wd = make_linear(oracle, din, dout, 3400 + i, device)
+        ws_.append(lin)
+        deqs.append(wd)
+    x, xt = acts(oracle, T, hidden, 3410 + T, torch.bfloat16, device)
+    lean = L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)
+    # up to 512 rows the default workspace is the fused kernels' with the
+    # split-K partials (down's two slabs of f32 here), not an expanded weight
+    room = L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16)
+    assert lean + 2 * T * hidden * 4 <= room < lean + 2 * T * hidden * 4 + 4096
+    g, u, d = (l.weight_struct() for l in ws_)
+    st = torch.cuda.current_stream().cuda_stream
+    h = oracle.silu_f64(x.astype(np.float64) @ deqs[0]) * (x.astype(np.float64) @ deqs[1])
+    ref = oracle.swiglu_ref_f64(x, *deqs)
+    outs = []
+    for need in (room, lean):
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        y = torch.empty(T, hidden, device=device)
+        L.check(L.lib().unifur_nf4_swiglu_forward(xt.data_ptr(), L.BF16, T, ctypes.byref(g), ctypes.byref(u),
+                                                  ctypes.byref(d), y.data_ptr(), L.F32, ws.data_ptr(), need, st))
+        check(y, ref, h, deqs[2], TOL_BF16, f"fused swiglu T={T} workspace {need}")
+        outs.append(y)
+    assert float((outs[0] - outs[1]).abs().max() / outs[1].abs().max()) < 1e-2

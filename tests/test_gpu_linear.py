@@ -163,14 +163,16 @@ def test_swiglu_config4(device, oracle, T, striped):
     check(y, ref, h, wd, TOL_BF16, f"swiglu config4 T={T} striped={striped}")
 
 
+@pytest.mark.parametrize("T", [200, 600])
 @pytest.mark.parametrize("striped", [True, False])
-def test_swiglu_prefill_expanded_and_fused(device, oracle, striped):
-    # more than 64 rows: with the default workspace each weight is expanded to
-    # bf16 and multiplied by the BLAS GEMM; with the minimum workspace the
-    # fused MFMA kernel runs; both within the bf16 tolerance
+def test_swiglu_prefill_expanded_and_fused(device, oracle, striped, T):
+    # more than 64 rows: with the default workspace up to 512 rows take the
+    # fused MFMA kernels (split-K where their grid is small), more rows expand
+    # each weight to bf16 for the BLAS GEMM; with the minimum workspace the
+    # fused kernels over whole d_in run; all within the bf16 tolerance
     from unifur_amd import _lib as L
     import ctypes
-    T, hidden, inter = 200, 1024, 2816
+    hidden, inter = 1024, 2816
     g, wg = make_linear(oracle, hidden, inter, 61, device, striped=striped)
     u, wu = make_linear(oracle, hidden, inter, 62, device, striped=striped)
     d, wd = make_linear(oracle, inter, hidden, 63, device, striped=striped)
@@ -179,7 +181,10 @@ def test_swiglu_prefill_expanded_and_fused(device, oracle, striped):
     h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
     full = L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16)
     lean = L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)
-    assert lean < hidden * inter * 2 < full
+    if T > 512:
+        assert full > lean + 2 * hidden * inter * 2  # the expanded gate and up weights
+    else:
+        assert lean < full < lean + hidden * inter * 2  # split-K partials, no expanded weight
     gs, us, ds = g.weight_struct(), u.weight_struct(), d.weight_struct()
     stream = torch.cuda.current_stream().cuda_stream
     for need in (full, lean):

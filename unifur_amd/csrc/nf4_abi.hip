@@ -193,7 +193,8 @@ struct LinearLayout {
   bool expand;  // kMfma: bf16 weight expanded in the workspace + BLAS GEMM (else the fused kernel)
   GemvPlan gemv;
   StripedPlan striped, striped_tail;  // skinny: the plan of each launch (the last of several f32 launches)
-  size_t partials, xa, lora_at, lora_bt, wt, blas, wf32, rm_codes, rm_scales, total;
+  int splits = 1;  // kMfma without expand: d_in slabs of the fused kernel
+  size_t partials, xa, lora_at, lora_bt, wt, blas, wf32, rm_codes, rm_scales, gemm_partials, total;
 };
 
 // Decode-sized batches (<= 4 rows) take a GEMV (the striped one for striped
@@ -205,7 +206,8 @@ struct LinearLayout {
 // matmul (a striped weight is first put back in row-major order in the
 // workspace).
 LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t lora_rank, const void* packed,
-                         int x_dtype, const void* x, bool striped, int scale_kind, bool expand = true) {
+                         int x_dtype, const void* x, bool striped, int scale_kind, bool expand = true,
+                         bool split = true) {
   LinearLayout L{};
   Carver c;
   const bool small = rows <= (uint64_t)kGemvMaxRows;
@@ -243,6 +245,10 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
     if (L.expand) {
       L.wt = c.take(d_in * d_out * sizeof(uint16_t));
       L.blas = c.take(kBlasWorkspace);
+    } else if (split && lora_rank == 0) {
+      // the fused kernel over too few tiles splits d_in (f32 partials)
+      L.splits = gemm_k_splits((int)rows, (int)d_in, (int)d_out);
+      if (L.splits > 1) L.gemm_partials = c.take((size_t)L.splits * rows * d_out * sizeof(float));
     }
   } else {
     L.path = LinearPath::kGeneric;
@@ -326,9 +332,19 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
     // a workspace too small for the expanded weight (or an output the BLAS
     // kernels cannot take with 16-byte accesses): the fused kernel
-    const LinearLayout lean =
+    LinearLayout lean =
         plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false);
+    if (workspace && workspace_bytes < lean.total)  // without the split-K partials
+      lean = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false,
+                         false);
     if (!workspace || workspace_bytes >= lean.total) L = lean;
+  }
+  if (L.path == LinearPath::kMfma && !L.expand && L.splits > 1 &&
+      ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
+    // no room for the split-K partials (or an output the reduction cannot
+    // store four at a time): the fused kernel over whole d_in
+    L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false,
+                    false);
   }
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
@@ -354,7 +370,8 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
                                       lora->scaling, at<uint16_t>(ws, L.lora_at), bt16, xa16, stream));
     }
     UNIFUR_HIP(launch_gemm(xb, w->packed, to_scales(w->scales), (int)rows, (int)w->d_in, (int)w->d_out, bias, xa16,
-                           bt16, (int)rank, y, ybf, is_striped(w), stream));
+                           bt16, (int)rank, y, ybf, is_striped(w), stream, L.splits,
+                           L.splits > 1 ? at<float>(ws, L.gemm_partials) : nullptr));
     return UNIFUR_NF4_OK;
   }
   if (lora) {
@@ -410,12 +427,15 @@ struct MlpLayout {
   bool expand;  // kMfma: each weight expanded to bf16 in turn + BLAS GEMMs (else the fused kernel)
   GemvPlan up_plan, down_plan;
   StripedPlan s_up, s_down;
-  size_t partials0, partials1, h, u, hb, wt, blas, wf32, rm_codes, rm_scales, total;
+  int split_up = 1, split_down = 1;  // kMfma without expand: d_in slabs of the fused kernel
+  size_t partials0, partials1, h, u, hb, wt, blas, wf32, rm_codes, rm_scales, gemm_partials, total;
 };
+
+constexpr int kFusedMlpMaxRows = 512;  // SwiGLU prefill: fused kernels up to this many rows
 
 MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_nf4_weight* g,
                    const unifur_nf4_weight* u, const unifur_nf4_weight* d, int x_dtype, const void* x,
-                   bool expand = true) {
+                   bool expand = true, bool split = true) {
   MlpLayout L{};
   Carver c;
   const bool all_striped = is_striped(g) && is_striped(u) && is_striped(d);
@@ -468,8 +488,11 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
     L.u = L.path == MlpPath::kGemv ? c.take((size_t)rows * inter * sizeof(float)) : 0;
   } else if (mfma) {
     L.path = MlpPath::kMfma;
-    L.expand = expand && expand_supported((int)hidden, (int)inter, 0) && expand_supported((int)inter, (int)hidden, 0) &&
-               2 * inter <= 0x7fffffffu;
+    // up to 512 rows the fused kernels with split-K win (7B-shaped MLP: 149
+    // against 181.5 us at 256 rows, 229.6 against 238 us at 512); above, the
+    // weights expanded once and the BLAS GEMMs
+    L.expand = expand && rows > (uint64_t)kFusedMlpMaxRows && expand_supported((int)hidden, (int)inter, 0) &&
+               expand_supported((int)inter, (int)hidden, 0) && 2 * inter <= 0x7fffffffu;
     if (L.expand) {
       // gate and up expanded side by side ([2 inter][hidden]: one GEMM with
       // f32 outputs [rows][2 inter], so silu(g) * u is rounded to bf16 once,
@@ -482,6 +505,13 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
       L.h = c.take((size_t)rows * inter * sizeof(float));
       L.u = c.take((size_t)rows * inter * sizeof(float));
       L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
+      if (split) {  // the fused kernel splits d_in where its grid is small (f32 partials)
+        L.split_up = gemm_k_splits((int)rows, (int)hidden, (int)inter);
+        L.split_down = gemm_k_splits((int)rows, (int)inter, (int)hidden);
+        const size_t part = std::max(L.split_up > 1 ? (size_t)L.split_up * rows * inter : 0,
+                                     L.split_down > 1 ? (size_t)L.split_down * rows * hidden : 0);
+        if (part) L.gemm_partials = c.take(part * sizeof(float));
+      }
     }
   } else {
     L.path = MlpPath::kGeneric;
@@ -514,9 +544,14 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   if (L.path == MlpPath::kMfma && L.expand && ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
     // a workspace too small for an expanded weight, or an output the BLAS
     // kernels cannot take with 16-byte accesses: the fused kernel
-    const MlpLayout lean = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x, false);
+    MlpLayout lean = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x, false);
+    if (workspace && workspace_bytes < lean.total)  // without the split-K partials
+      lean = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x, false, false);
     if (workspace_bytes >= lean.total || !workspace) L = lean;
   }
+  if (L.path == MlpPath::kMfma && !L.expand && L.gemm_partials &&
+      ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16)))
+    L = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x, false, false);  // without split-K
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool xbf = x_dtype == UNIFUR_NF4_BF16;
@@ -618,13 +653,14 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
         UNIFUR_HIP(blas_gemm_xwt(hb, wt, nullptr, m, hd, in, y, ybf, bw, kBlasWorkspace, stream));
         return UNIFUR_NF4_OK;
       }
+      float* gp = L.gemm_partials ? at<float>(ws, L.gemm_partials) : nullptr;
       UNIFUR_HIP(launch_gemm(xb, gate->packed, to_scales(gate->scales), (int)rows, (int)hidden, (int)inter, nullptr,
-                             nullptr, nullptr, 0, h, false, is_striped(gate), stream));
+                             nullptr, nullptr, 0, h, false, is_striped(gate), stream, L.split_up, gp));
       UNIFUR_HIP(launch_gemm(xb, up->packed, to_scales(up->scales), (int)rows, (int)hidden, (int)inter, nullptr,
-                             nullptr, nullptr, 0, u, false, is_striped(up), stream));
+                             nullptr, nullptr, 0, u, false, is_striped(up), stream, L.split_up, gp));
       UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
       UNIFUR_HIP(launch_gemm(hb, down->packed, to_scales(down->scales), (int)rows, (int)inter, (int)hidden, nullptr,
-                             nullptr, nullptr, 0, y, ybf, is_striped(down), stream));
+                             nullptr, nullptr, 0, y, ybf, is_striped(down), stream, L.split_down, gp));
       return UNIFUR_NF4_OK;
     }
     case MlpPath::kGeneric:
@@ -657,7 +693,8 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   return UNIFUR_NF4_OK;
 }
 
-uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype, bool expand) {
+uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype, bool expand,
+                          bool split = true) {
   if (rows == 0 || hidden == 0 || intermediate == 0) return 0;
   const uint8_t* p = reinterpret_cast<const uint8_t*>(uintptr_t{256});
   uint64_t need = 0;
@@ -671,7 +708,8 @@ uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate,
       unifur_nf4_weight d = g;
       d.d_in = intermediate;
       d.d_out = hidden;
-      need = std::max<uint64_t>(need, plan_mlp(rows, hidden, intermediate, &g, &u, &d, x_dtype, p, expand).total);
+      need = std::max<uint64_t>(need,
+                                plan_mlp(rows, hidden, intermediate, &g, &u, &d, x_dtype, p, expand, split).total);
     }
   }
   return need;
@@ -1238,8 +1276,10 @@ int run_linear_noalloc(const void* x, int x_dtype, uint64_t rows, const unifur_n
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
   const uint32_t rank = lora ? lora->rank : 0;
   if (lora) UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
-  const LinearLayout L =
+  LinearLayout L =
       plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false);
+  if (L.total > kStaticScratchBytes)  // without the split-K partials
+    L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false, false);
   if (L.total > kStaticScratchBytes)
     return fail(UNIFUR_NF4_ERR_WORKSPACE, "linear_forward_noalloc: this call needs " + std::to_string(L.total) +
                                               " bytes of scratch, the allocation-free entry point holds " +
@@ -1439,12 +1479,12 @@ uint64_t unifur_nf4_linear_min_workspace_size(uint64_t rows, uint64_t d_in, uint
   for (int striped = 0; striped < 2; ++striped)
     for (int kind = 0; kind < 2; ++kind)
       need = std::max<uint64_t>(need, plan_linear(rows, d_in, d_out, lora_rank, aligned, x_dtype, aligned,
-                                                  striped && d_out % 64 == 0, kind, false).total);
+                                                  striped && d_out % 64 == 0, kind, false, false).total);
   return need;
 }
 
 uint64_t unifur_nf4_swiglu_min_workspace_size(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype) {
-  return swiglu_workspace(rows, hidden, intermediate, x_dtype, false);
+  return swiglu_workspace(rows, hidden, intermediate, x_dtype, false, false);
 }
 
 int unifur_nf4_linear_forward(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weight* w,

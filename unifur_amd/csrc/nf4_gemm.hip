@@ -73,6 +73,11 @@ struct GemmArgs {
   int y_bf16;
   int y_aligned;  // y 16-byte aligned: the epilogue stores 4 outputs at once
   int tiles_n;  // N / kBN
+  // split-K: k_splits workgroups per output tile, each over k_steps K steps
+  // (the last over what is left), writing its raw f32 sums to partials
+  // [k_splits][M][N] (bias, adapter and rounding come in the reduction)
+  int k_splits, k_steps;
+  float* partials;
 };
 
 // 16-byte chunk swizzle of a 128-byte tile row (8 chunks).
@@ -294,9 +299,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   // sharing an X row band share that XCD's L2.
   const int nb = gridDim.x;
   const int b = blockIdx.x;
-  const int t = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+  const int tb = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+  const int split = tb % g.k_splits, t = tb / g.k_splits;
   const int m0 = (t / g.tiles_n) * kBM, n0 = (t % g.tiles_n) * kBN;
   const int row0 = m0 + 64 * w4;
+  const int kb = split * g.k_steps;  // this workgroup's first K step
+  const int kbase = kb * kBK;        // ... as a column of X / row of W
+  void* const yout = g.k_splits > 1 ? static_cast<void*>(g.partials + (size_t)split * g.M * g.N) : g.y;
 
   if (tid < 256) {
     float* lut = reinterpret_cast<float*>(smem + kLdsLut);
@@ -312,7 +321,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     if constexpr (DQ)
       reinterpret_cast<float*>(smem + kLdsDq)[tid] = ((float)tid / 255.0f) * (*g.scales.scale_of_scales);
   }
-  const int nk = g.K / kBK;
+  const int nk = min(g.k_steps, g.K / kBK - kb);  // K steps of this workgroup (>= 1)
 
   // Every role passes the same nk + 1 workgroup barriers: the LUTs, steps 0
   // and 1 ready, then one per further step.
@@ -321,20 +330,20 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     const int d = tid - 256;
     BStep Br[kBRing];
 #pragma unroll
-    for (int r = 0; r < kBRing; ++r) load_b<DQ, STRIPED>(Br[r], g, n0, min(r, nk - 1) * kBK, d);
+    for (int r = 0; r < kBRing; ++r) load_b<DQ, STRIPED>(Br[r], g, n0, kbase + min(r, nk - 1) * kBK, d);
     lds_barrier();  // LUTs visible
     store_b<DQ, STRIPED>(Br[0], smem, 0, d);
-    load_b<DQ, STRIPED>(Br[0], g, n0, min(kBRing, nk - 1) * kBK, d);
+    load_b<DQ, STRIPED>(Br[0], g, n0, kbase + min(kBRing, nk - 1) * kBK, d);
     if (nk > 1) {
       store_b<DQ, STRIPED>(Br[1], smem, 1, d);
-      load_b<DQ, STRIPED>(Br[1], g, n0, min(kBRing + 1, nk - 1) * kBK, d);
+      load_b<DQ, STRIPED>(Br[1], g, n0, kbase + min(kBRing + 1, nk - 1) * kBK, d);
     }
     lds_barrier();  // steps 0 and 1 ready
     // step t2 (from 2 on) into W buffer t2 % 3 from ring slot t2 % kBRing,
     // then the barrier that publishes it
     auto produce = [&](int t2, int slot) {
       store_b<DQ, STRIPED>(Br[slot], smem, t2 % kBStages, d);
-      load_b<DQ, STRIPED>(Br[slot], g, n0, min(t2 + kBRing, nk - 1) * kBK, d);
+      load_b<DQ, STRIPED>(Br[slot], g, n0, kbase + min(t2 + kBRing, nk - 1) * kBK, d);
       lds_barrier();
     };
     int t2 = 2;
@@ -361,8 +370,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  load_a(xr, g.K, row0, 0, awave, lane);
-  if (nk > 1) load_a(xr, g.K, row0, kBK, awave + kATileBytes, lane);
+  load_a(xr, g.K, row0, kbase, awave, lane);
+  if (nk > 1) load_a(xr, g.K, row0, kbase + kBK, awave + kATileBytes, lane);
   lds_barrier();  // LUTs visible
   lds_barrier();  // steps 0 and 1 ready
   if (nk > 1) UNIFUR_WAIT_VMCNT(8);  // this wave's X copies of step 0 landed
@@ -382,7 +391,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(0xc07f);
     // step s + 2 goes to the stage step s - 1 used: all its reads completed
     // before that step's last MFMAs issued
-    if constexpr (kCopy2) load_a(xr, g.K, row0, (s + 2) * kBK, awave + (sa == 0 ? 2 : sa - 1) * kATileBytes, lane);
+    if constexpr (kCopy2)
+      load_a(xr, g.K, row0, kbase + (s + 2) * kBK, awave + (sa == 0 ? 2 : sa - 1) * kATileBytes, lane);
     read_frags(Fb, ab, bb, 1, lane);
     mma_frags(acc, Fa);
     read_frags(Fa, ab, bb, 2, lane);
@@ -476,16 +486,16 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
           if constexpr (YBF16) {
             const u32x2 o = {pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
             if (g.y_aligned) {
-              *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(g.y) + idx) = o;
+              *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(yout) + idx) = o;
             } else {
-              uint16_t* p = reinterpret_cast<uint16_t*>(g.y) + idx;
+              uint16_t* p = reinterpret_cast<uint16_t*>(yout) + idx;
               p[0] = (uint16_t)(o.x & 0xffffu);
               p[1] = (uint16_t)(o.x >> 16);
               p[2] = (uint16_t)(o.y & 0xffffu);
               p[3] = (uint16_t)(o.y >> 16);
             }
           } else {
-            float* p = reinterpret_cast<float*>(g.y) + idx;
+            float* p = reinterpret_cast<float*>(yout) + idx;
             if (g.y_aligned) {
               *reinterpret_cast<f32x4*>(p) = f32x4{y0, y1, y2, y3};
             } else {
@@ -516,7 +526,7 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
     if (e != hipSuccess) return e;
     done.fetch_or(bit, std::memory_order_acq_rel);
   }
-  const int grid = ((g.M + kBM - 1) / kBM) * g.tiles_n;
+  const int grid = ((g.M + kBM - 1) / kBM) * g.tiles_n * g.k_splits;
   gemm_kernel<DQ, YBF16, LORA, STRIPED><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
   return hipGetLastError();
 }
@@ -633,9 +643,47 @@ hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* 
   return hipGetLastError();
 }
 
+namespace {
+
+// Split-K reduction: y[m][n] = sum over the splits, in split order, of
+// partials[s][m][n] (+ bias[n]), four consecutive outputs per thread.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partials, int splits,
+                                                            size_t mn4, int n4, const float* __restrict__ bias,
+                                                            void* __restrict__ y, int y_bf16) {
+  const size_t stride = mn4;  // f32x4 per split
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn4; i += (size_t)gridDim.x * blockDim.x) {
+    f32x4 v = reinterpret_cast<const f32x4*>(partials)[i];
+    for (int q = 1; q < splits; ++q) {
+      const f32x4 w = reinterpret_cast<const f32x4*>(partials)[i + q * stride];
+      v = f32x4{v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w};
+    }
+    if (bias) {
+      const f32x4 b4 = reinterpret_cast<const f32x4*>(bias)[i % (size_t)n4];
+      v = f32x4{v.x + b4.x, v.y + b4.y, v.z + b4.z, v.w + b4.w};
+    }
+    if (y_bf16)
+      reinterpret_cast<u32x2*>(y)[i] = u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+    else
+      reinterpret_cast<f32x4*>(y)[i] = v;
+  }
+}
+
+}  // namespace
+
+int gemm_k_splits(int M, int K, int N) {
+  // grids of fewer than ~200 tiles leave CUs idle (one 147 KiB workgroup per
+  // CU): split d_in so the grid reaches ~256 workgroups, each over at least
+  // 16 K steps
+  const long tiles = (long)((M + kBM - 1) / kBM) * (N / kBN);
+  const int steps = K / kBK;
+  int splits = 1;
+  while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= 16) splits *= 2;
+  return splits;
+}
+
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
                        const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
-                       bool y_bf16, bool striped, hipStream_t stream) {
+                       bool y_bf16, bool striped, hipStream_t stream, int k_splits, float* partials) {
   GemmArgs g{};
   g.x = x;
   g.packed = packed;
@@ -652,6 +700,27 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
   g.y_bf16 = y_bf16;
   g.y_aligned = (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
   g.tiles_n = N / kBN;
+  const int steps = K / kBK;
+  if (k_splits < 1 || (k_splits > 1 && (!partials || lora_xa || (reinterpret_cast<uintptr_t>(y) & 15u) != 0)))
+    return hipErrorInvalidValue;
+  g.k_splits = k_splits;
+  g.k_steps = (steps + k_splits - 1) / k_splits;
+  if (k_splits > 1 && g.k_steps * (k_splits - 1) >= steps) return hipErrorInvalidValue;  // every split has a step
+  g.partials = partials;
+  if (k_splits > 1) {
+    // raw f32 sums into the partials, then the ordered reduction
+    g.bias = nullptr;
+    g.y_bf16 = 0;
+    g.y_aligned = 1;
+    const bool dq0 = scales.kind == kScalesDQ;
+    hipError_t e = dq0 ? (striped ? launch_g<true, false, false, true>(g, stream) : launch_g<true, false, false, false>(g, stream))
+                       : (striped ? launch_g<false, false, false, true>(g, stream) : launch_g<false, false, false, false>(g, stream));
+    if (e != hipSuccess) return e;
+    const size_t mn4 = (size_t)M * N / 4;
+    const unsigned blocks = (unsigned)std::min<size_t>((mn4 + 255) / 256, 4096);
+    splitk_reduce_kernel<<<blocks, 256, 0, stream>>>(partials, k_splits, mn4, N / 4, bias, y, y_bf16);
+    return hipGetLastError();
+  }
   const bool dq = scales.kind == kScalesDQ;
   const bool lora = lora_xa != nullptr;
 #define UNIFUR_GEMM_CASE(D, B, R)                                                     \

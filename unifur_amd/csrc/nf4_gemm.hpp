@@ -24,8 +24,14 @@ hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* 
 // Y[M, N] = X deq(W) (+ bias) (+ xa B); xa and bt from launch_lora_operands, or null.
 // The weight is in the reference's row-major layout, or striped
 // (nf4_layout.hpp) when striped is set.
+// With k_splits > 1 (no adapter, y 16-byte aligned) the workgroups of a
+// tile split d_in and write f32 sums to partials (k_splits * M * N floats),
+// which a second launch adds in split order with the bias and rounding.
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
                        const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
-                       bool y_bf16, bool striped, hipStream_t stream);
+                       bool y_bf16, bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr);
+
+// d_in slabs the fused GEMM splits into for this shape (1: no split).
+int gemm_k_splits(int M, int K, int N);
 
 }  // namespace unifur
