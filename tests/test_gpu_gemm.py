@@ -233,7 +233,7 @@ def test_fused_split_k(device, oracle, M, K, N, ydt):
 @pytest.mark.parametrize("T", [256, 512])
 def test_fused_swiglu_split_k(device, oracle, T):
     # a 7B-shaped MLP at reduced width: down (inter -> hidden) has few tiles
-    # and splits d_in; gate/up may too
+    # and splits d_in; the gate/up pair (16 K steps) runs over whole d_in
     hidden, inter = 1024, 2816
     ws_, deqs = [], []
     for i, (din, dout) in enumerate([(hidden, inter), (hidden, inter), (inter, hidden)]):
@@ -259,3 +259,61 @@ def test_fused_swiglu_split_k(device, oracle, T):
         check(y, ref, h, deqs[2], TOL_BF16, f"fused swiglu T={T} workspace {need}")
         outs.append(y)
     assert float((outs[0] - outs[1]).abs().max() / outs[1].abs().max()) < 1e-2
+
+
+def swiglu_call(g, u, d, xt, T, hidden, need, device):
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    y = torch.empty(T, hidden, device=device)
+    L.check(L.lib().unifur_nf4_swiglu_forward(xt.data_ptr(), L.BF16, T, ctypes.byref(g), ctypes.byref(u),
+                                              ctypes.byref(d), y.data_ptr(), L.F32, ws.data_ptr(), need,
+                                              torch.cuda.current_stream().cuda_stream))
+    return y, ws
+
+
+def swiglu_layers(oracle, device, hidden, inter, seed, kinds=(True, True, True), striped=None):
+    lins = [make_linear(oracle, din, dout, seed + i, device, dq=dq, striped=striped)
+            for i, ((din, dout), dq) in enumerate(zip([(hidden, inter), (hidden, inter), (inter, hidden)], kinds))]
+    return [l for l, _ in lins], [w for _, w in lins]
+
+
+@pytest.mark.parametrize("striped,dq", [(True, True), (False, True), (True, False)])
+def test_fused_swiglu_pair(device, oracle, striped, dq):
+    # gate and up of one scale kind run as one pair launch whose epilogue
+    # forms silu(g) * u.  Here its grid has few output tiles over 64 K steps:
+    # with the default workspace it splits d_in and a reduction adds the
+    # slabs (in slab order) before the product; with the least workspace it
+    # runs over whole d_in.  Both against the oracle, and each deterministic.
+    hidden, inter, T = 4096, 1024, 256
+    lins, (wg, wu, wd) = swiglu_layers(oracle, device, hidden, inter, 3500, (dq, dq, dq), striped)
+    x, xt = acts(oracle, T, hidden, 3510, torch.bfloat16, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    room = L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16)
+    lean = L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)
+    assert room >= lean + 2 * T * 2 * inter * 4  # the pair's partials: gate and up, two or more slabs
+    g, u, d = (l.weight_struct() for l in lins)
+    outs = {}
+    for name, need in (("split", room), ("whole", lean)):
+        y, ws = swiglu_call(g, u, d, xt, T, hidden, need, device)
+        check(y, ref, h, wd, TOL_BF16, f"pair {name} striped={striped} dq={dq}")
+        y2, _ = swiglu_call(g, u, d, xt, T, hidden, need, device)
+        assert torch.equal(y, y2)
+        assert int(ws[:65536].count_nonzero()) == 0
+        outs[name] = y
+    assert float((outs["split"] - outs["whole"]).abs().max() / outs["whole"].abs().max()) < 1e-2
+
+
+def test_fused_swiglu_mixed_scale_kinds(device, oracle):
+    # gate double-quantized, up with f32 scales: no pair launch -- gate and
+    # up are two launches (f32 outputs, split over d_in with the default
+    # workspace) and the elementwise kernel forms silu(g) * u
+    hidden, inter, T = 4096, 1024, 256
+    lins, (wg, wu, wd) = swiglu_layers(oracle, device, hidden, inter, 3520, (True, False, True))
+    x, xt = acts(oracle, T, hidden, 3530, torch.bfloat16, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    g, u, d = (l.weight_struct() for l in lins)
+    for need in (L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16),
+                 L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)):
+        y, _ = swiglu_call(g, u, d, xt, T, hidden, need, device)
+        check(y, ref, h, wd, TOL_BF16, f"mixed kinds workspace {need}")

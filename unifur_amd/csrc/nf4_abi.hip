@@ -502,13 +502,18 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
       L.h = c.take((size_t)rows * 2 * inter * sizeof(float));
       L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
     } else {
-      L.h = c.take((size_t)rows * inter * sizeof(float));
-      L.u = c.take((size_t)rows * inter * sizeof(float));
+      // gate and up of one scale kind: one pair launch storing bf16
+      // silu(g) * u; else one launch each (f32 outputs) and the elementwise
+      // kernel
+      if (!same_kind) {
+        L.h = c.take((size_t)rows * inter * sizeof(float));
+        L.u = c.take((size_t)rows * inter * sizeof(float));
+      }
       L.hb = c.take((size_t)rows * inter * sizeof(uint16_t));
-      if (split) {  // the fused kernel splits d_in where its grid is small (f32 partials)
-        L.split_up = gemm_k_splits((int)rows, (int)hidden, (int)inter);
+      if (split) {  // the fused kernel splits d_in where its grid would leave CUs idle (f32 partials)
+        L.split_up = gemm_k_splits((int)rows, (int)hidden, (int)inter, same_kind);
         L.split_down = gemm_k_splits((int)rows, (int)inter, (int)hidden);
-        const size_t part = std::max(L.split_up > 1 ? (size_t)L.split_up * rows * inter : 0,
+        const size_t part = std::max(L.split_up > 1 ? (size_t)L.split_up * rows * inter * (same_kind ? 2 : 1) : 0,
                                      L.split_down > 1 ? (size_t)L.split_down * rows * hidden : 0);
         if (part) L.gemm_partials = c.take(part * sizeof(float));
       }
@@ -654,11 +659,16 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
         return UNIFUR_NF4_OK;
       }
       float* gp = L.gemm_partials ? at<float>(ws, L.gemm_partials) : nullptr;
-      UNIFUR_HIP(launch_gemm(xb, gate->packed, to_scales(gate->scales), (int)rows, (int)hidden, (int)inter, nullptr,
-                             nullptr, nullptr, 0, h, false, is_striped(gate), stream, L.split_up, gp));
-      UNIFUR_HIP(launch_gemm(xb, up->packed, to_scales(up->scales), (int)rows, (int)hidden, (int)inter, nullptr,
-                             nullptr, nullptr, 0, u, false, is_striped(up), stream, L.split_up, gp));
-      UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
+      if (gate->scales.kind == up->scales.kind) {
+        UNIFUR_HIP(launch_gemm_pair(xb, gate->packed, to_scales(gate->scales), up->packed, to_scales(up->scales),
+                                    (int)rows, (int)hidden, (int)inter, hb, is_striped(gate), stream, L.split_up, gp));
+      } else {
+        UNIFUR_HIP(launch_gemm(xb, gate->packed, to_scales(gate->scales), (int)rows, (int)hidden, (int)inter, nullptr,
+                               nullptr, nullptr, 0, h, false, is_striped(gate), stream, L.split_up, gp));
+        UNIFUR_HIP(launch_gemm(xb, up->packed, to_scales(up->scales), (int)rows, (int)hidden, (int)inter, nullptr,
+                               nullptr, nullptr, 0, u, false, is_striped(up), stream, L.split_up, gp));
+        UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
+      }
       UNIFUR_HIP(launch_gemm(hb, down->packed, to_scales(down->scales), (int)rows, (int)inter, (int)hidden, nullptr,
                              nullptr, nullptr, 0, y, ybf, is_striped(down), stream, L.split_down, gp));
       return UNIFUR_NF4_OK;

@@ -50,8 +50,8 @@ constexpr int kLutMode = UNIFUR_GEMM_LUT;
 static_assert(kLutMode >= 0 && kLutMode <= 2, "UNIFUR_GEMM_LUT");
 constexpr int kLutBytes = kLutMode == 1 ? 4 * 256 * 8 : kLutMode == 2 ? 16 * 4 : 256 * 8;
 constexpr int kLdsLut = kLdsB + kBStages * kBTileBytes;  // level LUT
-constexpr int kLdsDq = kLdsLut + kLutBytes;      // DQ scale LUT, 256 x f32
-constexpr size_t kGemmSmem = kLdsDq + 256 * 4;   // 147 KiB: one workgroup per CU
+constexpr int kLdsDq = kLdsLut + kLutBytes;      // DQ scale LUTs, 256 x f32 per weight (two in PAIR mode)
+constexpr size_t kGemmSmem = kLdsDq + 2 * 256 * 4;  // 148 KiB: one workgroup per CU
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -72,13 +72,24 @@ struct GemmArgs {
   void* y;  // [M, N] f32 or bf16
   int y_bf16;
   int y_aligned;  // y 16-byte aligned: the epilogue stores 4 outputs at once
-  int tiles_n;  // N / kBN
+  int tiles_n;  // N / kBN (N / 64 in PAIR mode)
   // split-K: k_splits workgroups per output tile, each over k_steps K steps
   // (the last over what is left), writing its raw f32 sums to partials
-  // [k_splits][M][N] (bias, adapter and rounding come in the reduction)
+  // [k_splits][M][ldy] (bias, adapter and rounding come in the reduction)
   int k_splits, k_steps;
   float* partials;
+  int ldy;  // row stride of the split-K partials: N, or 2 N in PAIR mode (gate columns, then up)
+  // PAIR mode (the SwiGLU gate/up pair over one X): the second weight (up),
+  // same shape, layout and scale kind as the first (gate).  A tile holds 64
+  // columns of each -- W tile columns 0-63 gate, 64-127 up -- and stores
+  // silu(gate x) * (up x) for its 64 columns.
+  const uint8_t* packed2;
+  ScalesArg scales2;
 };
+
+// silu(z) * u, the middle of QwenMlp::forward (src/qwennet.rs:816-819,
+// src/tensor_ext.rs:87-90), the expression the elementwise kernels use.
+__device__ __forceinline__ float silu_times(float z, float u) { return (z * (1.0f / (1.0f + __expf(-z)))) * u; }
 
 // 16-byte chunk swizzle of a 128-byte tile row (8 chunks).
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row & 7) ^ ((row >> 3) & 7)); }
@@ -113,12 +124,20 @@ struct BStep {
   uint32_t scale[2];  // f32 bits, or u8 DQ codes (striped DQ: both rows in scale[0])
 };
 
+// The weight a producer thread reads: its codes, scales and the first of its
+// 16 columns.
+struct BSrc {
+  const uint8_t* packed;
+  ScalesArg scales;
+  int n;
+};
+
 template <bool DQ, bool STRIPED>
-__device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int k0, int d) {
-  const int n = n0 + 16 * (d >> 5), k = k0 + 2 * (d & 31);
+__device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, const BSrc& w, int k0, int d) {
+  const int n = w.n, k = k0 + 2 * (d & 31);
   if constexpr (STRIPED) {
     // stripe n / 16 holds 8 bytes per row, rows consecutive
-    const uint8_t* cp = g.packed + ((size_t)(n / 16) * g.K + k) * 8;
+    const uint8_t* cp = w.packed + ((size_t)(n / 16) * g.K + k) * 8;
     const u32x2 r0 = *reinterpret_cast<const u32x2*>(cp);
     const u32x2 r1 = *reinterpret_cast<const u32x2*>(cp + 8);
     B.code[0] = r0.x;
@@ -131,16 +150,16 @@ __device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int 
       // the aligned dword holding both rows' u8 codes (bytes 2 (d % 2), + 1:
       // blk % 4 == k % 4 == 2 (d % 2)); a dword load leaves no zero-extension
       // for the compiler to place away from the decode
-      B.scale[0] = *reinterpret_cast<const uint32_t*>(g.scales.dq_codes + (blk & ~size_t{3}));
+      B.scale[0] = *reinterpret_cast<const uint32_t*>(w.scales.dq_codes + (blk & ~size_t{3}));
       B.scale[1] = 0u;
     } else {
-      const u32x2 s2 = *reinterpret_cast<const u32x2*>(g.scales.absmax + blk);
+      const u32x2 s2 = *reinterpret_cast<const u32x2*>(w.scales.absmax + blk);
       B.scale[0] = s2.x;
       B.scale[1] = s2.y;
     }
   } else {
     const size_t row_bytes = (size_t)g.N / 2, bpr = (size_t)g.N / kBlock;
-    const uint8_t* cp = g.packed + (size_t)k * row_bytes + n / 2;
+    const uint8_t* cp = w.packed + (size_t)k * row_bytes + n / 2;
     const u32x2 r0 = *reinterpret_cast<const u32x2*>(cp);
     const u32x2 r1 = *reinterpret_cast<const u32x2*>(cp + row_bytes);
     B.code[0] = r0.x;
@@ -149,11 +168,11 @@ __device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int 
     B.code[3] = r1.y;
     const size_t blk = (size_t)k * bpr + n / kBlock;
     if constexpr (DQ) {
-      B.scale[0] = g.scales.dq_codes[blk];
-      B.scale[1] = g.scales.dq_codes[blk + bpr];
+      B.scale[0] = w.scales.dq_codes[blk];
+      B.scale[1] = w.scales.dq_codes[blk + bpr];
     } else {
-      B.scale[0] = __float_as_uint(g.scales.absmax[blk]);
-      B.scale[1] = __float_as_uint(g.scales.absmax[blk + bpr]);
+      B.scale[0] = __float_as_uint(w.scales.absmax[blk]);
+      B.scale[1] = __float_as_uint(w.scales.absmax[blk + bpr]);
     }
   }
 }
@@ -164,9 +183,9 @@ __device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, int n0, int 
 // reference's dequantize), rounded to bf16, and the (k, k + 1) pair of a
 // column is one 4-byte LDS store.
 template <bool DQ, bool STRIPED>
-__device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int d) {
+__device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int d, int dq_table) {
   const int st = d >> 5, rp = d & 31;
-  const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq);
+  const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq + dq_table * 1024);
   float s0, s1;
   if constexpr (DQ && STRIPED) {
     const int sh = 16 * (d & 1);
@@ -287,8 +306,9 @@ __device__ __forceinline__ void lds_barrier() {
 // after the producers wrote step s + 2 and the MFMA waves read the last of
 // step s; X needs none (each MFMA wave reads only the rows it copied itself,
 // after waiting for its own copies).
-template <bool DQ, bool YBF16, bool LORA, bool STRIPED>
+template <bool DQ, bool YBF16, bool LORA, bool STRIPED, bool PAIR>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
+  static_assert(!(PAIR && LORA), "the SwiGLU pair has no adapter");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -301,11 +321,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   const int b = blockIdx.x;
   const int tb = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
   const int split = tb % g.k_splits, t = tb / g.k_splits;
-  const int m0 = (t / g.tiles_n) * kBM, n0 = (t % g.tiles_n) * kBN;
+  const int m0 = (t / g.tiles_n) * kBM, n0 = (t % g.tiles_n) * (PAIR ? kBN / 2 : kBN);
   const int row0 = m0 + 64 * w4;
   const int kb = split * g.k_steps;  // this workgroup's first K step
   const int kbase = kb * kBK;        // ... as a column of X / row of W
-  void* const yout = g.k_splits > 1 ? static_cast<void*>(g.partials + (size_t)split * g.M * g.N) : g.y;
+  void* const yout = g.k_splits > 1 ? static_cast<void*>(g.partials + (size_t)split * g.M * g.ldy) : g.y;
 
   if (tid < 256) {
     float* lut = reinterpret_cast<float*>(smem + kLdsLut);
@@ -318,8 +338,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
         lut[c * 512 + 2 * tid + 1] = level(tid >> 4);
       }
     }
-    if constexpr (DQ)
+    if constexpr (DQ) {
       reinterpret_cast<float*>(smem + kLdsDq)[tid] = ((float)tid / 255.0f) * (*g.scales.scale_of_scales);
+      if constexpr (PAIR)
+        reinterpret_cast<float*>(smem + kLdsDq + 1024)[tid] = ((float)tid / 255.0f) * (*g.scales2.scale_of_scales);
+    }
   }
   const int nk = min(g.k_steps, g.K / kBK - kb);  // K steps of this workgroup (>= 1)
 
@@ -328,22 +351,28 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   if (wave >= 4) {
     constexpr int kBRing = 4;
     const int d = tid - 256;
+    // thread d fills W tile columns 16 (d / 32) .. + 15; in PAIR mode the
+    // waves with d < 128 read gate, the others up (each wave one weight)
+    const int st = d >> 5;
+    const bool second = PAIR && st >= 4;
+    const BSrc src{second ? g.packed2 : g.packed, second ? g.scales2 : g.scales, n0 + 16 * (PAIR ? st & 3 : st)};
+    const int dqt = second ? 1 : 0;
     BStep Br[kBRing];
 #pragma unroll
-    for (int r = 0; r < kBRing; ++r) load_b<DQ, STRIPED>(Br[r], g, n0, kbase + min(r, nk - 1) * kBK, d);
+    for (int r = 0; r < kBRing; ++r) load_b<DQ, STRIPED>(Br[r], g, src, kbase + min(r, nk - 1) * kBK, d);
     lds_barrier();  // LUTs visible
-    store_b<DQ, STRIPED>(Br[0], smem, 0, d);
-    load_b<DQ, STRIPED>(Br[0], g, n0, kbase + min(kBRing, nk - 1) * kBK, d);
+    store_b<DQ, STRIPED>(Br[0], smem, 0, d, dqt);
+    load_b<DQ, STRIPED>(Br[0], g, src, kbase + min(kBRing, nk - 1) * kBK, d);
     if (nk > 1) {
-      store_b<DQ, STRIPED>(Br[1], smem, 1, d);
-      load_b<DQ, STRIPED>(Br[1], g, n0, kbase + min(kBRing + 1, nk - 1) * kBK, d);
+      store_b<DQ, STRIPED>(Br[1], smem, 1, d, dqt);
+      load_b<DQ, STRIPED>(Br[1], g, src, kbase + min(kBRing + 1, nk - 1) * kBK, d);
     }
     lds_barrier();  // steps 0 and 1 ready
     // step t2 (from 2 on) into W buffer t2 % 3 from ring slot t2 % kBRing,
     // then the barrier that publishes it
     auto produce = [&](int t2, int slot) {
-      store_b<DQ, STRIPED>(Br[slot], smem, t2 % kBStages, d);
-      load_b<DQ, STRIPED>(Br[slot], g, n0, kbase + min(t2 + kBRing, nk - 1) * kBK, d);
+      store_b<DQ, STRIPED>(Br[slot], smem, t2 % kBStages, d, dqt);
+      load_b<DQ, STRIPED>(Br[slot], g, src, kbase + min(t2 + kBRing, nk - 1) * kBK, d);
       lds_barrier();
     };
     int t2 = 2;
@@ -463,6 +492,52 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
       return (uint32_t)(awave + (r >> 4) * kATileBytes + (r & 15) * 512) +
              (((uint32_t)c * 4u) ^ ((uint32_t)((r >> 2) & 1) << 7));
     };
+    if constexpr (PAIR && YBF16) {
+      // silu(gate x) * (up x): acc[i][j] (gate columns 32 j ..) and
+      // acc[i][j + 2] (up, the same columns) hold their elements in the same
+      // lanes, so the product forms in registers; the 32 x 64 block of each
+      // half i is staged as above, then read back 16 lanes per row (columns
+      // 4 (l % 16) .. + 3 of row 4 q + l / 16) and stored as four bf16
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              *reinterpret_cast<__attribute__((address_space(3))) float*>(
+                  (size_t)stage_off(8 * a4 + 4 * (lane >> 5) + e, 32 * j + (lane & 31))) =
+                  silu_times(acc[i][j][4 * a4 + e], acc[i][j + 2][4 * a4 + e]);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        const int c4 = 4 * (lane & 15);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int r = 4 * q + (lane >> 4);
+          const int m = row0 + 32 * i + r;
+          const f32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>((size_t)stage_off(r, c4));
+          if (m < g.M) {
+            const u32x2 o = {pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+            uint16_t* p = reinterpret_cast<uint16_t*>(yout) + (size_t)m * g.N + n0 + c4;
+            if (g.y_aligned) {
+              *reinterpret_cast<u32x2*>(p) = o;
+            } else {
+              p[0] = (uint16_t)(o.x & 0xffffu);
+              p[1] = (uint16_t)(o.x >> 16);
+              p[2] = (uint16_t)(o.y & 0xffffu);
+              p[3] = (uint16_t)(o.y >> 16);
+            }
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();  // the next half reuses the chunks
+      }
+      return;
+    }
+    // columns of this lane's four outputs: PAIR split-K partials put the
+    // gate columns at n0 .. and the up columns at N + n0 .. of a 2 N row
+    const int col = PAIR && cq >= 64 ? g.N + n0 + cq - 64 : n0 + cq;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -481,7 +556,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
         const int m = row0 + 32 * i + r;
         const f32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>((size_t)stage_off(r, cq));
         if (m < g.M) {
-          const size_t idx = (size_t)m * g.N + n0 + cq;
+          const size_t idx = (size_t)m * g.ldy + col;
           const float y0 = v.x + bias4[0], y1 = v.y + bias4[1], y2 = v.z + bias4[2], y3 = v.w + bias4[3];
           if constexpr (YBF16) {
             const u32x2 o = {pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
@@ -513,21 +588,21 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   }
 }
 
-template <bool DQ, bool YBF16, bool LORA, bool STRIPED>
+template <bool DQ, bool YBF16, bool LORA, bool STRIPED, bool PAIR = false>
 hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   const uint64_t bit = 1ull << (dev & 63);
-  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<DQ, YBF16, LORA, STRIPED>);
+  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR>);
   if (!(done.load(std::memory_order_acquire) & bit)) {
     e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmSmem);
     if (e != hipSuccess) return e;
     done.fetch_or(bit, std::memory_order_acq_rel);
   }
   const int grid = ((g.M + kBM - 1) / kBM) * g.tiles_n * g.k_splits;
-  gemm_kernel<DQ, YBF16, LORA, STRIPED><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
+  gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
   return hipGetLastError();
 }
 
@@ -668,22 +743,48 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+// The SwiGLU pair's reduction: gate and up each summed over the splits in
+// split order from partials[s][m][2 N] (gate columns, then up), then
+// h[m][n] = bf16(silu(gate) * up), four outputs per thread.
+__global__ __launch_bounds__(256) void splitk_silu_reduce_kernel(const float* __restrict__ partials, int splits,
+                                                                 size_t split_stride, uint32_t n4_row, size_t mn4,
+                                                                 uint16_t* __restrict__ h) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn4; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t m = i / n4_row, c4 = i - m * n4_row;
+    const float* gp = partials + m * 8 * n4_row + c4 * 4;  // row m: 2 N floats
+    f32x4 gv = *reinterpret_cast<const f32x4*>(gp);
+    f32x4 uv = *reinterpret_cast<const f32x4*>(gp + 4 * n4_row);
+    for (int q = 1; q < splits; ++q) {
+      const f32x4 g2 = *reinterpret_cast<const f32x4*>(gp + q * split_stride);
+      const f32x4 u2 = *reinterpret_cast<const f32x4*>(gp + q * split_stride + 4 * n4_row);
+      gv = f32x4{gv.x + g2.x, gv.y + g2.y, gv.z + g2.z, gv.w + g2.w};
+      uv = f32x4{uv.x + u2.x, uv.y + u2.y, uv.z + u2.z, uv.w + u2.w};
+    }
+    reinterpret_cast<u32x2*>(h)[i] = u32x2{pack_bf16x2(silu_times(gv.x, uv.x), silu_times(gv.y, uv.y)),
+                                          pack_bf16x2(silu_times(gv.z, uv.z), silu_times(gv.w, uv.w))};
+  }
+}
+
 }  // namespace
 
-int gemm_k_splits(int M, int K, int N) {
-  // grids of fewer than ~200 tiles leave CUs idle (one 147 KiB workgroup per
+int gemm_k_splits(int M, int K, int N, bool pair) {
+  // grids of fewer than ~200 tiles leave CUs idle (one 148 KiB workgroup per
   // CU): split d_in so the grid reaches ~256 workgroups, each over at least
-  // 16 K steps
-  const long tiles = (long)((M + kBM - 1) / kBM) * (N / kBN);
+  // 16 K steps.  A grid of more than one round stays whole: with every CU
+  // busy the part runs at its power limit, and splitting the 344 tiles of
+  // the 7B-shaped gate/up pair at 512 rows two ways measured 134 us plus a
+  // 16 us reduction against 137 us whole.
+  const long tiles = (long)((M + kBM - 1) / kBM) * (pair ? N / (kBN / 2) : N / kBN);
   const int steps = K / kBK;
   int splits = 1;
   while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= 16) splits *= 2;
   return splits;
 }
 
-hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
-                       const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
-                       bool y_bf16, bool striped, hipStream_t stream, int k_splits, float* partials) {
+namespace {
+
+GemmArgs gemm_args(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N, void* y,
+                   bool y_bf16, int k_splits, float* partials) {
   GemmArgs g{};
   g.x = x;
   g.packed = packed;
@@ -691,22 +792,39 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
   g.M = M;
   g.K = K;
   g.N = N;
+  g.y = y;
+  g.y_bf16 = y_bf16;
+  g.y_aligned = (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+  g.tiles_n = N / kBN;
+  g.ldy = N;
+  const int steps = K / kBK;
+  g.k_splits = k_splits;
+  g.k_steps = (steps + k_splits - 1) / k_splits;
+  g.partials = partials;
+  return g;
+}
+
+// every split of k_splits has a K step
+bool splits_ok(int K, int k_splits) {
+  const int steps = K / kBK;
+  return k_splits >= 1 && (k_splits == 1 || ((steps + k_splits - 1) / k_splits) * (k_splits - 1) < steps);
+}
+
+unsigned reduce_blocks(size_t n4) { return (unsigned)std::min<size_t>((n4 + 255) / 256, 4096); }
+
+}  // namespace
+
+hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
+                       const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
+                       bool y_bf16, bool striped, hipStream_t stream, int k_splits, float* partials) {
+  if (!splits_ok(K, k_splits) || (k_splits > 1 && (!partials || lora_xa || (reinterpret_cast<uintptr_t>(y) & 15u) != 0)))
+    return hipErrorInvalidValue;
+  GemmArgs g = gemm_args(x, packed, scales, M, K, N, y, y_bf16, k_splits, partials);
   g.bias = bias;
   g.lora_xa = lora_xa;
   g.lora_bt = lora_bt;
   g.lora_rank = lora_rank;
   g.lora_pad = lora_pad(lora_rank);
-  g.y = y;
-  g.y_bf16 = y_bf16;
-  g.y_aligned = (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
-  g.tiles_n = N / kBN;
-  const int steps = K / kBK;
-  if (k_splits < 1 || (k_splits > 1 && (!partials || lora_xa || (reinterpret_cast<uintptr_t>(y) & 15u) != 0)))
-    return hipErrorInvalidValue;
-  g.k_splits = k_splits;
-  g.k_steps = (steps + k_splits - 1) / k_splits;
-  if (k_splits > 1 && g.k_steps * (k_splits - 1) >= steps) return hipErrorInvalidValue;  // every split has a step
-  g.partials = partials;
   if (k_splits > 1) {
     // raw f32 sums into the partials, then the ordered reduction
     g.bias = nullptr;
@@ -717,8 +835,7 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
                        : (striped ? launch_g<false, false, false, true>(g, stream) : launch_g<false, false, false, false>(g, stream));
     if (e != hipSuccess) return e;
     const size_t mn4 = (size_t)M * N / 4;
-    const unsigned blocks = (unsigned)std::min<size_t>((mn4 + 255) / 256, 4096);
-    splitk_reduce_kernel<<<blocks, 256, 0, stream>>>(partials, k_splits, mn4, N / 4, bias, y, y_bf16);
+    splitk_reduce_kernel<<<reduce_blocks(mn4), 256, 0, stream>>>(partials, k_splits, mn4, N / 4, bias, y, y_bf16);
     return hipGetLastError();
   }
   const bool dq = scales.kind == kScalesDQ;
@@ -736,6 +853,35 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
   UNIFUR_GEMM_CASE(false, false, false)
 #undef UNIFUR_GEMM_CASE
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_pair(const uint16_t* x, const uint8_t* gate_packed, const ScalesArg& gate_scales,
+                            const uint8_t* up_packed, const ScalesArg& up_scales, int M, int K, int N, uint16_t* h,
+                            bool striped, hipStream_t stream, int k_splits, float* partials) {
+  if (gate_scales.kind != up_scales.kind || N % 64 != 0 || !splits_ok(K, k_splits) ||
+      (k_splits > 1 && !partials))
+    return hipErrorInvalidValue;
+  GemmArgs g = gemm_args(x, gate_packed, gate_scales, M, K, N, h, true, k_splits, partials);
+  g.packed2 = up_packed;
+  g.scales2 = up_scales;
+  g.tiles_n = N / (kBN / 2);
+  const bool dq = gate_scales.kind == kScalesDQ;
+  if (k_splits == 1) {
+    return dq ? (striped ? launch_g<true, true, false, true, true>(g, stream) : launch_g<true, true, false, false, true>(g, stream))
+              : (striped ? launch_g<false, true, false, true, true>(g, stream) : launch_g<false, true, false, false, true>(g, stream));
+  }
+  // raw gate and up sums into partials[s][M][2 N], then the ordered
+  // reduction with silu(gate) * up
+  g.y_bf16 = 0;
+  g.y_aligned = 1;
+  g.ldy = 2 * N;
+  hipError_t e = dq ? (striped ? launch_g<true, false, false, true, true>(g, stream) : launch_g<true, false, false, false, true>(g, stream))
+                    : (striped ? launch_g<false, false, false, true, true>(g, stream) : launch_g<false, false, false, false, true>(g, stream));
+  if (e != hipSuccess) return e;
+  const size_t mn4 = (size_t)M * N / 4;
+  splitk_silu_reduce_kernel<<<reduce_blocks(mn4), 256, 0, stream>>>(partials, k_splits, (size_t)M * 2 * N,
+                                                                     (uint32_t)(N / 4), mn4, h);
+  return hipGetLastError();
 }
 
 }  // namespace unifur

@@ -31,7 +31,19 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
                        const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
                        bool y_bf16, bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr);
 
-// d_in slabs the fused GEMM splits into for this shape (1: no split).
-int gemm_k_splits(int M, int K, int N);
+// SwiGLU gate/up pair: h[M, N] = bf16(silu(X deq(gate)) * (X deq(up))),
+// both weights [K, N] of one layout and scale kind, N a multiple of 64, h
+// 8-byte aligned for its fast stores.  One launch: a workgroup computes 64
+// columns of both weights over 256 rows and forms the product in
+// registers.  With k_splits > 1 the workgroups of a tile split d_in and
+// write raw f32 sums to partials (k_splits * M * 2 N floats), which a second
+// launch adds in split order before the product.
+hipError_t launch_gemm_pair(const uint16_t* x, const uint8_t* gate_packed, const ScalesArg& gate_scales,
+                            const uint8_t* up_packed, const ScalesArg& up_scales, int M, int K, int N, uint16_t* h,
+                            bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr);
+
+// d_in slabs the fused GEMM splits into for this shape (1: no split); pair:
+// the gate/up pair launch over two [K, N] weights.
+int gemm_k_splits(int M, int K, int N, bool pair = false);
 
 }  // namespace unifur
