@@ -395,7 +395,8 @@ def bench_swiglu(torch, Q, L, tokens) -> dict:
     # then down with its 64 output tiles splitting d_in four ways (split-K).
     # The least workspace the library reports (sized for gate and up of
     # different scale kinds) holds this same plan.
-    out["T512"]["path"] = "fused MFMA kernels: gate/up pair launch + down, split-K (default workspace)"
+    if "T512" in out:
+        out["T512"]["path"] = "fused MFMA kernels: gate/up pair launch + down, split-K (default workspace)"
     out["rotation"] = f"{copies} blocks of {wbytes} B rotated (cold HBM)"
     return out
 

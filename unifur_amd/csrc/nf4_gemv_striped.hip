@@ -97,12 +97,12 @@ struct WaveW {
   __amdgpu_buffer_rsrc_t codes, scales;
 };
 
-template <int T, int NW, bool XBF16, bool DQ>
+template <int T, int NW, bool XBF16, bool DQ, bool NORM>
 __device__ __forceinline__ void issue_chunk(Chunk<T, NW, XBF16, DQ>& c, const WaveW (&ww)[NW],
                                             const __amdgpu_buffer_rsrc_t (&xr)[T], __amdgpu_buffer_rsrc_t gr,
                                             int chunk, int lane) {
   const uint32_t row = (uint32_t)(chunk * 64 + lane);
-  c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);  // 0 without a norm
+  if constexpr (NORM) c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);  // 0 without a norm
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     c.w[w].code = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
@@ -223,7 +223,7 @@ __device__ __forceinline__ void store_y(const GemvWeight& W, size_t idx, float y
     reinterpret_cast<float*>(W.y)[idx] = y;
 }
 
-template <int T, int W, int D, bool XBF16, bool DQ, bool PAIR>
+template <int T, int W, int D, bool XBF16, bool DQ, bool PAIR, bool NORM>
 __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   constexpr int NW = PAIR ? 2 : 1;
   static_assert(D % 2 == 0, "the lookup double buffer is indexed by chunk parity");
@@ -268,11 +268,15 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   }
   // folded QwenRmsNorm (src/qwennet.rs:104-109): the products take
   // x * (w + 1), each lane sums x^2 over its rows, and the column sums are
-  // scaled by the row's 1 / sqrt(mean(x^2) + eps) at the end.  Without a norm
-  // the weight buffer has no records: its loads read 0, so x is multiplied
-  // by exactly 1 -- the loop has no branch on the norm (a branch there made
-  // the compiler keep two versions of the loop and double the registers).
-  const bool norm = a.norm_w != nullptr;
+  // scaled by the row's 1 / sqrt(mean(x^2) + eps) at the end.  NORM kernels
+  // do this work in every chunk; one launched without a norm gets a weight
+  // buffer with no records, whose loads read 0, so x is multiplied by exactly
+  // 1 -- the loop has no branch on the norm (a branch there made the
+  // compiler keep two versions of the loop and double the registers).  The
+  // single-weight kernels come in both forms (the norm weight's load is a
+  // quarter of a chunk's loads: config 2 9.0 -> 8.5 us without it); the
+  // SwiGLU pair keeps one, which measured faster with the loads than without.
+  const bool norm = NORM && a.norm_w != nullptr;
   const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : a.x, norm ? (uint32_t)nrows * 4u : 0u);
 
   // The prologue issues the first D chunks, in chunk order like the steady
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   Chunk<T, NW, XBF16, DQ> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
-    issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, j, lane);
+    issue_chunk<T, NW, XBF16, DQ, NORM>(ring[j], ww, xr, gr, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
   float sos[NW];
@@ -330,12 +334,14 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         float xv = XBF16 ? bf16_bits_to_f32((uint32_t)ring[j].x[t]) : as_f((uint32_t)ring[j].x[t]);
-        xsq[t] = __builtin_fmaf(xv, xv, xsq[t]);
-        xv = xv * (as_f(ring[j].g) + 1.0f);
+        if constexpr (NORM) {
+          xsq[t] = __builtin_fmaf(xv, xv, xsq[t]);
+          xv = xv * (as_f(ring[j].g) + 1.0f);
+        }
 #pragma unroll
         for (int w = 0; w < NW; ++w) xs[w][t] = xv * lk[j & 1].scale[w];  // x * block scale, once per row
       }
-      issue_chunk<T, NW, XBF16, DQ>(ring[j], ww, xr, gr, c0 + j + D, lane);
+      issue_chunk<T, NW, XBF16, DQ, NORM>(ring[j], ww, xr, gr, c0 + j + D, lane);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
@@ -409,9 +415,9 @@ constexpr int kDepth = UNIFUR_GEMV_DEPTH;
 template <bool PAIR>
 constexpr int NWof() { return PAIR ? 2 : 1; }
 
-template <int T, int W, bool XBF16, bool DQ, bool PAIR>
+template <int T, int W, bool XBF16, bool DQ, bool PAIR, bool NORM>
 hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
-  auto* fn = &gemv_striped_kernel<T, W, kDepth, XBF16, DQ, PAIR>;
+  auto* fn = &gemv_striped_kernel<T, W, kDepth, XBF16, DQ, PAIR, NORM>;
   static std::atomic<uint64_t> done{0};  // dynamic LDS above 64 KiB: once per device
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -428,10 +434,18 @@ hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int T, int W, bool PAIR, bool NORM>
+hipError_t launch_norm(const StripedArgs& a, int grid, bool xbf16, bool dq, hipStream_t stream) {
+  if (xbf16)
+    return dq ? launch_t<T, W, true, true, PAIR, NORM>(a, grid, stream) : launch_t<T, W, true, false, PAIR, NORM>(a, grid, stream);
+  return dq ? launch_t<T, W, false, true, PAIR, NORM>(a, grid, stream) : launch_t<T, W, false, false, PAIR, NORM>(a, grid, stream);
+}
+
+// the SwiGLU pair always takes the NORM kernel (norm or not, see above)
 template <int T, int W, bool PAIR>
 hipError_t launch_flags(const StripedArgs& a, int grid, bool xbf16, bool dq, hipStream_t stream) {
-  if (xbf16) return dq ? launch_t<T, W, true, true, PAIR>(a, grid, stream) : launch_t<T, W, true, false, PAIR>(a, grid, stream);
-  return dq ? launch_t<T, W, false, true, PAIR>(a, grid, stream) : launch_t<T, W, false, false, PAIR>(a, grid, stream);
+  if (PAIR || a.norm_w) return launch_norm<T, W, PAIR, true>(a, grid, xbf16, dq, stream);
+  return launch_norm<T, W, PAIR, false>(a, grid, xbf16, dq, stream);
 }
 
 // 16 waves only where the registers fit at four waves per SIMD: one or two
