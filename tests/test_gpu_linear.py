@@ -100,6 +100,30 @@ def test_gemv_rows_and_shapes(device, oracle, rows, shape, striped):
     check(lin.forward(xt), oracle.linear_ref_f64(x, wdeq), x, wdeq, TOL_F32, f"gemv rows={rows} {shape}")
 
 
+@pytest.mark.parametrize("rows", [1, 2, 3, 4])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_striped_gemv_one_row_per_lane(device, oracle, rows, dt):
+    # The striped GEMV takes two rows per lane (paired loads) when d_in is
+    # even and x is aligned for the pairs; an odd d_in, or x one element off
+    # that alignment, takes one row per lane.  Both against the oracle.
+    tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+    lin, wdeq = make_linear(oracle, 1001, 192, 0x1001, device, striped=True)
+    x, xt = acts(oracle, rows, 1001, 0x1002 + rows, dt, device)
+    check(lin.forward(xt, out_dtype=torch.float32), oracle.linear_ref_f64(x, wdeq), x, wdeq, tol,
+          f"odd d_in rows={rows} {dt}")
+    lin, wdeq = make_linear(oracle, 1024, 192, 0x1003, device, striped=True)
+    x, xt = acts(oracle, rows, 1024, 0x1004 + rows, dt, device)
+    buf = torch.empty(rows * 1024 + 1, dtype=dt, device=device)
+    xs = buf[1:].view(rows, 1024)
+    xs.copy_(xt)
+    assert xs.data_ptr() % (8 if dt == torch.float32 else 4) != 0
+    ref = oracle.linear_ref_f64(x, wdeq)
+    y = lin.forward(xs, out_dtype=torch.float32)
+    check(y, ref, x, wdeq, tol, f"x off alignment rows={rows} {dt}")
+    y2 = lin.forward(xt, out_dtype=torch.float32)  # aligned: two rows per lane
+    check(y2, ref, x, wdeq, tol, f"aligned rows={rows} {dt}")
+
+
 @pytest.mark.parametrize("striped", [True, False])
 def test_gemv_bias_and_qlora(device, oracle, striped):
     d_in, d_out, r = 4096, 4096, 16

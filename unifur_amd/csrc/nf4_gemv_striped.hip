@@ -9,9 +9,11 @@
 //
 // One workgroup owns one stripe over all of K, so there is no cross-workgroup
 // reduction: its W waves take consecutive row ranges, and inside a wave lane
-// l takes row 64 c + l of every 64-row chunk c -- a wave's load of a chunk is
-// 512 contiguous bytes of codes, 64 contiguous scale codes and 64 contiguous
-// activations per x row.  Each wave keeps D chunks in flight in a register
+// l takes rows RPL (64 c + l) .. + RPL - 1 of every 64 RPL-row chunk c (RPL =
+// 2 for the single-weight and shared-input launches, 1 for the SwiGLU pair)
+// -- a wave's load of a chunk is 512 RPL contiguous bytes of codes, 64 RPL
+// contiguous scale codes and 64 RPL contiguous activations per x row.  Each
+// wave keeps D chunks in flight in a register
 // ring: chunk c + D is requested as soon as chunk c has been consumed, so the
 // memory stream and the decode overlap.  (Requesting everything up front
 // stalls the issue of the later loads behind the memory system, and the
@@ -74,22 +76,50 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// One chunk of one weight in flight: this lane's 8 code bytes and its scale.
+// One chunk of one weight in flight: this lane's code bytes (8 per row) and
+// row scales, for RPL consecutive rows per lane (a chunk is 64 RPL rows).
 // Narrow loads are kept in narrow fields: the ring is carried around the
 // chunk loop, and a widening of a loaded byte placed at the loop head would
 // wait there for the newest loads instead of the ones the step consumes.
-template <bool DQ>
+template <bool DQ, int RPL>
 struct ChunkW {
-  u32x2 code;
-  std::conditional_t<DQ, uint8_t, uint32_t> scale;  // the u8 DQ scale code, or f32 absmax bits
+  std::conditional_t<RPL == 1, u32x2, u32x4> code;
+  // u8 DQ scale codes (RPL of them), or f32 absmax bits
+  std::conditional_t<DQ, std::conditional_t<RPL == 1, uint8_t, uint16_t>, std::conditional_t<RPL == 1, uint32_t, u32x2>>
+      scale;
 };
 
-template <int T, int NW, bool XBF16, bool DQ>
+template <int T, int NW, bool XBF16, bool DQ, int RPL>
 struct Chunk {
-  ChunkW<DQ> w[NW];
-  std::conditional_t<XBF16, uint16_t, uint32_t> x[T];  // bf16 or f32 bits
-  uint32_t g;  // with a folded norm: the norm weight of this row (f32 bits)
+  ChunkW<DQ, RPL> w[NW];
+  // x of the RPL rows: bf16 or f32 bits
+  std::conditional_t<XBF16, std::conditional_t<RPL == 1, uint16_t, uint32_t>, std::conditional_t<RPL == 1, uint32_t, u32x2>>
+      x[T];
+  std::conditional_t<RPL == 1, uint32_t, u32x2> g;  // with a folded norm: the rows' norm weights (f32 bits)
 };
+
+// Field accessors by row r < RPL of the lane.
+template <bool DQ, int RPL>
+__device__ __forceinline__ uint32_t code_dword(const ChunkW<DQ, RPL>& c, int r, int d) {
+  return c.code[2 * r + d];
+}
+template <bool DQ, int RPL>
+__device__ __forceinline__ uint32_t scale_bits(const ChunkW<DQ, RPL>& c, int r) {
+  if constexpr (RPL == 1) return (uint32_t)c.scale;
+  else if constexpr (DQ) return ((uint32_t)c.scale >> (8 * r)) & 0xffu;
+  else return c.scale[r];
+}
+template <bool XBF16, typename X>
+__device__ __forceinline__ float x_value(const X& v, int r) {
+  if constexpr (std::is_same_v<X, uint16_t>) return bf16_bits_to_f32((uint32_t)v);
+  else if constexpr (std::is_same_v<X, uint32_t>) return XBF16 ? bf16_bits_to_f32((v >> (16 * r)) & 0xffffu) : __uint_as_float(v);
+  else return __uint_as_float(v[r]);
+}
+template <typename G>
+__device__ __forceinline__ float g_value(const G& v, int r) {
+  if constexpr (std::is_same_v<G, uint32_t>) return __uint_as_float(v);
+  else return __uint_as_float(v[r]);
+}
 
 // Wave-uniform resources of one weight, bounded to this wave's rows so that
 // every load past them reads zero (and touches no memory).
@@ -97,38 +127,52 @@ struct WaveW {
   __amdgpu_buffer_rsrc_t codes, scales;
 };
 
-template <int T, int NW, bool XBF16, bool DQ, bool NORM>
-__device__ __forceinline__ void issue_chunk(Chunk<T, NW, XBF16, DQ>& c, const WaveW (&ww)[NW],
+template <int T, int NW, bool XBF16, bool DQ, bool NORM, int RPL>
+__device__ __forceinline__ void issue_chunk(Chunk<T, NW, XBF16, DQ, RPL>& c, const WaveW (&ww)[NW],
                                             const __amdgpu_buffer_rsrc_t (&xr)[T], __amdgpu_buffer_rsrc_t gr,
                                             int chunk, int lane) {
-  const uint32_t row = (uint32_t)(chunk * 64 + lane);
-  if constexpr (NORM) c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);  // 0 without a norm
+  const uint32_t row = (uint32_t)((chunk * 64 + lane) * RPL);  // the lane's first row
+  if constexpr (NORM) {  // 0 without a norm
+    if constexpr (RPL == 1) c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);
+    else c.g = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(gr, row * 4u, 0, 0));
+  }
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    c.w[w].code = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
-    if constexpr (DQ)
-      c.w[w].scale = __builtin_amdgcn_raw_buffer_load_b8(ww[w].scales, row, 0, 0);
+    if constexpr (RPL == 1)
+      c.w[w].code = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].codes, row * 8u, 0, 0));
     else
+      c.w[w].code = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ww[w].codes, row * 8u, 0, 0));
+    if constexpr (DQ && RPL == 1)
+      c.w[w].scale = __builtin_amdgcn_raw_buffer_load_b8(ww[w].scales, row, 0, 0);
+    else if constexpr (DQ)
+      c.w[w].scale = __builtin_amdgcn_raw_buffer_load_b16(ww[w].scales, row, 0, 0);
+    else if constexpr (RPL == 1)
       c.w[w].scale = __builtin_amdgcn_raw_buffer_load_b32(ww[w].scales, row * 4u, 0, 0);
+    else
+      c.w[w].scale = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ww[w].scales, row * 4u, 0, 0));
   }
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    if constexpr (XBF16)
+    if constexpr (XBF16 && RPL == 1)
       c.x[t] = __builtin_amdgcn_raw_buffer_load_b16(xr[t], row * 2u, 0, 0);
-    else
+    else if constexpr (XBF16)
+      c.x[t] = __builtin_amdgcn_raw_buffer_load_b32(xr[t], row * 2u, 0, 0);
+    else if constexpr (RPL == 1)
       c.x[t] = __builtin_amdgcn_raw_buffer_load_b32(xr[t], row * 4u, 0, 0);
+    else
+      c.x[t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(xr[t], row * 4u, 0, 0));
   }
 }
 
-// Level pairs of this lane's 8 code bytes and the block scale, per weight.
-template <int NW>
+// Level pairs of this lane's code bytes and its row scales, per weight.
+template <int NW, int RPL>
 struct Looked {
-  f32x2 lv[NW][8];
-  float scale[NW];
+  f32x2 lv[NW][8 * RPL];
+  float scale[NW][RPL];
 };
 
-template <int T, int NW, bool XBF16, bool DQ>
-__device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW, XBF16, DQ>& c, const float* dq_lut,
+template <int T, int NW, bool XBF16, bool DQ, int RPL>
+__device__ __forceinline__ void lookup(Looked<NW, RPL>& o, const Chunk<T, NW, XBF16, DQ, RPL>& c, const float* dq_lut,
                                        const float (&sos)[NW], uint32_t lane_off) {
   // lane_off is (copy * 8) << (8 - log2(kLutCopies * 8 / 32)): the v_perm
   // puts the code byte in bits 8-15, and a shift brings the entry stride down
@@ -136,18 +180,23 @@ __device__ __forceinline__ void lookup(Looked<NW>& o, const Chunk<T, NW, XBF16, 
   constexpr int kShift = kLutCopies == 32 ? 0 : (kLutCopies == 16 ? 1 : 2);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    // DQ: ((float)q / 255.0f) * scale_of_scales (src/quantize.rs:349), the
-    // quotient from the table and the product here (the same two roundings)
-    o.scale[w] = DQ ? dq_lut[(uint32_t)c.w[w].scale] * sos[w] : as_f((uint32_t)c.w[w].scale);
 #pragma unroll
-    for (int d = 0; d < 2; ++d)
+    for (int r = 0; r < RPL; ++r) {
+      // DQ: ((float)q / 255.0f) * scale_of_scales (src/quantize.rs:349), the
+      // quotient from the table and the product here (the same two roundings)
+      const uint32_t sb = scale_bits<DQ, RPL>(c.w[w], r);
+      o.scale[w][r] = DQ ? dq_lut[sb] * sos[w] : as_f(sb);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        // LDS byte address = (byte b of the dword) << 8 | lane_off; the LUT
-        // sits at LDS address 0 (this kernel has no static LDS)
-        const uint32_t addr = perm_b32(c.w[w].code[d], lane_off, 0x0c0c0000u | ((4u + b) << 8)) >> kShift;
-        o.lv[w][d * 4 + b] = *reinterpret_cast<lds_f32x2*>((size_t)addr);
-      }
+      for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          // LDS byte address = (byte b of the dword) << 8 | lane_off; the LUT
+          // sits at LDS address 0 (this kernel has no static LDS)
+          const uint32_t addr =
+              perm_b32(code_dword<DQ, RPL>(c.w[w], r, d), lane_off, 0x0c0c0000u | ((4u + b) << 8)) >> kShift;
+          o.lv[w][r * 8 + d * 4 + b] = *reinterpret_cast<lds_f32x2*>((size_t)addr);
+        }
+    }
   }
 }
 
@@ -223,9 +272,10 @@ __device__ __forceinline__ void store_y(const GemvWeight& W, size_t idx, float y
     reinterpret_cast<float*>(W.y)[idx] = y;
 }
 
-template <int T, int W, int D, bool XBF16, bool DQ, bool PAIR, bool NORM>
+template <int T, int W, int D, bool XBF16, bool DQ, bool PAIR, bool NORM, int RPL>
 __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   constexpr int NW = PAIR ? 2 : 1;
+  static_assert(RPL == 1 || RPL == 2, "one or two rows per lane and chunk");
   static_assert(D % 2 == 0, "the lookup double buffer is indexed by chunk parity");
   static_assert(W >= 4, "the LUT build needs 256 threads");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -248,7 +298,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   const int K = a.d_in;
   const int kw = wave * a.rows_per_wave;
   const int nrows = max(0, min(a.rows_per_wave, K - kw));
-  const int nchunks = (nrows + 63) / 64;
+  const int nchunks = (nrows + 64 * RPL - 1) / (64 * RPL);
 
   WaveW ww[NW];
 #pragma unroll
@@ -286,10 +336,10 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   // 8.85 -> 8.65 us per launch).  The DQ table holds q / 255 and the scale
   // of scales (read through the scalar cache) is applied per row, so the
   // table does not wait for that load.
-  Chunk<T, NW, XBF16, DQ> ring[D];
+  Chunk<T, NW, XBF16, DQ, RPL> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
-    issue_chunk<T, NW, XBF16, DQ, NORM>(ring[j], ww, xr, gr, j, lane);
+    issue_chunk<T, NW, XBF16, DQ, NORM, RPL>(ring[j], ww, xr, gr, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
   float sos[NW];
@@ -320,8 +370,8 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #pragma unroll
   for (int t = 0; t < T; ++t) xsq[t] = 0.0f;
 
-  Looked<NW> lk[2];
-  lookup<T, NW, XBF16, DQ>(lk[0], ring[0], dq_lut, sos, lane_off);
+  Looked<NW, RPL> lk[2];
+  lookup<T, NW, XBF16, DQ, RPL>(lk[0], ring[0], dq_lut, sos, lane_off);
   for (int c0 = 0; c0 < nchunks; c0 += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
@@ -329,29 +379,33 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
       // chunk c0 + j + 1 is in ring[(j + 1) % D] (refilled at step 0 when
       // j + 1 == D).  Chunks past this wave's rows read as zero: x = 0.
       __builtin_amdgcn_sched_barrier(0);
-      lookup<T, NW, XBF16, DQ>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, sos, lane_off);
-      float xs[NW][T];
+      lookup<T, NW, XBF16, DQ, RPL>(lk[(j + 1) & 1], ring[(j + 1) % D], dq_lut, sos, lane_off);
+      float xs[NW][T][RPL];
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        float xv = XBF16 ? bf16_bits_to_f32((uint32_t)ring[j].x[t]) : as_f((uint32_t)ring[j].x[t]);
-        if constexpr (NORM) {
-          xsq[t] = __builtin_fmaf(xv, xv, xsq[t]);
-          xv = xv * (as_f(ring[j].g) + 1.0f);
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) {
+          float xv = x_value<XBF16>(ring[j].x[t], r);
+          if constexpr (NORM) {
+            xsq[t] = __builtin_fmaf(xv, xv, xsq[t]);
+            xv = xv * (g_value(ring[j].g, r) + 1.0f);
+          }
+#pragma unroll
+          for (int w = 0; w < NW; ++w) xs[w][t][r] = xv * lk[j & 1].scale[w][r];  // x * block scale, once per row
         }
-#pragma unroll
-        for (int w = 0; w < NW; ++w) xs[w][t] = xv * lk[j & 1].scale[w];  // x * block scale, once per row
-      }
-      issue_chunk<T, NW, XBF16, DQ, NORM>(ring[j], ww, xr, gr, c0 + j + D, lane);
+      issue_chunk<T, NW, XBF16, DQ, NORM, RPL>(ring[j], ww, xr, gr, c0 + j + D, lane);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int w = 0; w < NW; ++w)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int r = 0; r < RPL; ++r)
 #pragma unroll
-          for (int t = 0; t < T; ++t) {
-            acc[w][t][2 * i] = __builtin_fmaf(xs[w][t], lk[j & 1].lv[w][i].x, acc[w][t][2 * i]);
-            acc[w][t][2 * i + 1] = __builtin_fmaf(xs[w][t], lk[j & 1].lv[w][i].y, acc[w][t][2 * i + 1]);
-          }
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              acc[w][t][2 * i] = __builtin_fmaf(xs[w][t][r], lk[j & 1].lv[w][r * 8 + i].x, acc[w][t][2 * i]);
+              acc[w][t][2 * i + 1] = __builtin_fmaf(xs[w][t][r], lk[j & 1].lv[w][r * 8 + i].y, acc[w][t][2 * i + 1]);
+            }
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -411,13 +465,25 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #define UNIFUR_GEMV_DEPTH 4
 #endif
 constexpr int kDepth = UNIFUR_GEMV_DEPTH;
+// rows per lane of the single-weight and shared-input kernels, and their
+// ring depth: two rows per lane (one 16-byte code load, paired scale and x
+// loads: half the load instructions) with two chunks in flight -- the same
+// bytes in flight as four one-row chunks -- measured config 2 8.59 -> 8.33
+// us; four two-row chunks in flight 9.05 us
+#ifndef UNIFUR_GEMV_RPL
+#define UNIFUR_GEMV_RPL 2
+#endif
+#ifndef UNIFUR_GEMV_DEPTH2
+#define UNIFUR_GEMV_DEPTH2 2
+#endif
+constexpr int kRpl = UNIFUR_GEMV_RPL;
 
 template <bool PAIR>
 constexpr int NWof() { return PAIR ? 2 : 1; }
 
-template <int T, int W, bool XBF16, bool DQ, bool PAIR, bool NORM>
+template <int T, int W, bool XBF16, bool DQ, bool PAIR, bool NORM, int RPL = 1>
 hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
-  auto* fn = &gemv_striped_kernel<T, W, kDepth, XBF16, DQ, PAIR, NORM>;
+  auto* fn = &gemv_striped_kernel<T, W, RPL == 1 ? kDepth : UNIFUR_GEMV_DEPTH2, XBF16, DQ, PAIR, NORM, RPL>;
   static std::atomic<uint64_t> done{0};  // dynamic LDS above 64 KiB: once per device
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -436,6 +502,19 @@ hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
 
 template <int T, int W, bool PAIR, bool NORM>
 hipError_t launch_norm(const StripedArgs& a, int grid, bool xbf16, bool dq, hipStream_t stream) {
+  if constexpr (kRpl == 2 && !PAIR) {
+    // two rows per lane: even d_in (a lane's rows are both in or both past
+    // its wave's rows), x and the norm weight aligned for the paired loads
+    const size_t xa = xbf16 ? 4 : 8;
+    if (a.d_in % 2 == 0 && reinterpret_cast<uintptr_t>(a.x) % xa == 0 &&
+        reinterpret_cast<uintptr_t>(a.norm_w) % 8 == 0) {
+      if (xbf16)
+        return dq ? launch_t<T, W, true, true, PAIR, NORM, 2>(a, grid, stream)
+                  : launch_t<T, W, true, false, PAIR, NORM, 2>(a, grid, stream);
+      return dq ? launch_t<T, W, false, true, PAIR, NORM, 2>(a, grid, stream)
+                : launch_t<T, W, false, false, PAIR, NORM, 2>(a, grid, stream);
+    }
+  }
   if (xbf16)
     return dq ? launch_t<T, W, true, true, PAIR, NORM>(a, grid, stream) : launch_t<T, W, true, false, PAIR, NORM>(a, grid, stream);
   return dq ? launch_t<T, W, false, true, PAIR, NORM>(a, grid, stream) : launch_t<T, W, false, false, PAIR, NORM>(a, grid, stream);
