@@ -114,8 +114,60 @@ def graph_ms(torch, graph, reps: int) -> float:
     return (time.perf_counter() - t0) * 1e3 / reps
 
 
-def rand_weights(torch, Q, d_in, d_out, gen, dq=True, striped=True):
-    w = torch.randn(d_in * d_out, device="cuda", generator=gen) * 0.02
+def _i64(v: int) -> int:
+    return v - (1 << 64) if v >= 1 << 63 else v
+
+
+_GAMMA, _MIX1, _MIX2 = _i64(0x9E3779B97F4A7C15), _i64(0xBF58476D1CE4E5B9), _i64(0x94D049BB133111EB)
+
+
+def _lsr(z, s: int):
+    return (z >> s) & ((1 << (64 - s)) - 1)  # logical shift of int64 bits
+
+
+def _splitmix64(z):
+    z = (z ^ _lsr(z, 30)) * _MIX1
+    z = (z ^ _lsr(z, 27)) * _MIX2
+    return z ^ _lsr(z, 31)
+
+
+def seeded_normal(torch, seed: int, sigma: float, n: int, device="cuda"):
+    """n float32 values ~ N(0, sigma^2), the tests' input generator: value i is
+    the Box-Muller transform of the SplitMix64 outputs at seed + (2 i + 1) gamma
+    and seed + (2 i + 2) gamma (gamma = 0x9E3779B97F4A7C15), u1 in (0, 1],
+    u2 in [0, 1), evaluated in float64 -- counter-based, so computed here on
+    the device with wrapping int64 arithmetic."""
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    base = _i64(seed % (1 << 64))
+    step = 1 << 24
+    for s0 in range(0, n, step):
+        i = torch.arange(s0, min(n, s0 + step), dtype=torch.int64, device=device)
+        a = _splitmix64(base + (2 * i + 1) * _GAMMA)
+        b = _splitmix64(base + (2 * i + 2) * _GAMMA)
+        u1 = (_lsr(a, 11) + 1).double() * (1.0 / 9007199254740992.0)
+        u2 = _lsr(b, 11).double() * (1.0 / 9007199254740992.0)
+        z = torch.sqrt(-2.0 * torch.log(u1)) * torch.cos(6.283185307179586476925286766559 * u2)
+        out[s0:s0 + i.numel()] = (z * sigma).float()
+    return out
+
+
+class Rng:
+    """Seeded inputs of one workload: each draw is seeded_normal of its own
+    seed (the workload's seed plus a draw counter)."""
+
+    def __init__(self, torch, seed: int, device="cuda"):
+        self.torch, self.seed, self.device, self.count = torch, seed, device, 0
+
+    def normal(self, *shape, sigma: float = 1.0):
+        n = 1
+        for d in shape:
+            n *= d
+        self.count += 1
+        return seeded_normal(self.torch, (self.seed << 16) + self.count, sigma, n, self.device).view(*shape)
+
+
+def rand_weights(torch, Q, d_in, d_out, rng, dq=True, striped=True):
+    w = rng.normal(d_in * d_out, sigma=0.02)
     p = Q.PackedNf4Tensor.quantize(w)
     if dq:
         p = p.with_double_quantization()
@@ -134,13 +186,12 @@ def clone_linear(Q, lin):
 def bench_gemv(torch, Q, L, args) -> dict:
     d_in, d_out = 4096, 11008
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x4E463458)
+    g = Rng(torch, 0x4E463458)
     base = rand_weights(torch, Q, d_in, d_out, g)
     nbytes = gemv_bytes(d_in, d_out, dq=True)
     copies = max(2, -(-(2 * MALL_BYTES) // nbytes))  # >= 512 MiB of weights
     layers = [base] + [Q.Nf4Linear.from_packed(base.packed(), d_in, d_out) for _ in range(copies - 1)]
-    x = torch.randn(1, d_in, device=dev, generator=g)
+    x = g.normal(1, d_in)
     y = torch.empty(1, d_out, device=dev)
     structs = [lay.weight_struct() for lay in layers]
     lib = L.lib()
@@ -165,27 +216,36 @@ def bench_gemv(torch, Q, L, args) -> dict:
     torch.cuda.synchronize()
     # exactly `steps` launches, rotating over the copies: one graph of them
     # Each measurement times exactly `steps` launches between two
-    # synchronizations; it is repeated (at least 5 times and ~0.2 s in all)
-    # and the median taken, so that a short run (the driver's --steps 20 is
-    # ~0.2 ms of GPU work) is not one sample of host and graph-launch jitter.
+    # synchronizations, with HIP events recorded on the launch stream right
+    # before and after them (the GPU time of the K steps, launch gaps between
+    # them included; the host's own launch and wake-up latency around the
+    # replay is not a step's -- its wall time is reported beside it).  It is
+    # repeated (at least 5 times and ~0.2 s in all) and the median taken, so
+    # that a short run (the driver's --steps 20 is ~0.2 ms of GPU work) is not
+    # one sample of jitter.
     timed = capture(torch, launch, steps) if graph is not None else None
-    samples = []
+    samples, walls = [], []
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if timed is not None:
         timed.replay()  # once untimed (graph upload)
         torch.cuda.synchronize()
-    while len(samples) < 5 or (sum(samples) < 0.2 and len(samples) < 1000):
+    while len(samples) < 5 or (sum(walls) < 0.2 and len(samples) < 1000):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        ev0.record()
         if timed is not None:
             timed.replay()
         else:
             for i in range(steps):
                 launch(i)
+        ev1.record()
         torch.cuda.synchronize()
-        samples.append(time.perf_counter() - t0)
+        walls.append(time.perf_counter() - t0)
+        samples.append(ev0.elapsed_time(ev1) / 1e3)
     if timed is not None:
         del timed
     samples.sort()
+    walls.sort()
     elapsed = samples[len(samples) // 2]
     # per-launch kernel time: HIP events on the launch stream around graph
     # replays of the rotating launches (cold), and of one weight (warm)
@@ -199,6 +259,7 @@ def bench_gemv(torch, Q, L, args) -> dict:
         raise RuntimeError("GEMV result drifted during timing")
     out = {"steps": steps, "elapsed_s": elapsed, "bytes": nbytes, "copies": copies, "repeats": len(samples),
            "value_gbs": nbytes * steps / elapsed / 1e9, "ms_per_step": elapsed * 1e3 / steps,
+           "host_wall_ms_per_step": walls[len(walls) // 2] * 1e3 / steps,
            "kernel_cold_ms": cold_ms, "kernel_warm_ms": warm_ms, "graph": graph is not None}
     # bf16 activations (same weight bytes, x half the size)
     xb = x.to(torch.bfloat16)
@@ -260,10 +321,9 @@ def bench_codec(torch, Q, L) -> dict:
     """Config 1 (4096 x 4096 f32): quantize and dequantize kernels."""
     n = 4096 * 4096
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x4E463457)
+    g = Rng(torch, 0x4E463457)
     copies = 8  # 8 x (64 MiB + 8 MiB) > the Infinity Cache
-    vals = [torch.randn(n, device=dev, generator=g) * 0.02 for _ in range(copies)]
+    vals = [g.normal(n, sigma=0.02) for _ in range(copies)]
     packs = [Q.PackedNf4Tensor.quantize(v) for v in vals]
     outs = [torch.empty(n, device=dev) for _ in range(copies)]
     lib = L.lib()
@@ -295,12 +355,11 @@ def bench_gemm(torch, Q, L) -> dict:
     """Config 3: X bf16 [2048, 4096] . NF4 W [4096, 4096] + LoRA r 16 (scale 2), bf16 Y."""
     M, K, N, r = 2048, 4096, 4096, 16
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x4E463457 + 3)
+    g = Rng(torch, 0x4E463457 + 3)
     lin = rand_weights(torch, Q, K, N, g)
-    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
-    a = torch.randn(K, r, device=dev, generator=g) * 0.01
-    b = torch.randn(r, N, device=dev, generator=g) * 0.01
+    x = g.normal(M, K).to(torch.bfloat16)
+    a = g.normal(K, r, sigma=0.01)
+    b = g.normal(r, N, sigma=0.01)
     ql = Q.QloraLinear(lin, Q.LoraAdapter.from_parts(a, b, 2.0))
     y = ql.forward(x)
     ref = (x.float() @ lin.dequantized_weight()) + (x.float() @ a) @ b * 2.0
@@ -365,8 +424,7 @@ def bench_gemm(torch, Q, L) -> dict:
 def bench_swiglu(torch, Q, L, tokens) -> dict:
     hidden, inter = 4096, 11008
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x4E463457 + 4)
+    g = Rng(torch, 0x4E463457 + 4)
     wbytes = 2 * gemv_bytes(hidden, inter, True, 0, 0) + gemv_bytes(inter, hidden, True, 0, 0)
     # rotate >= 512 MiB of packed weights (twice the 256 MiB Infinity Cache):
     # 8 blocks of 69.7 MB, so every step streams its weights from HBM
@@ -376,7 +434,7 @@ def bench_swiglu(torch, Q, L, tokens) -> dict:
     blocks = [Q.QwenMlp(*base)] + [Q.QwenMlp(*[clone_linear(Q, w) for w in base]) for _ in range(copies - 1)]
     out = {}
     for T in tokens:
-        x = torch.randn(T, hidden, device=dev, generator=g).to(torch.bfloat16)
+        x = g.normal(T, hidden).to(torch.bfloat16)
         ys = [None] * copies
 
         def run(i: int) -> None:
@@ -409,10 +467,9 @@ QWEN_PROJ = [("q", 896, 896), ("k", 896, 128), ("v", 896, 128), ("o", 896, 896),
 
 def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x4E463457 + 5)
+    g = Rng(torch, 0x4E463457 + 5)
     # whole-model quantize pass: quantize + double-quantize + stripe, 168 weights
-    vals = [(torch.randn(di * do, device=dev, generator=g) * 0.02, di, do)
+    vals = [(g.normal(di * do, sigma=0.02), di, do)
             for _ in range(layers) for (_, di, do) in QWEN_PROJ]
     torch.cuda.synchronize()
 
@@ -453,7 +510,7 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
     models = [lins] + [[clone_linear(Q, lin) for lin in lins] for _ in range(mcopies - 1)]
     # batch 1 in f32 (the reference's precision), batch 32 in bf16 and in f32
     for b, xdt, tag in ((1, torch.float32, "b1"), (32, torch.bfloat16, "b32"), (32, torch.float32, "b32_f32")):
-        xs = {di: torch.randn(b, di, device=dev, generator=g).to(xdt) for (_, di, _) in QWEN_PROJ}
+        xs = {di: g.normal(b, di).to(xdt) for (_, di, _) in QWEN_PROJ}
 
         def step(i: int) -> None:
             for lin in models[i % mcopies]:
@@ -488,7 +545,7 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
         # SwiGLU + residual), each layer's output feeding the next; q stands
         # in for the attention output (the attention itself is not on the NF4
         # path and is not timed)
-        norms = [(torch.randn(896, device=dev, generator=g) * 0.1, torch.randn(896, device=dev, generator=g) * 0.1)
+        norms = [(g.normal(896, sigma=0.1), g.normal(896, sigma=0.1))
                  for _ in range(layers)]
         from unifur_amd import qwennet as N
         dec_sets = [[N.QwenDecoderLayer(*m[7 * l:7 * l + 4], Q.QwenMlp(*m[7 * l + 4:7 * l + 7]), *norms[l], 1e-6)
@@ -522,13 +579,12 @@ def bench_backward(torch, Q, L) -> dict:
     dx (bf16) and both adapter gradients (f32)."""
     M, K, N, r = 2048, 4096, 4096, 16
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x4E463457 + 7)
+    g = Rng(torch, 0x4E463457 + 7)
     lin = rand_weights(torch, Q, K, N, g)
-    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
-    dy = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
-    a = torch.randn(K, r, device=dev, generator=g) * 0.01
-    b = torch.randn(r, N, device=dev, generator=g) * 0.01
+    x = g.normal(M, K).to(torch.bfloat16)
+    dy = g.normal(M, N).to(torch.bfloat16)
+    a = g.normal(K, r, sigma=0.01)
+    b = g.normal(r, N, sigma=0.01)
     ql = Q.QloraLinear(lin, Q.LoraAdapter.from_parts(a, b, 2.0))
     lib = L.lib()
     ws_bytes = lib.unifur_nf4_linear_backward_workspace_size(M, K, N, L.BF16, r)
@@ -576,9 +632,10 @@ def bench_embedding(torch, Q, L) -> dict:
     from unifur_amd import qwennet as QN
     n_emb, d = 151936, 896
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
+    rng = Rng(torch, 0x4E463457 + 6)
+    g = torch.Generator(device=dev)  # token ids
     g.manual_seed(0x4E463457 + 6)
-    emb = QN.Nf4Embedding.from_values(torch.randn(n_emb * d, device=dev, generator=g) * 0.02, n_emb, d)
+    emb = QN.Nf4Embedding.from_values(rng.normal(n_emb * d, sigma=0.02), n_emb, d)
     out = {"table": f"{n_emb}x{d}", "resident_bytes": emb.resident_bytes()}
     for t in (32, 2048):
         ids = torch.randint(0, n_emb, (t,), device=dev, generator=g)
@@ -804,13 +861,15 @@ def main() -> int:
                         "block 64, double-quantized scales, y f32; weight held striped; "
                         f"{gemv['copies']} weight copies rotated (cold HBM)",
             "timing": ("HIP-graph replay of the launches" if gemv["graph"] else "eager launches") +
-                      f"; median of {gemv['repeats']} timed runs of exactly {gemv['steps']} steps",
+                      f"; median of {gemv['repeats']} runs of exactly {gemv['steps']} steps, each between two "
+                      "synchronizations and timed by HIP events on the launch stream "
+                      f"(host wall time {gemv['host_wall_ms_per_step'] * 1e3:.3f} us per step)",
             "d_in": 4096, "d_out": 11008, "rows": 1, "block_size": 64, "double_quantized": True,
             "bytes_per_step": gemv["bytes"],
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_striped_kernel<1,4,4,f32,dq>",
+            "kernel": "gemv_striped_kernel<1,4,2,f32,dq,·,·,2>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
