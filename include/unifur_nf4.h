@@ -344,7 +344,9 @@ typedef struct unifur_nf4_decoder_layer {
  * attention itself, which stay with the caller.  x [rows, hidden]; q, k, v
  * [rows, d_out of their weight]; all of dtype.  Decode batches (<= 4 rows)
  * over striped weights of one scale kind take one launch with the norm
- * folded in; other calls norm x into the workspace first. */
+ * folded in, and so do 5..64 bf16 (5..32 f32) rows over striped weights with
+ * double-quantized scales and a 16-byte aligned x; other calls norm x into
+ * the workspace first.  The workspace size covers those other calls. */
 uint64_t unifur_nf4_decoder_attn_in_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer *layer, int dtype);
 int unifur_nf4_decoder_attn_in(const void *x, int dtype, uint64_t rows, const unifur_nf4_decoder_layer *layer,
                                void *q, void *k, void *v, void *workspace, uint64_t workspace_bytes, void *stream);
@@ -354,7 +356,8 @@ int unifur_nf4_decoder_attn_in(const void *x, int dtype, uint64_t rows, const un
  * n = post_norm(x1).  x, y [rows, hidden]; ctx [rows, o.d_in] (the merged
  * attention heads); all of dtype; y may be x.  Decode batches over striped
  * weights add the residuals in the projections' epilogues and fold the norm
- * into the gate/up launch (<= 2 rows) or norm x1 once (3..64 bf16 rows). */
+ * into the gate/up launch (up to 4 rows; 5..64 bf16 or 5..32 f32 rows with
+ * double-quantized scales), else norm x1 once first. */
 uint64_t unifur_nf4_decoder_attn_out_mlp_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer *layer,
                                                         int dtype);
 int unifur_nf4_decoder_attn_out_mlp(const void *x, const void *ctx, int dtype, uint64_t rows,

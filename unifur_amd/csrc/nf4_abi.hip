@@ -1038,6 +1038,20 @@ bool attn_in_fused(uint64_t rows, const unifur_nf4_decoder_layer* l) {
   return rows >= 1 && rows <= (uint64_t)kGemvMaxRows;
 }
 
+// 5..64 bf16 (5..32 f32) rows: q, k, v in one skinny MFMA launch with the
+// input norm folded in, when the three are striped with double-quantized
+// scales, x suits the skinny kernel and its plan needs no d_in slabs
+bool attn_in_skinny(uint64_t rows, const unifur_nf4_decoder_layer* l, const void* x, int dtype, StripedPlan* plan) {
+  const unifur_nf4_weight* w[3] = {&l->q, &l->k, &l->v};
+  for (const auto* t : w)
+    if (!is_striped(t) || t->scales.kind != UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED) return false;
+  const bool f32 = dtype == UNIFUR_NF4_F32;
+  if (rows <= (uint64_t)kGemvMaxRows || !skinny_supported((int)rows, (int)l->q.d_in, x, f32)) return false;
+  const int dn[3] = {(int)l->q.d_out, (int)l->k.d_out, (int)l->v.d_out};
+  *plan = plan_skinny((int)rows, (int)l->q.d_in, dn, 3, false);
+  return plan->splits == 1;
+}
+
 struct AttnInLayout {
   size_t inner, normed, total;
 };
@@ -1072,6 +1086,13 @@ int run_attn_in(const void* x, int dtype, uint64_t rows, const unifur_nf4_decode
     const StripedPlan plan = plan_gemv_striped((int)rows, (int)l->q.d_in, dn, 3, false);
     UNIFUR_HIP(launch_gemv_striped(plan, x, bf, (int)rows, (int)l->q.d_in, gw, 3, false, stream, l->input_norm,
                                    l->eps));
+    return UNIFUR_NF4_OK;
+  }
+  StripedPlan sk{};
+  if (attn_in_skinny(rows, l, x, dtype, &sk)) {
+    GemvWeight gw[3];
+    for (int i = 0; i < 3; ++i) gw[i] = gemv_weight(&w[i], outs[i], bf, nullptr, nullptr);
+    UNIFUR_HIP(launch_skinny(sk, x, !bf, (int)rows, (int)l->q.d_in, gw, 3, false, stream, l->input_norm, l->eps));
     return UNIFUR_NF4_OK;
   }
   const AttnInLayout L = plan_attn_in(rows, l, dtype);
@@ -1201,14 +1222,20 @@ int run_attn_out_mlp(const void* x, const void* ctx, int dtype, uint64_t rows, c
       return UNIFUR_NF4_OK;
     }
     case MlpStage::kSkinny: {
-      // n = post_norm(x1) and the SwiGLU middle in the stage's dtype
-      void* n = at<void>(ws, L.nrm);
+      // the SwiGLU middle in the stage's dtype; the post norm folded into the
+      // gate/up launch (double-quantized scales, no d_in slabs), else n =
+      // post_norm(x1) first
       void* mid = bf ? at<void>(ws, L.hb) : static_cast<void*>(h);
       float* p0 = at<float>(ws, L.part0);
-      UNIFUR_HIP(launch_rms_norm(x1, bf, (int)rows, (int)hid, l->post_norm, l->eps, n, bf, stream));
       GemvWeight gw[2] = {gemv_weight(&l->gate, mid, bf, cnt, p0),
                           gemv_weight(&l->up, nullptr, bf, cnt, at<float>(ws, L.part1))};
-      UNIFUR_HIP(launch_skinny(L.up_plan, n, !bf, (int)rows, (int)hid, gw, 2, true, stream));
+      if (l->gate.scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED && L.up_plan.splits == 1) {
+        UNIFUR_HIP(launch_skinny(L.up_plan, x1, !bf, (int)rows, (int)hid, gw, 2, true, stream, l->post_norm, l->eps));
+      } else {
+        void* n = at<void>(ws, L.nrm);
+        UNIFUR_HIP(launch_rms_norm(x1, bf, (int)rows, (int)hid, l->post_norm, l->eps, n, bf, stream));
+        UNIFUR_HIP(launch_skinny(L.up_plan, n, !bf, (int)rows, (int)hid, gw, 2, true, stream));
+      }
       GemvWeight dw = gemv_weight(&l->down, y, bf, cnt, p0);
       dw.residual = x1;
       UNIFUR_HIP(launch_skinny(L.down_plan, mid, !bf, (int)rows, (int)inter, &dw, 1, false, stream));

@@ -68,8 +68,8 @@ struct StripedArgs {
   int nweights;
   GemvWeight w[kMaxGemvWeights];
   int stripe_begin[kMaxGemvWeights + 1];  // prefix sums of stripes per weight
-  // GEMV only (null for the skinny kernel): QwenRmsNorm folded into the
-  // launch, x -> x * rsqrt(mean(x^2) + norm_eps) * (norm_w + 1) per row
+  // QwenRmsNorm folded into the launch, x -> x * rsqrt(mean(x^2) +
+  // norm_eps) * (norm_w + 1) per row
   const float* norm_w;  // [d_in] or null
   float norm_eps;
 };
@@ -102,8 +102,12 @@ bool skinny_supported(int rows, int d_in, const void* x, bool x_f32 = false);
 
 StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool pair);
 
+// norm_w != null folds QwenRmsNorm (weight norm_w, epsilon norm_eps) over x
+// into the launch, as the GEMV does: needs double-quantized scales and a
+// plan without d_in slabs (plan.splits == 1).
 hipError_t launch_skinny(const StripedPlan& p, const void* x, bool x_f32, int rows, int d_in,
-                         const GemvWeight* weights, int nweights, bool pair, hipStream_t stream);
+                         const GemvWeight* weights, int nweights, bool pair, hipStream_t stream,
+                         const float* norm_w = nullptr, float norm_eps = 0.0f);
 
 // floats of GemvWeight::partials one weight of a skinny launch needs (0 without splits)
 size_t skinny_partial_floats(const StripedPlan& p, int rows, int d_out);

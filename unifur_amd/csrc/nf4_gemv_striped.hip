@@ -588,6 +588,7 @@ struct SkChunk {
   u32x2 code[NW][S];
   std::conditional_t<DQ, uint8_t, uint32_t> scale[NW];  // narrow, as in the GEMV ring
   u32x4 x[NT][XF32 ? 4 : 2];  // 16 activations of one token: bf16, or f32
+  uint32_t g;  // NORM kernels: the norm weight of this lane's row (f32 bits)
 };
 
 // Loads of chunk `chunk` of this wave: codes of row 64 chunk + lane of each
@@ -597,10 +598,12 @@ struct SkChunk {
 // next rows of their stripe, which meet zero scales and zero activations);
 // activation offsets past the wave's rows are sent out of the buffer (zero),
 // tokens past `rows` fall out of it by themselves.
-template <int NT, int NW, int S, bool DQ, bool XF32>
+template <int NT, int NW, int S, bool DQ, bool XF32, bool NORM>
 __device__ __forceinline__ void sk_issue(SkChunk<NT, NW, S, DQ, XF32>& c, const WaveW (&ww)[NW],
-                                         __amdgpu_buffer_rsrc_t xr, int K, int kw, int kend, int chunk, int lane) {
+                                         __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr, int K, int kw, int kend,
+                                         int chunk, int lane) {
   const uint32_t row = (uint32_t)(chunk * 64 + lane);
+  if constexpr (NORM) c.g = __builtin_amdgcn_raw_buffer_load_b32(gr, row * 4u, 0, 0);
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
 #pragma unroll
@@ -642,7 +645,7 @@ __device__ __forceinline__ void sk_lookup(f32x2 (&lv)[8], u32x2 code, uint32_t s
     }
 }
 
-template <int NT, int W, int D, int S, bool DQ, bool PAIR, bool XF32>
+template <int NT, int W, int D, int S, bool DQ, bool PAIR, bool XF32, bool NORM>
 __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   constexpr int NW = PAIR ? 2 : 1;
   constexpr int U = NW * S;  // units per chunk
@@ -679,13 +682,19 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
                       : make_rsrc(G.scales.absmax + srow, (uint32_t)nrows * 4u);
   }
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.rows * (uint32_t)K * (XF32 ? 4u : 2u));
+  // NORM: QwenRmsNorm over x folded in (src/qwennet.rs:104-109), over the
+  // whole of d_in in one workgroup (no d_in slabs): each row's (w + 1) rides
+  // on its block scale -- B = level * (scale * (w + 1)) -- each lane sums x^2
+  // of the activations it feeds the MFMAs, and the outputs of token t are
+  // scaled by 1 / sqrt(mean(x_t^2) + eps) before the epilogue
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM ? a.norm_w + kw : a.x, NORM ? (uint32_t)nrows * 4u : 0u);
 
   // as in the GEMV: the first chunks in flight before the LUT build, and the
   // scale of scales applied per row (the DQ table holds q / 255)
   SkChunk<NT, NW, S, DQ, XF32> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {  // in chunk order, as in the GEMV
-    sk_issue<NT, NW, S, DQ, XF32>(ring[j], ww, xr, K, kw, kw + nrows, j, lane);
+    sk_issue<NT, NW, S, DQ, XF32, NORM>(ring[j], ww, xr, gr, K, kw, kw + nrows, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
   float sos[NW];
@@ -714,10 +723,14 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
     for (int i = 0; i < S; ++i)
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) acc[w][i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float xsq[NT];  // NORM: this lane's sum of x^2 (token lane % 16 of each tile)
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) xsq[tt] = 0.0f;
 
   auto decode_scale = [&](const SkChunk<NT, NW, S, DQ, XF32>& c, int w) {
     // ((float)q / 255.0f) * scale_of_scales (src/quantize.rs:349)
-    return DQ ? dq_lut[(uint32_t)c.scale[w]] * sos[w] : as_f((uint32_t)c.scale[w]);
+    const float sc = DQ ? dq_lut[(uint32_t)c.scale[w]] * sos[w] : as_f((uint32_t)c.scale[w]);
+    return NORM ? sc * (as_f(c.g) + 1.0f) : sc;  // NORM: the row's (w + 1) with its scale
   };
   float sdec[2][NW];  // this lane's row scale, per chunk parity
   f32x2 lk[2][8];     // level pairs, per unit parity
@@ -772,10 +785,56 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
           }
         }
       }
-      sk_issue<NT, NW, S, DQ, XF32>(ring[j], ww, xr, K, kw, kw + nrows, c0 + j + D, lane);
+      if constexpr (NORM) {  // x^2 of this chunk's activations, once per chunk
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+          for (int q = 0; q < (XF32 ? 4 : 2); ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t u = ring[j].x[tt][q][e];
+              if constexpr (XF32) {
+                xsq[tt] = __builtin_fmaf(as_f(u), as_f(u), xsq[tt]);
+              } else {
+                const float lo = as_f(u << 16), hi = as_f(u & 0xffff0000u);
+                xsq[tt] = __builtin_fmaf(lo, lo, __builtin_fmaf(hi, hi, xsq[tt]));
+              }
+            }
+      }
+      sk_issue<NT, NW, S, DQ, XF32, NORM>(ring[j], ww, xr, gr, K, kw, kw + nrows, c0 + j + D, lane);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
+
+  // NORM: the token sums of x^2 over the lane groups (lanes t, t + 16, t + 32,
+  // t + 48 hold one token), then over the waves in wave order through LDS
+  // (past the wave reduction's space, inside the LUT's), and each token's
+  // 1 / sqrt(mean + eps) into LDS for the epilogue
+  float* inv_tok = reinterpret_cast<float*>(smem + 16384) + NT * W * 16;
+  if constexpr (NORM) {
+    float* sq = reinterpret_cast<float*>(smem + 16384);
+    float ss[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      float v = xsq[tt];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      ss[tt] = v;
+    }
+    __syncthreads();  // every wave is past its LUT lookups
+    if (lane < 16) {
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) sq[(tt * W + wave) * 16 + lane] = ss[tt];
+    }
+    __syncthreads();
+    if (tid < NT * 16) {
+      const int tt = tid >> 4, t = tid & 15;
+      float v = 0.0f;
+#pragma unroll
+      for (int q = 0; q < W; ++q) v += sq[(tt * W + q) * 16 + t];
+      inv_tok[tid] = 1.0f / __builtin_sqrtf(v / (float)K + a.norm_eps);
+    }
+  }
 
   // acc[w][i][tt][e] = C[token 16 tt + 4 (lane / 16) + e][column lane % 16 of
   // stripe s0 + i]; waves added through LDS (LUT space), one (tile, stripe)
@@ -878,29 +937,39 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   for (int tt = 0; tt < NT; ++tt) {
     const int t = 16 * tt + t_l;
     if (t >= a.rows) continue;
+    const float nrm = NORM ? inv_tok[tt * 16 + t_l] : 1.0f;
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int gcol = (s0 + i) * kStripeCols + cc;
-      float y = epilogue_value(G, sums[0][i][tt], t, gcol);
-      if constexpr (PAIR) y = silu_f32(y) * epilogue_value(a.w[1], sums[1][i][tt], t, gcol);
+      float y = epilogue_value(G, sums[0][i][tt] * nrm, t, gcol);
+      if constexpr (PAIR) y = silu_f32(y) * epilogue_value(a.w[1], sums[1][i][tt] * nrm, t, gcol);
       store_y(G, (size_t)t * G.d_out + gcol, y);
     }
   }
 }
 
-template <int NT, int W, int S, bool DQ, bool PAIR, bool XF32>
+template <int NT, int W, int S, bool DQ, bool PAIR, bool XF32, bool NORM = false>
 hipError_t sk_launch_t(const StripedArgs& a, int grid, int splits, hipStream_t stream) {
   constexpr int NW = PAIR ? 2 : 1;
   constexpr int D = (NT == 1 && S == 1) ? 4 : 2;
   constexpr int smem = kSkStageOffset + W * 512;
   static_assert(smem <= 65536, "skinny LDS");
-  static_assert(W * NW * 1024 <= kLutBytes, "the reduction reuses the LUT space");
-  skinny_kernel<NT, W, D, S, DQ, PAIR, XF32><<<dim3(grid, splits), W * 64, smem, stream>>>(a);
+  static_assert(W * NW * 1024 <= 16384, "the reduction reuses the LUT space below the norm's sums");
+  static_assert(16384 + (NT * W * 16 + NT * 16) * 4 <= kLutBytes, "the norm's sums fit the LUT space");
+  skinny_kernel<NT, W, D, S, DQ, PAIR, XF32, NORM><<<dim3(grid, splits), W * 64, smem, stream>>>(a);
   return hipGetLastError();
 }
 
+// a folded norm (a.norm_w) takes the NORM kernels, built for double-quantized
+// scales and whole-d_in grids (one slab)
 template <int NT, int S, bool PAIR, bool XF32>
 hipError_t sk_dispatch_w(const StripedArgs& a, int grid, int splits, int waves, bool dq, hipStream_t stream) {
+  if (a.norm_w) {
+    if (!dq || splits != 1) return hipErrorInvalidValue;
+    if (waves == 4) return sk_launch_t<NT, 4, S, true, PAIR, XF32, true>(a, grid, splits, stream);
+    if (waves == 8) return sk_launch_t<NT, 8, S, true, PAIR, XF32, true>(a, grid, splits, stream);
+    return hipErrorInvalidValue;
+  }
   if (waves == 4)
     return dq ? sk_launch_t<NT, 4, S, true, PAIR, XF32>(a, grid, splits, stream)
               : sk_launch_t<NT, 4, S, false, PAIR, XF32>(a, grid, splits, stream);
@@ -1054,7 +1123,8 @@ StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool
 }
 
 hipError_t launch_skinny(const StripedPlan& p, const void* x, bool x_f32, int rows, int d_in,
-                         const GemvWeight* weights, int nweights, bool pair, hipStream_t stream) {
+                         const GemvWeight* weights, int nweights, bool pair, hipStream_t stream, const float* norm_w,
+                         float norm_eps) {
   if (!skinny_supported(rows, d_in, x, x_f32) || nweights < 1 || nweights > kMaxGemvWeights || (pair && nweights != 2))
     return hipErrorInvalidValue;
   if ((p.group != 1 && p.group != 2 && p.group != 4) || p.splits < 1 || p.splits > 65535 ||
@@ -1062,6 +1132,8 @@ hipError_t launch_skinny(const StripedPlan& p, const void* x, bool x_f32, int ro
     return hipErrorInvalidValue;
   StripedArgs a{};
   a.x = x;
+  a.norm_w = norm_w;
+  a.norm_eps = norm_eps;
   a.rows = rows;
   a.d_in = d_in;
   a.rows_per_wave = p.rows_per_wave;
