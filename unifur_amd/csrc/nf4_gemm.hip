@@ -183,9 +183,10 @@ __device__ __forceinline__ void load_b(BStep& B, const GemmArgs& g, const BSrc& 
 // reference's dequantize), rounded to bf16, and the (k, k + 1) pair of a
 // column is one 4-byte LDS store.
 template <bool DQ, bool STRIPED>
-__device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int d, int dq_table) {
+__device__ __forceinline__ void store_b_at(const BStep& B, unsigned char* smem, int ring, int lut_off, int dq_off,
+                                           int buf, int d, int dq_table) {
   const int st = d >> 5, rp = d & 31;
-  const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq + dq_table * 1024);
+  const float* dq_lut = reinterpret_cast<const float*>(smem + dq_off + dq_table * 1024);
   float s0, s1;
   if constexpr (DQ && STRIPED) {
     const int sh = 16 * (d & 1);
@@ -198,7 +199,7 @@ __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int
     s0 = __uint_as_float(B.scale[0]);
     s1 = __uint_as_float(B.scale[1]);
   }
-  const int base = kLdsB + buf * kBTileBytes;
+  const int base = ring + buf * kBTileBytes;
   const int chunk = rp >> 2;                   // k = 2 rp lies in 16-byte chunk rp / 4 of a row
   const uint32_t within = (uint32_t)(rp & 3) * 4u;
   // all 16 lookups first, so that one LDS latency covers them (a producer
@@ -211,9 +212,9 @@ __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int
       for (int r = 0; r < 2; ++r) {
         const uint32_t w = B.code[2 * r + (j >> 2)], sh = 8 * (j & 3);
         l[r][j].x = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
-            (size_t)(kLdsLut + (((w >> sh) & 0xfu) << 2)));
+            (size_t)(lut_off + (((w >> sh) & 0xfu) << 2)));
         l[r][j].y = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
-            (size_t)(kLdsLut + (((w >> (sh + 4)) & 0xfu) << 2)));
+            (size_t)(lut_off + (((w >> (sh + 4)) & 0xfu) << 2)));
       }
     }
     __builtin_amdgcn_sched_group_barrier(0x100, 32, 1);  // the 32 level reads
@@ -224,7 +225,7 @@ __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const uint32_t byte = (B.code[2 * r + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
-        l[r][j] = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + copy + byte * 8));
+        l[r][j] = *reinterpret_cast<lds_f32x2_c*>((size_t)(lut_off + copy + byte * 8));
       }
     }
     __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // the 16 LUT reads
@@ -238,6 +239,11 @@ __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int
     *reinterpret_cast<lds_u32*>((size_t)(lds_addr(base, n, chunk) + within)) = even;
     *reinterpret_cast<lds_u32*>((size_t)(lds_addr(base, n + 1, chunk) + within)) = odd;
   }
+}
+
+template <bool DQ, bool STRIPED>
+__device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int d, int dq_table) {
+  store_b_at<DQ, STRIPED>(B, smem, kLdsB, kLdsLut, kLdsDq, buf, d, dq_table);
 }
 
 __device__ __forceinline__ bf16x8 read_frag(int base, int row, int chunk) {
@@ -291,6 +297,153 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// The end of a tile: the adapter's (x A) B added on MFMA (LORA), then the
+// store epilogue through this wave's 16 KiB of LDS staging -- rows 0-15 of
+// each 32-row half at stage0, rows 16-31 at stage1, 512 bytes a row.
+template <bool YBF16, bool LORA, bool PAIR>
+__device__ __forceinline__ void finish_tile(const GemmArgs& g, f32x16 (&acc)[2][4], void* yout, int row0, int n0,
+                                            int lane, uint32_t stage0, uint32_t stage1) {
+  if constexpr (LORA) {
+    // acc += xa[rows, r] . B[r, cols] (xa already scaled), one 32x32x16 MFMA
+    // per tile and 16 adapter columns; both operands are bf16 laid out so
+    // that each fragment is one 16-byte load (columns past the rank are zero).
+    const int kr = (lane >> 5) * 8;
+    for (int r0 = 0; r0 < g.lora_pad; r0 += 16) {
+      bf16x8 bfr[4], af[2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 32 * j + (lane & 31);
+        bfr[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(g.lora_bt + (size_t)n * g.lora_pad + r0 + kr));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int m = row0 + 32 * i + (lane & 31);
+        af[i] = m < g.M ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(g.lora_xa + (size_t)m * g.lora_pad + r0 + kr))
+                        : bf16x8{};
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Epilogue, through this wave's own X-stage chunks of stages 0 and 1 (its
+  // copies all landed and its reads completed in the last step; no other
+  // wave touches them).  acc[i][j][4 a + e] is C[row 32 i + 8 a + 4 (lane /
+  // 32) + e][col 32 j + lane % 32]; each half i (32 rows) of the wave's tile
+  // is staged as f32 -- row r at chunk r / 16, byte (r % 16) * 512 +
+  // (4 c ^ 128 * (r / 4 % 2)), so that the two row groups of a store land in
+  // different bank halves -- then read back row-contiguous: lane l takes
+  // columns 4 (l % 32) .. + 3 of row 2 q + l / 32 and writes them as one
+  // 16-byte (f32) or 8-byte (bf16) store, the bias added.
+  {
+    const int cq = 4 * (lane & 31);
+    float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (g.bias) {
+#pragma unroll
+      for (int t2 = 0; t2 < 4; ++t2) bias4[t2] = g.bias[n0 + cq + t2];
+    }
+    auto stage_off = [&](int r, int c) -> uint32_t {
+      return (r < 16 ? stage0 : stage1) + (uint32_t)((r & 15) * 512) +
+             (((uint32_t)c * 4u) ^ ((uint32_t)((r >> 2) & 1) << 7));
+    };
+    if constexpr (PAIR && YBF16) {
+      // silu(gate x) * (up x): acc[i][j] (gate columns 32 j ..) and
+      // acc[i][j + 2] (up, the same columns) hold their elements in the same
+      // lanes, so the product forms in registers; the 32 x 64 block of each
+      // half i is staged as above, then read back 16 lanes per row (columns
+      // 4 (l % 16) .. + 3 of row 4 q + l / 16) and stored as four bf16
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              *reinterpret_cast<__attribute__((address_space(3))) float*>(
+                  (size_t)stage_off(8 * a4 + 4 * (lane >> 5) + e, 32 * j + (lane & 31))) =
+                  silu_times(acc[i][j][4 * a4 + e], acc[i][j + 2][4 * a4 + e]);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        const int c4 = 4 * (lane & 15);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int r = 4 * q + (lane >> 4);
+          const int m = row0 + 32 * i + r;
+          const f32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>((size_t)stage_off(r, c4));
+          if (m < g.M) {
+            const u32x2 o = {pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+            uint16_t* p = reinterpret_cast<uint16_t*>(yout) + (size_t)m * g.N + n0 + c4;
+            if (g.y_aligned) {
+              *reinterpret_cast<u32x2*>(p) = o;
+            } else {
+              p[0] = (uint16_t)(o.x & 0xffffu);
+              p[1] = (uint16_t)(o.x >> 16);
+              p[2] = (uint16_t)(o.y & 0xffffu);
+              p[3] = (uint16_t)(o.y >> 16);
+            }
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();  // the next half reuses the chunks
+      }
+      return;
+    }
+    // columns of this lane's four outputs: PAIR split-K partials put the
+    // gate columns at n0 .. and the up columns at N + n0 .. of a 2 N row
+    const int col = PAIR && cq >= 64 ? g.N + n0 + cq - 64 : n0 + cq;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            *reinterpret_cast<__attribute__((address_space(3))) float*>(
+                (size_t)stage_off(8 * a4 + 4 * (lane >> 5) + e, 32 * j + (lane & 31))) = acc[i][j][4 * a4 + e];
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // a wave's LDS operations complete in order; be explicit
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int r = 2 * q + (lane >> 5);
+        const int m = row0 + 32 * i + r;
+        const f32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>((size_t)stage_off(r, cq));
+        if (m < g.M) {
+          const size_t idx = (size_t)m * g.ldy + col;
+          const float y0 = v.x + bias4[0], y1 = v.y + bias4[1], y2 = v.z + bias4[2], y3 = v.w + bias4[3];
+          if constexpr (YBF16) {
+            const u32x2 o = {pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+            if (g.y_aligned) {
+              *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(yout) + idx) = o;
+            } else {
+              uint16_t* p = reinterpret_cast<uint16_t*>(yout) + idx;
+              p[0] = (uint16_t)(o.x & 0xffffu);
+              p[1] = (uint16_t)(o.x >> 16);
+              p[2] = (uint16_t)(o.y & 0xffffu);
+              p[3] = (uint16_t)(o.y >> 16);
+            }
+          } else {
+            float* p = reinterpret_cast<float*>(yout) + idx;
+            if (g.y_aligned) {
+              *reinterpret_cast<f32x4*>(p) = f32x4{y0, y1, y2, y3};
+            } else {
+              p[0] = y0;
+              p[1] = y1;
+              p[2] = y2;
+              p[3] = y3;
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();  // the next half reuses the chunks
+    }
+  }
 }
 
 // Workgroup tile 256 x 128, warp-specialised: waves 0-3 ("MFMA waves") own
@@ -447,145 +600,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   if (s + 1 < nk) step(s++, no{}, yes{});
   step(s, no{}, no{});
 
-  if constexpr (LORA) {
-    // acc += xa[rows, r] . B[r, cols] (xa already scaled), one 32x32x16 MFMA
-    // per tile and 16 adapter columns; both operands are bf16 laid out so
-    // that each fragment is one 16-byte load (columns past the rank are zero).
-    const int kr = (lane >> 5) * 8;
-    for (int r0 = 0; r0 < g.lora_pad; r0 += 16) {
-      bf16x8 bfr[4], af[2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + 32 * j + (lane & 31);
-        bfr[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(g.lora_bt + (size_t)n * g.lora_pad + r0 + kr));
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int m = row0 + 32 * i + (lane & 31);
-        af[i] = m < g.M ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(g.lora_xa + (size_t)m * g.lora_pad + r0 + kr))
-                        : bf16x8{};
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-  }
-
-  // Epilogue, through this wave's own X-stage chunks of stages 0 and 1 (its
-  // copies all landed and its reads completed in the last step; no other
-  // wave touches them).  acc[i][j][4 a + e] is C[row 32 i + 8 a + 4 (lane /
-  // 32) + e][col 32 j + lane % 32]; each half i (32 rows) of the wave's tile
-  // is staged as f32 -- row r at chunk r / 16, byte (r % 16) * 512 +
-  // (4 c ^ 128 * (r / 4 % 2)), so that the two row groups of a store land in
-  // different bank halves -- then read back row-contiguous: lane l takes
-  // columns 4 (l % 32) .. + 3 of row 2 q + l / 32 and writes them as one
-  // 16-byte (f32) or 8-byte (bf16) store, the bias added.
-  {
-    const int cq = 4 * (lane & 31);
-    float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (g.bias) {
-#pragma unroll
-      for (int t2 = 0; t2 < 4; ++t2) bias4[t2] = g.bias[n0 + cq + t2];
-    }
-    auto stage_off = [&](int r, int c) -> uint32_t {
-      return (uint32_t)(awave + (r >> 4) * kATileBytes + (r & 15) * 512) +
-             (((uint32_t)c * 4u) ^ ((uint32_t)((r >> 2) & 1) << 7));
-    };
-    if constexpr (PAIR && YBF16) {
-      // silu(gate x) * (up x): acc[i][j] (gate columns 32 j ..) and
-      // acc[i][j + 2] (up, the same columns) hold their elements in the same
-      // lanes, so the product forms in registers; the 32 x 64 block of each
-      // half i is staged as above, then read back 16 lanes per row (columns
-      // 4 (l % 16) .. + 3 of row 4 q + l / 16) and stored as four bf16
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int a4 = 0; a4 < 4; ++a4)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              *reinterpret_cast<__attribute__((address_space(3))) float*>(
-                  (size_t)stage_off(8 * a4 + 4 * (lane >> 5) + e, 32 * j + (lane & 31))) =
-                  silu_times(acc[i][j][4 * a4 + e], acc[i][j + 2][4 * a4 + e]);
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
-        const int c4 = 4 * (lane & 15);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int r = 4 * q + (lane >> 4);
-          const int m = row0 + 32 * i + r;
-          const f32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>((size_t)stage_off(r, c4));
-          if (m < g.M) {
-            const u32x2 o = {pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
-            uint16_t* p = reinterpret_cast<uint16_t*>(yout) + (size_t)m * g.N + n0 + c4;
-            if (g.y_aligned) {
-              *reinterpret_cast<u32x2*>(p) = o;
-            } else {
-              p[0] = (uint16_t)(o.x & 0xffffu);
-              p[1] = (uint16_t)(o.x >> 16);
-              p[2] = (uint16_t)(o.y & 0xffffu);
-              p[3] = (uint16_t)(o.y >> 16);
-            }
-          }
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();  // the next half reuses the chunks
-      }
-      return;
-    }
-    // columns of this lane's four outputs: PAIR split-K partials put the
-    // gate columns at n0 .. and the up columns at N + n0 .. of a 2 N row
-    const int col = PAIR && cq >= 64 ? g.N + n0 + cq - 64 : n0 + cq;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            *reinterpret_cast<__attribute__((address_space(3))) float*>(
-                (size_t)stage_off(8 * a4 + 4 * (lane >> 5) + e, 32 * j + (lane & 31))) = acc[i][j][4 * a4 + e];
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // a wave's LDS operations complete in order; be explicit
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int r = 2 * q + (lane >> 5);
-        const int m = row0 + 32 * i + r;
-        const f32x4 v = *reinterpret_cast<__attribute__((address_space(3))) const f32x4*>((size_t)stage_off(r, cq));
-        if (m < g.M) {
-          const size_t idx = (size_t)m * g.ldy + col;
-          const float y0 = v.x + bias4[0], y1 = v.y + bias4[1], y2 = v.z + bias4[2], y3 = v.w + bias4[3];
-          if constexpr (YBF16) {
-            const u32x2 o = {pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
-            if (g.y_aligned) {
-              *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(yout) + idx) = o;
-            } else {
-              uint16_t* p = reinterpret_cast<uint16_t*>(yout) + idx;
-              p[0] = (uint16_t)(o.x & 0xffffu);
-              p[1] = (uint16_t)(o.x >> 16);
-              p[2] = (uint16_t)(o.y & 0xffffu);
-              p[3] = (uint16_t)(o.y >> 16);
-            }
-          } else {
-            float* p = reinterpret_cast<float*>(yout) + idx;
-            if (g.y_aligned) {
-              *reinterpret_cast<f32x4*>(p) = f32x4{y0, y1, y2, y3};
-            } else {
-              p[0] = y0;
-              p[1] = y1;
-              p[2] = y2;
-              p[3] = y3;
-            }
-          }
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      __builtin_amdgcn_wave_barrier();  // the next half reuses the chunks
-    }
-  }
+  finish_tile<YBF16, LORA, PAIR>(g, acc, yout, row0, n0, lane, (uint32_t)awave, (uint32_t)(awave + kATileBytes));
 }
 
 template <bool DQ, bool YBF16, bool LORA, bool STRIPED, bool PAIR = false>
