@@ -631,10 +631,11 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
 //     threads of a wave write at / read B at consecutive addresses);
 //   * lora_xa_kernel: xa[M][pad] = bf16(scaling * (X A)) -- the first factor
 //     of LoraAdapter::forward (src/quantize.rs:619-624) with the scaling
-//     folded in -- 16 rows x 16 columns per workgroup; eight waves split K
-//     (v_mfma_f32_16x16x32_bf16, X and at straight from memory, eight steps
-//     of 16-byte loads in flight) and add their slices through LDS in wave
-//     order.
+//     folded in -- R rows x 16 columns per workgroup (R = 16, or 8 or 4 when
+//     16-row workgroups would not cover the CUs: the MFMA's other rows read
+//     zero); eight waves split K (v_mfma_f32_16x16x32_bf16, X and at straight
+//     from memory, eight steps of 16-byte loads in flight) and add their
+//     slices through LDS in wave order.
 
 __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                         int K, int N, int rank, int pad, uint16_t* __restrict__ at,
@@ -662,12 +663,13 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
 constexpr int kXaWaves = 8;
 constexpr int kXaBatch = 8;  // k32 steps whose loads are in flight together
 
+template <int R>
 __global__ __launch_bounds__(64 * kXaWaves) void lora_xa_kernel(const uint16_t* __restrict__ x,
                                                                 const uint16_t* __restrict__ at, int M, int K,
                                                                 int pad, float scaling, uint16_t* __restrict__ xa) {
   __shared__ float red[kXaWaves][256];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int m0 = blockIdx.x * 16, c0 = blockIdx.y * 16;
+  const int m0 = blockIdx.x * R, c0 = blockIdx.y * 16;
   const int kq = K / kXaWaves;  // a multiple of 8 (K % 64 == 0)
   const int kbeg = wv * kq, kend = kbeg + kq;
   // rows past M read as zero (buffer bound), and so does a step past the
@@ -676,6 +678,7 @@ __global__ __launch_bounds__(64 * kXaWaves) void lora_xa_kernel(const uint16_t* 
       const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), 0x00020000);
   const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(at), (short)0, (int)((uint32_t)pad * (uint32_t)K * 2u), 0x00020000);
+  const bool row_ok = (lane & 15) < R;  // rows past the tile's R read zero
   const uint32_t xrow = (uint32_t)(m0 + (lane & 15)) * (uint32_t)K * 2u;
   const uint32_t arow = (uint32_t)(c0 + (lane & 15)) * (uint32_t)K * 2u;
   const int kl = 8 * (lane >> 4);  // this lane's 8 k of each 32
@@ -687,7 +690,7 @@ __global__ __launch_bounds__(64 * kXaWaves) void lora_xa_kernel(const uint16_t* 
       const int k = k0 + 32 * q + kl;
       const bool ok = k < kend;  // K / 8 may end inside a 32-k step: mask per 8-k group
       xv[q] = __builtin_bit_cast(
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? xrow + (uint32_t)k * 2u : 0xffffffffu, 0, 0));
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok && row_ok ? xrow + (uint32_t)k * 2u : 0xffffffffu, 0, 0));
       av[q] = __builtin_bit_cast(
           bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ar, ok ? arow + (uint32_t)k * 2u : 0xffffffffu, 0, 0));
     }
@@ -700,7 +703,7 @@ __global__ __launch_bounds__(64 * kXaWaves) void lora_xa_kernel(const uint16_t* 
   for (int e = 0; e < 4; ++e) red[wv][(4 * (lane >> 4) + e) * 16 + (lane & 15)] = acc[e];
   __syncthreads();
   const int t = threadIdx.x;
-  if (t < 256) {
+  if (t < 16 * R) {
     const int m = m0 + t / 16;
     if (m < M) {
       float v = red[0][t];
@@ -728,8 +731,15 @@ hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* 
   lora_prep_kernel<<<(unsigned)((K + N + 255) / 256), 256, 0, stream>>>(a, b, K, N, rank, pad, at, bt);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  lora_xa_kernel<<<dim3((unsigned)((M + 15) / 16), (unsigned)(pad / 16)), 64 * kXaWaves, 0, stream>>>(x, at, M, K, pad,
-                                                                                                    scaling, xa);
+  // rows per workgroup: 16 while that covers the CUs, else 8 or 4
+  const dim3 block(64 * kXaWaves);
+  const unsigned cols = (unsigned)(pad / 16);
+  if ((long)((M + 15) / 16) * cols >= 256)
+    lora_xa_kernel<16><<<dim3((unsigned)((M + 15) / 16), cols), block, 0, stream>>>(x, at, M, K, pad, scaling, xa);
+  else if ((long)((M + 7) / 8) * cols >= 256)
+    lora_xa_kernel<8><<<dim3((unsigned)((M + 7) / 8), cols), block, 0, stream>>>(x, at, M, K, pad, scaling, xa);
+  else
+    lora_xa_kernel<4><<<dim3((unsigned)((M + 3) / 4), cols), block, 0, stream>>>(x, at, M, K, pad, scaling, xa);
   return hipGetLastError();
 }
 
