@@ -67,7 +67,7 @@ def layer(oracle, device):
 
 @pytest.mark.parametrize("rows,dt", [(1, torch.float32), (2, torch.float32), (3, torch.float32), (4, torch.float32),
                                      (1, torch.bfloat16), (32, torch.bfloat16), (9, torch.float32),
-                                     (80, torch.bfloat16)])
+                                     (80, torch.bfloat16), (5, torch.bfloat16), (40, torch.float32)])
 def test_attn_in(device, oracle, layer, rows, dt):
     lay, w, g_in, _ = layer
     x, xt = acts(oracle, rows, HIDDEN, 0x58 + 5 + rows, dt, device)
@@ -90,7 +90,8 @@ def test_attn_in_fused_paths_need_no_workspace(layer):
 
 @pytest.mark.parametrize("rows,dt", [(1, torch.float32), (2, torch.float32), (3, torch.float32), (4, torch.float32),
                                      (2, torch.bfloat16), (32, torch.bfloat16), (64, torch.bfloat16),
-                                     (7, torch.float32), (80, torch.bfloat16)])
+                                     (7, torch.float32), (80, torch.bfloat16), (5, torch.bfloat16),
+                                     (40, torch.float32)])
 def test_attn_out_mlp(device, oracle, layer, rows, dt):
     lay, w, _, g_post = layer
     x, xt = acts(oracle, rows, HIDDEN, 0x5800 + rows, dt, device)
