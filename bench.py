@@ -688,7 +688,13 @@ def cpu_baseline(sample_s: float) -> dict:
         if time.perf_counter() - t0 >= sample_s:
             break
     dt = (time.perf_counter() - t0) / iters
+    # the same step with the matmul on one thread too (the dequantize already is)
+    t0 = time.perf_counter()
+    w = O.dequantize_packed(packed, v.size, None, q, sos)
+    O.linear_f32(x, w, d_in, d_out, threads=1)
+    dt1 = time.perf_counter() - t0
     return {"value": round(gemv_bytes(d_in, d_out, dq=True) / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
+            "value_one_thread": round(gemv_bytes(d_in, d_out, dq=True) / dt1 / 1e9, 4),
             "cpu_model": cpu_model(), "kind": "port",
             "sample": f"{iters} x config-2 GEMV (1-thread dequantize of the 4096x11008 DQ weight + {threads}-thread "
                       f"f32 GEMV), {dt * 1e3:.1f} ms each; oracle/nf4_oracle.c restatement of "
@@ -731,7 +737,7 @@ def cpu_beside() -> dict:
     x = O.fill_normal(0x5A, 1.0, rows * K).reshape(rows, K)
     a = O.fill_normal(0x41, 0.01, K * r).reshape(K, r)
     b = O.fill_normal(0x42, 0.01, r * N).reshape(r, N)
-    t0 = time.perf_counter()
+    t0 = t0_deq = time.perf_counter()
     O.dequantize_packed(packed, n, absmax)                           # per forward, serial
     t1 = time.perf_counter()
     O.linear_f32(x, w, K, N, threads=threads)                        # base, all cores
@@ -742,6 +748,17 @@ def cpu_beside() -> dict:
     flops = 2 * M * N * K + 2 * M * K * r + 2 * M * r * N
     out["qlora_gemm_config3"] = {"s": round(total, 3), "tflops": round(flops / total / 1e12, 5),
                                  "sample": f"{rows} of {M} rows timed, scaled", "threads": threads}
+    # the matmuls on one thread (a 4-row sample, scaled)
+    rows1 = 4
+    t0 = time.perf_counter()
+    O.linear_f32(x[:rows1], w, K, N, threads=1)
+    xa1 = O.linear_f32(x[:rows1], a, K, r, threads=1)
+    O.linear_f32(xa1, b, r, N, threads=1)
+    t2 = time.perf_counter()
+    total1 = (t1 - t0_deq) + (t2 - t0) * (M / rows1)
+    out["qlora_gemm_config3_one_thread"] = {"s": round(total1, 3), "tflops": round(flops / total1 / 1e12, 5),
+                                            "sample": f"{rows1} of {M} rows timed, scaled; dequantize as above",
+                                            "threads": 1}
     return out
 
 
