@@ -284,9 +284,18 @@ int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const un
  * the weight expanded to bf16 (with the adapter merged) and a BLAS GEMM;
  * f32 dy through the f32 dequantized weight.  The adapter gradients are
  * summed over the rows in a fixed order (deterministic); when dx takes the
- * BLAS path they run on the branch stream beside its GEMM. */
+ * BLAS path they run on the branch stream beside its GEMM.
+ * A workspace smaller than the default size but at least the minimum size
+ * below selects, for a striped weight with bf16 dy, d_in a multiple of 128
+ * and 16-byte aligned dy and dx, the fused NF4 MFMA kernel for dx: W's rows
+ * are its outputs and each W tile is dequantized on chip, so the only
+ * scratch is the adapter's bf16 operands (dx gains ((dy scaling) B^T) A^T
+ * in the kernel's epilogue, the adapter unmerged); for other weights and
+ * shapes the minimum is the default size. */
 uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
                                                    uint32_t lora_rank);
+uint64_t unifur_nf4_linear_backward_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
+                                                       uint32_t lora_rank);
 int unifur_nf4_linear_backward(const void *dy, int dy_dtype, uint64_t rows, const unifur_nf4_weight *w,
                                const unifur_nf4_lora *lora, const void *x, int x_dtype, void *dx, int dx_dtype,
                                float *grad_a, float *grad_b, void *workspace, uint64_t workspace_bytes,

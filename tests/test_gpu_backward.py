@@ -144,3 +144,67 @@ def test_gradients_only_and_empty_batch(device, oracle):
     lo = ad.struct()
     assert L.lib().unifur_nf4_linear_backward(dyt_.data_ptr(), L.F32, M, ctypes.byref(w), ctypes.byref(lo), None,
                                               L.F32, None, L.F32, g.data_ptr(), None, None, 0, st) == L.ERR_INVALID
+
+
+@pytest.mark.parametrize("case", [
+    # (M, K = d_in, N = d_out, r, dq, dx dtype): K a multiple of 128 (the
+    # fused kernel's output tiles), N of 64
+    (2048, 4096, 4096, 16, True, torch.bfloat16),   # the config-3 shapes in reverse
+    (300, 896, 4864, 16, True, torch.float32),      # a config-5 down-projection-shaped weight, ragged rows
+    (65, 1024, 512, 8, False, torch.float32),       # f32 block scales, one row tile
+    (257, 512, 1024, 64, True, torch.bfloat16),     # rank 64, rows past a 256-row tile
+])
+def test_fused_dx_with_the_minimum_workspace(device, oracle, case):
+    """A workspace too small for the expanded weight: dx through the fused
+    NF4 MFMA kernel over the striped weight's rows (the adapter term in its
+    epilogue), against the same float64 formulas and bars as the expanded
+    path, and the gradients unchanged."""
+    M, K, N, r, dq, dxt = case
+    lin, wdeq = make_linear(oracle, K, N, 1700 + M, device, dq=dq, striped=True)
+    s = 16.0 / r
+    a, b, ad = lora_parts(oracle, K, N, r, 1701 + r, device, scaling=s)
+    x, xt = acts(oracle, M, K, 1702, torch.bfloat16, device)
+    dy, dyt_ = acts(oracle, M, N, 1703, torch.bfloat16, device)
+    lib = L.lib()
+    need = lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r)
+    full = lib.unifur_nf4_linear_backward_workspace_size(M, K, N, L.BF16, r)
+    # the default size holds the expanded bf16 weight; the minimum does not
+    # (its scratch: the adapter's operands and the gradients')
+    assert need <= full - K * N * 2, (need, full)
+    ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)
+    ql = Q.QloraLinear(lin, ad)
+    dx, ga, gb = ql.backward(xt, dyt_, dx_dtype=dxt, workspace=ws[:need])
+    rdx, bdx, rga, bga, rgb, bgb = refs(x, dy, wdeq, a, b, s)
+    e_dx = normwise(dx.float().cpu(), rdx, bdx)
+    e_ga, e_gb = normwise(ga.cpu(), rga, bga), normwise(gb.cpu(), rgb, bgb)
+    print(f"fused dx {case}: dx {e_dx:.2e} grad_a {e_ga:.2e} grad_b {e_gb:.2e} (workspace {need} B)", flush=True)
+    assert e_dx <= 1e-2 and e_ga <= 1e-5 and e_gb <= 1e-5
+    # deterministic, and the expanded path agrees to the bf16 bar
+    dx2, _, _ = ql.backward(xt, dyt_, dx_dtype=dxt, workspace=ws[:need])
+    assert torch.equal(dx, dx2)
+    dxe, _, _ = ql.backward(xt, dyt_, dx_dtype=dxt)
+    assert normwise(dx.float().cpu(), dxe.float().cpu().numpy(), bdx) <= 2e-2
+    if need >= 256:
+        with pytest.raises(RuntimeError):
+            ql.backward(xt, dyt_, dx_dtype=dxt, workspace=ws[:need - 256])
+
+
+@pytest.mark.parametrize("M,work", [(64, 0), (64, 4 << 20), (512, 0)])
+def test_fused_dx_without_adapter(device, oracle, M, work):
+    """The base dx = dy W^T through the fused kernel: with no scratch at all
+    (whole d_out per tile) and with room for its split-K partials (64 rows
+    leave most CUs idle: d_out split, partials added in order)."""
+    K, N = 1024, 4096
+    lin, wdeq = make_linear(oracle, K, N, 1750 + M, device)
+    dy, dyt_ = acts(oracle, M, N, 1751, torch.bfloat16, device)
+    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, 0)
+    assert need <= 65536  # the workspace's fixed counter region only
+    size = max(work, need)
+    ws = torch.zeros(size, dtype=torch.uint8, device=device)
+    dx = lin.backward(dyt_, dx_dtype=torch.float32, workspace=ws)
+    ref = np.asarray(dy, np.float64) @ np.asarray(wdeq, np.float64).T
+    bound = np.abs(np.asarray(dy, np.float64)) @ np.abs(np.asarray(wdeq, np.float64)).T
+    e = normwise(dx.cpu(), ref, bound)
+    print(f"fused dx base M={M} workspace={work}: {e:.2e}", flush=True)
+    assert e <= 1e-2
+    assert torch.equal(dx, lin.backward(dyt_, dx_dtype=torch.float32, workspace=ws))

@@ -106,6 +106,7 @@ SIGNATURES = {
     "unifur_nf4_linear_forward_multi": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), _P, _P, _I,
                                              ctypes.c_uint32, _P, _U64, _P]),
     "unifur_nf4_linear_backward_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
+    "unifur_nf4_linear_backward_min_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
     "unifur_nf4_linear_backward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Lora), _P, _I,
                                         _P, _I, _P, _P, _P, _U64, _P]),
     "unifur_nf4_linear_min_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),

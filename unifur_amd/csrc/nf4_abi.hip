@@ -776,20 +776,43 @@ Branch branch_for(hipStream_t stream) {
 // generic dequantize (+ merge) and f32 GEMM; the adapter gradients through
 // x A, dY B^T and two row reductions.
 struct BackwardLayout {
-  bool blas;
-  size_t wt, blas_ws, wf32, rm_codes, rm_scales, grads, xa, u, partials, total;
+  bool blas, fused;
+  int splits;  // fused dX: d_out slabs (1: none)
+  size_t wt, blas_ws, wf32, rm_codes, rm_scales, lora_at, lora_bt, lora_xa, dx_partials, grads, xa, u, partials, total;
 };
 
+// dX paths: the weight expanded to bf16 once and a BLAS GEMM (blas), the
+// fused NF4 MFMA kernel over the striped weight's rows (fused: only the
+// adapter's bf16 operands, or split-K partials, as scratch), or the generic
+// f32 dequantize + GEMM.  allow_blas = false picks the fused kernel where it
+// applies (a workspace too small for the expanded weight); allow_split =
+// false leaves out its split-K partials.
 BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t rank, int dy_dtype, bool want_dx,
-                             bool want_grads, bool striped, int scale_kind, bool aligned) {
+                             bool want_grads, bool striped, int scale_kind, bool aligned, bool allow_blas = true,
+                             bool allow_split = true) {
   BackwardLayout L{};
+  L.splits = 1;
   Carver c;
   if (want_dx) {
-    L.blas = dy_dtype == UNIFUR_NF4_BF16 && aligned && rows <= 0x7fffffffu && d_in <= 0x7fffffffu &&
-             d_out <= 0x7fffffffu && expand_supported((int)d_in, (int)d_out, (int)rank);
+    const bool sizes = rows <= 0x7fffffffu && d_in <= 0x7fffffffu && d_out <= 0x7fffffffu;
+    const bool bf = dy_dtype == UNIFUR_NF4_BF16 && aligned && sizes;
+    L.blas = allow_blas && bf && expand_supported((int)d_in, (int)d_out, (int)rank);
+    // the dX GEMM's shape: M = rows, reduction d_out, outputs d_in
+    L.fused = !L.blas && bf && striped && rank <= 64 && rows >= 1 &&
+              gemm_supported((int)rows, (int)d_out, (int)d_in, reinterpret_cast<const void*>(uintptr_t{256}));
     if (L.blas) {
       L.wt = c.take(d_in * d_out * sizeof(uint16_t));
       L.blas_ws = c.take(kBlasWorkspace);
+    } else if (L.fused) {
+      if (rank) {
+        const uint64_t pad = (uint64_t)lora_pad((int)rank);
+        L.lora_at = c.take(pad * d_out * sizeof(uint16_t));
+        L.lora_bt = c.take(d_in * pad * sizeof(uint16_t));
+        L.lora_xa = c.take(rows * pad * sizeof(uint16_t));
+      } else if (allow_split) {
+        L.splits = gemm_k_splits((int)rows, (int)d_out, (int)d_in);
+        if (L.splits > 1) L.dx_partials = c.take((size_t)L.splits * rows * d_in * sizeof(float));
+      }
     } else {
       L.wf32 = c.take(d_in * d_out * sizeof(float));
       if (striped) {
@@ -839,8 +862,18 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
   const uint64_t K = w->d_in, N = w->d_out;
   UNIFUR_ARG(K <= 0x7fffffffu && N <= 0x7fffffffu, "weight too large");
   const bool aligned = aligned_to(dy, 16) && aligned_to(dx, 16);
-  const BackwardLayout L = plan_backward(rows, K, N, rank, dy_dtype, want_dx && rows > 0, want_grads, is_striped(w),
-                                         w->scales.kind, aligned);
+  BackwardLayout L = plan_backward(rows, K, N, rank, dy_dtype, want_dx && rows > 0, want_grads, is_striped(w),
+                                   w->scales.kind, aligned);
+  if (L.blas && workspace && workspace_bytes < L.total) {
+    // a workspace too small for the expanded weight: the fused dX kernel,
+    // with its split-K partials if they fit
+    BackwardLayout lean = plan_backward(rows, K, N, rank, dy_dtype, true, want_grads, is_striped(w), w->scales.kind,
+                                        aligned, false);
+    if (lean.fused && workspace_bytes < lean.total)
+      lean = plan_backward(rows, K, N, rank, dy_dtype, true, want_grads, is_striped(w), w->scales.kind, aligned,
+                           false, false);
+    if (lean.fused && workspace_bytes >= lean.total) L = lean;
+  }
   void* ws = nullptr;
   if (int r = resolve_workspace(workspace, workspace_bytes, L.total, stream, &ws)) return r;
   const bool dybf = dy_dtype == UNIFUR_NF4_BF16, xbf = x_dtype == UNIFUR_NF4_BF16;
@@ -885,6 +918,18 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       }
       grads_done = forked;
       UNIFUR_HIP(e);
+    } else if (L.fused) {
+      const uint16_t* dyb = static_cast<const uint16_t*>(dy);
+      uint16_t *xa16 = nullptr, *bt16 = nullptr;
+      if (lora) {
+        xa16 = at<uint16_t>(ws, L.lora_xa);
+        bt16 = at<uint16_t>(ws, L.lora_bt);
+        UNIFUR_HIP(launch_lora_operands_dx(dyb, lora->a, lora->b, m, k, n, (int)rank, lora->scaling,
+                                           at<uint16_t>(ws, L.lora_at), bt16, xa16, stream));
+      }
+      UNIFUR_HIP(launch_gemm_dx(dyb, w->packed, to_scales(w->scales), m, k, n, xa16, bt16, (int)rank, dx,
+                                dx_dtype == UNIFUR_NF4_BF16, stream, L.splits,
+                                L.splits > 1 ? at<float>(ws, L.dx_partials) : nullptr));
     } else {
       const uint8_t* packed = nullptr;
       ScalesArg scales{};
@@ -1461,6 +1506,19 @@ uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in,
       need = std::max<uint64_t>(need, plan_backward(rows, d_in, d_out, lora_rank, dy_dtype, rows > 0, lora_rank > 0,
                                                     striped && d_out % 64 == 0, kind, true)
                                           .total);
+  return need;
+}
+
+uint64_t unifur_nf4_linear_backward_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
+                                                       uint32_t lora_rank) {
+  if (d_in == 0 || d_out == 0) return 0;
+  uint64_t need = 0;
+  for (int kind = 0; kind < 2; ++kind) {
+    const BackwardLayout L = plan_backward(rows, d_in, d_out, lora_rank, dy_dtype, rows > 0, lora_rank > 0,
+                                           d_out % 64 == 0, kind, true, false, false);
+    if (rows > 0 && !L.fused) return unifur_nf4_linear_backward_workspace_size(rows, d_in, d_out, dy_dtype, lora_rank);
+    need = std::max<uint64_t>(need, L.total);
+  }
   return need;
 }
 

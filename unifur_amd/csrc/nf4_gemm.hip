@@ -246,6 +246,72 @@ __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int
   store_b_at<DQ, STRIPED>(B, smem, kLdsB, kLdsLut, kLdsDq, buf, d, dq_table);
 }
 
+// TRANS (dX = dY W^T over a striped weight W [d_in][d_out]): the tile's 128
+// outputs are W rows w.n .. w.n + 127 and a K step is W columns k0 .. k0 +
+// 63, one block.  Producer thread d takes stripe k0 / 16 + d / 64 (16
+// columns) of rows w.n + 2 (d % 64) and the next -- 8 code bytes each,
+// consecutive in the stripe -- and the two rows' scales of that block
+// (block-major, also consecutive); g.N is d_in here.
+template <bool DQ>
+__device__ __forceinline__ void load_bt(BStep& B, const GemmArgs& g, const BSrc& w, int k0, int d) {
+  const int r = w.n + 2 * (d & 63);
+  const uint8_t* cp = w.packed + ((size_t)(k0 / 16 + (d >> 6)) * g.N + r) * 8;
+  const u32x2 r0 = *reinterpret_cast<const u32x2*>(cp);
+  const u32x2 r1 = *reinterpret_cast<const u32x2*>(cp + 8);
+  B.code[0] = r0.x;
+  B.code[1] = r0.y;
+  B.code[2] = r1.x;
+  B.code[3] = r1.y;
+  const size_t blk = (size_t)(k0 / kBlock) * g.N + r;
+  if constexpr (DQ) {
+    // the aligned dword holding both rows' u8 codes: blk % 4 == r % 4 == 2 (d % 2)
+    B.scale[0] = *reinterpret_cast<const uint32_t*>(w.scales.dq_codes + (blk & ~size_t{3}));
+    B.scale[1] = 0u;
+  } else {
+    const u32x2 s2 = *reinterpret_cast<const u32x2*>(w.scales.absmax + blk);
+    B.scale[0] = s2.x;
+    B.scale[1] = s2.y;
+  }
+}
+
+// ... and its tile rows 2 (d % 64), + 1: byte j of a row holds columns 2j
+// (low nibble) and 2j + 1, i.e. k and k + 1 of the tile row, so each level
+// pair times the row's scale is one bf16 dword and the 16 values of a row
+// are the two 16-byte chunks 2 (d / 64), + 1 of that row.
+template <bool DQ>
+__device__ __forceinline__ void store_bt(const BStep& B, unsigned char* smem, int buf, int d) {
+  static_assert(kLutMode == 0, "the transposed producer reads the one-copy byte LUT");
+  const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq);
+  float sc[2];
+  if constexpr (DQ) {
+    const int sh = 16 * (d & 1);
+    sc[0] = dq_lut[(B.scale[0] >> sh) & 0xffu];
+    sc[1] = dq_lut[(B.scale[0] >> (sh + 8)) & 0xffu];
+  } else {
+    sc[0] = __uint_as_float(B.scale[0]);
+    sc[1] = __uint_as_float(B.scale[1]);
+  }
+  f32x2 l[2][8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t byte = (B.code[2 * r + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+      l[r][j] = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + byte * 8));
+    }
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // the 16 LUT reads first
+  __builtin_amdgcn_sched_group_barrier(0x002, 64, 1);  // then VALU
+  const int base = kLdsB + buf * kBTileBytes, row = 2 * (d & 63), ch = 2 * (d >> 6);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = pack_bf16x2(l[r][j].x * sc[r], l[r][j].y * sc[r]);
+    *reinterpret_cast<lds_u32x4*>((size_t)lds_addr(base, row + r, ch)) = u32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<lds_u32x4*>((size_t)lds_addr(base, row + r, ch + 1)) = u32x4{v[4], v[5], v[6], v[7]};
+  }
+}
+
 __device__ __forceinline__ bf16x8 read_frag(int base, int row, int chunk) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<lds_u32x4*>((size_t)lds_addr(base, row, chunk)));
 }
@@ -459,9 +525,10 @@ __device__ __forceinline__ void finish_tile(const GemmArgs& g, f32x16 (&acc)[2][
 // after the producers wrote step s + 2 and the MFMA waves read the last of
 // step s; X needs none (each MFMA wave reads only the rows it copied itself,
 // after waiting for its own copies).
-template <bool DQ, bool YBF16, bool LORA, bool STRIPED, bool PAIR>
+template <bool DQ, bool YBF16, bool LORA, bool STRIPED, bool PAIR, bool TRANS = false>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   static_assert(!(PAIR && LORA), "the SwiGLU pair has no adapter");
+  static_assert(!TRANS || (STRIPED && !PAIR), "the transposed weight is striped, one weight");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -508,24 +575,33 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     // waves with d < 128 read gate, the others up (each wave one weight)
     const int st = d >> 5;
     const bool second = PAIR && st >= 4;
-    const BSrc src{second ? g.packed2 : g.packed, second ? g.scales2 : g.scales, n0 + 16 * (PAIR ? st & 3 : st)};
+    const BSrc src{second ? g.packed2 : g.packed, second ? g.scales2 : g.scales,
+                   TRANS ? n0 : n0 + 16 * (PAIR ? st & 3 : st)};
     const int dqt = second ? 1 : 0;
+    auto ld = [&](BStep& B, int k0) {
+      if constexpr (TRANS) load_bt<DQ>(B, g, src, k0, d);
+      else load_b<DQ, STRIPED>(B, g, src, k0, d);
+    };
+    auto st_b = [&](const BStep& B, int buf) {
+      if constexpr (TRANS) store_bt<DQ>(B, smem, buf, d);
+      else store_b<DQ, STRIPED>(B, smem, buf, d, dqt);
+    };
     BStep Br[kBRing];
 #pragma unroll
-    for (int r = 0; r < kBRing; ++r) load_b<DQ, STRIPED>(Br[r], g, src, kbase + min(r, nk - 1) * kBK, d);
+    for (int r = 0; r < kBRing; ++r) ld(Br[r], kbase + min(r, nk - 1) * kBK);
     lds_barrier();  // LUTs visible
-    store_b<DQ, STRIPED>(Br[0], smem, 0, d, dqt);
-    load_b<DQ, STRIPED>(Br[0], g, src, kbase + min(kBRing, nk - 1) * kBK, d);
+    st_b(Br[0], 0);
+    ld(Br[0], kbase + min(kBRing, nk - 1) * kBK);
     if (nk > 1) {
-      store_b<DQ, STRIPED>(Br[1], smem, 1, d, dqt);
-      load_b<DQ, STRIPED>(Br[1], g, src, kbase + min(kBRing + 1, nk - 1) * kBK, d);
+      st_b(Br[1], 1);
+      ld(Br[1], kbase + min(kBRing + 1, nk - 1) * kBK);
     }
     lds_barrier();  // steps 0 and 1 ready
     // step t2 (from 2 on) into W buffer t2 % 3 from ring slot t2 % kBRing,
     // then the barrier that publishes it
     auto produce = [&](int t2, int slot) {
-      store_b<DQ, STRIPED>(Br[slot], smem, t2 % kBStages, d, dqt);
-      load_b<DQ, STRIPED>(Br[slot], g, src, kbase + min(t2 + kBRing, nk - 1) * kBK, d);
+      st_b(Br[slot], t2 % kBStages);
+      ld(Br[slot], kbase + min(t2 + kBRing, nk - 1) * kBK);
       lds_barrier();
     };
     int t2 = 2;
@@ -603,21 +679,21 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   finish_tile<YBF16, LORA, PAIR>(g, acc, yout, row0, n0, lane, (uint32_t)awave, (uint32_t)(awave + kATileBytes));
 }
 
-template <bool DQ, bool YBF16, bool LORA, bool STRIPED, bool PAIR = false>
+template <bool DQ, bool YBF16, bool LORA, bool STRIPED, bool PAIR = false, bool TRANS = false>
 hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
   static std::atomic<uint64_t> done{0};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   const uint64_t bit = 1ull << (dev & 63);
-  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR>);
+  const void* fn = reinterpret_cast<const void*>(&gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR, TRANS>);
   if (!(done.load(std::memory_order_acquire) & bit)) {
     e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmSmem);
     if (e != hipSuccess) return e;
     done.fetch_or(bit, std::memory_order_acq_rel);
   }
   const int grid = ((g.M + kBM - 1) / kBM) * g.tiles_n * g.k_splits;
-  gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
+  gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR, TRANS><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
   return hipGetLastError();
 }
 
@@ -637,13 +713,19 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
 //     from memory, eight steps of 16-byte loads in flight) and add their
 //     slices through LDS in wave order.
 
-__global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ a, const float* __restrict__ b,
-                                                        int K, int N, int rank, int pad, uint16_t* __restrict__ at,
+// The two factors are read through strides: element (k, j) of the first
+// at a[k sak + j saj], element (j, n) of the second at b[j sbj + n sbn]
+// (A [K][r] and B [r][N] as stored for the forward; B read as B^T and A as
+// A^T for dX = dY W^T, whose adapter term is ((dY scaling) B^T) A^T).
+__global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ a, size_t sak, size_t saj,
+                                                        const float* __restrict__ b, size_t sbj, size_t sbn, int K,
+                                                        int N, int rank, int pad, uint16_t* __restrict__ at,
                                                         uint16_t* __restrict__ bt) {
   const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (t < K) {
-    const float* row = a + (size_t)t * rank;  // A[t][0 .. rank)
-    for (int j = 0; j < pad; ++j) at[(size_t)j * K + t] = j < rank ? (uint16_t)(pack_bf16x2(row[j], 0.0f) & 0xffffu) : 0;
+    const float* row = a + (size_t)t * sak;  // first factor's row t
+    for (int j = 0; j < pad; ++j)
+      at[(size_t)j * K + t] = j < rank ? (uint16_t)(pack_bf16x2(row[(size_t)j * saj], 0.0f) & 0xffffu) : 0;
   } else if (t < K + N) {
     const int n = t - K;
     for (int c0 = 0; c0 < pad; c0 += 16) {
@@ -651,7 +733,8 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict_
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int r0 = c0 + 2 * j, r1 = r0 + 1;
-        w[j] = pack_bf16x2(r0 < rank ? b[(size_t)r0 * N + n] : 0.0f, r1 < rank ? b[(size_t)r1 * N + n] : 0.0f);
+        w[j] = pack_bf16x2(r0 < rank ? b[(size_t)r0 * sbj + (size_t)n * sbn] : 0.0f,
+                           r1 < rank ? b[(size_t)r1 * sbj + (size_t)n * sbn] : 0.0f);
       }
       u32x4* dst = reinterpret_cast<u32x4*>(bt + (size_t)n * pad + c0);
       dst[0] = u32x4{w[0], w[1], w[2], w[3]};
@@ -724,11 +807,15 @@ bool gemm_supported(int M, int K, int N, const void* x) {
 
 int lora_pad(int rank) { return (rank + 15) / 16 * 16; }
 
-hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* b, int M, int K, int N, int rank,
-                                float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa, hipStream_t stream) {
+namespace {
+
+hipError_t lora_operands(const uint16_t* x, const float* a, size_t sak, size_t saj, const float* b, size_t sbj,
+                         size_t sbn, int M, int K, int N, int rank, float scaling, uint16_t* at, uint16_t* bt,
+                         uint16_t* xa, hipStream_t stream) {
   if (rank < 1 || rank > 64 || K % 64 != 0) return hipErrorInvalidValue;
   const int pad = lora_pad(rank);
-  lora_prep_kernel<<<(unsigned)((K + N + 255) / 256), 256, 0, stream>>>(a, b, K, N, rank, pad, at, bt);
+  lora_prep_kernel<<<(unsigned)((K + N + 255) / 256), 256, 0, stream>>>(a, sak, saj, b, sbj, sbn, K, N, rank, pad,
+                                                                        at, bt);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // rows per workgroup: 16 while that covers the CUs, else 8 or 4
@@ -741,6 +828,21 @@ hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* 
   else
     lora_xa_kernel<4><<<dim3((unsigned)((M + 3) / 4), cols), block, 0, stream>>>(x, at, M, K, pad, scaling, xa);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* b, int M, int K, int N, int rank,
+                                float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa, hipStream_t stream) {
+  return lora_operands(x, a, (size_t)rank, 1, b, (size_t)N, 1, M, K, N, rank, scaling, at, bt, xa, stream);
+}
+
+hipError_t launch_lora_operands_dx(const uint16_t* dy, const float* a, const float* b, int M, int d_in, int d_out,
+                                   int rank, float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa,
+                                   hipStream_t stream) {
+  // first factor B^T [d_out][r] (B [r][d_out] read by columns), second A^T
+  // [r][d_in] (A [d_in][r] read by columns); K = d_out, N = d_in
+  return lora_operands(dy, b, 1, (size_t)d_out, a, 1, (size_t)rank, M, d_out, d_in, rank, scaling, at, bt, xa, stream);
 }
 
 namespace {
@@ -907,6 +1009,45 @@ hipError_t launch_gemm_pair(const uint16_t* x, const uint8_t* gate_packed, const
   splitk_silu_reduce_kernel<<<reduce_blocks(mn4), 256, 0, stream>>>(partials, k_splits, (size_t)M * 2 * N,
                                                                      (uint32_t)(N / 4), mn4, h);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_dx(const uint16_t* dy, const uint8_t* packed, const ScalesArg& scales, int M, int d_in, int d_out,
+                          const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* dx, bool dx_bf16,
+                          hipStream_t stream, int k_splits, float* partials) {
+  // outputs d_in (128-column tiles of W rows), reduction d_out (64-column blocks of W)
+  if (!splits_ok(d_out, k_splits) || d_in % kBN != 0 ||
+      (k_splits > 1 && (!partials || lora_xa || (reinterpret_cast<uintptr_t>(dx) & 15u) != 0)))
+    return hipErrorInvalidValue;
+  GemmArgs g = gemm_args(dy, packed, scales, M, d_out, d_in, dx, dx_bf16, k_splits, partials);
+  g.lora_xa = lora_xa;
+  g.lora_bt = lora_bt;
+  g.lora_rank = lora_rank;
+  g.lora_pad = lora_pad(lora_rank);
+  const bool dq = scales.kind == kScalesDQ;
+  if (k_splits > 1) {
+    g.y_bf16 = 0;
+    g.y_aligned = 1;
+    hipError_t e = dq ? launch_g<true, false, false, true, false, true>(g, stream)
+                      : launch_g<false, false, false, true, false, true>(g, stream);
+    if (e != hipSuccess) return e;
+    const size_t mn4 = (size_t)M * d_in / 4;
+    splitk_reduce_kernel<<<reduce_blocks(mn4), 256, 0, stream>>>(partials, k_splits, mn4, d_in / 4, nullptr, dx,
+                                                                 dx_bf16);
+    return hipGetLastError();
+  }
+  const bool lora = lora_xa != nullptr;
+#define UNIFUR_GEMM_DX_CASE(D, B, R) \
+  if (dq == D && dx_bf16 == B && lora == R) return launch_g<D, B, R, true, false, true>(g, stream);
+  UNIFUR_GEMM_DX_CASE(true, true, true)
+  UNIFUR_GEMM_DX_CASE(true, true, false)
+  UNIFUR_GEMM_DX_CASE(true, false, true)
+  UNIFUR_GEMM_DX_CASE(true, false, false)
+  UNIFUR_GEMM_DX_CASE(false, true, true)
+  UNIFUR_GEMM_DX_CASE(false, true, false)
+  UNIFUR_GEMM_DX_CASE(false, false, true)
+  UNIFUR_GEMM_DX_CASE(false, false, false)
+#undef UNIFUR_GEMM_DX_CASE
+  return hipErrorInvalidValue;
 }
 
 }  // namespace unifur

@@ -42,6 +42,22 @@ hipError_t launch_gemm_pair(const uint16_t* x, const uint8_t* gate_packed, const
                             const uint8_t* up_packed, const ScalesArg& up_scales, int M, int K, int N, uint16_t* h,
                             bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr);
 
+// dX[M, d_in] = dY[M, d_out] deq(W)^T (+ lora_xa lora_bt^T) for a striped
+// weight W [d_in, d_out] (d_in a multiple of 128): the fused kernel with the
+// weight's rows as its outputs, each W tile dequantized once per 256 rows of
+// dY.  The adapter operands come from launch_lora_operands_dx; k_splits as
+// in launch_gemm (split over d_out, no adapter).
+hipError_t launch_gemm_dx(const uint16_t* dy, const uint8_t* packed, const ScalesArg& scales, int M, int d_in, int d_out,
+                          const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* dx, bool dx_bf16,
+                          hipStream_t stream, int k_splits = 1, float* partials = nullptr);
+
+// The adapter operands of dX's epilogue: dX gains ((dY scaling) B^T) A^T,
+// so at = B [pad][d_out] and bt = A [d_in][pad] in bf16, and xa =
+// bf16(scaling dY B^T) [M][pad]; d_out a multiple of 64.
+hipError_t launch_lora_operands_dx(const uint16_t* dy, const float* a, const float* b, int M, int d_in, int d_out,
+                                   int rank, float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa,
+                                   hipStream_t stream);
+
 // d_in slabs the fused GEMM splits into for this shape (1: no split); pair:
 // the gate/up pair launch over two [K, N] weights.
 int gemm_k_splits(int M, int K, int N, bool pair = false);

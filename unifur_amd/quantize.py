@@ -427,7 +427,7 @@ class Nf4Linear:
     __call__ = forward
 
     def _backward(self, dy: torch.Tensor, lora: Optional[LoraAdapter], x: Optional[torch.Tensor], want_dx: bool,
-                  dx_dtype: Optional[torch.dtype]):
+                  dx_dtype: Optional[torch.dtype], workspace: Optional[torch.Tensor] = None):
         _require_cuda(dy, "dy")
         if dy.shape[-1] != self._d_out:
             raise ValueError(f"dy has last dim {dy.shape[-1]}, the layer gives {self._d_out}")
@@ -454,14 +454,20 @@ class Nf4Linear:
             x.data_ptr() if x is not None else None, _dtype_code(x.dtype) if x is not None else L.F32,
             dx.data_ptr() if dx is not None else None, _dtype_code(dx.dtype) if dx is not None else L.F32,
             ga.data_ptr() if ga is not None else None, gb.data_ptr() if gb is not None else None,
-            None, 0, _stream()))
+            workspace.data_ptr() if workspace is not None else None,
+            workspace.numel() * workspace.element_size() if workspace is not None else 0, _stream()))
         return dx, ga, gb
 
-    def backward(self, dy: torch.Tensor, dx_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    def backward(self, dy: torch.Tensor, dx_dtype: Optional[torch.dtype] = None,
+                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
         """dL/dx = dy W^T for dy = dL/dy: the gradient burn's autodiff
         takes through the detached dequantized weight (src/qwennet.rs:238-241
-        under src/qwentrain.rs:421-470); the frozen weight gets none."""
-        return self._backward(dy, None, None, True, dx_dtype)[0]
+        under src/qwentrain.rs:421-470); the frozen weight gets none.
+        workspace: optional device buffer (the library's per-stream cache
+        when None); one below the default size, down to
+        unifur_nf4_linear_backward_min_workspace_size, takes the fused dX
+        kernel."""
+        return self._backward(dy, None, None, True, dx_dtype, workspace)[0]
 
 
 def quantize_linears(weights) -> list:
@@ -551,12 +557,13 @@ class QloraLinear:
     __call__ = forward
 
     def backward(self, x: torch.Tensor, dy: torch.Tensor, want_dx: bool = True,
-                 dx_dtype: Optional[torch.dtype] = None):
+                 dx_dtype: Optional[torch.dtype] = None, workspace: Optional[torch.Tensor] = None):
         """Vector-Jacobian products of forward for dy = dL/dy: returns
         (dx, grad_a, grad_b), dx = dy W^T + ((dy s) B^T) A^T,
         grad_b = (x A)^T (dy s), grad_a = x^T ((dy s) B^T) (f32); dx is None
-        when want_dx is False.  The base weight is frozen."""
-        return self.base._backward(dy, self.adapter, x, want_dx, dx_dtype)
+        when want_dx is False.  The base weight is frozen.  workspace as in
+        Nf4Linear.backward."""
+        return self.base._backward(dy, self.adapter, x, want_dx, dx_dtype, workspace)
 
 
 class QwenMlp:
