@@ -95,6 +95,40 @@ def test_backward_replays(device, oracle):
     replay_matches(run, lambda: outs)
 
 
+@pytest.mark.parametrize("rank", [0, 16])
+def test_fused_dx_backward_replays(device, oracle, rank):
+    """The bounded-workspace backward (dX through the fused NF4 kernel over
+    the weight's rows; its adapter operands or split-K partials in the
+    caller's workspace) replays to the eager bits."""
+    M, K, N = 96, 512, 1024
+    lin, _ = make_linear(oracle, K, N, 2060 + rank, device)
+    _, xt = acts(oracle, M, K, 2061, torch.bfloat16, device)
+    _, dyt = acts(oracle, M, N, 2062, torch.bfloat16, device)
+    from unifur_amd import _lib as L
+    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, rank)
+    # room for the split-K partials without the adapter, the minimum with it
+    ws = torch.zeros(max(need, 2 << 20) if rank == 0 else need, dtype=torch.uint8, device=device)
+    dx = torch.empty(M, K, device=device)
+    if rank:
+        _, _, ad = lora_parts(oracle, K, N, rank, 2063, device)
+        ql = Q.QloraLinear(lin, ad)
+        ga = torch.empty(K, rank, device=device)
+        gb = torch.empty(rank, N, device=device)
+
+        def run():
+            d, a_, b_ = ql.backward(xt, dyt, dx_dtype=torch.float32, workspace=ws)
+            dx.copy_(d)
+            ga.copy_(a_)
+            gb.copy_(b_)
+
+        replay_matches(run, lambda: [dx, ga, gb])
+    else:
+        def run():
+            dx.copy_(lin.backward(dyt, dx_dtype=torch.float32, workspace=ws))
+
+        replay_matches(run, lambda: [dx])
+
+
 def test_skinny_split_and_gemv_replay(device, oracle):
     # the skinny kernel's split-d_in hand-off (arrival counters) and the GEMV
     lin, _ = make_linear(oracle, 11008, 4096, 2030, device, striped=True)
