@@ -606,8 +606,19 @@ def bench_backward(torch, Q, L) -> dict:
                                                gb.data_ptr(), ws.data_ptr(), ws_bytes,
                                                torch.cuda.current_stream().cuda_stream))
 
+    # the same step with the least workspace: dx through the fused NF4 kernel
+    # over W's rows (no expanded weight, no BLAS call)
+    lean_bytes = lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r)
+    lean = torch.zeros(lean_bytes, dtype=torch.uint8, device=dev)
+
+    def step_lean(i: int) -> None:
+        L.check(lib.unifur_nf4_linear_backward(dy.data_ptr(), L.BF16, M, ctypes.byref(w), ctypes.byref(lo),
+                                               x.data_ptr(), L.BF16, dx.data_ptr(), L.BF16, ga.data_ptr(),
+                                               gb.data_ptr(), lean.data_ptr(), lean_bytes,
+                                               torch.cuda.current_stream().cuda_stream))
+
     res = {}
-    for name, fn in (("ms", step), ("grads_only_ms", grads_only)):
+    for name, fn in (("ms", step), ("grads_only_ms", grads_only), ("lean_ms", step_lean)):
         for i in range(3):
             fn(i)
         graph = capture(torch, fn, 4)
@@ -619,7 +630,10 @@ def bench_backward(torch, Q, L) -> dict:
     return {"ms": round(ms, 5), "tflops": round(flops / ms / 1e9, 1),
             "frac": round(flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
             "grads_only_ms": round(res["grads_only_ms"], 5),
-            "grads_only_gbs": round(grads_bytes / res["grads_only_ms"] / 1e6, 1)}
+            "grads_only_gbs": round(grads_bytes / res["grads_only_ms"] / 1e6, 1),
+            "fused_dx": {"ms": round(res["lean_ms"], 5), "tflops": round(flops / res["lean_ms"] / 1e9, 1),
+                         "workspace_bytes": lean_bytes, "default_workspace_bytes": ws_bytes,
+                         "path": "least workspace: dx through the fused NF4 MFMA kernel over W's rows"}}
 
 
 # ------------------------------------------------------ next: embedding ----
