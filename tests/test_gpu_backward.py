@@ -208,3 +208,32 @@ def test_fused_dx_without_adapter(device, oracle, M, work):
     print(f"fused dx base M={M} workspace={work}: {e:.2e}", flush=True)
     assert e <= 1e-2
     assert torch.equal(dx, lin.backward(dyt_, dx_dtype=torch.float32, workspace=ws))
+
+
+@pytest.mark.parametrize("M,K,N,r,work", [
+    (33, 128, 64, 4, 0),          # one output tile, one K step
+    (33, 128, 128, 3, 0),         # two K steps, odd rank
+    (1, 256, 192, 0, 0),          # one row, three K steps, no adapter
+    (40, 384, 1344, 0, 4 << 20),  # no adapter, split over d_out (21 K steps: a ragged last slab)
+])
+def test_fused_dx_edge_shapes(device, oracle, M, K, N, r, work):
+    """The fused dX kernel's producer prologue with one and two K steps, a
+    single output tile, one row, and a split whose last slab is short."""
+    lin, wdeq = make_linear(oracle, K, N, 1800 + K + N, device)
+    dy, dyt_ = acts(oracle, M, N, 1801, torch.bfloat16, device)
+    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r)
+    ws = torch.zeros(max(need, work, 256), dtype=torch.uint8, device=device)
+    ws = ws[:max(need, work)] if max(need, work) > 0 else ws[:1]
+    dy64, w64 = np.asarray(dy, np.float64), np.asarray(wdeq, np.float64)
+    if r:
+        s = 16.0 / r
+        a, b, ad = lora_parts(oracle, K, N, r, 1802, device, scaling=s)
+        x, xt = acts(oracle, M, K, 1803, torch.bfloat16, device)
+        dx, _, _ = Q.QloraLinear(lin, ad).backward(xt, dyt_, dx_dtype=torch.float32, workspace=ws)
+        rdx, bdx, _, _, _, _ = refs(x, dy, wdeq, a, b, s)
+    else:
+        dx = lin.backward(dyt_, dx_dtype=torch.float32, workspace=ws)
+        rdx, bdx = dy64 @ w64.T, np.abs(dy64) @ np.abs(w64).T
+    e = normwise(dx.cpu(), rdx, bdx)
+    print(f"fused dx edge M={M} K={K} N={N} r={r} workspace={ws.numel()}: {e:.2e}", flush=True)
+    assert e <= 1e-2
