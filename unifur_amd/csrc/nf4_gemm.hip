@@ -241,9 +241,74 @@ __device__ __forceinline__ void store_b_at(const BStep& B, unsigned char* smem, 
   }
 }
 
+// The same tile in 8-byte stores: lanes d and d ^ 1 (row pairs 2i and 2i + 1
+// of one stripe: rows 4i .. 4i + 3) swap half their codes and their row
+// scales by DPP, so that the even lane holds columns 0-7 and the odd lane
+// columns 8-15 of all four rows; each of a lane's 8 columns then has its 4
+// consecutive k in one bf16 quad, one ds_write_b64 (8 stores per step
+// instead of 16 dword stores).
+#ifndef UNIFUR_GEMM_STORE64
+#define UNIFUR_GEMM_STORE64 1
+#endif
+__device__ __forceinline__ uint32_t swap_lane_pair(uint32_t v) {
+  return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+}
+
+template <bool DQ, bool STRIPED>
+__device__ __forceinline__ void store_b64(const BStep& B, unsigned char* smem, int buf, int d, int dq_table) {
+  static_assert(kLutMode == 0, "the paired store reads the one-copy byte LUT");
+  const int st = d >> 5, rp = d & 31;
+  const bool odd = (d & 1) != 0;
+  const float* dq_lut = reinterpret_cast<const float*>(smem + kLdsDq + dq_table * 1024);
+  float s0, s1;  // this lane's rows 2 rp, 2 rp + 1
+  if constexpr (DQ && STRIPED) {
+    const int sh = 16 * (d & 1);
+    s0 = dq_lut[(B.scale[0] >> sh) & 0xffu];
+    s1 = dq_lut[(B.scale[0] >> (sh + 8)) & 0xffu];
+  } else if constexpr (DQ) {
+    s0 = dq_lut[B.scale[0] & 0xffu];
+    s1 = dq_lut[B.scale[1] & 0xffu];
+  } else {
+    s0 = __uint_as_float(B.scale[0]);
+    s1 = __uint_as_float(B.scale[1]);
+  }
+  // even lane keeps bytes 0-3 (columns 0-7) and sends bytes 4-7; odd the reverse
+  const uint32_t r0 = swap_lane_pair(odd ? B.code[0] : B.code[1]);
+  const uint32_t r1 = swap_lane_pair(odd ? B.code[2] : B.code[3]);
+  const float t0 = __uint_as_float(swap_lane_pair(__float_as_uint(s0)));
+  const float t1 = __uint_as_float(swap_lane_pair(__float_as_uint(s1)));
+  // rows 4i .. 4i + 3 (i = rp / 2): the even lane's own two, then its partner's
+  const uint32_t w[4] = {odd ? r0 : B.code[0], odd ? r1 : B.code[2], odd ? B.code[1] : r0, odd ? B.code[3] : r1};
+  const float sc[4] = {odd ? t0 : s0, odd ? t1 : s1, odd ? s0 : t0, odd ? s1 : t1};
+  f32x2 l[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      l[q][j] = *reinterpret_cast<lds_f32x2_c*>((size_t)(kLdsLut + ((w[q] >> (8 * j)) & 0xffu) * 8));
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // the 16 LUT reads
+  __builtin_amdgcn_sched_group_barrier(0x002, 64, 1);  // then VALU
+  const int base = kLdsB + buf * kBTileBytes;
+  const int k4 = 4 * (rp >> 1);                       // first of the 4 rows (k of the tile)
+  const int n0 = 16 * st + 8 * (d & 1);               // first of the lane's 8 columns
+  const uint32_t within = (uint32_t)(k4 & 7) * 2u;    // byte offset of k4 in its 16-byte chunk
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const u32x2 even = {pack_bf16x2(l[0][j].x * sc[0], l[1][j].x * sc[1]),
+                        pack_bf16x2(l[2][j].x * sc[2], l[3][j].x * sc[3])};  // column 2j
+    const u32x2 oddc = {pack_bf16x2(l[0][j].y * sc[0], l[1][j].y * sc[1]),
+                        pack_bf16x2(l[2][j].y * sc[2], l[3][j].y * sc[3])};  // column 2j + 1
+    *reinterpret_cast<lds_u32x2*>((size_t)(lds_addr(base, n0 + 2 * j, k4 >> 3) + within)) = even;
+    *reinterpret_cast<lds_u32x2*>((size_t)(lds_addr(base, n0 + 2 * j + 1, k4 >> 3) + within)) = oddc;
+  }
+}
+
 template <bool DQ, bool STRIPED>
 __device__ __forceinline__ void store_b(const BStep& B, unsigned char* smem, int buf, int d, int dq_table) {
-  store_b_at<DQ, STRIPED>(B, smem, kLdsB, kLdsLut, kLdsDq, buf, d, dq_table);
+  if constexpr (UNIFUR_GEMM_STORE64 && kLutMode == 0)
+    store_b64<DQ, STRIPED>(B, smem, buf, d, dq_table);
+  else
+    store_b_at<DQ, STRIPED>(B, smem, kLdsB, kLdsLut, kLdsDq, buf, d, dq_table);
 }
 
 // TRANS (dX = dY W^T over a striped weight W [d_in][d_out]): the tile's 128
