@@ -248,7 +248,7 @@ __device__ __forceinline__ void store_b_at(const BStep& B, unsigned char* smem, 
 // consecutive k in one bf16 quad, one ds_write_b64 (8 stores per step
 // instead of 16 dword stores).
 #ifndef UNIFUR_GEMM_STORE64
-#define UNIFUR_GEMM_STORE64 1
+#define UNIFUR_GEMM_STORE64 2
 #endif
 __device__ __forceinline__ uint32_t swap_lane_pair(uint32_t v) {
   return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
@@ -280,6 +280,57 @@ __device__ __forceinline__ void store_b64(const BStep& B, unsigned char* smem, i
   // rows 4i .. 4i + 3 (i = rp / 2): the even lane's own two, then its partner's
   const uint32_t w[4] = {odd ? r0 : B.code[0], odd ? r1 : B.code[2], odd ? B.code[1] : r0, odd ? B.code[3] : r1};
   const float sc[4] = {odd ? t0 : s0, odd ? t1 : s1, odd ? s0 : t0, odd ? s1 : t1};
+  if constexpr (UNIFUR_GEMM_STORE64 == 2) {
+    // second exchange, lanes d and d ^ 2 (rows 8g .. 8g + 3 and 8g + 4 ..
+    // 8g + 7, g = rp / 4): each keeps 4 of its 8 columns (the u16 half e =
+    // bit 1 of d of every row dword) and takes the partner's rows of them, so
+    // a lane holds 8 rows x 4 columns and a column's 8 k are one 16-byte store
+    const uint32_t e = (uint32_t)(d >> 1) & 1u;
+    const uint32_t ks = (2u * e) | ((2u * e + 1u) << 8) | ((4u + 2u * e) << 16) | ((5u + 2u * e) << 24);
+    const uint32_t ss = ks ^ 0x02020202u;  // the other half
+    const uint32_t k01 = __builtin_amdgcn_perm(w[1], w[0], ks), k23 = __builtin_amdgcn_perm(w[3], w[2], ks);
+    const uint32_t r01 = __builtin_amdgcn_update_dpp(0u, __builtin_amdgcn_perm(w[1], w[0], ss), 0x4E, 0xF, 0xF, false);
+    const uint32_t r23 = __builtin_amdgcn_update_dpp(0u, __builtin_amdgcn_perm(w[3], w[2], ss), 0x4E, 0xF, 0xF, false);
+    float so[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      so[q] = __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(sc[q]), 0x4E, 0xF, 0xF, false));
+    // rows 8g + 2p, 8g + 2p + 1 in dword p (low, high u16)
+    const uint32_t D[4] = {e ? r01 : k01, e ? r23 : k23, e ? k01 : r01, e ? k23 : r23};
+    float s8[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      s8[q] = e ? so[q] : sc[q];
+      s8[4 + q] = e ? sc[q] : so[q];
+    }
+    f32x2 l8[8][2];
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        l8[rr][b] = *reinterpret_cast<lds_f32x2_c*>(
+            (size_t)(kLdsLut + ((D[rr >> 1] >> (16 * (rr & 1) + 8 * b)) & 0xffu) * 8));
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // the 16 LUT reads
+    __builtin_amdgcn_sched_group_barrier(0x002, 64, 1);  // then VALU
+    const int base = kLdsB + buf * kBTileBytes;
+    const int g8 = rp >> 2;                                   // chunk: k 8 g8 .. 8 g8 + 7
+    const int nc = 16 * st + 8 * (d & 1) + 4 * (int)e;        // first of the lane's 4 columns
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      u32x4 lo, hi;  // columns 2b (level .x) and 2b + 1 (.y)
+      lo.x = pack_bf16x2(l8[0][b].x * s8[0], l8[1][b].x * s8[1]);
+      lo.y = pack_bf16x2(l8[2][b].x * s8[2], l8[3][b].x * s8[3]);
+      lo.z = pack_bf16x2(l8[4][b].x * s8[4], l8[5][b].x * s8[5]);
+      lo.w = pack_bf16x2(l8[6][b].x * s8[6], l8[7][b].x * s8[7]);
+      hi.x = pack_bf16x2(l8[0][b].y * s8[0], l8[1][b].y * s8[1]);
+      hi.y = pack_bf16x2(l8[2][b].y * s8[2], l8[3][b].y * s8[3]);
+      hi.z = pack_bf16x2(l8[4][b].y * s8[4], l8[5][b].y * s8[5]);
+      hi.w = pack_bf16x2(l8[6][b].y * s8[6], l8[7][b].y * s8[7]);
+      *reinterpret_cast<lds_u32x4*>((size_t)lds_addr(base, nc + 2 * b, g8)) = lo;
+      *reinterpret_cast<lds_u32x4*>((size_t)lds_addr(base, nc + 2 * b + 1, g8)) = hi;
+    }
+    return;
+  }
   f32x2 l[4][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
