@@ -818,9 +818,8 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
 // fragments are single 16-byte loads (pad = rank rounded up to 16, zero past
 // the rank):
 //   * lora_prep_kernel: at[pad][K] = A transposed and bt[N][pad] = B
-//     transposed, one row k of A or one column n of B per thread (each
-//     thread reads a row of A / writes a row of bt contiguously, and the
-//     threads of a wave write at / read B at consecutive addresses);
+//     transposed, one element of at or bf16 pair of bt per thread (at
+//     config 3 its ~4.8 us are mostly the launch itself);
 //   * lora_xa_kernel: xa[M][pad] = bf16(scaling * (X A)) -- the first factor
 //     of LoraAdapter::forward (src/quantize.rs:619-624) with the scaling
 //     folded in -- R rows x 16 columns per workgroup (R = 16, or 8 or 4 when
@@ -836,26 +835,20 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
 __global__ __launch_bounds__(256) void lora_prep_kernel(const float* __restrict__ a, size_t sak, size_t saj,
                                                         const float* __restrict__ b, size_t sbj, size_t sbn, int K,
                                                         int N, int rank, int pad, uint16_t* __restrict__ at,
-                                                        uint16_t* __restrict__ bt) {
-  const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (t < K) {
-    const float* row = a + (size_t)t * sak;  // first factor's row t
-    for (int j = 0; j < pad; ++j)
-      at[(size_t)j * K + t] = j < rank ? (uint16_t)(pack_bf16x2(row[(size_t)j * saj], 0.0f) & 0xffffu) : 0;
-  } else if (t < K + N) {
-    const int n = t - K;
-    for (int c0 = 0; c0 < pad; c0 += 16) {
-      uint32_t w[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r0 = c0 + 2 * j, r1 = r0 + 1;
-        w[j] = pack_bf16x2(r0 < rank ? b[(size_t)r0 * sbj + (size_t)n * sbn] : 0.0f,
-                           r1 < rank ? b[(size_t)r1 * sbj + (size_t)n * sbn] : 0.0f);
-      }
-      u32x4* dst = reinterpret_cast<u32x4*>(bt + (size_t)n * pad + c0);
-      dst[0] = u32x4{w[0], w[1], w[2], w[3]};
-      dst[1] = u32x4{w[4], w[5], w[6], w[7]};
-    }
+                                                        uint32_t* __restrict__ bt2) {
+  // one thread per element of at [pad][K] (consecutive threads: consecutive
+  // k, so the stores coalesce), then one per bf16 pair of bt [N][pad]
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t n_at = (size_t)pad * K;
+  if (t < n_at) {
+    const int j = (int)(t / (size_t)K), k = (int)(t - (size_t)j * K);
+    at[t] = j < rank ? (uint16_t)(pack_bf16x2(a[(size_t)k * sak + (size_t)j * saj], 0.0f) & 0xffffu) : 0;
+  } else if (t < n_at + (size_t)N * pad / 2) {
+    const size_t u = t - n_at;  // bt element pair (n, 2 jp), (n, 2 jp + 1)
+    const int half = pad / 2;
+    const int n = (int)(u / (size_t)half), r0 = 2 * (int)(u - (size_t)n * half), r1 = r0 + 1;
+    bt2[u] = pack_bf16x2(r0 < rank ? b[(size_t)r0 * sbj + (size_t)n * sbn] : 0.0f,
+                         r1 < rank ? b[(size_t)r1 * sbj + (size_t)n * sbn] : 0.0f);
   }
 }
 
@@ -930,8 +923,9 @@ hipError_t lora_operands(const uint16_t* x, const float* a, size_t sak, size_t s
                          uint16_t* xa, hipStream_t stream) {
   if (rank < 1 || rank > 64 || K % 64 != 0) return hipErrorInvalidValue;
   const int pad = lora_pad(rank);
-  lora_prep_kernel<<<(unsigned)((K + N + 255) / 256), 256, 0, stream>>>(a, sak, saj, b, sbj, sbn, K, N, rank, pad,
-                                                                        at, bt);
+  const size_t prep = (size_t)pad * K + (size_t)N * pad / 2;
+  lora_prep_kernel<<<(unsigned)((prep + 255) / 256), 256, 0, stream>>>(a, sak, saj, b, sbj, sbn, K, N, rank, pad, at,
+                                                                       reinterpret_cast<uint32_t*>(bt));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // rows per workgroup: 16 while that covers the CUs, else 8 or 4
