@@ -317,3 +317,31 @@ def test_fused_swiglu_mixed_scale_kinds(device, oracle):
                  L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)):
         y, _ = swiglu_call(g, u, d, xt, T, hidden, need, device)
         check(y, ref, h, wd, TOL_BF16, f"mixed kinds workspace {need}")
+
+
+@pytest.mark.parametrize("T,hidden,inter,pair", [(512, 4096, 9600, True), (512, 2048, 19200, False)])
+def test_fused_swiglu_tail_round(device, oracle, T, hidden, inter, pair):
+    # 300 output tiles: one whole round of 256 tiles, then a last round of 44.
+    # With the default workspace the whole round runs whole and the last
+    # round's tiles split d_in (4 ways for the pair launch, 2 for gate and up
+    # as separate launches), an ordered reduction of just those tiles; with
+    # the least workspace every tile runs whole (up to 512 rows the default
+    # workspace is the fused kernels', not the expanded weights).  Both
+    # against the oracle.
+    kinds = (True, True, True) if pair else (True, False, True)
+    lins, (wg, wu, wd) = swiglu_layers(oracle, device, hidden, inter, 3600 + T, kinds)
+    x, xt = acts(oracle, T, hidden, 3610, torch.bfloat16, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    room = L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16)
+    lean = L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)
+    assert room > lean
+    g, u, d = (l.weight_struct() for l in lins)
+    outs = {}
+    for name, need in (("tail", room), ("whole", lean)):
+        y, ws = swiglu_call(g, u, d, xt, T, hidden, need, device)
+        check(y, ref, h, wd, TOL_BF16, f"swiglu tail round {name} T={T} pair={pair}")
+        y2, _ = swiglu_call(g, u, d, xt, T, hidden, need, device)
+        assert torch.equal(y, y2)
+        outs[name] = y
+    assert float((outs["tail"] - outs["whole"]).abs().max() / outs["whole"].abs().max()) < 1e-2

@@ -194,6 +194,7 @@ struct LinearLayout {
   GemvPlan gemv;
   StripedPlan striped, striped_tail;  // skinny: the plan of each launch (the last of several f32 launches)
   int splits = 1;  // kMfma without expand: d_in slabs of the fused kernel
+  int tail = 1;    // ... or of only its last, partly filled round of tiles
   size_t partials, xa, lora_at, lora_bt, wt, blas, wf32, rm_codes, rm_scales, gemm_partials, total;
 };
 
@@ -248,7 +249,9 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
     } else if (split && lora_rank == 0) {
       // the fused kernel over too few tiles splits d_in (f32 partials)
       L.splits = gemm_k_splits((int)rows, (int)d_in, (int)d_out);
-      if (L.splits > 1) L.gemm_partials = c.take((size_t)L.splits * rows * d_out * sizeof(float));
+      if (L.splits == 1) L.tail = gemm_tail_splits((int)rows, (int)d_in, (int)d_out);
+      const int slabs = std::max(L.splits, L.tail);
+      if (slabs > 1) L.gemm_partials = c.take((size_t)slabs * rows * d_out * sizeof(float));
     }
   } else {
     L.path = LinearPath::kGeneric;
@@ -339,7 +342,7 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
                          false);
     if (!workspace || workspace_bytes >= lean.total) L = lean;
   }
-  if (L.path == LinearPath::kMfma && !L.expand && L.splits > 1 &&
+  if (L.path == LinearPath::kMfma && !L.expand && (L.splits > 1 || L.tail > 1) &&
       ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
     // no room for the split-K partials (or an output the reduction cannot
     // store four at a time): the fused kernel over whole d_in
@@ -371,7 +374,7 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     }
     UNIFUR_HIP(launch_gemm(xb, w->packed, to_scales(w->scales), (int)rows, (int)w->d_in, (int)w->d_out, bias, xa16,
                            bt16, (int)rank, y, ybf, is_striped(w), stream, L.splits,
-                           L.splits > 1 ? at<float>(ws, L.gemm_partials) : nullptr));
+                           L.splits > 1 || L.tail > 1 ? at<float>(ws, L.gemm_partials) : nullptr, L.tail));
     return UNIFUR_NF4_OK;
   }
   if (lora) {
@@ -428,6 +431,7 @@ struct MlpLayout {
   GemvPlan up_plan, down_plan;
   StripedPlan s_up, s_down;
   int split_up = 1, split_down = 1;  // kMfma without expand: d_in slabs of the fused kernel
+  int tail_up = 1, tail_down = 1;    // ... or of only its last, partly filled round of tiles
   size_t partials0, partials1, h, u, hb, wt, blas, wf32, rm_codes, rm_scales, gemm_partials, total;
 };
 
@@ -513,8 +517,11 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
       if (split) {  // the fused kernel splits d_in where its grid would leave CUs idle (f32 partials)
         L.split_up = gemm_k_splits((int)rows, (int)hidden, (int)inter, same_kind);
         L.split_down = gemm_k_splits((int)rows, (int)inter, (int)hidden);
-        const size_t part = std::max(L.split_up > 1 ? (size_t)L.split_up * rows * inter * (same_kind ? 2 : 1) : 0,
-                                     L.split_down > 1 ? (size_t)L.split_down * rows * hidden : 0);
+        if (L.split_up == 1) L.tail_up = gemm_tail_splits((int)rows, (int)hidden, (int)inter, same_kind);
+        if (L.split_down == 1) L.tail_down = gemm_tail_splits((int)rows, (int)inter, (int)hidden);
+        const size_t up_slabs = (size_t)std::max(L.split_up, L.tail_up), down_slabs = std::max(L.split_down, L.tail_down);
+        const size_t part = std::max(up_slabs > 1 ? up_slabs * rows * inter * (same_kind ? 2 : 1) : 0,
+                                     down_slabs > 1 ? down_slabs * rows * hidden : 0);
         if (part) L.gemm_partials = c.take(part * sizeof(float));
       }
     }
@@ -661,16 +668,17 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
       float* gp = L.gemm_partials ? at<float>(ws, L.gemm_partials) : nullptr;
       if (gate->scales.kind == up->scales.kind) {
         UNIFUR_HIP(launch_gemm_pair(xb, gate->packed, to_scales(gate->scales), up->packed, to_scales(up->scales),
-                                    (int)rows, (int)hidden, (int)inter, hb, is_striped(gate), stream, L.split_up, gp));
+                                    (int)rows, (int)hidden, (int)inter, hb, is_striped(gate), stream, L.split_up, gp,
+                                    L.tail_up));
       } else {
         UNIFUR_HIP(launch_gemm(xb, gate->packed, to_scales(gate->scales), (int)rows, (int)hidden, (int)inter, nullptr,
-                               nullptr, nullptr, 0, h, false, is_striped(gate), stream, L.split_up, gp));
+                               nullptr, nullptr, 0, h, false, is_striped(gate), stream, L.split_up, gp, L.tail_up));
         UNIFUR_HIP(launch_gemm(xb, up->packed, to_scales(up->scales), (int)rows, (int)hidden, (int)inter, nullptr,
-                               nullptr, nullptr, 0, u, false, is_striped(up), stream, L.split_up, gp));
+                               nullptr, nullptr, 0, u, false, is_striped(up), stream, L.split_up, gp, L.tail_up));
         UNIFUR_HIP(launch_silu_mul_bf16(h, u, (size_t)rows * inter, hb, stream));
       }
       UNIFUR_HIP(launch_gemm(hb, down->packed, to_scales(down->scales), (int)rows, (int)inter, (int)hidden, nullptr,
-                             nullptr, nullptr, 0, y, ybf, is_striped(down), stream, L.split_down, gp));
+                             nullptr, nullptr, 0, y, ybf, is_striped(down), stream, L.split_down, gp, L.tail_down));
       return UNIFUR_NF4_OK;
     }
     case MlpPath::kGeneric:

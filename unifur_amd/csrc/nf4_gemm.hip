@@ -85,6 +85,9 @@ struct GemmArgs {
   // silu(gate x) * (up x) for its 64 columns.
   const uint8_t* packed2;
   ScalesArg scales2;
+  // tiles of this launch: tile_count tiles from tile_begin in the (m, n)
+  // row-major tile order (tile_count 0: all of them)
+  int tile_begin, tile_count;
 };
 
 // silu(z) * u, the middle of QwenMlp::forward (src/qwennet.rs:816-819,
@@ -656,7 +659,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   const int nb = gridDim.x;
   const int b = blockIdx.x;
   const int tb = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
-  const int split = tb % g.k_splits, t = tb / g.k_splits;
+  const int split = tb % g.k_splits, t = g.tile_begin + tb / g.k_splits;
   const int m0 = (t / g.tiles_n) * kBM, n0 = (t % g.tiles_n) * (PAIR ? kBN / 2 : kBN);
   const int row0 = m0 + 64 * w4;
   const int kb = split * g.k_steps;  // this workgroup's first K step
@@ -808,8 +811,8 @@ hipError_t launch_g(const GemmArgs& g, hipStream_t stream) {
     if (e != hipSuccess) return e;
     done.fetch_or(bit, std::memory_order_acq_rel);
   }
-  const int grid = ((g.M + kBM - 1) / kBM) * g.tiles_n * g.k_splits;
-  gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR, TRANS><<<grid, kGemmThreads, kGemmSmem, stream>>>(g);
+  const int tiles = g.tile_count ? g.tile_count : ((g.M + kBM - 1) / kBM) * g.tiles_n;
+  gemm_kernel<DQ, YBF16, LORA, STRIPED, PAIR, TRANS><<<tiles * g.k_splits, kGemmThreads, kGemmSmem, stream>>>(g);
   return hipGetLastError();
 }
 
@@ -1002,7 +1005,66 @@ __global__ __launch_bounds__(256) void splitk_silu_reduce_kernel(const float* __
   }
 }
 
+// The split-K reduction of only the tiles [t0, t0 + gridDim.x / 8) of a
+// launch (its other tiles were computed whole): 8 workgroups per tile, 32 of
+// its rows each, four outputs per thread, the splits added in order; PAIR:
+// gate and up summed, then bf16 silu(gate) * up into h.
+template <bool PAIR>
+__global__ __launch_bounds__(256) void splitk_reduce_tiles_kernel(const float* __restrict__ partials, int splits,
+                                                                  size_t split_stride, int M, int N, int tiles_n,
+                                                                  int t0, const float* __restrict__ bias,
+                                                                  void* __restrict__ y, int y_bf16) {
+  constexpr int kCols = PAIR ? kBN / 2 : kBN, kC4 = kCols / 4;
+  const int t = t0 + (int)blockIdx.x / 8;
+  const int m0 = (t / tiles_n) * kBM + ((int)blockIdx.x % 8) * 32, n0 = (t % tiles_n) * kCols;
+  const size_t ldp = PAIR ? 2 * (size_t)N : (size_t)N;  // a partial row: gate columns, then up
+  for (int i = threadIdx.x; i < 32 * kC4; i += 256) {
+    const int m = m0 + i / kC4, n = n0 + 4 * (i % kC4);
+    if (m >= M) continue;
+    const float* p = partials + (size_t)m * ldp + n;
+    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    f32x4 u = PAIR ? *reinterpret_cast<const f32x4*>(p + N) : f32x4{};
+    for (int q = 1; q < splits; ++q) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(p + q * split_stride);
+      v = f32x4{v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w};
+      if constexpr (PAIR) {
+        const f32x4 w2 = *reinterpret_cast<const f32x4*>(p + q * split_stride + N);
+        u = f32x4{u.x + w2.x, u.y + w2.y, u.z + w2.z, u.w + w2.w};
+      }
+    }
+    const size_t o = (size_t)m * N + n;
+    if constexpr (PAIR) {
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(y) + o) =
+          u32x2{pack_bf16x2(silu_times(v.x, u.x), silu_times(v.y, u.y)),
+                pack_bf16x2(silu_times(v.z, u.z), silu_times(v.w, u.w))};
+    } else {
+      if (bias) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(bias + n);
+        v = f32x4{v.x + b4.x, v.y + b4.y, v.z + b4.z, v.w + b4.w};
+      }
+      if (y_bf16)
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(y) + o) = u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+      else
+        *reinterpret_cast<f32x4*>(static_cast<float*>(y) + o) = v;
+    }
+  }
+}
+
 }  // namespace
+
+int gemm_tail_splits(int M, int K, int N, bool pair) {
+  // a grid of more than one round whose last round is at most half full:
+  // the whole rounds' tiles run whole and the last round's tiles split d_in
+  // (f32 partials, an ordered reduction of those tiles), so that the last
+  // round fills the CUs instead of leaving most of them idle
+  const long tiles = (long)((M + kBM - 1) / kBM) * (pair ? N / (kBN / 2) : N / kBN);
+  const long rem = tiles % 256;
+  if (tiles <= 256 || rem == 0 || gemm_k_splits(M, K, N, pair) > 1) return 1;
+  const int steps = K / kBK;
+  int splits = 1;
+  while (rem * splits * 2 <= 256 && steps / (splits * 2) >= 16) splits *= 2;
+  return splits;
+}
 
 int gemm_k_splits(int M, int K, int N, bool pair) {
   // grids of fewer than ~200 tiles leave CUs idle (one 148 KiB workgroup per
@@ -1053,7 +1115,7 @@ unsigned reduce_blocks(size_t n4) { return (unsigned)std::min<size_t>((n4 + 255)
 
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
                        const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
-                       bool y_bf16, bool striped, hipStream_t stream, int k_splits, float* partials) {
+                       bool y_bf16, bool striped, hipStream_t stream, int k_splits, float* partials, int tail_splits) {
   if (!splits_ok(K, k_splits) || (k_splits > 1 && (!partials || lora_xa || (reinterpret_cast<uintptr_t>(y) & 15u) != 0)))
     return hipErrorInvalidValue;
   GemmArgs g = gemm_args(x, packed, scales, M, K, N, y, y_bf16, k_splits, partials);
@@ -1077,6 +1139,28 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
   }
   const bool dq = scales.kind == kScalesDQ;
   const bool lora = lora_xa != nullptr;
+  if (tail_splits > 1) {
+    if (lora || !partials || (reinterpret_cast<uintptr_t>(y) & 15u) != 0 || !splits_ok(K, tail_splits))
+      return hipErrorInvalidValue;
+    // the whole rounds' tiles, then the last round's split (see gemm_tail_splits)
+    const int tiles = ((M + kBM - 1) / kBM) * g.tiles_n, whole = tiles - tiles % 256;
+    g.tile_count = whole;
+    hipError_t e = dq ? (y_bf16 ? (striped ? launch_g<true, true, false, true>(g, stream) : launch_g<true, true, false, false>(g, stream))
+                                : (striped ? launch_g<true, false, false, true>(g, stream) : launch_g<true, false, false, false>(g, stream)))
+                      : (y_bf16 ? (striped ? launch_g<false, true, false, true>(g, stream) : launch_g<false, true, false, false>(g, stream))
+                                : (striped ? launch_g<false, false, false, true>(g, stream) : launch_g<false, false, false, false>(g, stream)));
+    if (e != hipSuccess) return e;
+    GemmArgs t = gemm_args(x, packed, scales, M, K, N, partials, false, tail_splits, partials);
+    t.y_aligned = 1;
+    t.tile_begin = whole;
+    t.tile_count = tiles - whole;
+    e = dq ? (striped ? launch_g<true, false, false, true>(t, stream) : launch_g<true, false, false, false>(t, stream))
+           : (striped ? launch_g<false, false, false, true>(t, stream) : launch_g<false, false, false, false>(t, stream));
+    if (e != hipSuccess) return e;
+    splitk_reduce_tiles_kernel<false><<<(tiles - whole) * 8, 256, 0, stream>>>(
+        partials, tail_splits, (size_t)M * N, M, N, g.tiles_n, whole, bias, y, y_bf16);
+    return hipGetLastError();
+  }
 #define UNIFUR_GEMM_CASE(D, B, R)                                                     \
   if (dq == D && y_bf16 == B && lora == R)                                          \
     return striped ? launch_g<D, B, R, true>(g, stream) : launch_g<D, B, R, false>(g, stream);
@@ -1094,7 +1178,7 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
 
 hipError_t launch_gemm_pair(const uint16_t* x, const uint8_t* gate_packed, const ScalesArg& gate_scales,
                             const uint8_t* up_packed, const ScalesArg& up_scales, int M, int K, int N, uint16_t* h,
-                            bool striped, hipStream_t stream, int k_splits, float* partials) {
+                            bool striped, hipStream_t stream, int k_splits, float* partials, int tail_splits) {
   if (gate_scales.kind != up_scales.kind || N % 64 != 0 || !splits_ok(K, k_splits) ||
       (k_splits > 1 && !partials))
     return hipErrorInvalidValue;
@@ -1103,6 +1187,30 @@ hipError_t launch_gemm_pair(const uint16_t* x, const uint8_t* gate_packed, const
   g.scales2 = up_scales;
   g.tiles_n = N / (kBN / 2);
   const bool dq = gate_scales.kind == kScalesDQ;
+  if (k_splits == 1 && tail_splits > 1) {
+    if (!partials || !splits_ok(K, tail_splits)) return hipErrorInvalidValue;
+    // the whole rounds' tiles store silu(g) * u; the last round's tiles
+    // split d_in (see gemm_tail_splits)
+    const int tiles = ((M + kBM - 1) / kBM) * g.tiles_n, whole = tiles - tiles % 256;
+    g.tile_count = whole;
+    hipError_t e = dq ? (striped ? launch_g<true, true, false, true, true>(g, stream) : launch_g<true, true, false, false, true>(g, stream))
+                      : (striped ? launch_g<false, true, false, true, true>(g, stream) : launch_g<false, true, false, false, true>(g, stream));
+    if (e != hipSuccess) return e;
+    GemmArgs t = gemm_args(x, gate_packed, gate_scales, M, K, N, partials, false, tail_splits, partials);
+    t.packed2 = up_packed;
+    t.scales2 = up_scales;
+    t.tiles_n = g.tiles_n;
+    t.y_aligned = 1;
+    t.ldy = 2 * N;
+    t.tile_begin = whole;
+    t.tile_count = tiles - whole;
+    e = dq ? (striped ? launch_g<true, false, false, true, true>(t, stream) : launch_g<true, false, false, false, true>(t, stream))
+           : (striped ? launch_g<false, false, false, true, true>(t, stream) : launch_g<false, false, false, false, true>(t, stream));
+    if (e != hipSuccess) return e;
+    splitk_reduce_tiles_kernel<true><<<(tiles - whole) * 8, 256, 0, stream>>>(
+        partials, tail_splits, (size_t)M * 2 * N, M, N, g.tiles_n, whole, nullptr, h, 1);
+    return hipGetLastError();
+  }
   if (k_splits == 1) {
     return dq ? (striped ? launch_g<true, true, false, true, true>(g, stream) : launch_g<true, true, false, false, true>(g, stream))
               : (striped ? launch_g<false, true, false, true, true>(g, stream) : launch_g<false, true, false, false, true>(g, stream));

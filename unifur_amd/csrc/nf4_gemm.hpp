@@ -29,7 +29,8 @@ hipError_t launch_lora_operands(const uint16_t* x, const float* a, const float* 
 // which a second launch adds in split order with the bias and rounding.
 hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg& scales, int M, int K, int N,
                        const float* bias, const uint16_t* lora_xa, const uint16_t* lora_bt, int lora_rank, void* y,
-                       bool y_bf16, bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr);
+                       bool y_bf16, bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr,
+                       int tail_splits = 1);
 
 // SwiGLU gate/up pair: h[M, N] = bf16(silu(X deq(gate)) * (X deq(up))),
 // both weights [K, N] of one layout and scale kind, N a multiple of 64, h
@@ -40,7 +41,8 @@ hipError_t launch_gemm(const uint16_t* x, const uint8_t* packed, const ScalesArg
 // launch adds in split order before the product.
 hipError_t launch_gemm_pair(const uint16_t* x, const uint8_t* gate_packed, const ScalesArg& gate_scales,
                             const uint8_t* up_packed, const ScalesArg& up_scales, int M, int K, int N, uint16_t* h,
-                            bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr);
+                            bool striped, hipStream_t stream, int k_splits = 1, float* partials = nullptr,
+                            int tail_splits = 1);
 
 // dX[M, d_in] = dY[M, d_out] deq(W)^T (+ lora_xa lora_bt^T) for a striped
 // weight W [d_in, d_out] (d_in a multiple of 128): the fused kernel with the
@@ -57,6 +59,13 @@ hipError_t launch_gemm_dx(const uint16_t* dy, const uint8_t* packed, const Scale
 hipError_t launch_lora_operands_dx(const uint16_t* dy, const float* a, const float* b, int M, int d_in, int d_out,
                                    int rank, float scaling, uint16_t* at, uint16_t* bt, uint16_t* xa,
                                    hipStream_t stream);
+
+// tail_splits > 1 (k_splits 1, no adapter, y 16-byte aligned; partials as
+// for k_splits = tail_splits): the tiles of the grid's whole rounds run
+// whole and those of its last, partly filled round split d_in
+// tail_splits ways, with an ordered reduction of just those tiles.
+// gemm_tail_splits gives the count for a shape (1: no tail split).
+int gemm_tail_splits(int M, int K, int N, bool pair = false);
 
 // d_in slabs the fused GEMM splits into for this shape (1: no split); pair:
 // the gate/up pair launch over two [K, N] weights.
