@@ -728,10 +728,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int u = 0; u < kBRing; ++u) produce(t2 + u, (2 + u) % kBRing);
     }
-    for (int u = 0; t2 < nk; ++t2, ++u) {
-      if (u == 0) produce(t2, 2);
-      else if (u == 1) produce(t2, 3);
-      else produce(t2, 0);
+    // the last (at most 3) steps straight-line: in a loop the compiler's
+    // wait for the ring slot's codes degrades to vmcnt(0), which also waits
+    // for the loads issued one step earlier
+    if (t2 < nk) {
+      produce(t2++, 2);
+      if (t2 < nk) {
+        produce(t2++, 3);
+        if (t2 < nk) produce(t2++, 0);
+      }
     }
     if (nk >= 2) lds_barrier();  // the last step's barrier: nothing left to produce
     UNIFUR_WAIT_VMCNT(0);        // drain the clamped reloads before the wave exits
