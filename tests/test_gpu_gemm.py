@@ -160,6 +160,16 @@ def test_fused_prefill_kernel_config3_shapes(device, oracle, M):
     _qlora_with_workspace(device, oracle, M, K, N, r, lean, 700 + M)
 
 
+@pytest.mark.parametrize("striped", [True, False])
+@pytest.mark.parametrize("K", [64, 128, 192, 256, 320, 448])
+def test_fused_prefill_few_k_steps(device, oracle, K, striped):
+    # 1-7 K steps of 64 per workgroup: the dequantizing waves' prologue
+    # (one or two steps) and their last 0-3 steps after the 4-step main loop
+    M, N, r = 300, 256, 8
+    lean = L.lib().unifur_nf4_linear_min_workspace_size(M, K, N, L.BF16, r)
+    _qlora_with_workspace(device, oracle, M, K, N, r, lean, 900 + K, striped=striped)
+
+
 @pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shift", [0, 1, 2])
 def test_fused_prefill_output_alignment(device, oracle, ydt, shift):
