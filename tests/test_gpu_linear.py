@@ -92,7 +92,7 @@ def test_gemv_config2_4096_to_11008(device, oracle, dq, x_dtype, striped):
 @pytest.mark.parametrize("striped", [True, False])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4])
 @pytest.mark.parametrize("shape", [(896, 4864), (4864, 896), (896, 128), (256, 64), (4096, 4096), (100, 192),
-                                   (11008, 4096)])
+                                   (11008, 4096), (64, 128), (192, 256), (320, 896)])
 def test_gemv_rows_and_shapes(device, oracle, rows, shape, striped):
     d_in, d_out = shape
     lin, wdeq = make_linear(oracle, d_in, d_out, 11 + d_in + d_out, device, striped=striped)
