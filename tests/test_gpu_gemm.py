@@ -355,3 +355,20 @@ def test_fused_swiglu_tail_round(device, oracle, T, hidden, inter, pair):
         assert torch.equal(y, y2)
         outs[name] = y
     assert float((outs["tail"] - outs["whole"]).abs().max() / outs["whole"].abs().max()) < 1e-2
+
+
+@pytest.mark.parametrize("hidden", [64, 192, 256, 320])
+def test_fused_swiglu_pair_few_k_steps(device, oracle, hidden):
+    # the gate/up pair launch at 1-5 K steps of 64 (d_in = hidden): the
+    # dequantizing waves' prologue and their last 1-3 steps in PAIR mode,
+    # with the default and the least workspace, against the oracle
+    inter, T = 384, 300
+    lins, (wg, wu, wd) = swiglu_layers(oracle, device, hidden, inter, 3700 + hidden)
+    x, xt = acts(oracle, T, hidden, 3710 + hidden, torch.bfloat16, device)
+    ref = oracle.swiglu_ref_f64(x, wg, wu, wd)
+    h = oracle.silu_f64(x.astype(np.float64) @ wg) * (x.astype(np.float64) @ wu)
+    g, u, d = (l.weight_struct() for l in lins)
+    for need in (L.lib().unifur_nf4_swiglu_workspace_size(T, hidden, inter, L.BF16),
+                 L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)):
+        y, _ = swiglu_call(g, u, d, xt, T, hidden, need, device)
+        check(y, ref, h, wd, TOL_BF16, f"pair hidden={hidden} workspace {need}")
