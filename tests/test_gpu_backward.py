@@ -214,6 +214,8 @@ def test_fused_dx_without_adapter(device, oracle, M, work):
     (33, 128, 64, 4, 0),          # one output tile, one K step
     (33, 128, 128, 3, 0),         # two K steps, odd rank
     (1, 256, 192, 0, 0),          # one row, three K steps, no adapter
+    (20, 128, 256, 8, 0),         # four K steps: two after the prologue
+    (20, 256, 320, 0, 0),         # five K steps: three after the prologue
     (40, 384, 1344, 0, 4 << 20),  # no adapter, split over d_out (21 K steps: a ragged last slab)
 ])
 def test_fused_dx_edge_shapes(device, oracle, M, K, N, r, work):
