@@ -205,6 +205,34 @@ def lora_ref_f64(x, a, b, scaling) -> np.ndarray:
     return (x64 @ np.asarray(a, np.float64)) @ np.asarray(b, np.float64) * float(scaling)
 
 
+def linear_backward_ref_f64(x, dy, w_deq, a, b, scaling):
+    """Vector-Jacobian products of y = x W + ((x A) B) s, the function of
+    QloraLinear::forward (src/qwennet.rs:325-345) with LoraAdapter::forward
+    (src/quantize.rs:619-624), that burn's autodiff takes under
+    src/qwentrain.rs:421-470 with the base weight frozen, in float64:
+
+        dx     = dy W^T + ((dy s) B^T) A^T
+        grad_a = x^T ((dy s) B^T)
+        grad_b = (x A)^T (dy s)
+
+    Returns (dx, dx_bound, grad_a, grad_a_bound, grad_b, grad_b_bound); each
+    bound is the same sum of products over absolute values, the scale of the
+    accumulated terms for a normwise error."""
+    x = np.asarray(x, np.float64)
+    dy = np.asarray(dy, np.float64)
+    w = np.asarray(w_deq, np.float64)
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    g = dy * float(scaling)
+    dx = dy @ w.T + (g @ b.T) @ a.T
+    dx_bound = np.abs(dy) @ np.abs(w).T + (np.abs(g) @ np.abs(b).T) @ np.abs(a).T
+    gb = (x @ a).T @ g
+    gb_bound = (np.abs(x) @ np.abs(a)).T @ np.abs(g)
+    ga = x.T @ (g @ b.T)
+    ga_bound = np.abs(x).T @ (np.abs(g) @ np.abs(b).T)
+    return dx, dx_bound, ga, ga_bound, gb, gb_bound
+
+
 def silu_f64(z):
     z = np.asarray(z, np.float64)
     return z / (1.0 + np.exp(-z))

@@ -8,7 +8,9 @@ src/qwentrain.rs:421-470, the base weight frozen:
     grad_b = (x A)^T (dy s)
     grad_a = x^T ((dy s) B^T)
 
-Each is checked against the float64 evaluation of those formulas with the
+Each is checked against the float64 evaluation of those formulas
+(``oracle.linear_backward_ref_f64``, pinned against torch.autograd and
+central differences in tests/test_oracle.py) with the
 oracle's dequantized weight (bit-identical to the reference's), by the larger of the
 per-element normwise error (max_i |got_i - ref_i| over that element's sum of
 absolute products) and the literal max|got - ref| / max|ref|: f32 dy through the f32
@@ -28,6 +30,7 @@ import torch
 from unifur_amd import _lib as L
 from unifur_amd import quantize as Q
 
+from oracle.oracle import linear_backward_ref_f64 as refs
 from test_gpu_gemm import lora_parts
 from test_gpu_linear import acts, make_linear
 
@@ -44,22 +47,6 @@ def normwise(got, ref, bound):
     per_elem = float(np.max(np.abs(got - ref) / np.maximum(np.asarray(bound, np.float64), 1e-30)))
     literal = float(np.max(np.abs(got - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
     return max(per_elem, literal)
-
-
-def refs(x, dy, wdeq, a, b, s):
-    x = np.asarray(x, np.float64)
-    dy = np.asarray(dy, np.float64)
-    w = np.asarray(wdeq, np.float64)
-    a = np.asarray(a, np.float64)
-    b = np.asarray(b, np.float64)
-    g = dy * s
-    dx = dy @ w.T + (g @ b.T) @ a.T
-    dx_bound = np.abs(dy) @ np.abs(w).T + (np.abs(g) @ np.abs(b).T) @ np.abs(a).T
-    gb = (x @ a).T @ g
-    gb_bound = (np.abs(x) @ np.abs(a)).T @ np.abs(g)
-    ga = x.T @ (g @ b.T)
-    ga_bound = np.abs(x).T @ (np.abs(g) @ np.abs(b).T)
-    return dx, dx_bound, ga, ga_bound, gb, gb_bound
 
 
 @pytest.mark.parametrize("case", [

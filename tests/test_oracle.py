@@ -377,3 +377,130 @@ def test_thresholds_sit_far_from_bucket_edges_and_from_each_other():
     assert edge.min() > 2.0 ** -20 + 2.0 ** -22
     assert edge.min() > 2.0 ** -10  # in fact more than 2^-10
     assert np.diff(np.sort(T)).min() > 1.0 / 16
+
+
+# ---------------------------------------- SwiGLU, LoRA and backward refs --
+
+def test_swiglu_ref_known_answers(oracle):
+    """QwenMlp::forward (src/qwennet.rs:816-819) is down(silu(gate x) * up x):
+    silu goes through the gate product only, down is applied last."""
+    one = np.array([[1.0]])
+    y = oracle.swiglu_ref_f64(one, one, 2.0 * one, one)
+    # silu(1) * 2 = 2 / (1 + e^-1); with gate and up swapped: silu(2) * 1
+    assert abs(y[0, 0] - 1.4621171572600098) < 1e-15
+    assert abs(oracle.swiglu_ref_f64(one, 2.0 * one, one, one)[0, 0] - 1.7615941559557649) < 1e-15
+    rng = np.random.default_rng(21)
+    x = rng.normal(size=(3, 5))
+    wg, wu, wd = rng.normal(size=(5, 7)), rng.normal(size=(5, 7)), rng.normal(size=(7, 4))
+    assert np.all(oracle.swiglu_ref_f64(x, wg, np.zeros((5, 7)), wd) == 0.0)  # up = 0
+    assert np.all(oracle.swiglu_ref_f64(x, np.zeros((5, 7)), wu, wd) == 0.0)  # silu(0) = 0
+    # orientation of down: hidden 2 -> intermediate 1 -> hidden 2
+    y = oracle.swiglu_ref_f64([[1.0, 0.0]], [[1.0], [0.0]], [[2.0], [0.0]], [[3.0, -1.0]])
+    h = 2.0 / (1.0 + np.exp(-1.0))
+    np.testing.assert_allclose(y, [[3.0 * h, -h]], rtol=1e-15)
+
+
+def test_swiglu_ref_matches_torch_float64(oracle):
+    """Against an independent evaluation (torch's silu on the CPU, float64)."""
+    import torch
+    rng = np.random.default_rng(22)
+    x = rng.normal(size=(6, 32))
+    wg, wu, wd = (rng.normal(scale=0.2, size=s) for s in ((32, 48), (32, 48), (48, 32)))
+    t = lambda a: torch.from_numpy(a)
+    ref = (torch.nn.functional.silu(t(x) @ t(wg)) * (t(x) @ t(wu))) @ t(wd)
+    np.testing.assert_allclose(oracle.swiglu_ref_f64(x, wg, wu, wd), ref.numpy(), rtol=1e-12, atol=1e-14)
+    swapped = (torch.nn.functional.silu(t(x) @ t(wu)) * (t(x) @ t(wg))) @ t(wd)
+    assert np.max(np.abs(oracle.swiglu_ref_f64(x, wg, wu, wd) - swapped.numpy())) > 1e-2
+
+
+def test_lora_ref_scaling_and_dense_identity(oracle):
+    """src/quantize.rs:1027-1047: LoraConfig::new(12, 6, 3).with_alpha(6)
+    scales by alpha / rank = 2, and the factored (x A) B s equals x (s A B)."""
+    from unifur_amd.quantize import LoraConfig
+    cfg = LoraConfig.new(12, 6, 3).with_alpha(6.0)
+    assert cfg.scaling() == 2.0
+    assert LoraConfig.new(16, 8, 4).scaling() == 1.0  # alpha defaults to the rank
+    rng = np.random.default_rng(23)
+    x = rng.uniform(-1, 1, size=(4, 12))
+    a = rng.normal(scale=1 / np.sqrt(3), size=(12, 3))
+    b = rng.uniform(-0.5, 0.5, size=(3, 6))
+    factored = oracle.lora_ref_f64(x, a, b, cfg.scaling())
+    np.testing.assert_allclose(factored, x @ (cfg.scaling() * (a @ b)), rtol=1e-12, atol=1e-14)
+    # B = 0 at init: an exact no-op (src/quantize.rs:1011-1025)
+    assert np.all(oracle.lora_ref_f64(x, a, np.zeros((3, 6)), 2.0) == 0.0)
+
+
+def test_lora_ref_hand_computed(oracle):
+    """x A = [1, 2], (x A) B = [2, 1], times 0.5; B A order would give
+    [1.5, 2], A transposed [1.5, 0.5]."""
+    x = np.array([[1.0, 0.0]])
+    a = np.array([[1.0, 2.0], [3.0, 4.0]])
+    b = np.array([[0.0, 1.0], [1.0, 0.0]])
+    np.testing.assert_array_equal(oracle.lora_ref_f64(x, a, b, 0.5), [[1.0, 0.5]])
+
+
+def _qlora_forward_f64(x, w, a, b, s):
+    return x @ w + (x @ a) @ b * s
+
+
+def test_backward_ref_matches_autograd(oracle):
+    """The VJP formulas against torch.autograd of the float64 forward
+    x W + ((x A) B) s on the CPU, with s != 1 and non-square factors so that
+    a missing or doubled s, or a dropped transpose, cannot agree."""
+    import torch
+    rng = np.random.default_rng(24)
+    M, K, N, r, s = 5, 7, 6, 3, 2.5
+    x, w = rng.normal(size=(M, K)), rng.normal(size=(K, N))
+    a, b, dy = rng.normal(size=(K, r)), rng.normal(size=(r, N)), rng.normal(size=(M, N))
+    tx, ta, tb = (torch.tensor(v, requires_grad=True) for v in (x, a, b))
+    y = _qlora_forward_f64(tx, torch.from_numpy(w), ta, tb, s)
+    y.backward(torch.from_numpy(dy))
+    dx, _, ga, _, gb, _ = oracle.linear_backward_ref_f64(x, dy, w, a, b, s)
+    for got, want in ((dx, tx.grad), (ga, ta.grad), (gb, tb.grad)):
+        np.testing.assert_allclose(got, want.numpy(), rtol=1e-12, atol=1e-12)
+    # the same check rejects the plausible mistakes
+    g = dy * s
+    wrong = {
+        "s twice in dx": dy @ w.T + ((g * s) @ b.T) @ a.T,
+        "s dropped in grad_a": x.T @ (dy @ b.T),
+        "s twice in grad_b": (x @ a).T @ (g * s),
+    }
+    assert np.max(np.abs(wrong["s twice in dx"] - tx.grad.numpy())) > 1e-3
+    assert np.max(np.abs(wrong["s dropped in grad_a"] - ta.grad.numpy())) > 1e-3
+    assert np.max(np.abs(wrong["s twice in grad_b"] - tb.grad.numpy())) > 1e-3
+
+
+def test_backward_ref_matches_central_differences(oracle):
+    """The forward is linear in x, in A and in B separately, so a central
+    difference of <dy, y> is exact up to rounding: every entry of each
+    gradient is checked that way."""
+    rng = np.random.default_rng(25)
+    M, K, N, r, s = 3, 5, 4, 2, 0.75
+    x, w = rng.normal(size=(M, K)), rng.normal(size=(K, N))
+    a, b, dy = rng.normal(size=(K, r)), rng.normal(size=(r, N)), rng.normal(size=(M, N))
+    dx, _, ga, _, gb, _ = oracle.linear_backward_ref_f64(x, dy, w, a, b, s)
+    loss = lambda x_, a_, b_: float(np.sum(dy * _qlora_forward_f64(x_, w, a_, b_, s)))
+    h = 1e-3
+    for arr, grad, which in ((x, dx, 0), (a, ga, 1), (b, gb, 2)):
+        for idx in np.ndindex(arr.shape):
+            args_p = [x.copy(), a.copy(), b.copy()]
+            args_m = [x.copy(), a.copy(), b.copy()]
+            args_p[which][idx] += h
+            args_m[which][idx] -= h
+            fd = (loss(*args_p) - loss(*args_m)) / (2 * h)
+            assert abs(fd - grad[idx]) < 1e-9 * max(1.0, abs(fd)), (which, idx)
+
+
+def test_backward_ref_bounds_dominate(oracle):
+    """Each bound is the sum of the absolute products: never below the
+    magnitude of its gradient, equal to it for non-negative inputs."""
+    rng = np.random.default_rng(26)
+    M, K, N, r, s = 4, 6, 5, 2, 3.0
+    args = [rng.normal(size=sh) for sh in ((M, K), (M, N), (K, N), (K, r), (r, N))]
+    dx, bdx, ga, bga, gb, bgb = oracle.linear_backward_ref_f64(*args, s)
+    for g, bd in ((dx, bdx), (ga, bga), (gb, bgb)):
+        assert np.all(np.abs(g) <= bd * (1 + 1e-12))
+    pos = [np.abs(v) for v in args]
+    dx, bdx, ga, bga, gb, bgb = oracle.linear_backward_ref_f64(*pos, s)
+    for g, bd in ((dx, bdx), (ga, bga), (gb, bgb)):
+        np.testing.assert_allclose(g, bd, rtol=1e-12)
