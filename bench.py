@@ -276,32 +276,65 @@ def bench_gemv(torch, Q, L, args) -> dict:
 
 # ----------------------------------------------------------- HBM ceiling --
 
-def bench_ceiling(torch, L, nbytes: int) -> dict:
+_PROBE = None
+
+
+def probe_lib():
+    """The bench's streaming probes (unifur_amd/bench_probe, built beside the
+    library by unifur_amd.build; not part of libunifur_nf4.so)."""
+    global _PROBE
+    if _PROBE is None:
+        from unifur_amd import build as B
+        if not os.path.exists(B.PROBE_LIB):
+            raise RuntimeError(f"{B.PROBE_LIB} is not built: run python -m unifur_amd.build")
+        lib = ctypes.CDLL(B.PROBE_LIB)
+        P, U64, U32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32
+        lib.unifur_bench_stream_probe.argtypes = [P, U64, P, P, U32, P]
+        lib.unifur_bench_stream_mixed.argtypes = [P, P, U64, U32, U32, P]
+        _PROBE = lib
+    return _PROBE
+
+
+def _probe_check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"stream probe failed with status {rc}")
+
+
+def bench_ceiling(torch, L, nbytes: int, write_ratio: int = 0) -> dict:
     """What this part streams for buffers of the GEMV's size, timed as the
     GEMV is (graph replay over copies rotated past the Infinity Cache, one
-    event pair around the replays): the library's streaming probe
-    (unifur_nf4_stream_probe, 16-byte accesses, grid-stride) as a plain read
-    of nbytes and as a copy of nbytes / 2 (nbytes moved), the best over a few
-    grid sizes."""
+    event pair around the replays): the bench's streaming probe (16-byte
+    accesses, grid-stride) as a plain read of nbytes and as a copy of
+    nbytes / 2 (nbytes moved), the best over a few grid sizes.  With
+    write_ratio R > 0, also a write-dominated stream of nbytes in all:
+    nbytes R / (R + 1) written and 1 / (R + 1) of it read (R = 8 is the
+    dequantize's mix, 8.9 MB read for 67 MB written at 4096 x 4096)."""
     dev = torch.device("cuda:0")
     nbytes = nbytes // 64 * 64
     copies = max(2, -(-(2 * MALL_BYTES) // nbytes))
     bufs = [torch.ones(nbytes // 4, device=dev) for _ in range(copies)]
-    dsts = [torch.empty(nbytes // 8, device=dev) for _ in range(copies)]
+    dsts = [torch.empty(nbytes // 4, device=dev) for _ in range(copies)]
     sink = torch.zeros(64, dtype=torch.int32, device=dev)
-    lib = L.lib()
-    out = {"bytes": nbytes, "copies": copies, "kernel": "unifur_nf4_stream_probe"}
-    for name, moved in (("read", nbytes), ("copy", nbytes)):
+    lib = probe_lib()
+    out = {"bytes": nbytes, "copies": copies, "kernel": "bench_probe/stream_probe.hip"}
+    kinds = [("read", nbytes), ("copy", nbytes)]
+    if write_ratio:
+        w_bytes = nbytes * write_ratio // (write_ratio + 1) // 16 * 16
+        kinds.append(("write_dominated", w_bytes + w_bytes // write_ratio))
+    for name, moved in kinds:
         best = None
         for grid in (256, 512, 1024, 2048, 4096):
             def fn(i: int, grid=grid, name=name) -> None:
+                st = torch.cuda.current_stream().cuda_stream
                 if name == "read":
-                    L.check(lib.unifur_nf4_stream_probe(bufs[i % copies].data_ptr(), nbytes, None, sink.data_ptr(),
-                                                        grid, torch.cuda.current_stream().cuda_stream))
+                    _probe_check(lib.unifur_bench_stream_probe(bufs[i % copies].data_ptr(), nbytes, None,
+                                                               sink.data_ptr(), grid, st))
+                elif name == "copy":
+                    _probe_check(lib.unifur_bench_stream_probe(bufs[i % copies].data_ptr(), nbytes // 2,
+                                                               dsts[i % copies].data_ptr(), sink.data_ptr(), grid, st))
                 else:
-                    L.check(lib.unifur_nf4_stream_probe(bufs[i % copies].data_ptr(), nbytes // 2,
-                                                        dsts[i % copies].data_ptr(), sink.data_ptr(), grid,
-                                                        torch.cuda.current_stream().cuda_stream))
+                    _probe_check(lib.unifur_bench_stream_mixed(bufs[i % copies].data_ptr(), dsts[i % copies].data_ptr(),
+                                                               w_bytes, write_ratio, grid, st))
             gr = capture(torch, fn, copies)
             ms = replay_event_ms(torch, gr, copies) if gr is not None else event_ms(torch, fn, 2 * copies)
             if best is None or ms < best[0]:
@@ -608,7 +641,7 @@ def bench_backward(torch, Q, L) -> dict:
 
     # the same step with the least workspace: dx through the fused NF4 kernel
     # over W's rows (no expanded weight, no BLAS call)
-    lean_bytes = lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r)
+    lean_bytes = lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r, L.LAYOUT_STRIPED)
     lean = torch.zeros(lean_bytes, dtype=torch.uint8, device=dev)
 
     def step_lean(i: int) -> None:
@@ -841,18 +874,22 @@ def main() -> int:
     gemv = bench_gemv(torch, Q, L, args)
     ceiling = bench_ceiling(torch, L, gemv["bytes"])
     codec = bench_codec(torch, Q, L)
+    ceiling1 = bench_ceiling(torch, L, codec["bytes"], write_ratio=8)
     secondary = {
         "hbm_ceiling_gemv_size": ceiling,
-        "hbm_ceiling_config1_size": bench_ceiling(torch, L, codec["bytes"]),
+        "hbm_ceiling_config1_size": ceiling1,
         "gemv_warm": {"kernel_ms": round(gemv["kernel_warm_ms"], 5),
                       "gbs": round(gemv["bytes"] / gemv["kernel_warm_ms"] / 1e6, 1)},
         "gemv_bf16_activations_cold": {
             "kernel_ms": round(gemv["kernel_cold_ms_bf16x"], 5),
             "gbs": round(gemv_bytes(4096, 11008, True, 2, 4) / gemv["kernel_cold_ms_bf16x"] / 1e6, 1)},
         "dequantize_f32_config1": {"kernel_ms": round(codec["dequant_ms"], 5), "gbs": round(codec["dequant_gbs"], 1),
-                                   "frac": round(codec["dequant_gbs"] / HBM_PEAK_GBS, 4)},
+                                   "frac": round(codec["dequant_gbs"] / HBM_PEAK_GBS, 4),
+                                   "frac_of_write_dominated_ceiling":
+                                       round(codec["dequant_gbs"] / ceiling1["write_dominated_gbs"], 4)},
         "quantize_config1": {"kernel_ms": round(codec["quantize_ms"], 5), "gbs": round(codec["quantize_gbs"], 1),
-                             "frac": round(codec["quantize_gbs"] / HBM_PEAK_GBS, 4)},
+                             "frac": round(codec["quantize_gbs"] / HBM_PEAK_GBS, 4),
+                             "frac_of_read_ceiling": round(codec["quantize_gbs"] / ceiling1["read_gbs"], 4)},
     }
     if not args.quick:
         gemm = bench_gemm(torch, Q, L)

@@ -256,8 +256,10 @@ int unifur_nf4_linear_forward_multi(const void *x, int x_dtype, uint64_t rows, c
  * It allocates nothing -- no hipMalloc / hipFree, no allocating library
  * call -- and uses a static device scratch of 16 MiB per GPU (held until the
  * process ends).  Batches of more than 64 bf16 rows take the fused MFMA
- * kernel (the unifur_nf4_linear_min_workspace_size path), never the expanded
- * weight.  A call whose scratch need exceeds 16 MiB fails with
+ * kernel, never the expanded weight, with its split-K partials where they
+ * fit the scratch (bit-identical to unifur_nf4_linear_forward given a 16 MiB
+ * workspace; with the least workspace the fused kernel runs over whole d_in
+ * and its f32 sums may differ in order).  A call whose scratch need exceeds 16 MiB fails with
  * UNIFUR_NF4_ERR_WORKSPACE and a message naming the size.  All calls on one
  * GPU share that scratch: calls that overlap on one GPU (concurrent streams
  * or threads) race and must be serialized by the caller. */
@@ -290,12 +292,13 @@ int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const un
  * and 16-byte aligned dy and dx, the fused NF4 MFMA kernel for dx: W's rows
  * are its outputs and each W tile is dequantized on chip, so the only
  * scratch is the adapter's bf16 operands (dx gains ((dy scaling) B^T) A^T
- * in the kernel's epilogue, the adapter unmerged); for other weights and
- * shapes the minimum is the default size. */
+ * in the kernel's epilogue, the adapter unmerged); for other layouts
+ * (layout is the weight's UNIFUR_NF4_LAYOUT_*) and shapes the minimum is the
+ * default size. */
 uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
                                                    uint32_t lora_rank);
 uint64_t unifur_nf4_linear_backward_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
-                                                       uint32_t lora_rank);
+                                                       uint32_t lora_rank, int layout);
 int unifur_nf4_linear_backward(const void *dy, int dy_dtype, uint64_t rows, const unifur_nf4_weight *w,
                                const unifur_nf4_lora *lora, const void *x, int x_dtype, void *dx, int dx_dtype,
                                float *grad_a, float *grad_b, void *workspace, uint64_t workspace_bytes,
@@ -372,16 +375,6 @@ uint64_t unifur_nf4_decoder_attn_out_mlp_workspace_size(uint64_t rows, const uni
 int unifur_nf4_decoder_attn_out_mlp(const void *x, const void *ctx, int dtype, uint64_t rows,
                                     const unifur_nf4_decoder_layer *layer, void *y, void *workspace,
                                     uint64_t workspace_bytes, void *stream);
-
-/* ---- measurement --------------------------------------------------------- */
-
-/* No counterpart in the reference: the ceiling the decode GEMV's roofline
- * fraction is compared with.  Streams `bytes` (a multiple of 16) from src with
- * 16-byte loads over `workgroups` workgroups: a read only (dst == NULL;
- * sink, 64 u32, is written only if the data XOR to a fixed odd value) or a
- * copy to dst.  16-byte aligned buffers. */
-int unifur_nf4_stream_probe(const void *src, uint64_t bytes, void *dst, uint32_t *sink, uint32_t workgroups,
-                            void *stream);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,17 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
 
 
+def test_library_exports_nothing_beyond_the_header(lib):
+    """The product library's exported C symbols are exactly the header's: the
+    bench's measurement kernels live in their own library."""
+    import subprocess
+    from unifur_amd import _lib
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.split() and line.split()[-1].startswith("unifur_")}
+    assert exported == set(declared_symbols()), sorted(exported ^ set(declared_symbols()))
+
+
 def test_levels_match_oracle(lib, oracle):
     out = (ctypes.c_float * 16)()
     assert lib.unifur_nf4_levels(out) == 0

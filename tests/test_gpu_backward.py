@@ -153,7 +153,7 @@ def test_fused_dx_with_the_minimum_workspace(device, oracle, case):
     x, xt = acts(oracle, M, K, 1702, torch.bfloat16, device)
     dy, dyt_ = acts(oracle, M, N, 1703, torch.bfloat16, device)
     lib = L.lib()
-    need = lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r)
+    need = lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r, L.LAYOUT_STRIPED)
     full = lib.unifur_nf4_linear_backward_workspace_size(M, K, N, L.BF16, r)
     # the default size holds the expanded bf16 weight; the minimum does not
     # (its scratch: the adapter's operands and the gradients')
@@ -176,6 +176,28 @@ def test_fused_dx_with_the_minimum_workspace(device, oracle, case):
             ql.backward(xt, dyt_, dx_dtype=dxt, workspace=ws[:need - 256])
 
 
+def test_min_workspace_for_a_row_major_weight(device, oracle):
+    """Only a striped weight takes the fused dX kernel: for a row-major one
+    the least workspace is the default size, and a backward given exactly
+    that succeeds (through the expanded weight) within the bars."""
+    M, K, N, r = 96, 512, 1024, 8
+    lib = L.lib()
+    need = lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r, L.LAYOUT_ROW_MAJOR)
+    assert need == lib.unifur_nf4_linear_backward_workspace_size(M, K, N, L.BF16, r)
+    assert need > lib.unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r, L.LAYOUT_STRIPED)
+    lin, wdeq = make_linear(oracle, K, N, 1760, device, striped=False)
+    s = 2.0
+    a, b, ad = lora_parts(oracle, K, N, r, 1761, device, scaling=s)
+    x, xt = acts(oracle, M, K, 1762, torch.bfloat16, device)
+    dy, dyt_ = acts(oracle, M, N, 1763, torch.bfloat16, device)
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    dx, ga, gb = Q.QloraLinear(lin, ad).backward(xt, dyt_, dx_dtype=torch.float32, workspace=ws)
+    rdx, bdx, rga, bga, rgb, bgb = refs(x, dy, wdeq, a, b, s)
+    e = (normwise(dx.cpu(), rdx, bdx), normwise(ga.cpu(), rga, bga), normwise(gb.cpu(), rgb, bgb))
+    print(f"row-major min workspace {need} B: dx {e[0]:.2e} grad_a {e[1]:.2e} grad_b {e[2]:.2e}", flush=True)
+    assert e[0] <= 1e-2 and e[1] <= 1e-5 and e[2] <= 1e-5
+
+
 @pytest.mark.parametrize("M,work", [(64, 0), (64, 4 << 20), (512, 0)])
 def test_fused_dx_without_adapter(device, oracle, M, work):
     """The base dx = dy W^T through the fused kernel: with no scratch at all
@@ -184,7 +206,7 @@ def test_fused_dx_without_adapter(device, oracle, M, work):
     K, N = 1024, 4096
     lin, wdeq = make_linear(oracle, K, N, 1750 + M, device)
     dy, dyt_ = acts(oracle, M, N, 1751, torch.bfloat16, device)
-    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, 0)
+    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, 0, L.LAYOUT_STRIPED)
     assert need <= 65536  # the workspace's fixed counter region only
     size = max(work, need)
     ws = torch.zeros(size, dtype=torch.uint8, device=device)
@@ -210,7 +232,7 @@ def test_fused_dx_edge_shapes(device, oracle, M, K, N, r, work):
     single output tile, one row, and a split whose last slab is short."""
     lin, wdeq = make_linear(oracle, K, N, 1800 + K + N, device)
     dy, dyt_ = acts(oracle, M, N, 1801, torch.bfloat16, device)
-    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r)
+    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r, L.LAYOUT_STRIPED)
     ws = torch.zeros(max(need, work, 256), dtype=torch.uint8, device=device)
     ws = ws[:max(need, work)] if max(need, work) > 0 else ws[:1]
     dy64, w64 = np.asarray(dy, np.float64), np.asarray(wdeq, np.float64)

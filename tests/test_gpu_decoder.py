@@ -106,6 +106,31 @@ def test_attn_out_mlp(device, oracle, layer, rows, dt):
                  f"attn_out_mlp rows={rows} {dt}")
 
 
+@pytest.mark.parametrize("rows,dt", [(32, torch.bfloat16), (16, torch.float32)])
+def test_attn_out_mlp_misaligned_ctx_fits_the_queried_workspace(device, oracle, layer, rows, dt):
+    """A ctx one element off the 16-byte alignment moves o off the skinny
+    kernel: a workspace of exactly the queried size still serves the call."""
+    import ctypes
+    lay, w, _, g_post = layer
+    x, xt = acts(oracle, rows, HIDDEN, 0x5A00 + rows, dt, device)
+    ctx, ct = acts(oracle, rows, HEADS * DIM, 0x5B00 + rows, dt, device)
+    buf = torch.empty(rows * HEADS * DIM + 1, dtype=dt, device=device)
+    buf[1:].copy_(ct.reshape(-1))
+    ct_off = buf[1:].view(rows, HEADS * DIM)
+    s = lay.layer_struct()
+    code = L.BF16 if dt == torch.bfloat16 else L.F32
+    need = L.lib().unifur_nf4_decoder_attn_out_mlp_workspace_size(rows, s, code)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)
+    y = torch.empty_like(xt)
+    L.check(L.lib().unifur_nf4_decoder_attn_out_mlp(xt.data_ptr(), ct_off.data_ptr(), code, rows, ctypes.byref(s),
+                                                     y.data_ptr(), ws.data_ptr(), need,
+                                                     torch.cuda.current_stream().cuda_stream))
+    _, ref = oracle.decoder_attn_out_mlp_ref_f64(x, ctx, g_post, EPS, w["o"], w["gate"], w["up"], w["down"])
+    tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+    assert_close(y.float().cpu().numpy(), ref, out_mlp_bound(oracle, x, ctx, w, g_post), tol,
+                 f"attn_out_mlp misaligned ctx rows={rows} {dt}")
+
+
 def test_attn_out_mlp_in_place(device, oracle, layer):
     lay, w, _, g_post = layer
     x, xt = acts(oracle, 1, HIDDEN, 0x5A00, torch.float32, device)

@@ -105,7 +105,7 @@ def test_fused_dx_backward_replays(device, oracle, rank):
     _, xt = acts(oracle, M, K, 2061, torch.bfloat16, device)
     _, dyt = acts(oracle, M, N, 2062, torch.bfloat16, device)
     from unifur_amd import _lib as L
-    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, rank)
+    need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, rank, L.LAYOUT_STRIPED)
     # room for the split-K partials without the adapter, the minimum with it
     ws = torch.zeros(max(need, 2 << 20) if rank == 0 else need, dtype=torch.uint8, device=device)
     dx = torch.empty(M, K, device=device)

@@ -5,8 +5,10 @@ callers that cannot allocate, running on a static per-GPU scratch.  Each case
 calls it through the C ABI twice in a row -- the second call with a smaller
 input, so that it runs on the scratch the first call left behind -- and
 compares every output bit for bit with unifur_nf4_linear_forward given its
-least workspace (unifur_nf4_linear_min_workspace_size: the same kernels), and
-the prefill case also against the float64 product within the bf16 bar.
+least workspace (unifur_nf4_linear_min_workspace_size: the same kernels), or,
+for prefill calls without an adapter (the fused kernel's split-K partials
+fit the scratch), given the scratch's 16 MiB; prefill cases are also checked
+against the float64 product within the bf16 bar.
 """
 from __future__ import annotations
 
@@ -29,13 +31,19 @@ def _dt(t: torch.dtype) -> int:
     return L.BF16 if t == torch.bfloat16 else L.F32
 
 
-def existing(lin, x, lora, y_dtype, bias=None):
-    """unifur_nf4_linear_forward with the least workspace it accepts."""
+SCRATCH = 16 << 20  # the allocation-free entry point's static scratch
+
+
+def existing(lin, x, lora, y_dtype, bias=None, workspace=None):
+    """unifur_nf4_linear_forward with the least workspace it accepts, or with
+    ``workspace`` bytes."""
     lib = L.lib()
     w = lin.weight_struct()
     rows, d_in = x.shape
     rank = lora.rank if lora is not None else 0
     need = lib.unifur_nf4_linear_min_workspace_size(rows, d_in, lin.d_output(), _dt(x.dtype), rank)
+    if workspace is not None:
+        need = workspace
     ws = torch.zeros(max(int(need), 1), dtype=torch.uint8, device=x.device)
     y = torch.empty(rows, lin.d_output(), dtype=y_dtype, device=x.device)
     L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), _dt(x.dtype), rows, ctypes.byref(w),
@@ -87,6 +95,26 @@ def test_noalloc_matches_linear_forward_twice(device, oracle, case):
             if r:
                 ref = ref + oracle.lora_ref_f64(x, a, b, ad.scaling())
             check(got, ref, x, wdeq, TOL_BF16, f"noalloc rows {m}")
+
+
+@pytest.mark.parametrize("rows", [(100, 40), (300, 130)])
+def test_noalloc_split_k_without_adapter(device, oracle, rows):
+    """Without an adapter the fused kernel's split-K partials fit the scratch
+    (100 x 4096 x 4096 takes two d_in slabs): bit for bit what
+    unifur_nf4_linear_forward gives with a 16 MiB workspace, and within the
+    bf16 bar of the float64 product, twice in a row."""
+    k = n = 4096
+    print(f"noalloc split-K rows {rows}", flush=True)
+    lin, wdeq = make_linear(oracle, k, n, 5200, device, dq=True, striped=True)
+    bias = torch.from_numpy(oracle.fill_normal(5201, 0.1, n)).to(device)
+    for m, seed in zip(rows, (5202, 5203)):
+        x, xd = acts(oracle, m, k, seed, torch.bfloat16, device)
+        got = noalloc(lin, xd, None, torch.bfloat16, bias)
+        want = existing(lin, xd, None, torch.bfloat16, bias, workspace=SCRATCH)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"rows {m}: noalloc differs from linear_forward with a 16 MiB workspace"
+        check(got, oracle.linear_ref_f64(x, wdeq, oracle.fill_normal(5201, 0.1, n)), x, wdeq, TOL_BF16,
+              f"noalloc split-K rows {m}")
 
 
 def test_noalloc_refuses_what_does_not_fit(device, oracle):

@@ -106,7 +106,7 @@ SIGNATURES = {
     "unifur_nf4_linear_forward_multi": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), _P, _P, _I,
                                              ctypes.c_uint32, _P, _U64, _P]),
     "unifur_nf4_linear_backward_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
-    "unifur_nf4_linear_backward_min_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
+    "unifur_nf4_linear_backward_min_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32, _I]),
     "unifur_nf4_linear_backward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Lora), _P, _I,
                                         _P, _I, _P, _P, _P, _U64, _P]),
     "unifur_nf4_linear_min_workspace_size": (_U64, [_U64, _U64, _U64, _I, ctypes.c_uint32]),
@@ -116,7 +116,6 @@ SIGNATURES = {
                                                _I, _P]),
     "unifur_nf4_qlora_forward": (_I, [_P, _I, _U64, ctypes.POINTER(Weight), ctypes.POINTER(Lora), _P, _I, _P,
                                       _U64, _P]),
-    "unifur_nf4_stream_probe": (_I, [_P, _U64, _P, _P, ctypes.c_uint32, _P]),
     "unifur_nf4_decoder_attn_in_workspace_size": (_U64, [_U64, ctypes.POINTER(DecoderLayer), _I]),
     "unifur_nf4_decoder_attn_in": (_I, [_P, _I, _U64, ctypes.POINTER(DecoderLayer), _P, _P, _P, _P, _U64, _P]),
     "unifur_nf4_decoder_attn_out_mlp_workspace_size": (_U64, [_U64, ctypes.POINTER(DecoderLayer), _I]),

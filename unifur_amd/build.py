@@ -19,6 +19,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libunifur_nf4.so")
+PROBE_DIR = os.path.join(HERE, "bench_probe")
+PROBE_LIB = os.path.join(PROBE_DIR, "libunifur_bench_probe.so")
 ARCH = os.environ.get("UNIFUR_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (the host pass warns
@@ -49,19 +51,28 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp, *LINK_LIBS]
+def _link(objs, out: str, libs) -> None:
+    tmp = out + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp, *libs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """libunifur_nf4.so (the product) and, beside it, the bench's streaming
+    probes (bench_probe/libunifur_bench_probe.so: measurement kernels that are
+    not part of the product's ABI)."""
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    probe_src = os.path.join(PROBE_DIR, "stream_probe.hip")
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources) + 1)) as ex:
+        objs = list(ex.map(_compile, sources + [probe_src]))
+    _link(objs[:-1], LIB, LINK_LIBS)
+    _link(objs[-1:], PROBE_LIB, [])
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB}")
     return LIB
 
 

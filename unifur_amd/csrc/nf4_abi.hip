@@ -21,7 +21,6 @@
 #include "nf4_generic.hpp"
 #include "nf4_gemv.hpp"
 #include "nf4_layout.hpp"
-#include "nf4_probe.hpp"
 
 namespace unifur {
 namespace {
@@ -133,11 +132,16 @@ int internal_workspace(size_t bytes, hipStream_t stream, void** out) {
                   "the internal workspace of this stream holds " + std::to_string(slot.second) + " bytes, " +
                       std::to_string(bytes) + " needed, and the stream is capturing: make one eager call of "
                       "this shape first or pass a workspace");
-    // grow at least twofold, so a rising sequence of shapes retires few buffers
+    // grow at least twofold, so a rising sequence of shapes retires few
+    // buffers; if the doubled size does not fit, try the size this call needs
     const size_t want = std::max<size_t>({bytes, size_t{1} << 20, 2 * slot.second});
-    const size_t sz = align_up(want);
+    size_t sz = align_up(want);
     void* p = nullptr;
-    UNIFUR_HIP(hipMalloc(&p, sz));
+    if (hipMalloc(&p, sz) != hipSuccess) {
+      (void)hipGetLastError();  // clear the failed allocation's error
+      sz = align_up(std::max<size_t>(bytes, size_t{1} << 20));
+      UNIFUR_HIP(hipMalloc(&p, sz));
+    }
     UNIFUR_HIP(hipMemsetAsync(p, 0, sz, stream));
     slot = {p, sz};  // the outgrown buffer stays allocated until the process ends
   }
@@ -343,9 +347,9 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     if (!workspace || workspace_bytes >= lean.total) L = lean;
   }
   if (L.path == LinearPath::kMfma && !L.expand && (L.splits > 1 || L.tail > 1) &&
-      ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
-    // no room for the split-K partials (or an output the reduction cannot
-    // store four at a time): the fused kernel over whole d_in
+      ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16) || !aligned_to(bias, 16))) {
+    // no room for the split-K partials (or an output or bias the reduction
+    // cannot access four at a time): the fused kernel over whole d_in
     L = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false,
                     false);
   }
@@ -1204,8 +1208,13 @@ AttnOutLayout plan_attn_out(uint64_t rows, const unifur_nf4_decoder_layer* l, in
     L.mlp = MlpStage::kGeneral;
   }
   uint64_t inner = kCounterRegion;
-  if (L.o_path == OutPath::kGeneral)
+  if (L.o_path == OutPath::kGeneral) {
+    // the o linear's own plan for this ctx (a misaligned ctx can take the
+    // generic path, which needs more than the aligned size query says)
     inner = std::max<uint64_t>(inner, unifur_nf4_linear_workspace_size(rows, ctx_dim, hid, dtype, 0));
+    inner = std::max<uint64_t>(inner, plan_linear(rows, ctx_dim, hid, 0, l->o.packed, dtype, ctx, is_striped(&l->o),
+                                                  l->o.scales.kind).total);
+  }
   if (L.mlp == MlpStage::kGeneral)
     inner = std::max<uint64_t>(inner, swiglu_workspace(rows, hid, inter, dtype, true));
   Carver c;
@@ -1477,8 +1486,12 @@ int unifur_nf4_decoder_attn_in(const void* x, int dtype, uint64_t rows, const un
 uint64_t unifur_nf4_decoder_attn_out_mlp_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer* layer,
                                                         int dtype) {
   if (rows == 0 || check_layer(layer) != UNIFUR_NF4_OK || !valid_dtype(dtype)) return 0;
+  // a ctx off the 16-byte alignment can move the o projection to the
+  // general path, whose workspace differs: the larger of both plans
   const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
-  return plan_attn_out(rows, layer, dtype, aligned, aligned).total;
+  const void* ragged = reinterpret_cast<const void*>(uintptr_t{256} + (dtype == UNIFUR_NF4_BF16 ? 2 : 4));
+  return std::max<uint64_t>(plan_attn_out(rows, layer, dtype, aligned, aligned).total,
+                            plan_attn_out(rows, layer, dtype, ragged, aligned).total);
 }
 
 int unifur_nf4_decoder_attn_out_mlp(const void* x, const void* ctx, int dtype, uint64_t rows,
@@ -1518,12 +1531,16 @@ uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in,
 }
 
 uint64_t unifur_nf4_linear_backward_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
-                                                       uint32_t lora_rank) {
+                                                       uint32_t lora_rank, int layout) {
   if (d_in == 0 || d_out == 0) return 0;
+  // only a striped weight can take the fused dX kernel; any other layout
+  // (or an unknown value) gets the default size
+  if (layout != UNIFUR_NF4_LAYOUT_STRIPED || d_out % 64 != 0)
+    return unifur_nf4_linear_backward_workspace_size(rows, d_in, d_out, dy_dtype, lora_rank);
   uint64_t need = 0;
   for (int kind = 0; kind < 2; ++kind) {
     const BackwardLayout L = plan_backward(rows, d_in, d_out, lora_rank, dy_dtype, rows > 0, lora_rank > 0,
-                                           d_out % 64 == 0, kind, true, false, false);
+                                           true, kind, true, false, false);
     if (rows > 0 && !L.fused) return unifur_nf4_linear_backward_workspace_size(rows, d_in, d_out, dy_dtype, lora_rank);
     need = std::max<uint64_t>(need, L.total);
   }
@@ -1730,17 +1747,6 @@ int unifur_nf4_unstripe_weight(const unifur_nf4_weight* src, uint8_t* dst_packed
   UNIFUR_HIP(launch_stripe_codes(src->packed, dst_packed, src->d_in, src->d_out, false, st));
   UNIFUR_HIP(launch_stripe_scales(dq ? (const void*)src->scales.dq_codes : (const void*)src->scales.absmax,
                                   dst_scales, src->d_in, src->d_out, dq, false, st));
-  return UNIFUR_NF4_OK;
-}
-
-int unifur_nf4_stream_probe(const void* src, uint64_t bytes, void* dst, uint32_t* sink, uint32_t workgroups,
-                            void* stream) {
-  if (bytes == 0) return UNIFUR_NF4_OK;
-  UNIFUR_ARG(src && sink, "src or sink is NULL");
-  UNIFUR_ARG(bytes % 16 == 0 && aligned_to(src, 16) && aligned_to(dst, 16), "bytes and buffers must be 16-byte multiples");
-  UNIFUR_ARG(workgroups >= 1 && workgroups <= 65536, "workgroups must be in [1, 65536]");
-  UNIFUR_HIP(launch_stream_probe(src, bytes / 16, dst, 0x9e3779b9u, sink, (int)workgroups,
-                                 static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
 }
 
