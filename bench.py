@@ -532,9 +532,20 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
     q_kernel_ms = event_ms(torch, lambda i: Q.quantize_linears(vals), 3)
     params = sum(di * do for (_, di, do) in vals)
     q_bytes = 4 * params + params // 2 + 4 * (params // 64)  # f32 in, codes + f32 absmax out (config 5 unit)
+    # the same pass from bf16 checkpoint tensors as they lie ([out, in], PyTorch
+    # order: qwen_linear's input), transposed inside the quantize kernel
+    ckpt = [v.view(di, do).t().contiguous().to(torch.bfloat16) for (v, di, do) in vals]
     del vals
+    torch.cuda.synchronize()
+    c_s, _ = best_of_three(lambda: Q.quantize_checkpoint_linears(ckpt))
+    c_kernel_ms = event_ms(torch, lambda i: Q.quantize_checkpoint_linears(ckpt), 3)
+    c_bytes = 2 * params + params // 2 + 4 * (params // 64)  # bf16 in
+    del ckpt
     out = {"quantize_pass_ms": round(q_s * 1e3, 3), "quantize_pass_gbs": round(q_bytes / q_s / 1e9, 1),
            "quantize_pass_per_weight_ms": round(q_each_s * 1e3, 3), "quantize_pass_events_ms": round(q_kernel_ms, 3),
+           "quantize_pass_bf16_checkpoint_ms": round(c_s * 1e3, 3),
+           "quantize_pass_bf16_checkpoint_events_ms": round(c_kernel_ms, 3),
+           "quantize_pass_bf16_checkpoint_gbs": round(c_bytes / c_s / 1e9, 1),
            "params": params}
     wbytes = sum(gemv_bytes(lin.d_input(), lin.d_output(), True, 0, 0) for lin in lins)
     # the 184.5 MB model fits the 256 MiB Infinity Cache: rotate model copies

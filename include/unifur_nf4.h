@@ -176,6 +176,15 @@ int unifur_nf4_embedding_forward(const uint8_t *packed, const unifur_nf4_scales 
 int unifur_nf4_quantize_transposed(const void *src, int src_dtype, uint64_t out_features, uint64_t in_features,
                                    uint8_t *packed, float *absmax, void *stream);
 
+/* transpose2d (src/qwennet.rs:1375-1390) of a decoded checkpoint linear:
+ * dst [in_features, out_features] f32 = the transpose of src [out_features,
+ * in_features] (f32, or bf16 decoded exactly, src/import.rs:323-327), for
+ * weights whose out_features is not a multiple of 64 (their blocks straddle
+ * the rows of the transposed buffer, so they are quantized flat after this).
+ * out_features <= 65535 * 64. */
+int unifur_nf4_transpose_checkpoint(const void *src, int src_dtype, uint64_t out_features, uint64_t in_features,
+                                    float *dst, void *stream);
+
 /* The quantize pass over a model's linears (QwenTrunk::to_nf4,
  * src/qwennet.rs:1185-1269, which runs Nf4Linear::from_values,
  * src/qwennet.rs:196-205 -- PackedNf4Tensor::quantize then
@@ -193,6 +202,20 @@ uint64_t unifur_nf4_quantize_linears_workspace_size(const uint64_t *d_in, const 
 int unifur_nf4_quantize_linears(const float *const *values, const uint64_t *d_in, const uint64_t *d_out, uint32_t n,
                                 uint8_t *const *packed, uint8_t *const *dq_codes, float *const *scale_of_scales,
                                 void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* The same pass from checkpoint tensors as they lie (qwen_linear,
+ * src/qwennet.rs:1687-1726, over each decoded linear of the checkpoint):
+ * values[i] is the PyTorch-order [d_out[i], d_in[i]] weight in src_dtype
+ * (f32, or bf16 decoded exactly as src/import.rs:323-327 does), transposed on
+ * the fly (transpose2d, src/qwennet.rs:1375-1390) -- packed[i], dq_codes[i]
+ * and scale_of_scales[i] are byte for byte what unifur_nf4_quantize_linears
+ * writes for the transposed f32 copy.  d_out % 64 == 0, values aligned to
+ * their dtype (rows of a multiple of 16 bytes take the vector loads), packed
+ * 8-byte aligned.  Workspace as unifur_nf4_quantize_linears. */
+int unifur_nf4_quantize_checkpoint_linears(const void *const *values, int src_dtype, const uint64_t *d_in,
+                                           const uint64_t *d_out, uint32_t n, uint8_t *const *packed,
+                                           uint8_t *const *dq_codes, float *const *scale_of_scales, void *workspace,
+                                           uint64_t workspace_bytes, void *stream);
 
 /* ---- device layout of a linear weight ------------------------------------------ */
 

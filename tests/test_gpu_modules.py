@@ -57,13 +57,30 @@ def test_quantize_transposed_is_transpose_then_quantize(device, oracle, dtype, s
     assert np.array_equal(absmax.cpu().numpy().view(np.uint32), absmax_ref.view(np.uint32))
 
 
-def test_qwen_linear_with_ragged_out_features_falls_back_to_separate_transpose(device, oracle):
-    out_f, in_f = 100, 96
-    v, t = checkpoint_linear(oracle, out_f, in_f, 0x7B, torch.float32)
-    packed_ref, _ = oracle.quantize_packed(oracle.transpose(v.reshape(-1), out_f, in_f))
-    lin, _ = QN.qwen_linear(t, QN.WeightStore.NF4)
-    assert np.array_equal(lin.inner.packed().codes.cpu().numpy(), packed_ref)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(100, 96), (70, 129), (1, 64), (130, 1)])
+def test_qwen_linear_with_ragged_out_features_falls_back_to_separate_transpose(device, oracle, dtype, shape):
+    """out % 64 != 0: the library transposes (unifur_nf4_transpose_checkpoint,
+    bf16 decoded exactly) and the flat buffer is quantized; codes, DQ codes and
+    scale of scales equal the oracle's transpose + quantize + double quantize."""
+    out_f, in_f = shape
+    v, t = checkpoint_linear(oracle, out_f, in_f, 0x7B + out_f, dtype)
+    tv = oracle.transpose(v.reshape(-1), out_f, in_f)
+    packed_ref, absmax_ref = oracle.quantize_packed(tv)
+    q_ref, sos_ref = oracle.double_quantize(absmax_ref)
+    lin, nbytes = QN.qwen_linear(t, QN.WeightStore.NF4)
+    p = lin.inner.packed()
+    assert np.array_equal(p.codes.cpu().numpy(), packed_ref)
+    assert np.array_equal(p.dq_codes.cpu().numpy(), q_ref)
+    assert p.scale_of_scales.cpu().numpy()[0].view(np.uint32) == np.float32(sos_ref).view(np.uint32)
     assert not lin.inner.is_striped()
+    assert nbytes == oracle.estimated_resident_bytes(out_f * in_f, True)
+    # the transpose entry point itself: bit for bit the oracle's transpose2d
+    from unifur_amd import _lib as L
+    dst = torch.empty(out_f * in_f, dtype=torch.float32, device=device)
+    L.check(L.lib().unifur_nf4_transpose_checkpoint(t.data_ptr(), Q._dtype_code(dtype), out_f, in_f, dst.data_ptr(),
+                                                    Q._stream()))
+    assert np.array_equal(dst.cpu().numpy().view(np.uint32), tv.view(np.uint32))
 
 
 def test_qwen_linear_f32_store_and_forward(device, oracle):

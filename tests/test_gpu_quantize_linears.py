@@ -6,7 +6,10 @@ write, for each weight, exactly the bytes of the per-weight path -- quantize
 layout -- whose codec is pinned bit-exact against the oracle by the codec
 tests.  Shapes cover the config-5 projections, spans that cross rows or end
 inside a 1024-value span, one-row weights, groups of more than 48 weights,
-and blocks of zeros, NaN, infinities and subnormals.
+and blocks of zeros, NaN, infinities and subnormals.  The checkpoint form
+(unifur_nf4_quantize_checkpoint_linears) takes the PyTorch-order [out, in]
+tensors (f32 or bf16) that qwen_linear receives (src/qwennet.rs:1687-1726)
+and must write the bytes of the transposed copies, tested the same ways.
 """
 from __future__ import annotations
 
@@ -130,3 +133,91 @@ def test_forward_matches_and_argument_errors(device, oracle):
     assert lib.unifur_nf4_quantize_linears(None, U(1), U(64), 1, P(buf.data_ptr()), P(buf.data_ptr() + 256),
                                            P(buf.data_ptr() + 512), None, 0, st) == L.ERR_INVALID
     assert lib.unifur_nf4_quantize_linears(None, None, None, 0, None, None, None, None, 0, st) == 0
+
+
+# ------------------------------------------------- checkpoint [out, in] form --
+
+def checkpoint_tensors(oracle, shapes, seed, dtype, device):
+    """[out = d_out, in = d_in] tensors; bf16 ones hold exactly the oracle's
+    RNE rounding of the f32 draw (the values the reference decodes)."""
+    host, dev = [], []
+    for i, (di, do) in enumerate(shapes):
+        v = oracle.fill_normal(seed + 0x10000 * i, 0.02, di * do)
+        if dtype == torch.bfloat16:
+            v = oracle.round_bf16(v)
+        v = v.reshape(do, di)
+        host.append(v)
+        dev.append(torch.from_numpy(v).to(device).to(dtype))
+    return host, dev
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_checkpoint_config5_all_weights_against_the_oracle(device, oracle, dtype):
+    """All 168 config-5 projections from checkpoint tensors as they lie, in
+    one call: each weight's striped codes, u8 scales and scale of scales equal
+    the oracle's transpose2d + PackedNf4Tensor::quantize +
+    with_double_quantization in the striped permutation."""
+    from test_gpu_layout import striped_codes_np, striped_scales_np
+    per_layer = [(896, 896), (896, 128), (896, 128), (896, 896), (896, 4864), (896, 4864), (4864, 896)]
+    shapes = per_layer * 24
+    host, dev = checkpoint_tensors(oracle, shapes, 0x4E463457 + 5, dtype, device)
+    got = Q.quantize_checkpoint_linears(dev)
+    torch.cuda.synchronize()
+    assert len(got) == 168
+    for i, ((di, do), v, g) in enumerate(zip(shapes, host, got)):
+        tv = oracle.transpose(v.reshape(-1), do, di)  # [in, out]
+        packed, absmax = oracle.quantize_packed(tv)
+        q, sos = oracle.double_quantize(absmax)
+        assert g.is_striped() and (g.d_input(), g.d_output()) == (di, do)
+        assert np.array_equal(g._codes.cpu().numpy(), striped_codes_np(packed, di, do)), f"weight {i}: codes"
+        assert np.array_equal(g._scales.cpu().numpy(), striped_scales_np(q, di, do)), f"weight {i}: u8 scales"
+        assert g._sos.cpu().numpy().view(np.uint32)[0] == np.float32(sos).view(np.uint32), f"weight {i}: sos"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_checkpoint_ragged_shapes_match_the_transposed_pass(device, oracle, dtype):
+    """d_in not a multiple of 64 (a partial source tile), of 8 or 4 (the
+    element-load path), one-row and one-column weights, two groups: the same
+    bytes as the f32 pass over the transposed copies."""
+    shapes = [(1, 64), (7, 128), (100, 192), (130, 64), (64, 64), (3, 960), (65, 320)] * 7 + [(896, 128)]
+    host, dev = checkpoint_tensors(oracle, shapes, 3400, dtype, device)
+    got = Q.quantize_checkpoint_linears(dev)
+    ref = Q.quantize_linears([(t.float().t().contiguous().view(-1), di, do) for t, (di, do) in zip(dev, shapes)])
+    for g, r in zip(got, ref):
+        same_bytes(g, r)
+
+
+def test_checkpoint_special_values(device, oracle):
+    do, di = 256, 9  # [out, in]
+    v = oracle.fill_normal(3500, 0.02, di * do).reshape(do, di).copy()
+    v[0:64, 0] = 0.0        # a zero block (column 0 of the transposed weight, rows 0-63)
+    v[64:128, 1] = 1e-40    # a subnormal block
+    v[3, 2] = np.nan
+    v[130, 3] = np.inf
+    v[192:256, 4] = np.nan  # an all-NaN block
+    v[5, 5] = -0.0
+    v[70, 6] = 3.0e38       # large absmax: the exact path
+    t = torch.from_numpy(v).cuda()
+    got = Q.quantize_checkpoint_linears([t])[0]
+    same_bytes(got, Q.quantize_linears([(t.t().contiguous().view(-1), di, do)])[0])
+
+
+def test_checkpoint_argument_errors(device):
+    a = torch.zeros(64, 8, device="cuda")
+    b = torch.zeros(64, 8, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        Q.quantize_checkpoint_linears([a, b])  # mixed dtypes in one call
+    with pytest.raises(ValueError):
+        Q.quantize_checkpoint_linears([torch.zeros(100, 8, device="cuda")])  # out % 64 != 0
+    lib = L.lib()
+    P = ctypes.c_void_p * 1
+    U = ctypes.c_uint64 * 1
+    buf = torch.zeros(1024, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    # bf16 values off their 2-byte alignment, and a bad dtype
+    assert lib.unifur_nf4_quantize_checkpoint_linears(P(b.data_ptr() + 1), L.BF16, U(8), U(64), 1, P(buf.data_ptr()),
+                                                      P(buf.data_ptr() + 256), P(buf.data_ptr() + 512), None, 0,
+                                                      st) == L.ERR_INVALID
+    assert lib.unifur_nf4_quantize_checkpoint_linears(P(a.data_ptr()), 5, U(8), U(64), 1, P(buf.data_ptr()),
+                                                      P(buf.data_ptr() + 256), P(buf.data_ptr() + 512), None, 0,
+                                                      st) == L.ERR_INVALID

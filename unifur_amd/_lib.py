@@ -94,6 +94,8 @@ SIGNATURES = {
     "unifur_nf4_quantize_transposed": (_I, [_P, _I, _U64, _U64, _P, _P, _P]),
     "unifur_nf4_quantize_linears_workspace_size": (_U64, [_P, _P, ctypes.c_uint32]),
     "unifur_nf4_quantize_linears": (_I, [_P, _P, _P, ctypes.c_uint32, _P, _P, _P, _P, _U64, _P]),
+    "unifur_nf4_transpose_checkpoint": (_I, [_P, _I, _U64, _U64, _P, _P]),
+    "unifur_nf4_quantize_checkpoint_linears": (_I, [_P, _I, _P, _P, ctypes.c_uint32, _P, _P, _P, _P, _U64, _P]),
     "unifur_nf4_dense_linear_workspace_size": (_U64, [_U64, ctypes.c_uint32]),
     "unifur_nf4_dense_linear_forward": (_I, [_P, _I, _U64, _P, _U64, _U64, _P, ctypes.POINTER(Lora), _P, _I, _P,
                                              _U64, _P]),

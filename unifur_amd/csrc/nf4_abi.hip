@@ -1652,17 +1652,21 @@ uint64_t unifur_nf4_quantize_linears_workspace_size(const uint64_t* d_in, const 
   return c.off;
 }
 
-int unifur_nf4_quantize_linears(const float* const* values, const uint64_t* d_in, const uint64_t* d_out, uint32_t n,
-                                uint8_t* const* packed, uint8_t* const* dq_codes, float* const* scale_of_scales,
-                                void* workspace, uint64_t workspace_bytes, void* stream) {
+namespace {
+
+int run_quantize_linears(const void* const* values, int src_kind, const uint64_t* d_in, const uint64_t* d_out,
+                         uint32_t n, uint8_t* const* packed, uint8_t* const* dq_codes,
+                         float* const* scale_of_scales, void* workspace, uint64_t workspace_bytes, void* stream) {
   if (n == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(values && d_in && d_out && packed && dq_codes && scale_of_scales, "an argument array is NULL");
+  const uintptr_t align = src_kind == kQuantSrcF32 ? 16 : src_kind == kQuantSrcF32T ? 4 : 2;
   for (uint32_t i = 0; i < n; ++i) {
     UNIFUR_ARG(d_in[i] > 0 && d_out[i] > 0 && d_out[i] % 64 == 0, "quantize_linears needs d_out % 64 == 0");
     UNIFUR_ARG(d_in[i] <= 0x7fffffffu && d_out[i] <= 0x7fffffffu, "quantize_linears: weight too large");
     UNIFUR_ARG(values[i] && packed[i] && dq_codes[i] && scale_of_scales[i], "a tensor pointer is NULL");
-    UNIFUR_ARG(aligned_to(values[i], 16) && aligned_to(packed[i], 8) && aligned_to(scale_of_scales[i], 4),
-               "values must be 16-byte, packed 8-byte aligned");
+    UNIFUR_ARG(aligned_to(values[i], align) && aligned_to(packed[i], 8) && aligned_to(scale_of_scales[i], 4),
+               src_kind == kQuantSrcF32 ? "values must be 16-byte, packed 8-byte aligned"
+                                        : "values must be aligned to their dtype, packed 8-byte aligned");
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t need = quantize_linears_scratch_bytes(d_in, d_out, n);
@@ -1670,8 +1674,40 @@ int unifur_nf4_quantize_linears(const float* const* values, const uint64_t* d_in
   Carver c;
   const size_t off = c.take(need);
   if (int r = resolve_workspace(workspace, workspace_bytes, c.off, st, &ws)) return r;
-  UNIFUR_HIP(launch_quantize_linears(values, d_in, d_out, n, packed, dq_codes, scale_of_scales, at<void>(ws, off), st));
+  UNIFUR_HIP(launch_quantize_linears(values, src_kind, d_in, d_out, n, packed, dq_codes, scale_of_scales,
+                                     at<void>(ws, off), st));
   return UNIFUR_NF4_OK;
+}
+
+}  // namespace
+
+int unifur_nf4_quantize_linears(const float* const* values, const uint64_t* d_in, const uint64_t* d_out, uint32_t n,
+                                uint8_t* const* packed, uint8_t* const* dq_codes, float* const* scale_of_scales,
+                                void* workspace, uint64_t workspace_bytes, void* stream) {
+  return run_quantize_linears(reinterpret_cast<const void* const*>(values), kQuantSrcF32, d_in, d_out, n, packed,
+                              dq_codes, scale_of_scales, workspace, workspace_bytes, stream);
+}
+
+int unifur_nf4_transpose_checkpoint(const void* src, int src_dtype, uint64_t out_features, uint64_t in_features,
+                                    float* dst, void* stream) {
+  UNIFUR_ARG(valid_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  if (out_features == 0 || in_features == 0) return UNIFUR_NF4_OK;
+  UNIFUR_ARG(src && dst, "src or dst is NULL");
+  UNIFUR_ARG(out_features <= 65535ull * 64ull, "out_features exceeds 65535 * 64");
+  UNIFUR_ARG(aligned_to(src, src_dtype == UNIFUR_NF4_BF16 ? 2 : 4) && aligned_to(dst, 4),
+             "src or dst misaligned for its dtype");
+  UNIFUR_HIP(launch_transpose_decode(src, src_dtype == UNIFUR_NF4_BF16, out_features, in_features, dst,
+                                     static_cast<hipStream_t>(stream)));
+  return UNIFUR_NF4_OK;
+}
+
+int unifur_nf4_quantize_checkpoint_linears(const void* const* values, int src_dtype, const uint64_t* d_in,
+                                           const uint64_t* d_out, uint32_t n, uint8_t* const* packed,
+                                           uint8_t* const* dq_codes, float* const* scale_of_scales, void* workspace,
+                                           uint64_t workspace_bytes, void* stream) {
+  UNIFUR_ARG(valid_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  return run_quantize_linears(values, src_dtype == UNIFUR_NF4_BF16 ? kQuantSrcBf16T : kQuantSrcF32T, d_in, d_out, n,
+                              packed, dq_codes, scale_of_scales, workspace, workspace_bytes, stream);
 }
 
 uint64_t unifur_nf4_dense_linear_workspace_size(uint64_t rows, uint32_t lora_rank) {

@@ -471,6 +471,114 @@ __global__ __launch_bounds__(kQuantThreads) void qgroup_quantize_kernel(QGroupAr
   }
 }
 
+// The same first pass from checkpoint tensors as they lie: values[i] is the
+// PyTorch-order [N][K] weight (f32, or bf16 decoded exactly), i.e. the
+// transpose of the [K][N] weight to quantize (qwen_linear's transpose2d,
+// src/qwennet.rs:1375-1390, fused away).  A workgroup per 64 x 64 source
+// tile (k tile kt, block column b): rows o = 64 b .. + 63 of the source,
+// columns k = 64 kt .. + 63, through LDS (padded rows); then wave w takes
+// tile rows k = 16 w .. + 15, lane l block row k = 16 w + l / 4 and the
+// quarter q = l % 4 of its 64 values, which is exactly stripe 4 b + q of
+// that row: a 4-lane absmax, 16 codes, one 8-byte store (the four lanes of
+// a row write its four stripes, the 16 rows of a wave 128 contiguous bytes
+// per stripe).  VEC: rows 16-byte aligned (K a multiple of 8 for bf16, 4
+// for f32), the tile loaded 16 bytes per thread and load.
+template <bool BF16, bool VEC>
+__global__ __launch_bounds__(256) void qgroup_quantize_t_kernel(QGroupArgs a) {
+  __shared__ BucketEntry tab[33];
+  __shared__ float tile[64][65];
+  build_bucket_table(tab);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (uint32_t span = blockIdx.x; span < a.spans; span += gridDim.x) {
+    int lo = 0, hi = a.n - 1;  // the tensor holding this tile (uniform binary search)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (span >= a.t[mid].span_begin) lo = mid;
+      else hi = mid - 1;
+    }
+    const QGroupTensor& T = a.t[lo];
+    const uint32_t bpr = T.N / kBlock;
+    const uint32_t local = span - T.span_begin;
+    const uint32_t kt = local / bpr, b = local - kt * bpr;
+    const uint32_t k0 = 64u * kt;
+    const uint64_t o0 = 64ull * b;
+    __syncthreads();  // the bucket table built; the previous tile's reads done
+    if constexpr (VEC) {
+      constexpr int kPer = BF16 ? 8 : 4;  // values per 16-byte load
+      constexpr int kRowLoads = 64 / kPer;
+      for (int i = tid; i < 64 * kRowLoads; i += 256) {
+        const int o = i / kRowLoads, kc = (i % kRowLoads) * kPer;
+        float v[kPer];
+        if (k0 + kc < T.K) {  // K is a multiple of kPer: the load lies inside the row
+          const uint64_t idx = (o0 + o) * T.K + k0 + kc;
+          const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(T.values) +
+                                                          idx * (BF16 ? 2 : 4));
+          if constexpr (BF16) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[2 * e] = __uint_as_float(w[e] << 16);
+              v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(w[e]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) v[e] = 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) tile[o][kc + e] = v[e];
+      }
+    } else {
+      for (int i = tid; i < 64 * 64; i += 256) {
+        const int o = i >> 6, k = i & 63;
+        float v = 0.0f;
+        if (k0 + k < T.K) {
+          const uint64_t idx = (o0 + o) * T.K + k0 + k;
+          v = BF16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(T.values)[idx]) : T.values[idx];
+        }
+        tile[o][k] = v;
+      }
+    }
+    __syncthreads();
+    const int q = lane & 3;
+    const int kr = wave * 16 + (lane >> 2);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = tile[q * 16 + i][kr];
+    // absmax = fold(0, max(acc, |v|)) over the block (src/quantize.rs:103)
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1, 4));
+    m = fmaxf(m, __shfl_xor(m, 2, 4));
+    // the codes as quantize_full_kernel: classify v * rcp(absmax), divide
+    // exactly near a threshold or for an absmax outside the normal range
+    bool exact = !(m >= 1.1754943508222875e-38f && m <= 8.507059173023462e+37f);
+    const float r = __builtin_amdgcn_rcpf(m);
+    uint32_t c[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c[i] = code_fast(v[i], r, tab, exact);
+    if (exact) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) c[i] = code_exact(v[i], m, tab);
+    }
+    uint32_t w0 = 0, w1 = 0;  // byte j: codes of columns 2 j (low nibble) and 2 j + 1
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      w0 |= c[i] << (4 * i);
+      w1 |= c[8 + i] << (4 * i);
+    }
+    const uint32_t k = k0 + (uint32_t)kr;
+    if (k < T.K) {
+      const uint64_t stripe = 4ull * b + (uint64_t)q;
+      *reinterpret_cast<u32x2*>(T.packed + (stripe * T.K + k) * 8) = u32x2{w0, w1};
+      if (q == 0) T.absmax[(uint64_t)b * T.K + k] = m;
+    }
+  }
+}
+
 // The scale of scales of tensor blockIdx.x: the max of its block scales
 // (src/quantize.rs:285-290), one workgroup per tensor.  The values are >= 0
 // and never NaN, so the order of the max does not matter.
@@ -637,18 +745,21 @@ size_t quantize_linears_scratch_bytes(const uint64_t* d_in, const uint64_t* d_ou
   return total;
 }
 
-hipError_t launch_quantize_linears(const float* const* values, const uint64_t* d_in, const uint64_t* d_out,
-                                   uint32_t n, uint8_t* const* packed, uint8_t* const* dq, float* const* sos,
-                                   void* scratch, hipStream_t stream) {
+hipError_t launch_quantize_linears(const void* const* values, int src_kind, const uint64_t* d_in,
+                                   const uint64_t* d_out, uint32_t n, uint8_t* const* packed, uint8_t* const* dq,
+                                   float* const* sos, void* scratch, hipStream_t stream) {
+  const bool transposed = src_kind != kQuantSrcF32;
+  const bool bf16 = src_kind == kQuantSrcBf16T;
   char* tmp = static_cast<char*>(scratch);
   for (uint32_t g0 = 0; g0 < n; g0 += kQGroupMax) {
     QGroupArgs a{};
     a.n = (int)std::min<uint32_t>(kQGroupMax, n - g0);
     uint64_t spans = 0, max_nb = 0;
+    bool vec = true;
     for (int i = 0; i < a.n; ++i) {
       const uint32_t j = g0 + i;
       QGroupTensor& T = a.t[i];
-      T.values = values[j];
+      T.values = static_cast<const float*>(values[j]);
       T.packed = packed[j];
       T.dq = dq[j];
       T.absmax = reinterpret_cast<float*>(tmp);
@@ -658,12 +769,24 @@ hipError_t launch_quantize_linears(const float* const* values, const uint64_t* d
       T.span_begin = (uint32_t)spans;
       const uint64_t nb = d_in[j] * (d_out[j] / kBlock);
       tmp += ((size_t)nb * 4 + 255) & ~size_t{255};
-      spans += (d_in[j] + 15) / 16 * (d_out[j] / kBlock);  // 16-row groups x block columns
+      // 16-row groups (64-row source tiles when transposed) x block columns
+      spans += (d_in[j] + (transposed ? 63 : 15)) / (transposed ? 64 : 16) * (d_out[j] / kBlock);
       max_nb = std::max(max_nb, nb);
+      vec = vec && (reinterpret_cast<uintptr_t>(values[j]) & 15u) == 0 && d_in[j] % (bf16 ? 8 : 4) == 0;
     }
     if (spans > 0xffffffffull) return hipErrorInvalidValue;
     a.spans = (uint32_t)spans;
-    if (spans) qgroup_quantize_kernel<<<grid_for(spans, kQuantWaves, 8192), kQuantThreads, 0, stream>>>(a);
+    if (spans && !transposed) {
+      qgroup_quantize_kernel<<<grid_for(spans, kQuantWaves, 8192), kQuantThreads, 0, stream>>>(a);
+    } else if (spans) {
+      const int grid = (int)std::min<uint64_t>(spans, 8192);
+      if (bf16)
+        vec ? qgroup_quantize_t_kernel<true, true><<<grid, 256, 0, stream>>>(a)
+            : qgroup_quantize_t_kernel<true, false><<<grid, 256, 0, stream>>>(a);
+      else
+        vec ? qgroup_quantize_t_kernel<false, true><<<grid, 256, 0, stream>>>(a)
+            : qgroup_quantize_t_kernel<false, false><<<grid, 256, 0, stream>>>(a);
+    }
     qgroup_max_kernel<<<(unsigned)a.n, 1024, 0, stream>>>(a);
     if (max_nb) {
       const unsigned gx = (unsigned)std::min<uint64_t>((max_nb + 255) / 256, 256);

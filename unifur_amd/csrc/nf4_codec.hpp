@@ -35,8 +35,14 @@ hipError_t launch_pack_codes(const uint8_t* codes, size_t len, uint8_t* packed, 
 // three launches per group of up to 48 tensors; scratch holds the f32 block
 // scales (quantize_linears_scratch_bytes).
 size_t quantize_linears_scratch_bytes(const uint64_t* d_in, const uint64_t* d_out, uint32_t n);
-hipError_t launch_quantize_linears(const float* const* values, const uint64_t* d_in, const uint64_t* d_out,
-                                   uint32_t n, uint8_t* const* packed, uint8_t* const* dq, float* const* sos,
-                                   void* scratch, hipStream_t stream);
+// src_kind: kQuantSrcF32 -- values[i] f32 [d_in][d_out] (16-byte
+// aligned); kQuantSrcF32T / kQuantSrcBf16T -- the PyTorch-order
+// [d_out][d_in] tensor (f32, or bf16 decoded exactly), transposed on the fly,
+// 4- or 2-byte aligned.  The outputs are the same for a tensor and its
+// transposed copy.
+enum { kQuantSrcF32 = 0, kQuantSrcF32T = 1, kQuantSrcBf16T = 2 };
+hipError_t launch_quantize_linears(const void* const* values, int src_kind, const uint64_t* d_in,
+                                   const uint64_t* d_out, uint32_t n, uint8_t* const* packed, uint8_t* const* dq,
+                                   float* const* sos, void* scratch, hipStream_t stream);
 
 }  // namespace unifur

@@ -53,7 +53,46 @@ hipError_t launch_transpose(const void* src, void* dst, uint64_t rows, uint64_t 
   return hipGetLastError();
 }
 
+// dst[c][r] = decode(src[r][c]) into f32: the checkpoint's [out, in]
+// weight (f32, or bf16 widened exactly) to the [in, out] f32 values that
+// quantize takes.
+template <bool BF16>
+__global__ __launch_bounds__(256) void transpose_decode_kernel(const void* __restrict__ src, float* __restrict__ dst,
+                                                               uint64_t rows, uint64_t cols) {
+  __shared__ float tile[kTile][kTile + 1];
+  const int tid = threadIdx.x;
+  const uint64_t r0 = (uint64_t)blockIdx.y * kTile, c0 = (uint64_t)blockIdx.x * kTile;
+  const int lc = tid & 63, lr = tid >> 6;
+#pragma unroll
+  for (int i = 0; i < kTile / 4; ++i) {
+    const int r = lr + 4 * i;
+    if (r0 + r < rows && c0 + lc < cols) {
+      const uint64_t idx = (r0 + r) * cols + c0 + lc;
+      tile[r][lc] = BF16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(src)[idx]) : static_cast<const float*>(src)[idx];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kTile / 4; ++i) {
+    const int c = lr + 4 * i;
+    if (c0 + c < cols && r0 + lc < rows) dst[(c0 + c) * rows + r0 + lc] = tile[lc][c];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_transpose_decode(const void* src, bool bf16, uint64_t rows, uint64_t cols, float* dst,
+                                   hipStream_t stream) {
+  if (rows == 0 || cols == 0) return hipSuccess;
+  const uint64_t gx = (cols + kTile - 1) / kTile, gy = (rows + kTile - 1) / kTile;
+  if (gx > 0x7fffffffu || gy > 65535u) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)gx, (unsigned)gy);
+  if (bf16)
+    transpose_decode_kernel<true><<<grid, 256, 0, stream>>>(src, dst, rows, cols);
+  else
+    transpose_decode_kernel<false><<<grid, 256, 0, stream>>>(src, dst, rows, cols);
+  return hipGetLastError();
+}
 
 hipError_t launch_stripe_codes(const uint8_t* src, uint8_t* dst, uint64_t d_in, uint64_t d_out, bool to_striped,
                                hipStream_t stream) {

@@ -470,6 +470,10 @@ class Nf4Linear:
         return self._backward(dy, None, None, True, dx_dtype, workspace)[0]
 
 
+# weights per launch sequence of the library's grouped quantize pass
+_QGROUP = 48
+
+
 def quantize_linears(weights) -> list:
     """Nf4Linear.from_values on every (values, d_input, d_output) of
     ``weights`` -- the quantize pass of QwenTrunk::to_nf4
@@ -478,28 +482,40 @@ def quantize_linears(weights) -> list:
     d_output % 64 == 0; the layers come back striped and double quantized,
     their buffers slices of one allocation each for codes, scales and scales
     of scales."""
+    return _quantize_grouped(weights, checkpoint=False)
+
+
+def quantize_checkpoint_linears(tensors) -> list:
+    """The same pass from checkpoint linears as they lie: each tensor is the
+    PyTorch-order [out, in] weight (f32 or bf16, on the device), as
+    qwen_linear (src/qwennet.rs:1687-1726) receives it, transposed to
+    [in, out] on the fly (transpose2d, src/qwennet.rs:1375-1390) inside the
+    grouped quantize kernel; out % 64 == 0.  Byte for byte what
+    quantize_linears gives for the transposed f32 copies."""
+    ws = []
+    for t in tensors:
+        if t.dim() != 2:
+            raise ValueError(f"tensor of shape {tuple(t.shape)} is not rank-2")
+        ws.append((t, int(t.shape[1]), int(t.shape[0])))
+    return _quantize_grouped(ws, checkpoint=True)
+
+
+def _quantize_grouped(weights, checkpoint: bool) -> list:
     n = len(weights)
     if n == 0:
         return []
-    vals, dims, v_ptrs = [], [], []
-    for (v, di, do) in weights:
-        di, do = int(di), int(do)
-        if not v.is_cuda:
-            raise ValueError("values must be a CUDA (HIP) device tensor")
-        if v.dtype != torch.float32 or v.numel() != di * do:
-            raise ValueError(f"values must be float32 with {di} x {do} elements")
-        if do % 64 != 0:
-            raise ValueError("quantize_linears needs d_output % 64 == 0")
-        if not v.is_contiguous() or v.data_ptr() % 16 != 0:
-            v = v.contiguous().clone()
-        vals.append(v)
-        dims.append((di, do))
-        v_ptrs.append(v.data_ptr())
-    dev = vals[0].device
+    dims = [(int(di), int(do)) for (_, di, do) in weights]
+    for (di, do) in dims:
+        if di <= 0 or do % 64 != 0 or do <= 0:
+            raise ValueError("quantize_linears needs d_input > 0 and d_output a positive multiple of 64")
+    dev = weights[0][0].device
     # back to back: code sizes are multiples of 32 bytes (d_output % 64 == 0),
     # so every slice stays 8-byte aligned; u8 scales need no alignment.  The
-    # slices' addresses are computed before the launch and their views made
-    # after it (the host work then overlaps the kernels).
+    # buffers are allocated from the shapes alone, then the values are checked
+    # and launched a group at a time (the library's grouped pass takes 48
+    # weights per launch sequence), so that the first kernels start while the
+    # later groups are still being checked; the views are made after the last
+    # launch (that host work overlaps the kernels).
     c_sizes = [di * do // 2 for (di, do) in dims]
     s_sizes = [di * do // 64 for (di, do) in dims]
     codes = torch.empty(sum(c_sizes), dtype=torch.uint8, device=dev)
@@ -508,14 +524,51 @@ def quantize_linears(weights) -> list:
     c_off = list(itertools.accumulate(c_sizes, initial=0))
     s_off = list(itertools.accumulate(s_sizes, initial=0))
     cb, db, sb = codes.data_ptr(), dq.data_ptr(), sos.data_ptr()
-    P = ctypes.c_void_p * n
-    U = ctypes.c_uint64 * n
-    L.check(L.lib().unifur_nf4_quantize_linears(
-        P(*v_ptrs), U(*[di for (di, _) in dims]), U(*[do for (_, do) in dims]), n,
-        P(*[cb + o for o in c_off[:n]]), P(*[db + o for o in s_off[:n]]), P(*[sb + 4 * i for i in range(n)]),
-        None, 0, _stream()))
-    return [Nf4Linear._from_striped(codes[c_off[i]:c_off[i + 1]], dq[s_off[i]:s_off[i + 1]], sos[i:i + 1], di, do)
-            for i, (di, do) in enumerate(dims)]
+    keep = []  # contiguous copies made here stay alive until their launch is queued
+    stream = _stream()
+    lib = L.lib()
+    src_dtype = None
+    for g0 in range(0, n, _QGROUP):
+        idx = range(g0, min(n, g0 + _QGROUP))
+        v_ptrs = []
+        for i in idx:
+            v = weights[i][0]
+            di, do = dims[i]
+            if not v.is_cuda:
+                raise ValueError("values must be a CUDA (HIP) device tensor")
+            if checkpoint:
+                if v.dtype not in (torch.float32, torch.bfloat16) or tuple(v.shape) != (do, di):
+                    raise ValueError(f"checkpoint linears must be f32 or bf16 [{do}, {di}]")
+                if src_dtype is None:
+                    src_dtype = v.dtype
+                elif v.dtype != src_dtype:
+                    raise ValueError("checkpoint linears of one call share a dtype")
+                if not v.is_contiguous():
+                    v = v.contiguous()
+                    keep.append(v)
+            else:
+                if v.dtype != torch.float32 or v.numel() != di * do:
+                    raise ValueError(f"values must be float32 with {di} x {do} elements")
+                if not v.is_contiguous() or v.data_ptr() % 16 != 0:
+                    v = v.contiguous().clone()
+                    keep.append(v)
+            v_ptrs.append(v.data_ptr())
+        m = len(v_ptrs)
+        P = ctypes.c_void_p * m
+        U = ctypes.c_uint64 * m
+        tail = (U(*[dims[i][0] for i in idx]), U(*[dims[i][1] for i in idx]), m,
+                P(*[cb + c_off[i] for i in idx]), P(*[db + s_off[i] for i in idx]), P(*[sb + 4 * i for i in idx]),
+                None, 0, stream)
+        if checkpoint:
+            L.check(lib.unifur_nf4_quantize_checkpoint_linears(P(*v_ptrs), _dtype_code(src_dtype), *tail))
+        else:
+            L.check(lib.unifur_nf4_quantize_linears(P(*v_ptrs), *tail))
+    # the views in three C++ calls (one per buffer) rather than a Python
+    # slice per weight and buffer
+    cv = codes.split(c_sizes)
+    dv = dq.split(s_sizes)
+    sv = sos.split(1)
+    return [Nf4Linear._from_striped(cv[i], dv[i], sv[i], di, do) for i, (di, do) in enumerate(dims)]
 
 
 def forward_shared_input(x: torch.Tensor, layers, out_dtype: Optional[torch.dtype] = None) -> list:

@@ -210,26 +210,32 @@ def qwen_linear(tensor: torch.Tensor, store: WeightStore) -> tuple:
     """src/qwennet.rs:1687-1726: one decoded checkpoint linear [out, in]
     (f32 or bf16, on the device) into a QwenLinear in the requested storage,
     with the resident bytes of the chosen form.  Nf4: transposed to
-    [in, out] and quantized in one kernel, then double-quantized."""
+    [in, out], quantized and double-quantized -- for out % 64 == 0 in one
+    grouped pass straight into the striped resident form
+    (quantize_checkpoint_linears: transpose, quantize and the scales' max in
+    the kernels, three launches); otherwise the blocks straddle rows of the
+    transposed buffer, which the library transposes first
+    (unifur_nf4_transpose_checkpoint) and quantizes flat."""
     if tensor.dim() != 2:
         raise ValueError(f"tensor of shape {tuple(tensor.shape)} is not rank-2")
     Q._require_cuda(tensor, "tensor")
     rows, cols = tensor.shape  # [out, in]
-    if store == WeightStore.F32:
-        w = tensor.float().t().contiguous()
+    if tensor.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("checkpoint linears are f32 or bf16")
+    src = tensor.contiguous()
+    if store == WeightStore.F32:  # linear_param (src/qwennet.rs:1396-1420): the transposed f32 weight
+        w = torch.empty(cols, rows, dtype=torch.float32, device=src.device)
+        L.check(L.lib().unifur_nf4_transpose_checkpoint(src.data_ptr(), Q._dtype_code(src.dtype), rows, cols,
+                                                        w.data_ptr(), Q._stream()))
         return QwenLinear(QwenLinear.F32, Q.DenseLinear(w)), 4 * tensor.numel()
-    n = rows * cols
     if rows % 64 == 0:
-        codes = torch.empty((n + 1) // 2, dtype=torch.uint8, device=tensor.device)
-        absmax = torch.empty((n + 63) // 64, dtype=torch.float32, device=tensor.device)
-        L.check(L.lib().unifur_nf4_quantize_transposed(tensor.data_ptr(), Q._dtype_code(tensor.dtype), rows, cols,
-                                                       codes.data_ptr(), absmax.data_ptr(), Q._stream()))
-        packed = Q.PackedNf4Tensor(codes, n, absmax=absmax)
-    else:  # blocks straddle rows of the transposed buffer: transpose, then quantize
-        packed = Q.PackedNf4Tensor.quantize(tensor.float().t().contiguous().view(-1))
-    packed = packed.with_double_quantization()
-    nbytes = packed.resident_bytes()
-    return QwenLinear(QwenLinear.NF4, Q.Nf4Linear.from_packed(packed, cols, rows)), nbytes
+        lin = Q.quantize_checkpoint_linears([src])[0]
+    else:
+        flat = torch.empty(rows * cols, dtype=torch.float32, device=src.device)
+        L.check(L.lib().unifur_nf4_transpose_checkpoint(src.data_ptr(), Q._dtype_code(src.dtype), rows, cols,
+                                                        flat.data_ptr(), Q._stream()))
+        lin = Q.Nf4Linear.from_packed(Q.PackedNf4Tensor.quantize(flat).with_double_quantization(), cols, rows)
+    return QwenLinear(QwenLinear.NF4, lin), lin.resident_bytes()
 
 
 def projections_to_nf4(projections: dict, report: Optional[Nf4ResidencyReport] = None) -> dict:
