@@ -99,8 +99,12 @@ def test_backward_and_prefill_workspace_sizes(lib):
         if rows:  # bf16 dy: the expanded bf16 weight is part of it
             assert bw >= 4096 * 4096 * 2
         assert lib.unifur_nf4_linear_backward_workspace_size(rows, 100, 70, 0, 3) >= 65536
-    # f32 dy: the f32 dequantized weight
-    assert lib.unifur_nf4_linear_backward_workspace_size(8, 256, 128, 0, 0) >= 256 * 128 * 4
+    # f32 dy over whole 64-column blocks: the f32 MFMA kernel, no weight copy
+    assert 65536 <= lib.unifur_nf4_linear_backward_workspace_size(8, 256, 128, 0, 0) < 256 * 128 * 4
+    # ... with d_out off the blocks: the generic path's f32 dequantized weight
+    assert lib.unifur_nf4_linear_backward_workspace_size(8, 256, 100, 0, 0) >= 256 * 100 * 4
+    # f32 activations past 64 rows: no weight copy either
+    assert lib.unifur_nf4_linear_workspace_size(2048, 4096, 4096, 0, 16) < 4096 * 4096 * 4
     # prefill: the default holds the bf16 expansion, the minimum does not
     full = lib.unifur_nf4_linear_workspace_size(2048, 4096, 4096, 1, 16)
     lean = lib.unifur_nf4_linear_min_workspace_size(2048, 4096, 4096, 1, 16)

@@ -118,17 +118,27 @@ def test_noalloc_split_k_without_adapter(device, oracle, rows):
 
 
 def test_noalloc_refuses_what_does_not_fit(device, oracle):
-    # f32 activations over 64 rows take the generic path: the whole weight
-    # dequantized to f32 (4096 * 11008 * 4 bytes) does not fit the scratch
+    # f32 activations over 64 rows off the 16-byte alignment take the generic
+    # path: the whole weight dequantized to f32 (4096 * 11008 * 4 bytes) does
+    # not fit the scratch
     lin, _ = make_linear(oracle, 4096, 11008, 5100, device)
-    _, x = acts(oracle, 100, 4096, 5101, torch.float32, device)
+    _, x = acts(oracle, 101, 4096, 5101, torch.float32, device)
+    xm = x.view(-1)[1:1 + 100 * 4096]  # 4 bytes past the allocation's alignment
     w = lin.weight_struct()
     y = torch.empty(100, 11008, device=device)
     lib = L.lib()
     stream = torch.cuda.current_stream().cuda_stream
-    st = lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), L.F32, 100, ctypes.byref(w), None, None, y.data_ptr(),
+    st = lib.unifur_nf4_linear_forward_noalloc(xm.data_ptr(), L.F32, 100, ctypes.byref(w), None, None, y.data_ptr(),
                                                L.F32, stream)
     assert st == L.ERR_WORKSPACE and b"16777216" in lib.unifur_nf4_last_error()
+    # aligned, the same call runs on the f32 MFMA kernel without weight-sized
+    # scratch, as the entry point with a workspace does
+    L.check(lib.unifur_nf4_linear_forward_noalloc(x.data_ptr(), L.F32, 100, ctypes.byref(w), None, None,
+                                                  y.data_ptr(), L.F32, stream))
+    y2 = torch.empty_like(y)
+    L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), L.F32, 100, ctypes.byref(w), None, None, y2.data_ptr(),
+                                          L.F32, None, 0, stream))
+    assert torch.equal(y, y2)
     # 5..64 f32 rows run on MFMA over the striped weight and fit: the same
     # result as the entry point with a workspace
     y8 = torch.empty(8, 11008, device=device)

@@ -18,6 +18,7 @@
 #include "nf4_embedding.hpp"
 #include "nf4_expand.hpp"
 #include "nf4_gemm.hpp"
+#include "nf4_gemm_f32.hpp"
 #include "nf4_generic.hpp"
 #include "nf4_gemv.hpp"
 #include "nf4_layout.hpp"
@@ -183,7 +184,7 @@ struct Carver {
 
 // ------------------------------------------------------------- linear plans --
 
-enum class LinearPath { kGemvStriped, kGemv, kSkinny, kMfma, kGeneric };
+enum class LinearPath { kGemvStriped, kGemv, kSkinny, kMfma, kMfmaF32, kGeneric };
 
 // The row-major GEMV needs whole 64-blocks per weight row (d_out % 64 == 0),
 // 16-byte aligned code rows and a weight that 32-bit buffer offsets reach
@@ -257,6 +258,11 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
       const int slabs = std::max(L.splits, L.tail);
       if (slabs > 1) L.gemm_partials = c.take((size_t)slabs * rows * d_out * sizeof(float));
     }
+  } else if (xf32 && rows <= 0x7fffffffu && d_in <= 0x7fffffffu && d_out <= 0x7fffffffu && aligned_to(packed, 8) &&
+             gemm_f32_mfma_supported((int)rows, (int)d_in, (int)d_out, (int)d_out, x)) {
+    // f32 activations past the skinny kernel: the f32 MFMA kernel over W
+    // tiles dequantized in LDS (no weight-sized scratch)
+    L.path = LinearPath::kMfmaF32;
   } else {
     L.path = LinearPath::kGeneric;
     L.wf32 = c.take((size_t)d_in * d_out * sizeof(float));
@@ -413,6 +419,27 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     }
     return UNIFUR_NF4_OK;
   }
+  // f32 activations on MFMA: W tiles dequantized exactly in LDS
+  if (L.path == LinearPath::kMfmaF32) {
+    F32GemmArgs a{};
+    a.x = static_cast<const float*>(x);
+    a.packed = w->packed;
+    a.scales = to_scales(w->scales);
+    a.M = (int)rows;
+    a.K = (int)w->d_in;
+    a.N = (int)w->d_out;
+    a.bias = bias;
+    a.lora_xa = xa;
+    a.lora_b = lora ? lora->b : nullptr;
+    a.lora_sbj = w->d_out;
+    a.lora_sbn = 1;
+    a.lora_rank = (int)rank;
+    a.lora_scaling = lora ? lora->scaling : 0.0f;
+    a.y = y;
+    UNIFUR_HIP(launch_gemm_f32_mfma(a, w->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED, is_striped(w), false, ybf,
+                                    stream));
+    return UNIFUR_NF4_OK;
+  }
   // Generic: the reference's own sequence -- dequantize the whole weight to
   // f32 (bit-exact), then an f32 matmul.
   const uint8_t* packed = nullptr;
@@ -436,6 +463,7 @@ struct MlpLayout {
   StripedPlan s_up, s_down;
   int split_up = 1, split_down = 1;  // kMfma without expand: d_in slabs of the fused kernel
   int tail_up = 1, tail_down = 1;    // ... or of only its last, partly filled round of tiles
+  bool f32_mfma = false;             // kGeneric with f32 activations: the f32 MFMA kernel per linear
   size_t partials0, partials1, h, u, hb, wt, blas, wf32, rm_codes, rm_scales, gemm_partials, total;
 };
 
@@ -531,9 +559,18 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
     }
   } else {
     L.path = MlpPath::kGeneric;
-    L.wf32 = c.take((size_t)hidden * inter * sizeof(float));
+    // f32 activations: the three linears on the f32 MFMA kernel (no f32 weight copy)
+    L.f32_mfma = x_dtype == UNIFUR_NF4_F32 && rows <= 0x7fffffffu && hidden <= 0x7fffffffu && inter <= 0x7fffffffu &&
+                 hidden % 64 == 0 && aligned_to(g->packed, 8) && aligned_to(u->packed, 8) && aligned_to(d->packed, 8) && gemm_f32_mfma_supported((int)rows, (int)hidden, (int)inter, (int)inter, x) &&
+                 gemm_f32_mfma_supported((int)rows, (int)inter, (int)hidden, (int)hidden,
+                                         reinterpret_cast<const void*>(uintptr_t{256}));
     L.h = c.take((size_t)rows * inter * sizeof(float));
     L.u = c.take((size_t)rows * inter * sizeof(float));
+    if (L.f32_mfma) {
+      L.total = c.off;
+      return L;
+    }
+    L.wf32 = c.take((size_t)hidden * inter * sizeof(float));
     if (is_striped(g) || is_striped(u) || is_striped(d)) {
       L.rm_codes = c.take(ceil_div_u64(hidden * inter, 2));
       L.rm_scales = c.take(4 * ceil_div_u64(hidden * inter, 64));
@@ -688,6 +725,26 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     case MlpPath::kGeneric:
       break;
   }
+  if (L.f32_mfma) {  // f32 activations: three f32 MFMA launches and the elementwise middle
+    float* u = at<float>(ws, L.u);
+    const unifur_nf4_weight* ws3[3] = {gate, up, down};
+    void* outs[3] = {h, u, y};
+    for (int i = 0; i < 3; ++i) {
+      const unifur_nf4_weight* w = ws3[i];
+      F32GemmArgs a{};
+      a.x = i < 2 ? static_cast<const float*>(x) : h;
+      a.packed = w->packed;
+      a.scales = to_scales(w->scales);
+      a.M = (int)rows;
+      a.K = (int)w->d_in;
+      a.N = (int)w->d_out;
+      a.y = outs[i];
+      UNIFUR_HIP(launch_gemm_f32_mfma(a, w->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED, is_striped(w), false,
+                                      i == 2 && ybf, stream));
+      if (i == 1) UNIFUR_HIP(launch_silu_mul(h, u, (size_t)rows * inter, h, stream));
+    }
+    return UNIFUR_NF4_OK;
+  }
   // Generic: three dequantize + f32 matmul linears and the elementwise middle.
   float* wf = at<float>(ws, L.wf32);
   float* u = at<float>(ws, L.u);
@@ -790,6 +847,8 @@ Branch branch_for(hipStream_t stream) {
 struct BackwardLayout {
   bool blas, fused;
   int splits;  // fused dX: d_out slabs (1: none)
+  bool mfma_f32;  // f32 dY: the f32 MFMA kernel over W's rows (dY B^T in dy_bt when there is an adapter)
+  size_t dy_bt;
   size_t wt, blas_ws, wf32, rm_codes, rm_scales, lora_at, lora_bt, lora_xa, dx_partials, grads, xa, u, partials, total;
 };
 
@@ -801,7 +860,7 @@ struct BackwardLayout {
 // false leaves out its split-K partials.
 BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t rank, int dy_dtype, bool want_dx,
                              bool want_grads, bool striped, int scale_kind, bool aligned, bool allow_blas = true,
-                             bool allow_split = true) {
+                             bool allow_split = true, bool codes_aligned = true) {
   BackwardLayout L{};
   L.splits = 1;
   Carver c;
@@ -825,6 +884,12 @@ BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint3
         L.splits = gemm_k_splits((int)rows, (int)d_out, (int)d_in);
         if (L.splits > 1) L.dx_partials = c.take((size_t)L.splits * rows * d_in * sizeof(float));
       }
+    } else if (dy_dtype == UNIFUR_NF4_F32 && aligned && codes_aligned && sizes && d_out % 64 == 0 &&
+               gemm_f32_mfma_supported((int)rows, (int)d_out, (int)d_in, (int)d_out,
+                                       reinterpret_cast<const void*>(uintptr_t{256}))) {
+      // f32 dY: dX on the f32 MFMA kernel with W's rows as its outputs
+      L.mfma_f32 = true;
+      if (rank) L.dy_bt = c.take((size_t)rows * rank * sizeof(float));
     } else {
       L.wf32 = c.take(d_in * d_out * sizeof(float));
       if (striped) {
@@ -875,7 +940,7 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
   UNIFUR_ARG(K <= 0x7fffffffu && N <= 0x7fffffffu, "weight too large");
   const bool aligned = aligned_to(dy, 16) && aligned_to(dx, 16);
   BackwardLayout L = plan_backward(rows, K, N, rank, dy_dtype, want_dx && rows > 0, want_grads, is_striped(w),
-                                   w->scales.kind, aligned);
+                                   w->scales.kind, aligned, true, true, aligned_to(w->packed, 8));
   if (L.blas && workspace && workspace_bytes < L.total) {
     // a workspace too small for the expanded weight: the fused dX kernel,
     // with its split-K partials if they fit
@@ -942,6 +1007,30 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       UNIFUR_HIP(launch_gemm_dx(dyb, w->packed, to_scales(w->scales), m, k, n, xa16, bt16, (int)rank, dx,
                                 dx_dtype == UNIFUR_NF4_BF16, stream, L.splits,
                                 L.splits > 1 ? at<float>(ws, L.dx_partials) : nullptr));
+    } else if (L.mfma_f32) {
+      // dX = dY W^T + scaling (dY B^T) A^T: u = dY B^T (f32, [rows][rank]),
+      // then the adapter term (A^T read through strides) on the kernel's MFMAs
+      float* u = nullptr;
+      if (lora) {
+        u = at<float>(ws, L.dy_bt);
+        UNIFUR_HIP(launch_lora_xa_strided(dy, false, lora->b, 1, N, m, n, (int)rank, u, stream));
+      }
+      F32GemmArgs a{};
+      a.x = static_cast<const float*>(dy);
+      a.packed = w->packed;
+      a.scales = to_scales(w->scales);
+      a.M = m;
+      a.K = n;  // the reduction: d_out
+      a.N = k;  // the outputs: d_in
+      a.lora_xa = u;
+      a.lora_b = lora ? lora->a : nullptr;  // A^T: element (j, i) = A[i][j]
+      a.lora_sbj = 1;
+      a.lora_sbn = rank;
+      a.lora_rank = (int)rank;
+      a.lora_scaling = lora ? lora->scaling : 0.0f;
+      a.y = dx;
+      UNIFUR_HIP(launch_gemm_f32_mfma(a, w->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED, is_striped(w), true,
+                                      dx_dtype == UNIFUR_NF4_BF16, stream));
     } else {
       const uint8_t* packed = nullptr;
       ScalesArg scales{};
