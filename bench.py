@@ -36,6 +36,7 @@ if ROOT not in sys.path:
 METRIC = "NF4 dequant/GEMV GB/s and prefill GEMM TFLOP/s, % of MI355X roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+F32_MFMA_PEAK_TFLOPS = 157.3
 MALL_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gemv_config2.txt")
 
@@ -319,7 +320,8 @@ def bench_ceiling(torch, L, nbytes: int, write_ratio: int = 0) -> dict:
     out = {"bytes": nbytes, "copies": copies, "kernel": "bench_probe/stream_probe.hip"}
     kinds = [("read", nbytes), ("copy", nbytes)]
     if write_ratio:
-        w_bytes = nbytes * write_ratio // (write_ratio + 1) // 16 * 16
+        unit = 16 * write_ratio * 256  # the probe writes whole 256-unit blocks
+        w_bytes = nbytes * write_ratio // (write_ratio + 1) // unit * unit
         kinds.append(("write_dominated", w_bytes + w_bytes // write_ratio))
     for name, moved in kinds:
         best = None
@@ -447,9 +449,45 @@ def bench_gemm(torch, Q, L) -> dict:
         f_flops = flops if name == "qlora" else base_flops
         fused[name] = {"ms": round(f_ms, 5), "tflops": round(f_flops / f_ms / 1e9, 1),
                        "frac": round(f_flops / f_ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+    # f32 activations at the same shapes (the reference's precision): the f32
+    # MFMA kernel over NF4 tiles dequantized exactly in LDS, with the adapter,
+    # and the backward's dX for f32 dY through its transposed form
+    x32 = x.float()
+    y32 = torch.empty(M, N, device=dev)
+    ws32 = lib.unifur_nf4_linear_workspace_size(M, K, N, L.F32, r)
+    w32 = torch.zeros(max(ws32, 1), dtype=torch.uint8, device=dev)
+
+    def f32_launch(i: int) -> None:
+        L.check(lib.unifur_nf4_qlora_forward(x32.data_ptr(), L.F32, M, ctypes.byref(w), ctypes.byref(lo),
+                                             y32.data_ptr(), L.F32, w32.data_ptr(), ws32,
+                                             torch.cuda.current_stream().cuda_stream))
+    f32_launch(0)
+    torch.cuda.synchronize()
+    e32 = float((y32 - ref).abs().max() / ref.abs().max())
+    if not e32 < 1e-3:
+        raise RuntimeError(f"f32 GEMM sanity check failed: {e32:.3e}")
+    g32 = capture(torch, f32_launch, 4)
+    ms32 = graph_ms(torch, g32, 5) / 4 if g32 is not None else event_ms(torch, f32_launch, 8)
+    dy32 = g.normal(M, N)
+    dx32 = torch.empty(M, K, device=dev)
+    wsb = lib.unifur_nf4_linear_backward_workspace_size(M, K, N, L.F32, 0)
+    wb = torch.zeros(max(wsb, 1), dtype=torch.uint8, device=dev)
+
+    def dx_launch(i: int) -> None:
+        L.check(lib.unifur_nf4_linear_backward(dy32.data_ptr(), L.F32, M, ctypes.byref(w), None, None, L.F32,
+                                               dx32.data_ptr(), L.F32, None, None, wb.data_ptr(), wsb,
+                                               torch.cuda.current_stream().cuda_stream))
+    dx_launch(0)
+    gdx = capture(torch, dx_launch, 4)
+    msdx = graph_ms(torch, gdx, 5) / 4 if gdx is not None else event_ms(torch, dx_launch, 8)
+    f32 = {"path": "f32 MFMA (v_mfma_f32_32x32x2f32) over NF4 tiles dequantized exactly in LDS",
+           "qlora_ms": round(ms32, 5), "qlora_tflops": round(flops / ms32 / 1e9, 1),
+           "frac_of_f32_mfma_peak": round(flops / ms32 / 1e9 / F32_MFMA_PEAK_TFLOPS, 4),
+           "backward_dx_ms": round(msdx, 5), "backward_dx_tflops": round(base_flops / msdx / 1e9, 1),
+           "max_rel_err": e32}
     return {"ms": ms, "tflops": flops / ms / 1e9, "frac": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
             "base_kernel_ms": base_ms, "base_tflops": base_flops / base_ms / 1e9, "max_rel_err": err,
-            "fused": fused}
+            "fused": fused, "f32": f32}
 
 
 # --------------------------------------------------------------- config 4 --
@@ -912,6 +950,7 @@ def main() -> int:
         secondary["prefill_fused_gemm_config3"] = dict(
             path="least workspace: the fused MFMA kernel (NF4 tiles dequantized in LDS, LoRA in the epilogue)",
             **gemm["fused"])
+        secondary["prefill_f32_activations_config3_shapes"] = gemm["f32"]
         secondary["swiglu_config4"] = bench_swiglu(torch, Q, L, (1, 16, 512))
         secondary["qwen05b_config5"] = bench_qwen(torch, Q, L)
         secondary["embedding_qwen05b"] = bench_embedding(torch, Q, L)

@@ -53,18 +53,21 @@ __global__ __launch_bounds__(kProbeThreads) void stream_copy_kernel(const u32x4*
   for (; i < n16; i += stride) dst[i] = src[i];
 }
 
-__global__ __launch_bounds__(kProbeThreads) void stream_mixed_kernel(const u32x4* __restrict__ src, size_t n_write16,
+__global__ __launch_bounds__(kProbeThreads) void stream_mixed_kernel(const u32x4* __restrict__ src, size_t n_read16,
                                                                      uint32_t ratio, u32x4* __restrict__ dst) {
+  // a block's 256 source units i0 .. i0 + 255 fan out to its own ratio x 256
+  // destination units, written as ratio runs of 4 KiB (each store instruction
+  // a contiguous 1 KiB per wave); loads issued a step ahead
   const size_t stride = (size_t)gridDim.x * kProbeThreads;
   size_t i = (size_t)blockIdx.x * kProbeThreads + threadIdx.x;
-  for (; i + (kProbeUnroll - 1) * stride < n_write16; i += kProbeUnroll * stride) {
-    u32x4 v[kProbeUnroll];
-#pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) v[u] = src[(i + u * stride) / ratio];
-#pragma unroll
-    for (int u = 0; u < kProbeUnroll; ++u) dst[i + u * stride] = v[u] ^ (uint32_t)(i + u * stride);
+  u32x4 v = i < n_read16 ? src[i] : u32x4{0u, 0u, 0u, 0u};
+  for (; i < n_read16; i += stride) {
+    const size_t nx = i + stride;
+    const u32x4 next = nx < n_read16 ? src[nx] : u32x4{0u, 0u, 0u, 0u};
+    u32x4* d = dst + (i - threadIdx.x) * ratio + threadIdx.x;
+    for (uint32_t u = 0; u < ratio; ++u) d[(size_t)u * kProbeThreads] = v ^ u;
+    v = next;
   }
-  for (; i < n_write16; i += stride) dst[i] = src[i / ratio] ^ (uint32_t)i;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -92,16 +95,17 @@ int unifur_bench_stream_probe(const void* src, uint64_t bytes, void* dst, uint32
   return (int)hipGetLastError();
 }
 
-// Writes `write_bytes` to dst while reading write_bytes / ratio from src
-// (src must hold that many bytes, rounded up to 16).
+// Writes `write_bytes` to dst while reading write_bytes / ratio from src;
+// write_bytes a multiple of 16 * ratio * 256 (whole blocks).
 int unifur_bench_stream_mixed(const void* src, void* dst, uint64_t write_bytes, uint32_t ratio, uint32_t workgroups,
                               void* stream) {
   if (write_bytes == 0) return 0;
   if (!src || !dst || write_bytes % 16 || ratio < 1 || !aligned16(src) || !aligned16(dst) || workgroups < 1 ||
       workgroups > 65536)
     return -1;
+  if (write_bytes % (16ull * ratio * kProbeThreads)) return -1;  // whole 256-unit blocks
   stream_mixed_kernel<<<workgroups, kProbeThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const u32x4*>(src), write_bytes / 16, ratio, static_cast<u32x4*>(dst));
+      static_cast<const u32x4*>(src), write_bytes / 16 / ratio, ratio, static_cast<u32x4*>(dst));
   return (int)hipGetLastError();
 }
 

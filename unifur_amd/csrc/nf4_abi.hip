@@ -279,6 +279,11 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
     L.xa = c.take((size_t)rows * pad * 2);
     L.lora_at = c.take(pad * d_in * 2);
     L.lora_bt = c.take((size_t)d_out * pad * 2);
+  } else if (L.path == LinearPath::kMfmaF32 && lora_rank) {
+    // x A by the f32 MFMA row products ([rows][rank bucket] + their slab
+    // partials), or the narrow kernel's [rows][rank]
+    L.xa = c.take(std::max<size_t>((size_t)rows * lora_rank * sizeof(float),
+                                   adapter_row_product_scratch_bytes((int)rows, (int)d_in, (int)lora_rank)));
   } else {
     L.xa = c.take((size_t)rows * lora_rank * sizeof(float));
   }
@@ -387,6 +392,40 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
                            L.splits > 1 || L.tail > 1 ? at<float>(ws, L.gemm_partials) : nullptr, L.tail));
     return UNIFUR_NF4_OK;
   }
+  // f32 activations on MFMA: W tiles dequantized exactly in LDS; x A by the
+  // f32 MFMA row products where they take the operands
+  if (L.path == LinearPath::kMfmaF32) {
+    int ld = (int)rank;
+    if (lora) {
+      xa = at<float>(ws, L.xa);
+      if (adapter_row_product_supported(x, lora->a, (int)rows, (int)w->d_in, (int)rank)) {
+        UNIFUR_HIP(launch_adapter_row_product(0, x, false, lora->a, (int)rows, (int)w->d_in, (int)rank, xa,
+                                              at<unsigned>(ws, 0), kMaxCounters, stream));
+        ld = adapter_row_product_ld((int)rank);
+      } else {
+        UNIFUR_HIP(launch_lora_xa(x, false, lora->a, (int)rows, (int)w->d_in, (int)rank, xa, stream));
+      }
+    }
+    F32GemmArgs a{};
+    a.x = static_cast<const float*>(x);
+    a.packed = w->packed;
+    a.scales = to_scales(w->scales);
+    a.M = (int)rows;
+    a.K = (int)w->d_in;
+    a.N = (int)w->d_out;
+    a.bias = bias;
+    a.lora_xa = xa;
+    a.lora_ld = ld;
+    a.lora_b = lora ? lora->b : nullptr;
+    a.lora_sbj = w->d_out;
+    a.lora_sbn = 1;
+    a.lora_rank = (int)rank;
+    a.lora_scaling = lora ? lora->scaling : 0.0f;
+    a.y = y;
+    UNIFUR_HIP(launch_gemm_f32_mfma(a, w->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED, is_striped(w), false, ybf,
+                                    stream));
+    return UNIFUR_NF4_OK;
+  }
   if (lora) {
     xa = at<float>(ws, L.xa);
     UNIFUR_HIP(launch_lora_xa(x, xbf, lora->a, (int)rows, (int)w->d_in, (int)rank, xa, stream));
@@ -417,27 +456,6 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     } else {
       UNIFUR_HIP(launch_gemv(L.gemv, x, xbf, (int)rows, (int)w->d_in, &gw, 1, stream));
     }
-    return UNIFUR_NF4_OK;
-  }
-  // f32 activations on MFMA: W tiles dequantized exactly in LDS
-  if (L.path == LinearPath::kMfmaF32) {
-    F32GemmArgs a{};
-    a.x = static_cast<const float*>(x);
-    a.packed = w->packed;
-    a.scales = to_scales(w->scales);
-    a.M = (int)rows;
-    a.K = (int)w->d_in;
-    a.N = (int)w->d_out;
-    a.bias = bias;
-    a.lora_xa = xa;
-    a.lora_b = lora ? lora->b : nullptr;
-    a.lora_sbj = w->d_out;
-    a.lora_sbn = 1;
-    a.lora_rank = (int)rank;
-    a.lora_scaling = lora ? lora->scaling : 0.0f;
-    a.y = y;
-    UNIFUR_HIP(launch_gemm_f32_mfma(a, w->scales.kind == UNIFUR_NF4_SCALES_DOUBLE_QUANTIZED, is_striped(w), false, ybf,
-                                    stream));
     return UNIFUR_NF4_OK;
   }
   // Generic: the reference's own sequence -- dequantize the whole weight to
@@ -889,7 +907,9 @@ BackwardLayout plan_backward(uint64_t rows, uint64_t d_in, uint64_t d_out, uint3
                                        reinterpret_cast<const void*>(uintptr_t{256}))) {
       // f32 dY: dX on the f32 MFMA kernel with W's rows as its outputs
       L.mfma_f32 = true;
-      if (rank) L.dy_bt = c.take((size_t)rows * rank * sizeof(float));
+      if (rank)
+        L.dy_bt = c.take(std::max<size_t>((size_t)rows * rank * sizeof(float),
+                                          adapter_row_product_scratch_bytes((int)rows, (int)d_out, (int)rank)));
     } else {
       L.wf32 = c.take(d_in * d_out * sizeof(float));
       if (striped) {
@@ -1011,9 +1031,16 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       // dX = dY W^T + scaling (dY B^T) A^T: u = dY B^T (f32, [rows][rank]),
       // then the adapter term (A^T read through strides) on the kernel's MFMAs
       float* u = nullptr;
+      int ld = (int)rank;
       if (lora) {
         u = at<float>(ws, L.dy_bt);
-        UNIFUR_HIP(launch_lora_xa_strided(dy, false, lora->b, 1, N, m, n, (int)rank, u, stream));
+        if (adapter_row_product_supported(dy, lora->b, m, n, (int)rank)) {
+          UNIFUR_HIP(launch_adapter_row_product(1, dy, false, lora->b, m, n, (int)rank, u, static_cast<unsigned*>(ws),
+                                                kMaxCounters, stream));
+          ld = adapter_row_product_ld((int)rank);
+        } else {
+          UNIFUR_HIP(launch_lora_xa_strided(dy, false, lora->b, 1, N, m, n, (int)rank, u, stream));
+        }
       }
       F32GemmArgs a{};
       a.x = static_cast<const float*>(dy);
@@ -1023,6 +1050,7 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
       a.K = n;  // the reduction: d_out
       a.N = k;  // the outputs: d_in
       a.lora_xa = u;
+      a.lora_ld = ld;
       a.lora_b = lora ? lora->a : nullptr;  // A^T: element (j, i) = A[i][j]
       a.lora_sbj = 1;
       a.lora_sbn = rank;

@@ -521,6 +521,43 @@ bool adapter_grads_supported(const void* x, const void* dy, const float* b, int 
 
 size_t adapter_grads_scratch_bytes(int M, int K, int N, int rank) { return make_plan(M, K, N, rank).total; }
 
+int adapter_row_product_ld(int rank) { return rank_bucket(rank); }
+
+bool adapter_row_product_supported(const void* src, const float* w, int M, int kdim, int rank) {
+  return adapter_grads_supported(src, src, w, M, kdim, kdim, rank);
+}
+
+size_t adapter_row_product_scratch_bytes(int M, int kdim, int rank) {
+  const Plan P = make_plan(M, kdim, kdim, rank);
+  return align256((size_t)M * P.rb * sizeof(float)) + P.row_part[0];
+}
+
+hipError_t launch_adapter_row_product(int p, const void* src, bool src_bf16, const float* w, int M, int kdim,
+                                      int rank, void* scratch, unsigned* counters, int max_counters,
+                                      hipStream_t stream) {
+  if ((p != 0 && p != 1) || !adapter_row_product_supported(src, w, M, kdim, rank)) return hipErrorInvalidValue;
+  if (M == 0) return hipSuccess;
+  const Plan P = make_plan(M, kdim, kdim, rank);  // both products over kdim: the same slabs
+  char* base = static_cast<char*>(scratch);
+  RowArgs ra{};
+  for (int q = 0; q < 2; ++q) {
+    ra.src[q] = src;
+    ra.w[q] = w;
+    ra.kdim[q] = kdim;
+    ra.out[q] = reinterpret_cast<float*>(base);
+    ra.partials[q] = reinterpret_cast<float*>(base + align256((size_t)M * P.rb * sizeof(float)));
+    ra.counters[q] = counters;
+    ra.slabs[q] = P.row_slabs[q];
+    ra.kslab[q] = P.row_kslab[q];
+  }
+  ra.M = M, ra.rank = rank, ra.first = p;
+  if (P.row_slabs[p] > 1 && P.row_tiles > max_counters) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)P.row_tiles, (unsigned)P.row_slabs[p], 1u);
+  return P.rb == 16   ? launch_rows<16>(ra, src_bf16, src_bf16, grid, stream)
+         : P.rb == 32 ? launch_rows<32>(ra, src_bf16, src_bf16, grid, stream)
+                      : launch_rows<64>(ra, src_bf16, src_bf16, grid, stream);
+}
+
 hipError_t launch_adapter_grads(const void* x, bool x_bf16, const void* dy, bool dy_bf16, const float* a,
                                 const float* b, int M, int K, int N, int rank, float scaling, float* grad_a,
                                 float* grad_b, void* scratch, unsigned* counters, int max_counters,

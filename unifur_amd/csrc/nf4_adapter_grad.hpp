@@ -28,4 +28,17 @@ hipError_t launch_adapter_grads(const void* x, bool x_bf16, const void* dy, bool
                                 float* grad_b, void* scratch, unsigned* counters, int max_counters,
                                 hipStream_t stream);
 
+// One row product on its own, out [M][adapter_row_product_ld(rank)] f32 at
+// scratch (zero past the rank; slab partials after it): p = 0: x A with A
+// [kdim][rank] (the forward adapter's first factor); p = 1: dy B^T with B
+// [rank][kdim] (the backward dX adapter term's first factor).  src [M][kdim]
+// f32 or bf16; the same operand conditions as the gradients (kdim % 8 == 0,
+// src and w 16-byte aligned); counters as in launch_adapter_grads.
+bool adapter_row_product_supported(const void* src, const float* w, int M, int kdim, int rank);
+int adapter_row_product_ld(int rank);
+size_t adapter_row_product_scratch_bytes(int M, int kdim, int rank);
+hipError_t launch_adapter_row_product(int p, const void* src, bool src_bf16, const float* w, int M, int kdim,
+                                      int rank, void* scratch, unsigned* counters, int max_counters,
+                                      hipStream_t stream);
+
 }  // namespace unifur

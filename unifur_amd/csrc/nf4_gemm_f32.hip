@@ -178,7 +178,7 @@ __global__ __launch_bounds__(kFThreads) void gemm_f32_mfma_kernel(F32GemmArgs g)
   }
 
   // the adapter: acc += (xa scaling) B over the rank, on the same MFMAs; xa
-  // [M][rank] f32 and B element (j, n) at lora_b[j sbj + n sbn]
+  // [M][lora_ld] f32 and B element (j, n) at lora_b[j sbj + n sbn]
   if (g.lora_xa) {
     for (int j0 = 0; j0 < g.lora_rank; j0 += 2) {
       const int j = j0 + kl;
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kFThreads) void gemm_f32_mfma_kernel(F32GemmArgs g)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int m = m0 + arow + 32 * i;
-        a[i] = (jl && m < g.M) ? g.lora_xa[(size_t)m * g.lora_rank + j] * g.lora_scaling : 0.0f;
+        a[i] = (jl && m < g.M) ? g.lora_xa[(size_t)m * g.lora_ld + j] * g.lora_scaling : 0.0f;
       }
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {

@@ -12,7 +12,8 @@ struct F32GemmArgs {
   ScalesArg scales;
   int M, K, N;  // rows, reduction, outputs: (M, d_in, d_out), or with trans (M, d_out, d_in)
   const float* bias;      // [N] or null
-  const float* lora_xa;   // [M][lora_rank] f32 (x A, or dY B^T with trans), or null
+  const float* lora_xa;   // [M][lora_ld] f32 (x A, or dY B^T with trans; lora_rank columns used), or null
+  int lora_ld;
   const float* lora_b;    // element (j, n) of the second factor at lora_b[j lora_sbj + n lora_sbn]
   size_t lora_sbj, lora_sbn;
   int lora_rank;
