@@ -275,6 +275,55 @@ def bench_gemv(torch, Q, L, args) -> dict:
     return out
 
 
+def bench_gemv_stripes(torch, Q, L) -> dict:
+    """The config-2 GEMV (d_in 4096, DQ, f32 x) at d_out of 544, 688, 768 and
+    1024 stripes of 16 columns (2.125, 2.69, 3 and 4 workgroups per CU of the
+    256; every point past 512 stripes, so all take the 4-wave kernel): the
+    fixed and per-stripe cost of a launch, and whether config 2's 2.69
+    stripes per CU cost like a whole 3, cold weights, per-launch time by HIP
+    events around graph replays."""
+    d_in = 4096
+    dev = torch.device("cuda:0")
+    g = Rng(torch, 0x4E463459)
+    lib = L.lib()
+    out = {}
+    for d_out in (8704, 11008, 12288, 16384):
+        base = rand_weights(torch, Q, d_in, d_out, g)
+        nbytes = gemv_bytes(d_in, d_out, dq=True)
+        copies = max(2, -(-(2 * MALL_BYTES) // nbytes))
+        layers = [base] + [Q.Nf4Linear.from_packed(base.packed(), d_in, d_out) for _ in range(copies - 1)]
+        structs = [lay.weight_struct() for lay in layers]
+        x = g.normal(1, d_in)
+        y = torch.empty(1, d_out, device=dev)
+
+        def launch(i: int, structs=structs, x=x, y=y, copies=copies) -> None:
+            L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), L.F32, 1, ctypes.byref(structs[i % copies]), None,
+                                                  None, y.data_ptr(), L.F32, None, 0,
+                                                  torch.cuda.current_stream().cuda_stream))
+        for i in range(copies):
+            launch(i)
+        graph = capture(torch, launch, copies)
+        ms = replay_event_ms(torch, graph, copies) if graph is not None else event_ms(torch, launch, 4 * copies)
+        stripes = d_out // 16
+        out[f"d_out_{d_out}"] = {"stripes": stripes, "stripes_per_cu": round(stripes / 256, 3),
+                                 "kernel_us": round(ms * 1e3, 3), "gbs": round(nbytes / ms / 1e6, 1),
+                                 "ns_per_stripe": round(ms * 1e6 / stripes, 2)}
+        del layers, structs, graph
+    # the line through the whole-number points (3 and 4 per CU), and what it
+    # predicts below them: a launch paced by its fullest CU would cost the
+    # same at 544 and 688 stripes as at 768
+    a, b = out["d_out_12288"], out["d_out_16384"]
+    slope = (b["kernel_us"] - a["kernel_us"]) / (b["stripes"] - a["stripes"])
+    icpt = a["kernel_us"] - slope * a["stripes"]
+    out["fit_3_and_4_per_cu"] = {"fixed_us": round(icpt, 3), "ns_per_stripe": round(slope * 1e3, 3),
+                                 "marginal_gbs": round(gemv_bytes(d_in, 16 * 1024, dq=True) / 1024 / slope / 1e3, 1),
+                                 "predicted_544_us": round(icpt + slope * 544, 3),
+                                 "measured_544_us": out["d_out_8704"]["kernel_us"],
+                                 "predicted_688_us": round(icpt + slope * 688, 3),
+                                 "measured_688_us": out["d_out_11008"]["kernel_us"]}
+    return out
+
+
 # ----------------------------------------------------------- HBM ceiling --
 
 _PROBE = None
@@ -798,14 +847,23 @@ def cpu_baseline(sample_s: float) -> dict:
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: model name, vendor, family /
+    model / stepping, and the logical CPUs this process may use."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if fields:
+                        break  # the first processor's block is enough
+                    continue
+                k, v = (t.strip() for t in line.split(":", 1))
+                fields.setdefault(k, v)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ident = ", ".join(f"{k} {fields[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ident}; {len(os.sched_getaffinity(0))} logical CPUs usable)"
 
 
 def cpu_beside() -> dict:
@@ -813,8 +871,9 @@ def cpu_beside() -> dict:
     figures of configs 1 and 3, on this host: quantize and dequantize of the
     4096 x 4096 config-1 tensor on one thread (the reference's loops are
     serial), and the config-3 QLoRA layer as the reference runs it --
-    serial dequantize, then an all-core f32 matmul plus the adapter -- timed
-    on a 32-row sample of X and scaled to the 2048 rows."""
+    serial dequantize, then an all-core f32 matmul plus the adapter -- with
+    the oracle's row loop (a 32-row sample of X, scaled to the 2048 rows) and
+    with a blocked sgemm of the matrixmultiply scheme (all 2048 rows)."""
     from oracle import oracle as O
     threads = len(os.sched_getaffinity(0))
     out = {"cores": threads, "cpu_model": cpu_model()}
@@ -833,9 +892,10 @@ def cpu_beside() -> dict:
     x = O.fill_normal(0x5A, 1.0, rows * K).reshape(rows, K)
     a = O.fill_normal(0x41, 0.01, K * r).reshape(K, r)
     b = O.fill_normal(0x42, 0.01, r * N).reshape(r, N)
-    t0 = t0_deq = time.perf_counter()
+    t0 = time.perf_counter()
     O.dequantize_packed(packed, n, absmax)                           # per forward, serial
     t1 = time.perf_counter()
+    t_deq = t1 - t0
     O.linear_f32(x, w, K, N, threads=threads)                        # base, all cores
     xa = O.linear_f32(x, a, K, r, threads=threads)                   # adapter: (x A) B * scaling
     O.linear_f32(xa, b, r, N, threads=threads)
@@ -843,7 +903,25 @@ def cpu_beside() -> dict:
     total = (t1 - t0) + (t2 - t1) * (M / rows)
     flops = 2 * M * N * K + 2 * M * K * r + 2 * M * r * N
     out["qlora_gemm_config3"] = {"s": round(total, 3), "tflops": round(flops / total / 1e12, 5),
-                                 "sample": f"{rows} of {M} rows timed, scaled", "threads": threads}
+                                 "sample": f"{rows} of {M} rows timed, scaled", "threads": threads,
+                                 "gemm": "the oracle's OpenMP row loop (oracle/nf4_oracle.c nf4o_linear_f32), "
+                                         "not cache-blocked like matrixmultiply's sgemm"}
+    # the same layer with a blocked f32 GEMM (oracle/cpu_sgemm.c: the packed
+    # Goto/BLIS scheme of the matrixmultiply crate burn-ndarray runs on),
+    # all 2048 rows timed
+    xf = O.fill_normal(0x5A, 1.0, M * K).reshape(M, K)
+    w2 = w.reshape(K, N)
+    t0 = time.perf_counter()
+    O.dequantize_packed(packed, n, absmax)                           # per forward, serial
+    O.sgemm_blocked(xf, w2, threads)
+    O.sgemm_blocked(O.sgemm_blocked(xf, a, threads), b, threads)
+    total_b = time.perf_counter() - t0
+    out["qlora_gemm_config3_blocked"] = {
+        "s": round(total_b, 3), "tflops": round(flops / total_b / 1e12, 5),
+        "sample": f"all {M} rows; serial dequantize as above", "threads": threads,
+        "gemm": "oracle/cpu_sgemm.c: cache-blocked packed sgemm, 6x16 AVX2/FMA register tile "
+                "(the scheme of matrixmultiply 0.3.x)"}
+    del xf
     # the matmuls on one thread (a 4-row sample, scaled)
     rows1 = 4
     t0 = time.perf_counter()
@@ -851,7 +929,7 @@ def cpu_beside() -> dict:
     xa1 = O.linear_f32(x[:rows1], a, K, r, threads=1)
     O.linear_f32(xa1, b, r, N, threads=1)
     t2 = time.perf_counter()
-    total1 = (t1 - t0_deq) + (t2 - t0) * (M / rows1)
+    total1 = t_deq + (t2 - t0) * (M / rows1)
     out["qlora_gemm_config3_one_thread"] = {"s": round(total1, 3), "tflops": round(flops / total1 / 1e12, 5),
                                             "sample": f"{rows1} of {M} rows timed, scaled; dequantize as above",
                                             "threads": 1}
@@ -877,6 +955,7 @@ PARTS = {
     "embedding": lambda torch, Q, L: bench_embedding(torch, Q, L),
     "backward": lambda torch, Q, L: bench_backward(torch, Q, L),
     "ceiling": lambda torch, Q, L: {f"{mib}MiB": bench_ceiling(torch, L, mib << 20) for mib in (22, 69, 256)},
+    "gemv_stripes": lambda torch, Q, L: bench_gemv_stripes(torch, Q, L),
 }
 
 

@@ -85,6 +85,13 @@ void nf4o_silu_vec(const float *x, size_t n, float *out);
 void nf4o_linear_f32(const float *x, size_t rows, const float *w, size_t d_in, size_t d_out,
                      const float *bias, float *y, int threads);
 
+/* CPU baseline only (oracle/cpu_sgemm.c): c[m][n] = a[m][k] b[k][n], all
+ * row-major, by a cache-blocked packed sgemm (6 x 16 FMA register tile, the
+ * scheme of the matrixmultiply crate burn-ndarray runs on) on `threads`
+ * OpenMP threads (0: the default).  Returns 0, or -1 if its packing buffers
+ * cannot be allocated. */
+int nf4o_sgemm_blocked(const float *a, size_t m, size_t k, const float *b, size_t n, float *c, int threads);
+
 /* Counter-based seeded N(0, sigma^2) generator shared by tests and bench
  * inputs: element i draws two SplitMix64 outputs at counters 2i+1, 2i+2,
  * Box-Muller in f64, times sigma, rounded to f32. */

@@ -59,6 +59,9 @@ def lib():
         L.nf4o_silu_vec.argtypes = [_f32p, ctypes.c_size_t, _f32p]
         L.nf4o_linear_f32.argtypes = [_f32p, ctypes.c_size_t, _f32p, ctypes.c_size_t,
                                       ctypes.c_size_t, _f32p, _f32p, ctypes.c_int]
+        L.nf4o_sgemm_blocked.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, _f32p, ctypes.c_size_t,
+                                         _f32p, ctypes.c_int]
+        L.nf4o_sgemm_blocked.restype = ctypes.c_int
         L.nf4o_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_double, ctypes.c_size_t, _f32p]
         L.nf4o_round_bf16.argtypes = [_f32p, ctypes.c_size_t, _f32p]
         _lib = L
@@ -174,6 +177,21 @@ def linear_f32(x, w, d_in: int, d_out: int, bias=None, threads: int = 0) -> np.n
     lib().nf4o_linear_f32(_p(xv, _f32p), xv.shape[0], _p(wv, _f32p), d_in, d_out,
                           None if b is None else _p(b, _f32p), _p(y, _f32p), int(threads))
     return y
+
+
+def sgemm_blocked(a, b, threads: int = 0) -> np.ndarray:
+    """a [m, k] @ b [k, n] in f32 by the blocked, packed CPU sgemm
+    (oracle/cpu_sgemm.c): the CPU baseline's stand-in for the matrixmultiply
+    crate that burn-ndarray's matmul runs on.  Not a parity reference."""
+    av = np.ascontiguousarray(a, np.float32)
+    bv = np.ascontiguousarray(b, np.float32)
+    if av.ndim != 2 or bv.ndim != 2 or av.shape[1] != bv.shape[0]:
+        raise ValueError(f"sgemm_blocked: shapes {av.shape} and {bv.shape} do not chain")
+    c = np.empty((av.shape[0], bv.shape[1]), np.float32)
+    if lib().nf4o_sgemm_blocked(_p(av, _f32p), av.shape[0], av.shape[1], _p(bv, _f32p), bv.shape[1],
+                                _p(c, _f32p), int(threads)) != 0:
+        raise MemoryError("sgemm_blocked: packing buffers")
+    return c
 
 
 def fill_normal(seed: int, sigma: float, n: int) -> np.ndarray:

@@ -295,6 +295,23 @@ def test_linear_f32_matches_f64_product(oracle):
     assert oracle.normwise_error(y, ref, x, np.abs(x) @ np.abs(w)) < 1e-5
 
 
+@pytest.mark.parametrize("m,k,n", [(2, 3, 3), (7, 300, 70), (97, 513, 2050), (6, 256, 16), (1, 1, 1), (5, 0, 4)])
+def test_sgemm_blocked_matches_f64_product(oracle, m, k, n):
+    # the CPU baseline's blocked sgemm: ragged edges of every block size
+    # (MR 6, NR 16, KC 256, MC 96, NC 2048), a second k block, empty k
+    rng = np.random.default_rng(m * 1000 + k + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    c = oracle.sgemm_blocked(a, b, threads=3)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    assert c.shape == (m, n)
+    assert np.all(np.abs(c - ref) <= 1e-5 * np.maximum(bound, 1e-30) + (k == 0) * 0.0)
+    # orientation: the known answer of nf4o_linear_f32's test
+    y = oracle.sgemm_blocked(np.array([[1.0, -1.0]]), np.arange(1, 7, dtype=np.float32).reshape(2, 3))
+    assert np.array_equal(y, [[-3.0, -3.0, -3.0]])
+
+
 def test_silu_closed_forms(oracle):
     z = np.array([0.0, 30.0, -30.0, 1.0, -2.5, 1e-3], np.float32)
     s = oracle.silu(z)
