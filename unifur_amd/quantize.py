@@ -367,6 +367,36 @@ class Nf4Linear:
         self._packed = None
         return self
 
+    @classmethod
+    def _from_group(cls, group: tuple, i: int, d_input: int, d_output: int) -> "Nf4Linear":
+        """Layer i of a grouped quantize pass: group = (codes, code offsets,
+        dq codes, scale offsets, scales of scales), one allocation each for
+        the whole pass.  Its slices of them are made on first use (slicing
+        three views per layer up front cost a 168-weight pass more host time
+        than its launches)."""
+        self = cls.__new__(cls)
+        self._d_in, self._d_out = d_input, d_output
+        self.bias = None
+        self._striped = True
+        self._len = d_input * d_output
+        self._dq = True
+        self._packed = None
+        self._group = (group, i)
+        return self
+
+    def __getattr__(self, name: str):
+        # reached only for attributes not set: the slices of a grouped pass
+        if name in ("_codes", "_scales", "_sos"):
+            g = self.__dict__.get("_group")
+            if g is not None:
+                (codes, c_off, dq, s_off, sos), i = g
+                self._codes = codes[c_off[i]:c_off[i + 1]]
+                self._scales = dq[s_off[i]:s_off[i + 1]]
+                self._sos = sos[i:i + 1]
+                del self._group
+                return self.__dict__[name]
+        raise AttributeError(f"{type(self).__name__!r} object has no attribute {name!r}")
+
     def d_input(self) -> int:
         return self._d_in
 
@@ -494,9 +524,10 @@ def quantize_checkpoint_linears(tensors) -> list:
     quantize_linears gives for the transposed f32 copies."""
     ws = []
     for t in tensors:
-        if t.dim() != 2:
-            raise ValueError(f"tensor of shape {tuple(t.shape)} is not rank-2")
-        ws.append((t, int(t.shape[1]), int(t.shape[0])))
+        shape = t.shape
+        if len(shape) != 2:
+            raise ValueError(f"tensor of shape {tuple(shape)} is not rank-2")
+        ws.append((t, shape[1], shape[0]))
     return _quantize_grouped(ws, checkpoint=True)
 
 
@@ -514,8 +545,8 @@ def _quantize_grouped(weights, checkpoint: bool) -> list:
     # buffers are allocated from the shapes alone, then the values are checked
     # and launched a group at a time (the library's grouped pass takes 48
     # weights per launch sequence), so that the first kernels start while the
-    # later groups are still being checked; the views are made after the last
-    # launch (that host work overlaps the kernels).
+    # later groups are still being checked; each layer makes its views of
+    # the three buffers when first used.
     c_sizes = [di * do // 2 for (di, do) in dims]
     s_sizes = [di * do // 64 for (di, do) in dims]
     codes = torch.empty(sum(c_sizes), dtype=torch.uint8, device=dev)
@@ -537,12 +568,15 @@ def _quantize_grouped(weights, checkpoint: bool) -> list:
             if not v.is_cuda:
                 raise ValueError("values must be a CUDA (HIP) device tensor")
             if checkpoint:
-                if v.dtype not in (torch.float32, torch.bfloat16) or tuple(v.shape) != (do, di):
+                dt = v.dtype
+                if dt is not src_dtype:
+                    if dt is not torch.float32 and dt is not torch.bfloat16:
+                        raise ValueError(f"checkpoint linears must be f32 or bf16 [{do}, {di}]")
+                    if src_dtype is not None:
+                        raise ValueError("checkpoint linears of one call share a dtype")
+                    src_dtype = dt
+                if v.shape != (do, di):
                     raise ValueError(f"checkpoint linears must be f32 or bf16 [{do}, {di}]")
-                if src_dtype is None:
-                    src_dtype = v.dtype
-                elif v.dtype != src_dtype:
-                    raise ValueError("checkpoint linears of one call share a dtype")
                 if not v.is_contiguous():
                     v = v.contiguous()
                     keep.append(v)
@@ -563,12 +597,8 @@ def _quantize_grouped(weights, checkpoint: bool) -> list:
             L.check(lib.unifur_nf4_quantize_checkpoint_linears(P(*v_ptrs), _dtype_code(src_dtype), *tail))
         else:
             L.check(lib.unifur_nf4_quantize_linears(P(*v_ptrs), *tail))
-    # the views in three C++ calls (one per buffer) rather than a Python
-    # slice per weight and buffer
-    cv = codes.split(c_sizes)
-    dv = dq.split(s_sizes)
-    sv = sos.split(1)
-    return [Nf4Linear._from_striped(cv[i], dv[i], sv[i], di, do) for i, (di, do) in enumerate(dims)]
+    group = (codes, c_off, dq, s_off, sos)
+    return [Nf4Linear._from_group(group, i, di, do) for i, (di, do) in enumerate(dims)]
 
 
 def forward_shared_input(x: torch.Tensor, layers, out_dtype: Optional[torch.dtype] = None) -> list:
