@@ -307,7 +307,10 @@ int unifur_nf4_qlora_forward(const void *x, int x_dtype, uint64_t rows, const un
  * the vector-Jacobian products of LoraAdapter::forward ((x A) B scaling,
  * src/quantize.rs:619-624) and of the base product.  bf16 dy goes through
  * the weight expanded to bf16 (with the adapter merged) and a BLAS GEMM;
- * f32 dy through the f32 dequantized weight.  The adapter gradients are
+ * f32 dy through an f32 MFMA GEMM over the NF4 tiles dequantized exactly on
+ * chip, W's rows as its outputs and the adapter term in its epilogue (no
+ * weight copy; shapes it does not take use an f32 dequantized copy of the
+ * weight).  The adapter gradients are
  * summed over the rows in a fixed order (deterministic); when dx takes the
  * BLAS path they run on the branch stream beside its GEMM.
  * A workspace smaller than the default size but at least the minimum size
