@@ -295,6 +295,19 @@ def test_linear_f32_matches_f64_product(oracle):
     assert oracle.normwise_error(y, ref, x, np.abs(x) @ np.abs(w)) < 1e-5
 
 
+def test_error_metrics_known_answers(oracle):
+    # normwise: the largest |y - r| over the bound of the same element, not
+    # over the largest bound; literal: the largest |y - r| over the largest |r|
+    y = np.array([[1.0, 2.5], [0.0, -4.0]])
+    r = np.array([[1.0, 2.0], [0.1, -4.0]])
+    bound = np.array([[10.0, 5.0], [0.2, 8.0]])
+    assert oracle.normwise_error(y, r, None, bound) == pytest.approx(0.5)   # 0.1 / 0.2
+    assert oracle.max_rel_error(y, r) == pytest.approx(0.125)              # 0.5 / 4
+    assert oracle.normwise_error(r, r, None, bound) == 0.0
+    assert oracle.max_rel_error(np.zeros(3), np.zeros(3)) == 0.0            # no division by zero
+    assert oracle.num_blocks(0) == 0 and oracle.num_blocks(64) == 1 and oracle.num_blocks(65) == 2
+
+
 @pytest.mark.parametrize("m,k,n", [(2, 3, 3), (7, 300, 70), (97, 513, 2050), (6, 256, 16), (1, 1, 1), (5, 0, 4)])
 def test_sgemm_blocked_matches_f64_product(oracle, m, k, n):
     # the CPU baseline's blocked sgemm: ragged edges of every block size
@@ -306,7 +319,7 @@ def test_sgemm_blocked_matches_f64_product(oracle, m, k, n):
     ref = a.astype(np.float64) @ b.astype(np.float64)
     bound = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
     assert c.shape == (m, n)
-    assert np.all(np.abs(c - ref) <= 1e-5 * np.maximum(bound, 1e-30) + (k == 0) * 0.0)
+    assert np.all(np.abs(c - ref) <= 1e-5 * np.maximum(bound, 1e-30))
     # orientation: the known answer of nf4o_linear_f32's test
     y = oracle.sgemm_blocked(np.array([[1.0, -1.0]]), np.arange(1, 7, dtype=np.float32).reshape(2, 3))
     assert np.array_equal(y, [[-3.0, -3.0, -3.0]])
