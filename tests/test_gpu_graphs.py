@@ -129,6 +129,73 @@ def test_fused_dx_backward_replays(device, oracle, rank):
         replay_matches(run, lambda: [dx])
 
 
+@pytest.mark.parametrize("rank", [0, 16])
+def test_f32_mfma_forward_and_dx_replay(device, oracle, rank):
+    """f32 activations past the skinny rows and f32 dY: the f32 MFMA GEMM
+    (and with an adapter its x A / dY B^T row products, whose slab sums
+    use arrival counters) replays to the eager bits."""
+    M, K, N = 300, 1024, 512
+    lin, _ = make_linear(oracle, K, N, 2070 + rank, device)
+    lin.bias = torch.from_numpy(oracle.fill_normal(2071, 0.1, N)).to(device)
+    _, xt = acts(oracle, M, K, 2072, torch.float32, device)
+    _, dyt = acts(oracle, M, N, 2073, torch.float32, device)
+    layer = lin
+    if rank:
+        _, _, ad = lora_parts(oracle, K, N, rank, 2074, device)
+        layer = Q.QloraLinear(lin, ad)
+    y = torch.empty(M, N, device=device)
+    dx = torch.empty(M, K, device=device)
+
+    def run():
+        y.copy_(layer.forward(xt, out_dtype=torch.float32))
+        if rank:
+            dx.copy_(layer.backward(xt, dyt, dx_dtype=torch.float32)[0])
+        else:
+            dx.copy_(layer.backward(dyt, dx_dtype=torch.float32))
+
+    replay_matches(run, lambda: [y, dx])
+
+
+def test_grouped_quantize_pass_replays(device, oracle):
+    """The grouped quantize pass (f32 values and bf16 checkpoint tensors,
+    more weights than one launch group takes) replays to the eager bytes."""
+    shapes = [(64 * (1 + i % 3), 64 * (1 + i % 4)) for i in range(53)]
+    vals = [(torch.from_numpy(oracle.fill_normal(2080 + i, 0.02, di * do)).to(device), di, do)
+            for i, (di, do) in enumerate(shapes)]
+    ckpt = [v.view(di, do).t().contiguous().to(torch.bfloat16) for (v, di, do) in vals]
+    outs = []
+
+    def run():
+        lins = Q.quantize_linears(vals) + Q.quantize_checkpoint_linears(ckpt)
+        if not outs:
+            outs.extend([torch.empty_like(t) for lin in lins for t in (lin._codes, lin._scales, lin._sos)])
+        for o, t in zip(outs, [t for lin in lins for t in (lin._codes, lin._scales, lin._sos)]):
+            o.copy_(t)
+
+    # as replay_matches, with zeros instead of NaN between the replays (the
+    # code and scale buffers are bytes)
+    run()
+    torch.cuda.synchronize()
+    want = [o.clone() for o in outs]
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        run()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=st):
+            run()
+    torch.cuda.current_stream().wait_stream(st)
+    for _ in range(4):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, w in zip(outs, want):
+            assert torch.equal(o, w), "graph replay differs from the eager result"
+
+
 def test_skinny_split_and_gemv_replay(device, oracle):
     # the skinny kernel's split-d_in hand-off (arrival counters) and the GEMV
     lin, _ = make_linear(oracle, 11008, 4096, 2030, device, striped=True)
