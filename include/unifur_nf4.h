@@ -284,8 +284,13 @@ int unifur_nf4_linear_forward_multi(const void *x, int x_dtype, uint64_t rows, c
  * workspace; with the least workspace the fused kernel runs over whole d_in
  * and its f32 sums may differ in order).  A call whose scratch need exceeds 16 MiB fails with
  * UNIFUR_NF4_ERR_WORKSPACE and a message naming the size.  All calls on one
- * GPU share that scratch: calls that overlap on one GPU (concurrent streams
- * or threads) race and must be serialized by the caller. */
+ * GPU share that scratch.  The library orders eager calls: a call on another
+ * stream than the previous call's waits on the GPU for that call's work (an
+ * event the library records after each call's launches), and calls from
+ * several host threads enqueue one at a time, so overlapping calls run one
+ * after the other.  Calls made under stream capture are not ordered against
+ * other calls: the caller must keep a captured graph's replays from
+ * overlapping other calls on the same GPU. */
 int unifur_nf4_linear_forward_noalloc(const void *x, int x_dtype, uint64_t rows, const unifur_nf4_weight *w,
                                       const float *bias, const unifur_nf4_lora *lora, void *y, int y_dtype,
                                       void *stream);

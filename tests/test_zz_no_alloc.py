@@ -8,7 +8,8 @@ compares every output bit for bit with unifur_nf4_linear_forward given its
 least workspace (unifur_nf4_linear_min_workspace_size: the same kernels), or,
 for prefill calls without an adapter (the fused kernel's split-K partials
 fit the scratch), given the scratch's 16 MiB; prefill cases are also checked
-against the float64 product within the bf16 bar.
+against the float64 product within the bf16 bar.  Calls alternating between
+two streams are checked to come out in order.
 """
 from __future__ import annotations
 
@@ -115,6 +116,31 @@ def test_noalloc_split_k_without_adapter(device, oracle, rows):
         assert torch.equal(got, want), f"rows {m}: noalloc differs from linear_forward with a 16 MiB workspace"
         check(got, oracle.linear_ref_f64(x, wdeq, oracle.fill_normal(5201, 0.1, n)), x, wdeq, TOL_BF16,
               f"noalloc split-K rows {m}")
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(device, oracle):
+    """Calls from two streams share the GPU's scratch; the entry point makes a
+    call on another stream than the previous call's wait for it on the GPU,
+    so six fused-prefill calls with an adapter (its x A operands live in the
+    scratch), alternating between two streams with no host synchronisation,
+    each give linear_forward's bits."""
+    m, k, n, r = 300, 1024, 768, 16
+    lin, _ = make_linear(oracle, k, n, 5300, device, dq=True, striped=True)
+    _, _, ad = lora_parts(oracle, k, n, r, 5301, device)
+    lora = ad.struct()
+    xs = [acts(oracle, m, k, 5302 + i, torch.bfloat16, device)[1] for i in range(6)]
+    want = [existing(lin, x, lora, torch.bfloat16) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    got = []
+    for i, x in enumerate(xs):
+        with torch.cuda.stream(streams[i % 2]):
+            got.append(noalloc(lin, x, lora, torch.bfloat16))
+    torch.cuda.synchronize()
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert torch.equal(g, w), f"call {i} (stream {i % 2}) differs from linear_forward"
 
 
 def test_noalloc_refuses_what_does_not_fit(device, oracle):

@@ -1448,6 +1448,11 @@ __global__ void zero_words_kernel(uint32_t* p, size_t words) {
 struct StaticScratch {
   std::mutex mu;
   std::map<int, void*> ptr;  // device -> address of its copy of `scratch`
+  // Ordering of the calls that share a device's scratch: the event recorded
+  // after the last eager call's launches and that call's stream.
+  std::mutex order_mu;
+  std::map<int, hipEvent_t> done;
+  std::map<int, hipStream_t> last;
 };
 
 StaticScratch& static_scratch() {
@@ -1500,9 +1505,35 @@ int run_linear_noalloc(const void* x, int x_dtype, uint64_t rows, const unifur_n
     return fail(UNIFUR_NF4_ERR_WORKSPACE, "linear_forward_noalloc: this call needs " + std::to_string(L.total) +
                                               " bytes of scratch, the allocation-free entry point holds " +
                                               std::to_string(kStaticScratchBytes));
+  // Calls on one GPU share its scratch.  An eager call on another stream
+  // than the previous eager call's first waits on the GPU for that call's
+  // work (an event recorded after its launches, the set-up's fill included),
+  // and the lock keeps a second host thread from launching in between, so
+  // calls from different streams and threads run one after the other
+  // instead of racing.  Calls made under stream capture are not ordered this
+  // way (their replays are the caller's to order).
+  StaticScratch& s = static_scratch();
+  std::lock_guard<std::mutex> lock(s.order_mu);
   void* p = nullptr;
   if (int r = static_scratch_address(stream, &p)) return r;
-  return run_linear(x, x_dtype, rows, w, bias, lora, y, y_dtype, p, kStaticScratchBytes, stream, false);
+  int dev = 0;
+  UNIFUR_HIP(hipGetDevice(&dev));
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  UNIFUR_HIP(hipStreamIsCapturing(stream, &cap));
+  const bool eager = cap == hipStreamCaptureStatusNone;
+  hipEvent_t* ev = nullptr;
+  if (eager) {
+    ev = &s.done[dev];
+    if (*ev == nullptr) UNIFUR_HIP(hipEventCreateWithFlags(ev, hipEventDisableTiming));  // set-up, once per device
+    const auto it = s.last.find(dev);
+    if (it != s.last.end() && it->second != stream) UNIFUR_HIP(hipStreamWaitEvent(stream, *ev, 0));
+  }
+  const int r = run_linear(x, x_dtype, rows, w, bias, lora, y, y_dtype, p, kStaticScratchBytes, stream, false);
+  if (eager) {
+    UNIFUR_HIP(hipEventRecord(*ev, stream));
+    s.last[dev] = stream;
+  }
+  return r;
 }
 
 }  // namespace
