@@ -56,8 +56,13 @@ enum {
   UNIFUR_NF4_ERR_WORKSPACE = -3,   /* workspace smaller than required */
 };
 
-/* Element types of activations and outputs. */
-enum { UNIFUR_NF4_F32 = 0, UNIFUR_NF4_BF16 = 1 };
+/* Element types of activations and outputs (F32, BF16), and of checkpoint
+ * sources (also F16). */
+enum { UNIFUR_NF4_F32 = 0, UNIFUR_NF4_BF16 = 1,
+       /* checkpoint sources only (quantize_transposed, transpose_checkpoint,
+        * quantize_checkpoint_linears): binary16 decoded exactly as
+        * f16_to_f32, src/import.rs:283-317 */
+       UNIFUR_NF4_F16 = 2 };
 
 /* Index types of embedding lookups. */
 enum { UNIFUR_NF4_IDS_I32 = 0, UNIFUR_NF4_IDS_I64 = 1 };
@@ -167,8 +172,9 @@ int unifur_nf4_embedding_forward(const uint8_t *packed, const unifur_nf4_scales 
                                  int out_dtype, void *stream);
 
 /* Loader step of qwen_linear (src/qwennet.rs:1687-1726): a checkpoint weight
- * src [out_features, in_features] row-major (PyTorch order), f32 or bf16
- * (bf16 decoded exactly, src/import.rs:323-327), is transposed to
+ * src [out_features, in_features] row-major (PyTorch order), f32, bf16 or
+ * f16 (src_dtype UNIFUR_NF4_F32 / _BF16 / _F16; bf16 and f16 decoded exactly
+ * as read_tensor_f32 does, src/import.rs:255-272, :283-327), is transposed to
  * [in_features, out_features] (transpose2d, src/qwennet.rs:1375-1390) and
  * quantized (PackedNf4Tensor::quantize, src/quantize.rs:262-279) in one pass:
  * packed/absmax are bit-identical to quantizing the transposed copy.
@@ -178,7 +184,7 @@ int unifur_nf4_quantize_transposed(const void *src, int src_dtype, uint64_t out_
 
 /* transpose2d (src/qwennet.rs:1375-1390) of a decoded checkpoint linear:
  * dst [in_features, out_features] f32 = the transpose of src [out_features,
- * in_features] (f32, or bf16 decoded exactly, src/import.rs:323-327), for
+ * in_features] (f32, or bf16 / f16 decoded exactly, src/import.rs:255-327), for
  * weights whose out_features is not a multiple of 64 (their blocks straddle
  * the rows of the transposed buffer, so they are quantized flat after this).
  * out_features <= 65535 * 64. */
@@ -206,7 +212,7 @@ int unifur_nf4_quantize_linears(const float *const *values, const uint64_t *d_in
 /* The same pass from checkpoint tensors as they lie (qwen_linear,
  * src/qwennet.rs:1687-1726, over each decoded linear of the checkpoint):
  * values[i] is the PyTorch-order [d_out[i], d_in[i]] weight in src_dtype
- * (f32, or bf16 decoded exactly as src/import.rs:323-327 does), transposed on
+ * (f32, or bf16 / f16 decoded exactly as src/import.rs:255-327 does), transposed on
  * the fly (transpose2d, src/qwennet.rs:1375-1390) -- packed[i], dq_codes[i]
  * and scale_of_scales[i] are byte for byte what unifur_nf4_quantize_linears
  * writes for the transposed f32 copy.  d_out % 64 == 0, values aligned to

@@ -24,6 +24,10 @@
  *   nf4o_silu                closed-form limits and an f64 evaluation
  *   nf4o_transpose           involution and index identity
  *   nf4o_fill_normal         determinism and moments (input generator only)
+ *   nf4o_f16_to_f32          all 65536 bit patterns: IEEE widening (numpy) for
+ *                            every non-NaN, subnormals against mant * 2^-24 in
+ *                            f64, NaNs with the quiet bit forced, known answers
+ *   nf4o_bf16_to_f32         all 65536 bit patterns against bits << 16
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp).
  */
@@ -264,6 +268,45 @@ void nf4o_fill_normal(uint64_t seed, double sigma, size_t n, float *out) {
         double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);         /* [0, 1) */
         double z = sqrt(-2.0 * log(u1)) * cos(two_pi * u2);
         out[i] = (float)(z * sigma);
+    }
+}
+
+/* Checkpoint element decode (read_tensor_f32, src/import.rs:243-280): f16
+ * bits to f32 as f16_to_f32 (src/import.rs:283-317) -- zero kept signed, a
+ * subnormal renormalised by the same shift loop, infinity kept, a NaN's
+ * payload moved up 13 bits with the quiet bit forced -- and bf16 bits to f32
+ * as bf16_to_f32 (src/import.rs:321-327): the top 16 bits. */
+void nf4o_f16_to_f32(const uint16_t *in, size_t n, float *out) {
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t bits = in[i];
+        const uint32_t sign = (bits >> 15) & 1u, exp = (bits >> 10) & 0x1fu, mant = bits & 0x3ffu;
+        uint32_t o;
+        if (exp == 0) {
+            if (mant == 0) {
+                o = sign << 31;
+            } else {
+                uint32_t m = mant, e = 127u - 14u;
+                while ((m & 0x400u) == 0) {
+                    m <<= 1;
+                    e -= 1u;
+                }
+                m &= 0x3ffu;
+                o = (sign << 31) | (e << 23) | (m << 13);
+            }
+        } else if (exp == 0x1fu) {
+            const uint32_t payload = mant == 0 ? 0u : (((mant << 13) | 0x00400000u) & 0x007fffffu);
+            o = (sign << 31) | (0xffu << 23) | payload;
+        } else {
+            o = (sign << 31) | ((exp + (127u - 15u)) << 23) | (mant << 13);
+        }
+        memcpy(&out[i], &o, 4);
+    }
+}
+
+void nf4o_bf16_to_f32(const uint16_t *in, size_t n, float *out) {
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t o = (uint32_t)in[i] << 16;
+        memcpy(&out[i], &o, 4);
     }
 }
 

@@ -100,6 +100,12 @@ void nf4o_fill_normal(uint64_t seed, double sigma, size_t n, float *out);
 /* Round f32 to bf16 (RNE) and back to f32, elementwise. */
 void nf4o_round_bf16(const float *in, size_t n, float *out);
 
+/* Checkpoint element decode (src/import.rs:255-272): binary16 bits to f32 as
+ * f16_to_f32 (src/import.rs:283-317: exact; NaN payload kept, quiet bit set),
+ * bfloat16 bits to f32 as bf16_to_f32 (src/import.rs:321-327). */
+void nf4o_f16_to_f32(const uint16_t *in, size_t n, float *out);
+void nf4o_bf16_to_f32(const uint16_t *in, size_t n, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,9 @@ def lib():
         L.nf4o_sgemm_blocked.restype = ctypes.c_int
         L.nf4o_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_double, ctypes.c_size_t, _f32p]
         L.nf4o_round_bf16.argtypes = [_f32p, ctypes.c_size_t, _f32p]
+        _u16p = ctypes.POINTER(ctypes.c_uint16)
+        for name in ("nf4o_f16_to_f32", "nf4o_bf16_to_f32"):
+            getattr(L, name).argtypes = [_u16p, ctypes.c_size_t, _f32p]
         _lib = L
     return _lib
 
@@ -197,6 +200,17 @@ def sgemm_blocked(a, b, threads: int = 0) -> np.ndarray:
 def fill_normal(seed: int, sigma: float, n: int) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().nf4o_fill_normal(ctypes.c_uint64(seed), float(sigma), n, _p(out, _f32p))
+    return out
+
+
+def decode_checkpoint(bits, dtype: str) -> np.ndarray:
+    """Checkpoint elements (u16 bit patterns) to f32 as read_tensor_f32 does
+    (src/import.rs:255-272): ``dtype`` "f16" (f16_to_f32, src/import.rs:283-317)
+    or "bf16" (bf16_to_f32, src/import.rs:321-327)."""
+    b = np.ascontiguousarray(bits, np.uint16)
+    out = np.empty(b.shape, np.float32)
+    fn = {"f16": lib().nf4o_f16_to_f32, "bf16": lib().nf4o_bf16_to_f32}[dtype]
+    fn(b.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), b.size, _p(out, _f32p))
     return out
 
 

@@ -27,12 +27,17 @@ pytestmark = pytest.mark.gpu
 def checkpoint_linear(oracle, out_f, in_f, seed, dtype):
     """A decoded checkpoint tensor [out, in] (numpy f32 values, device tensor)."""
     v = oracle.fill_normal(seed, 0.05, out_f * in_f).reshape(out_f, in_f)
+    if dtype == torch.float16:
+        # binary16 draws (numpy's RNE narrowing), and the f32 values the
+        # reference decodes from them (f16_to_f32, src/import.rs:283-317)
+        h = v.astype(np.float16)
+        return oracle.decode_checkpoint(h.view(np.uint16), "f16").reshape(out_f, in_f), torch.from_numpy(h).to("cuda:0")
     if dtype == torch.bfloat16:
         v = oracle.round_bf16(v).reshape(out_f, in_f)
     return v, torch.from_numpy(v).to("cuda:0").to(dtype)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(64, 1), (64, 7), (128, 64), (192, 100), (896, 896), (4864, 130)])
 def test_quantize_transposed_is_transpose_then_quantize(device, oracle, dtype, shape):
     out_f, in_f = shape
@@ -51,13 +56,13 @@ def test_quantize_transposed_is_transpose_then_quantize(device, oracle, dtype, s
     codes = torch.empty((out_f * in_f + 1) // 2, dtype=torch.uint8, device=device)
     absmax = torch.empty((out_f * in_f + 63) // 64, dtype=torch.float32, device=device)
     from unifur_amd import _lib as L
-    L.check(L.lib().unifur_nf4_quantize_transposed(t.data_ptr(), Q._dtype_code(dtype), out_f, in_f,
+    L.check(L.lib().unifur_nf4_quantize_transposed(t.data_ptr(), Q._src_dtype_code(dtype), out_f, in_f,
                                                    codes.data_ptr(), absmax.data_ptr(), Q._stream()))
     assert np.array_equal(codes.cpu().numpy(), packed_ref)
     assert np.array_equal(absmax.cpu().numpy().view(np.uint32), absmax_ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(100, 96), (70, 129), (1, 64), (130, 1)])
 def test_qwen_linear_with_ragged_out_features_falls_back_to_separate_transpose(device, oracle, dtype, shape):
     """out % 64 != 0: the library transposes (unifur_nf4_transpose_checkpoint,
@@ -78,9 +83,25 @@ def test_qwen_linear_with_ragged_out_features_falls_back_to_separate_transpose(d
     # the transpose entry point itself: bit for bit the oracle's transpose2d
     from unifur_amd import _lib as L
     dst = torch.empty(out_f * in_f, dtype=torch.float32, device=device)
-    L.check(L.lib().unifur_nf4_transpose_checkpoint(t.data_ptr(), Q._dtype_code(dtype), out_f, in_f, dst.data_ptr(),
+    L.check(L.lib().unifur_nf4_transpose_checkpoint(t.data_ptr(), Q._src_dtype_code(dtype), out_f, in_f, dst.data_ptr(),
                                                     Q._stream()))
     assert np.array_equal(dst.cpu().numpy().view(np.uint32), tv.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_transpose_checkpoint_decodes_every_half_bit_pattern(device, oracle, dtype):
+    """All 65536 binary16 (or bfloat16) patterns, NaN payloads, infinities
+    and subnormals included, as a [256, 256] checkpoint tensor: the f32
+    transpose is bit for bit the oracle's decode (read_tensor_f32,
+    src/import.rs:255-317) then transpose2d."""
+    from unifur_amd import _lib as L
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    t = torch.from_numpy(bits.view(np.int16)).to(device).view(torch.float16 if dtype == "f16" else torch.bfloat16)
+    ref = oracle.transpose(oracle.decode_checkpoint(bits, dtype), 256, 256)
+    dst = torch.empty(1 << 16, dtype=torch.float32, device=device)
+    L.check(L.lib().unifur_nf4_transpose_checkpoint(t.data_ptr(), Q._src_dtype_code(t.dtype), 256, 256,
+                                                    dst.data_ptr(), Q._stream()))
+    assert np.array_equal(dst.cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
 def test_qwen_linear_f32_store_and_forward(device, oracle):

@@ -139,10 +139,16 @@ def test_forward_matches_and_argument_errors(device, oracle):
 
 def checkpoint_tensors(oracle, shapes, seed, dtype, device):
     """[out = d_out, in = d_in] tensors; bf16 ones hold exactly the oracle's
-    RNE rounding of the f32 draw (the values the reference decodes)."""
+    RNE rounding of the f32 draw, f16 ones numpy's (host: the f32 values the
+    reference decodes from them)."""
     host, dev = [], []
     for i, (di, do) in enumerate(shapes):
         v = oracle.fill_normal(seed + 0x10000 * i, 0.02, di * do)
+        if dtype == torch.float16:
+            h = v.astype(np.float16)  # binary16 draws; f32 as f16_to_f32 decodes them
+            host.append(oracle.decode_checkpoint(h.view(np.uint16), "f16").reshape(do, di))
+            dev.append(torch.from_numpy(h.reshape(do, di)).to(device))
+            continue
         if dtype == torch.bfloat16:
             v = oracle.round_bf16(v)
         v = v.reshape(do, di)
@@ -151,7 +157,7 @@ def checkpoint_tensors(oracle, shapes, seed, dtype, device):
     return host, dev
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 def test_checkpoint_config5_all_weights_against_the_oracle(device, oracle, dtype):
     """All 168 config-5 projections from checkpoint tensors as they lie, in
     one call: each weight's striped codes, u8 scales and scale of scales equal
@@ -174,7 +180,7 @@ def test_checkpoint_config5_all_weights_against_the_oracle(device, oracle, dtype
         assert g._sos.cpu().numpy().view(np.uint32)[0] == np.float32(sos).view(np.uint32), f"weight {i}: sos"
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 def test_checkpoint_ragged_shapes_match_the_transposed_pass(device, oracle, dtype):
     """d_in not a multiple of 64 (a partial source tile), of 8 or 4 (the
     element-load path), one-row and one-column weights, two groups: the same
@@ -200,6 +206,34 @@ def test_checkpoint_special_values(device, oracle):
     t = torch.from_numpy(v).cuda()
     got = Q.quantize_checkpoint_linears([t])[0]
     same_bytes(got, Q.quantize_linears([(t.t().contiguous().view(-1), di, do)])[0])
+
+
+def test_checkpoint_f16_special_values(device, oracle):
+    """binary16 sources with infinities, NaNs (quiet and signalling), signed
+    zeros and subnormals, in a zero, a subnormal-only and an all-NaN block:
+    the same bytes as the f32 pass over the oracle's decode, transposed."""
+    do, di = 192, 16  # [out, in]
+    h = oracle.fill_normal(3600, 0.05, di * do).astype(np.float16).reshape(do, di).copy()
+    hb = h.view(np.uint16)
+    hb[0:64, 0] = 0x0000                                   # a zero block
+    hb[64:128, 1] = np.arange(64, dtype=np.uint16) + 1     # subnormals only
+    hb[128:192, 2] = 0x7D01                                # signalling NaNs: an all-NaN block
+    hb[3, 3], hb[4, 3], hb[5, 3] = 0x7C00, 0xFC00, 0x7E55  # +inf, -inf, a quiet NaN with a payload
+    hb[6, 4], hb[7, 4] = 0x8000, 0x8001                    # -0, the smallest negative subnormal
+    hb[8, 5] = 0x7BFF                                      # the largest finite half
+    t = torch.from_numpy(h).to(device)
+    f = oracle.decode_checkpoint(hb.reshape(-1), "f16").reshape(do, di)
+    ref_t = torch.from_numpy(np.ascontiguousarray(f.T)).to(device).view(-1)
+    got = Q.quantize_checkpoint_linears([t])[0]
+    same_bytes(got, Q.quantize_linears([(ref_t, di, do)])[0])
+    # the single-tensor entry point, before double quantization, is the oracle's
+    packed_ref, absmax_ref = oracle.quantize_packed(np.ascontiguousarray(f.T).reshape(-1))
+    codes = torch.empty(do * di // 2, dtype=torch.uint8, device=device)
+    absmax = torch.empty(do * di // 64, dtype=torch.float32, device=device)
+    L.check(L.lib().unifur_nf4_quantize_transposed(t.data_ptr(), L.F16, do, di, codes.data_ptr(),
+                                                   absmax.data_ptr(), Q._stream()))
+    assert np.array_equal(codes.cpu().numpy(), packed_ref)
+    assert np.array_equal(absmax.cpu().numpy().view(np.uint32), absmax_ref.view(np.uint32))
 
 
 def test_checkpoint_argument_errors(device):

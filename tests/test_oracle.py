@@ -325,6 +325,38 @@ def test_sgemm_blocked_matches_f64_product(oracle, m, k, n):
     assert np.array_equal(y, [[-3.0, -3.0, -3.0]])
 
 
+def test_checkpoint_f16_decode_all_bit_patterns(oracle):
+    # f16_to_f32 (src/import.rs:283-317) over every binary16 pattern
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = oracle.decode_checkpoint(bits, "f16").view(np.uint32)
+    ieee = bits.view(np.float16).astype(np.float32).view(np.uint32)  # exact widening
+    exp, mant = (bits.astype(np.uint32) >> 10) & 0x1F, bits.astype(np.uint32) & 0x3FF
+    nan = (exp == 0x1F) & (mant != 0)
+    assert np.array_equal(got[~nan], ieee[~nan])
+    # NaN: payload moved up 13 bits and the quiet bit forced (a signalling
+    # input cannot trap downstream)
+    assert np.array_equal(got[nan], ieee[nan] | np.uint32(0x00400000))
+    assert np.all((got[nan] & np.uint32(0x7FC00000)) == np.uint32(0x7FC00000))
+    # subnormals: mant * 2^-24 exactly, from the mathematics rather than numpy
+    sub = (exp == 0) & (mant != 0)
+    vals = got[sub].view(np.float32).astype(np.float64)
+    sign = np.where(bits[sub] & 0x8000, -1.0, 1.0)
+    assert np.array_equal(vals, sign * mant[sub].astype(np.float64) * 2.0 ** -24)
+    known = {0x3C00: 1.0, 0xC000: -2.0, 0x7BFF: 65504.0, 0x0001: 2.0 ** -24, 0x03FF: 1023 * 2.0 ** -24,
+             0x0400: 2.0 ** -14, 0x3555: 0.333251953125}
+    for b, v in known.items():
+        assert float(oracle.decode_checkpoint(np.array([b]), "f16")[0]) == v, hex(b)
+    inf = oracle.decode_checkpoint(np.array([0x7C00, 0xFC00, 0x8000]), "f16")
+    assert inf[0] == np.inf and inf[1] == -np.inf and inf[2] == 0.0 and np.signbit(inf[2])
+
+
+def test_checkpoint_bf16_decode_all_bit_patterns(oracle):
+    # bf16_to_f32 (src/import.rs:321-327): the top 16 bits of the f32
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = oracle.decode_checkpoint(bits, "bf16").view(np.uint32)
+    assert np.array_equal(got, bits.astype(np.uint32) << 16)
+
+
 def test_silu_closed_forms(oracle):
     z = np.array([0.0, 30.0, -30.0, 1.0, -2.5, 1e-3], np.float32)
     s = oracle.silu(z)

@@ -18,6 +18,7 @@ ERR_WORKSPACE = -3
 
 F32 = 0
 BF16 = 1
+F16 = 2  # checkpoint sources only
 
 IDS_I32 = 0
 IDS_I64 = 1

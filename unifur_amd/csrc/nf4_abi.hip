@@ -56,6 +56,12 @@ bool u32_aligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) =
 
 bool valid_dtype(int d) { return d == UNIFUR_NF4_F32 || d == UNIFUR_NF4_BF16; }
 
+// Element types a checkpoint tensor may arrive in (src/import.rs:255-272):
+// F32, BF16 and F16, each decoded to f32 exactly.  Only the checkpoint
+// entry points take F16; activations are f32 or bf16.
+bool valid_src_dtype(int d) { return d == UNIFUR_NF4_F32 || d == UNIFUR_NF4_BF16 || d == UNIFUR_NF4_F16; }
+int src_kind_of(int d) { return d == UNIFUR_NF4_BF16 ? kSrcBf16 : d == UNIFUR_NF4_F16 ? kSrcF16 : kSrcF32; }
+
 ScalesArg to_scales(const unifur_nf4_scales& s) {
   return ScalesArg{s.kind, s.absmax, s.dq_codes, s.scale_of_scales};
 }
@@ -1781,14 +1787,14 @@ uint64_t unifur_nf4_swiglu_workspace_size(uint64_t rows, uint64_t hidden, uint64
 }
 int unifur_nf4_quantize_transposed(const void* src, int src_dtype, uint64_t out_features, uint64_t in_features,
                                    uint8_t* packed, float* absmax, void* stream) {
-  UNIFUR_ARG(valid_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  UNIFUR_ARG(valid_src_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32, UNIFUR_NF4_BF16 or UNIFUR_NF4_F16");
   if (out_features == 0 || in_features == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(src && packed && absmax, "src, packed or absmax is NULL");
   UNIFUR_ARG(out_features % 64 == 0, "quantize_transposed needs out_features % 64 == 0");
   UNIFUR_ARG(out_features / 64 <= 65535u && in_features <= 0x7fffffffffull, "quantize_transposed: shape too large");
   UNIFUR_ARG(aligned_to(packed, 8), "packed must be 8-byte aligned");
-  UNIFUR_ARG(aligned_to(src, src_dtype == UNIFUR_NF4_BF16 ? 2 : 4), "src is misaligned for its dtype");
-  UNIFUR_HIP(launch_quantize_transposed(src, src_dtype == UNIFUR_NF4_BF16, out_features, in_features, packed, absmax,
+  UNIFUR_ARG(aligned_to(src, src_dtype == UNIFUR_NF4_F32 ? 4 : 2), "src is misaligned for its dtype");
+  UNIFUR_HIP(launch_quantize_transposed(src, src_kind_of(src_dtype), out_features, in_features, packed, absmax,
                                         static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
 }
@@ -1838,13 +1844,13 @@ int unifur_nf4_quantize_linears(const float* const* values, const uint64_t* d_in
 
 int unifur_nf4_transpose_checkpoint(const void* src, int src_dtype, uint64_t out_features, uint64_t in_features,
                                     float* dst, void* stream) {
-  UNIFUR_ARG(valid_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
+  UNIFUR_ARG(valid_src_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32, UNIFUR_NF4_BF16 or UNIFUR_NF4_F16");
   if (out_features == 0 || in_features == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(src && dst, "src or dst is NULL");
   UNIFUR_ARG(out_features <= 65535ull * 64ull, "out_features exceeds 65535 * 64");
-  UNIFUR_ARG(aligned_to(src, src_dtype == UNIFUR_NF4_BF16 ? 2 : 4) && aligned_to(dst, 4),
+  UNIFUR_ARG(aligned_to(src, src_dtype == UNIFUR_NF4_F32 ? 4 : 2) && aligned_to(dst, 4),
              "src or dst misaligned for its dtype");
-  UNIFUR_HIP(launch_transpose_decode(src, src_dtype == UNIFUR_NF4_BF16, out_features, in_features, dst,
+  UNIFUR_HIP(launch_transpose_decode(src, src_kind_of(src_dtype), out_features, in_features, dst,
                                      static_cast<hipStream_t>(stream)));
   return UNIFUR_NF4_OK;
 }
@@ -1853,9 +1859,11 @@ int unifur_nf4_quantize_checkpoint_linears(const void* const* values, int src_dt
                                            const uint64_t* d_out, uint32_t n, uint8_t* const* packed,
                                            uint8_t* const* dq_codes, float* const* scale_of_scales, void* workspace,
                                            uint64_t workspace_bytes, void* stream) {
-  UNIFUR_ARG(valid_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32 or UNIFUR_NF4_BF16");
-  return run_quantize_linears(values, src_dtype == UNIFUR_NF4_BF16 ? kQuantSrcBf16T : kQuantSrcF32T, d_in, d_out, n,
-                              packed, dq_codes, scale_of_scales, workspace, workspace_bytes, stream);
+  UNIFUR_ARG(valid_src_dtype(src_dtype), "src_dtype must be UNIFUR_NF4_F32, UNIFUR_NF4_BF16 or UNIFUR_NF4_F16");
+  const int kind = src_dtype == UNIFUR_NF4_BF16 ? kQuantSrcBf16T : src_dtype == UNIFUR_NF4_F16 ? kQuantSrcF16T
+                                                                                              : kQuantSrcF32T;
+  return run_quantize_linears(values, kind, d_in, d_out, n, packed, dq_codes, scale_of_scales, workspace,
+                              workspace_bytes, stream);
 }
 
 uint64_t unifur_nf4_dense_linear_workspace_size(uint64_t rows, uint32_t lora_rank) {

@@ -311,8 +311,8 @@ __global__ void dequantize_tail_kernel(const uint8_t* __restrict__ packed, Scale
 
 // ------------------------------------------------------ transpose-quantize --
 // The loader's step (src/qwennet.rs:1687-1726): a checkpoint weight
-// src[out_f][in_f] (PyTorch [out, in], f32 or bf16 decoded exactly as
-// src/import.rs:323-327) is transposed to [in_f][out_f] (transpose2d,
+// src[out_f][in_f] (PyTorch [out, in], f32, or bf16 / f16 decoded exactly as
+// src/import.rs:255-272 does) is transposed to [in_f][out_f] (transpose2d,
 // src/qwennet.rs:1375-1390) and quantized (PackedNf4Tensor::quantize) -- here
 // in one pass, without the transposed f32 copy.  With out_f % 64 == 0 every
 // 64-value block of the transposed buffer is 64 consecutive output features
@@ -320,7 +320,7 @@ __global__ void dequantize_tail_kernel(const uint8_t* __restrict__ packed, Scale
 // Tile in LDS (padded rows), then wave lane l takes block row k = l / 4 of
 // its 16 and the quarter l % 4 of the block: a 4-lane absmax, 16 codes, one
 // 8-byte store.  Arithmetic identical to quantize_full_kernel.
-template <bool kBf16In>
+template <int SRC>
 __global__ __launch_bounds__(256) void quantize_transposed_kernel(const void* __restrict__ src, uint64_t out_f,
                                                                   uint64_t in_f, uint8_t* __restrict__ packed,
                                                                   float* __restrict__ absmax) {
@@ -335,8 +335,7 @@ __global__ __launch_bounds__(256) void quantize_transposed_kernel(const void* __
     float v = 0.0f;
     if (k0 + k < in_f) {
       const uint64_t idx = (o0 + o) * in_f + k0 + k;
-      v = kBf16In ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(src)[idx])
-                  : reinterpret_cast<const float*>(src)[idx];
+      v = decode_src<SRC>(src, idx);
     }
     tile[o][k] = v;
   }
@@ -525,7 +524,7 @@ __global__ __launch_bounds__(kQuantThreads) void qgroup_quantize_kernel(QGroupAr
 }
 
 // The same first pass from checkpoint tensors as they lie: values[i] is the
-// PyTorch-order [N][K] weight (f32, or bf16 decoded exactly), i.e. the
+// PyTorch-order [N][K] weight (f32, or bf16 / f16 decoded exactly), i.e. the
 // transpose of the [K][N] weight to quantize (qwen_linear's transpose2d,
 // src/qwennet.rs:1375-1390, fused away).  A workgroup per 64 x 64 source
 // tile (k tile kt, block column b): rows o = 64 b .. + 63 of the source,
@@ -534,10 +533,11 @@ __global__ __launch_bounds__(kQuantThreads) void qgroup_quantize_kernel(QGroupAr
 // quarter q = l % 4 of its 64 values, which is exactly stripe 4 b + q of
 // that row: a 4-lane absmax, 16 codes, one 8-byte store (the four lanes of
 // a row write its four stripes, the 16 rows of a wave 128 contiguous bytes
-// per stripe).  VEC: rows 16-byte aligned (K a multiple of 8 for bf16, 4
-// for f32), the tile loaded 16 bytes per thread and load.
-template <bool BF16, bool VEC>
+// per stripe).  VEC: rows 16-byte aligned (K a multiple of 8 for bf16 and
+// f16, 4 for f32), the tile loaded 16 bytes per thread and load.
+template <int SRC, bool VEC>
 __global__ __launch_bounds__(256) void qgroup_quantize_t_kernel(QGroupArgs a) {
+  constexpr bool HALF = SRC != kSrcF32;  // 2-byte elements
   __shared__ BucketEntry tab[33];
   __shared__ float tile[64][65];
   build_bucket_table(tab);
@@ -551,7 +551,7 @@ __global__ __launch_bounds__(256) void qgroup_quantize_t_kernel(QGroupArgs a) {
     const uint64_t o0 = 64ull * b;
     __syncthreads();  // the bucket table built; the previous tile's reads done
     if constexpr (VEC) {
-      constexpr int kPer = BF16 ? 8 : 4;  // values per 16-byte load
+      constexpr int kPer = HALF ? 8 : 4;  // values per 16-byte load
       constexpr int kRowLoads = 64 / kPer;
       for (int i = tid; i < 64 * kRowLoads; i += 256) {
         const int o = i / kRowLoads, kc = (i % kRowLoads) * kPer;
@@ -559,12 +559,12 @@ __global__ __launch_bounds__(256) void qgroup_quantize_t_kernel(QGroupArgs a) {
         if (k0 + kc < T.K) {  // K is a multiple of kPer: the load lies inside the row
           const uint64_t idx = (o0 + o) * T.K + k0 + kc;
           const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(T.values) +
-                                                          idx * (BF16 ? 2 : 4));
-          if constexpr (BF16) {
+                                                          idx * (HALF ? 2 : 4));
+          if constexpr (HALF) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              v[2 * e] = __uint_as_float(w[e] << 16);
-              v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+              v[2 * e] = decode_half<SRC>(w[e] & 0xffffu);
+              v[2 * e + 1] = decode_half<SRC>(w[e] >> 16);
             }
           } else {
 #pragma unroll
@@ -583,8 +583,7 @@ __global__ __launch_bounds__(256) void qgroup_quantize_t_kernel(QGroupArgs a) {
         float v = 0.0f;
         if (k0 + k < T.K) {
           const uint64_t idx = (o0 + o) * T.K + k0 + k;
-          v = BF16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(T.values)[idx])
-                   : static_cast<const float*>(T.values)[idx];
+          v = decode_src<SRC>(T.values, idx);
         }
         tile[o][k] = v;
       }
@@ -734,17 +733,18 @@ hipError_t launch_dequantize(const uint8_t* packed, const ScalesArg& scales, siz
   return hipGetLastError();
 }
 
-hipError_t launch_quantize_transposed(const void* src, bool bf16_in, uint64_t out_f, uint64_t in_f, uint8_t* packed,
+hipError_t launch_quantize_transposed(const void* src, int src_kind, uint64_t out_f, uint64_t in_f, uint8_t* packed,
                                       float* absmax, hipStream_t stream) {
   if (out_f == 0 || in_f == 0) return hipSuccess;
   const uint64_t gx = (in_f + 63) / 64, gy = out_f / 64;
   if (out_f % 64 != 0 || gx > 0x7fffffffu || gy > 65535u) return hipErrorInvalidValue;
-  if (bf16_in)
-    quantize_transposed_kernel<true><<<dim3((unsigned)gx, (unsigned)gy), 256, 0, stream>>>(src, out_f, in_f, packed,
-                                                                                           absmax);
-  else
-    quantize_transposed_kernel<false><<<dim3((unsigned)gx, (unsigned)gy), 256, 0, stream>>>(src, out_f, in_f, packed,
-                                                                                            absmax);
+  const dim3 grid((unsigned)gx, (unsigned)gy);
+  switch (src_kind) {
+    case kSrcF32: quantize_transposed_kernel<kSrcF32><<<grid, 256, 0, stream>>>(src, out_f, in_f, packed, absmax); break;
+    case kSrcBf16: quantize_transposed_kernel<kSrcBf16><<<grid, 256, 0, stream>>>(src, out_f, in_f, packed, absmax); break;
+    case kSrcF16: quantize_transposed_kernel<kSrcF16><<<grid, 256, 0, stream>>>(src, out_f, in_f, packed, absmax); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -797,7 +797,7 @@ hipError_t launch_quantize_linears(const void* const* values, int src_kind, cons
                                    const uint64_t* d_out, uint32_t n, uint8_t* const* packed, uint8_t* const* dq,
                                    float* const* sos, void* scratch, hipStream_t stream) {
   const bool transposed = src_kind != kQuantSrcF32;
-  const bool bf16 = src_kind == kQuantSrcBf16T;
+  const bool half = src_kind == kQuantSrcBf16T || src_kind == kQuantSrcF16T;
   char* tmp = static_cast<char*>(scratch);
   for (uint32_t g0 = 0; g0 < n; g0 += kQGroupMax) {
     QGroupArgs a{};
@@ -820,7 +820,7 @@ hipError_t launch_quantize_linears(const void* const* values, int src_kind, cons
       // 16-row groups (64-row source tiles when transposed) x block columns
       spans += (d_in[j] + (transposed ? 63 : 15)) / (transposed ? 64 : 16) * (d_out[j] / kBlock);
       max_nb = std::max(max_nb, nb);
-      vec = vec && (reinterpret_cast<uintptr_t>(values[j]) & 15u) == 0 && d_in[j] % (bf16 ? 8 : 4) == 0;
+      vec = vec && (reinterpret_cast<uintptr_t>(values[j]) & 15u) == 0 && d_in[j] % (half ? 8 : 4) == 0;
     }
     if (spans > 0xffffffffull) return hipErrorInvalidValue;
     a.spans = (uint32_t)spans;
@@ -828,12 +828,15 @@ hipError_t launch_quantize_linears(const void* const* values, int src_kind, cons
       qgroup_quantize_kernel<<<grid_for(spans, kQuantWaves, 8192), kQuantThreads, 0, stream>>>(a);
     } else if (spans) {
       const int grid = (int)std::min<uint64_t>(spans, 8192);
-      if (bf16)
-        vec ? qgroup_quantize_t_kernel<true, true><<<grid, 256, 0, stream>>>(a)
-            : qgroup_quantize_t_kernel<true, false><<<grid, 256, 0, stream>>>(a);
+      if (src_kind == kQuantSrcBf16T)
+        vec ? qgroup_quantize_t_kernel<kSrcBf16, true><<<grid, 256, 0, stream>>>(a)
+            : qgroup_quantize_t_kernel<kSrcBf16, false><<<grid, 256, 0, stream>>>(a);
+      else if (src_kind == kQuantSrcF16T)
+        vec ? qgroup_quantize_t_kernel<kSrcF16, true><<<grid, 256, 0, stream>>>(a)
+            : qgroup_quantize_t_kernel<kSrcF16, false><<<grid, 256, 0, stream>>>(a);
       else
-        vec ? qgroup_quantize_t_kernel<false, true><<<grid, 256, 0, stream>>>(a)
-            : qgroup_quantize_t_kernel<false, false><<<grid, 256, 0, stream>>>(a);
+        vec ? qgroup_quantize_t_kernel<kSrcF32, true><<<grid, 256, 0, stream>>>(a)
+            : qgroup_quantize_t_kernel<kSrcF32, false><<<grid, 256, 0, stream>>>(a);
     }
     qgroup_max_kernel<<<(unsigned)a.n, 1024, 0, stream>>>(a);
     if (max_nb) {

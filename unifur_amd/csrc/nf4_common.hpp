@@ -45,6 +45,42 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
+// binary16 bits -> f32, exact, as the reference's checkpoint decode
+// (f16_to_f32, src/import.rs:283-317): a subnormal renormalised (its value
+// mant * 2^-24), infinities kept, a NaN's payload kept with the quiet bit set.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+  uint32_t out;
+  if (exp == 0u) {
+    if (mant == 0u) {
+      out = sign;
+    } else {
+      const uint32_t s = (uint32_t)__builtin_clz(mant) - 21u;  // shifts that bring the leading one to bit 10
+      out = sign | ((113u - s) << 23) | (((mant << s) & 0x3ffu) << 13);
+    }
+  } else if (exp == 0x1fu) {
+    out = sign | 0x7f800000u | (mant == 0u ? 0u : (((mant << 13) | 0x00400000u) & 0x007fffffu));
+  } else {
+    out = sign | ((exp + 112u) << 23) | (mant << 13);
+  }
+  return __uint_as_float(out);
+}
+
+// Element types a checkpoint tensor may arrive in (src/import.rs:255-272),
+// each decoded to f32 exactly.
+enum { kSrcF32 = 0, kSrcBf16 = 1, kSrcF16 = 2 };
+template <int SRC>
+__device__ __forceinline__ float decode_src(const void* base, uint64_t idx) {
+  if constexpr (SRC == kSrcF32) return static_cast<const float*>(base)[idx];
+  else if constexpr (SRC == kSrcBf16) return bf16_bits_to_f32(static_cast<const uint16_t*>(base)[idx]);
+  else return f16_bits_to_f32(static_cast<const uint16_t*>(base)[idx]);
+}
+template <int SRC>
+__device__ __forceinline__ float decode_half(uint32_t h16) {
+  if constexpr (SRC == kSrcBf16) return bf16_bits_to_f32(h16);
+  else return f16_bits_to_f32(h16);
+}
+
 // v_perm_b32: result byte i = byte sel[i] of the 8-byte value {a:b}
 // (bytes 0-3 come from b, 4-7 from a, selector 0x0c yields 0x00).
 __device__ __forceinline__ uint32_t perm_b32(uint32_t a, uint32_t b, uint32_t sel) {

@@ -54,9 +54,9 @@ hipError_t launch_transpose(const void* src, void* dst, uint64_t rows, uint64_t 
 }
 
 // dst[c][r] = decode(src[r][c]) into f32: the checkpoint's [out, in]
-// weight (f32, or bf16 widened exactly) to the [in, out] f32 values that
-// quantize takes.
-template <bool BF16>
+// weight (f32, or bf16 / f16 decoded exactly) to the [in, out] f32 values
+// that quantize takes.
+template <int SRC>
 __global__ __launch_bounds__(256) void transpose_decode_kernel(const void* __restrict__ src, float* __restrict__ dst,
                                                                uint64_t rows, uint64_t cols) {
   __shared__ float tile[kTile][kTile + 1];
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void transpose_decode_kernel(const void* __res
     const int r = lr + 4 * i;
     if (r0 + r < rows && c0 + lc < cols) {
       const uint64_t idx = (r0 + r) * cols + c0 + lc;
-      tile[r][lc] = BF16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(src)[idx]) : static_cast<const float*>(src)[idx];
+      tile[r][lc] = decode_src<SRC>(src, idx);
     }
   }
   __syncthreads();
@@ -81,16 +81,18 @@ __global__ __launch_bounds__(256) void transpose_decode_kernel(const void* __res
 
 }  // namespace
 
-hipError_t launch_transpose_decode(const void* src, bool bf16, uint64_t rows, uint64_t cols, float* dst,
+hipError_t launch_transpose_decode(const void* src, int src_kind, uint64_t rows, uint64_t cols, float* dst,
                                    hipStream_t stream) {
   if (rows == 0 || cols == 0) return hipSuccess;
   const uint64_t gx = (cols + kTile - 1) / kTile, gy = (rows + kTile - 1) / kTile;
   if (gx > 0x7fffffffu || gy > 65535u) return hipErrorInvalidValue;
   const dim3 grid((unsigned)gx, (unsigned)gy);
-  if (bf16)
-    transpose_decode_kernel<true><<<grid, 256, 0, stream>>>(src, dst, rows, cols);
-  else
-    transpose_decode_kernel<false><<<grid, 256, 0, stream>>>(src, dst, rows, cols);
+  switch (src_kind) {
+    case kSrcF32: transpose_decode_kernel<kSrcF32><<<grid, 256, 0, stream>>>(src, dst, rows, cols); break;
+    case kSrcBf16: transpose_decode_kernel<kSrcBf16><<<grid, 256, 0, stream>>>(src, dst, rows, cols); break;
+    case kSrcF16: transpose_decode_kernel<kSrcF16><<<grid, 256, 0, stream>>>(src, dst, rows, cols); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -19,9 +19,9 @@ hipError_t launch_stripe_codes(const uint8_t* src, uint8_t* dst, uint64_t d_in, 
 hipError_t launch_stripe_scales(const void* src, void* dst, uint64_t d_in, uint64_t d_out, bool dq, bool to_striped,
                                 hipStream_t stream);
 
-// dst [cols][rows] f32 = the transpose of src [rows][cols] (f32, or bf16
-// widened exactly); rows up to 65535 * 64.
-hipError_t launch_transpose_decode(const void* src, bool bf16, uint64_t rows, uint64_t cols, float* dst,
+// dst [cols][rows] f32 = the transpose of src [rows][cols] (kSrcF32, or
+// kSrcBf16 / kSrcF16 decoded exactly: nf4_common.hpp); rows up to 65535 * 64.
+hipError_t launch_transpose_decode(const void* src, int src_kind, uint64_t rows, uint64_t cols, float* dst,
                                    hipStream_t stream);
 
 }  // namespace unifur

@@ -54,6 +54,16 @@ def _dtype_code(dtype: torch.dtype) -> int:
     raise ValueError(f"unsupported dtype {dtype}; the NF4 path takes float32 or bfloat16")
 
 
+def _src_dtype_code(dtype: torch.dtype) -> int:
+    """A checkpoint tensor's element type: the three read_tensor_f32 decodes
+    (src/import.rs:255-272)."""
+    if dtype == torch.float16:
+        return L.F16
+    if dtype in (torch.float32, torch.bfloat16):
+        return _dtype_code(dtype)
+    raise ValueError(f"unsupported checkpoint dtype {dtype}; checkpoints are float32, bfloat16 or float16")
+
+
 def _require_cuda(t: torch.Tensor, name: str) -> None:
     if not t.is_cuda:
         raise ValueError(f"{name} must be a CUDA (HIP) device tensor")
@@ -517,7 +527,7 @@ def quantize_linears(weights) -> list:
 
 def quantize_checkpoint_linears(tensors) -> list:
     """The same pass from checkpoint linears as they lie: each tensor is the
-    PyTorch-order [out, in] weight (f32 or bf16, on the device), as
+    PyTorch-order [out, in] weight (f32, bf16 or f16, on the device), as
     qwen_linear (src/qwennet.rs:1687-1726) receives it, transposed to
     [in, out] on the fly (transpose2d, src/qwennet.rs:1375-1390) inside the
     grouped quantize kernel; out % 64 == 0.  Byte for byte what
@@ -570,13 +580,13 @@ def _quantize_grouped(weights, checkpoint: bool) -> list:
             if checkpoint:
                 dt = v.dtype
                 if dt is not src_dtype:
-                    if dt is not torch.float32 and dt is not torch.bfloat16:
-                        raise ValueError(f"checkpoint linears must be f32 or bf16 [{do}, {di}]")
+                    if dt is not torch.float32 and dt is not torch.bfloat16 and dt is not torch.float16:
+                        raise ValueError(f"checkpoint linears must be f32, bf16 or f16 [{do}, {di}]")
                     if src_dtype is not None:
                         raise ValueError("checkpoint linears of one call share a dtype")
                     src_dtype = dt
                 if v.shape != (do, di):
-                    raise ValueError(f"checkpoint linears must be f32 or bf16 [{do}, {di}]")
+                    raise ValueError(f"checkpoint linears must be f32, bf16 or f16 [{do}, {di}]")
                 if not v.is_contiguous():
                     v = v.contiguous()
                     keep.append(v)
@@ -594,7 +604,7 @@ def _quantize_grouped(weights, checkpoint: bool) -> list:
                 P(*[cb + c_off[i] for i in idx]), P(*[db + s_off[i] for i in idx]), P(*[sb + 4 * i for i in idx]),
                 None, 0, stream)
         if checkpoint:
-            L.check(lib.unifur_nf4_quantize_checkpoint_linears(P(*v_ptrs), _dtype_code(src_dtype), *tail))
+            L.check(lib.unifur_nf4_quantize_checkpoint_linears(P(*v_ptrs), _src_dtype_code(src_dtype), *tail))
         else:
             L.check(lib.unifur_nf4_quantize_linears(P(*v_ptrs), *tail))
     group = (codes, c_off, dq, s_off, sos)

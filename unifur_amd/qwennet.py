@@ -208,7 +208,7 @@ class Nf4ResidencyReport:
 
 def qwen_linear(tensor: torch.Tensor, store: WeightStore) -> tuple:
     """src/qwennet.rs:1687-1726: one decoded checkpoint linear [out, in]
-    (f32 or bf16, on the device) into a QwenLinear in the requested storage,
+    (f32, bf16 or f16, on the device) into a QwenLinear in the requested storage,
     with the resident bytes of the chosen form.  Nf4: transposed to
     [in, out], quantized and double-quantized -- for out % 64 == 0 in one
     grouped pass straight into the striped resident form
@@ -220,19 +220,19 @@ def qwen_linear(tensor: torch.Tensor, store: WeightStore) -> tuple:
         raise ValueError(f"tensor of shape {tuple(tensor.shape)} is not rank-2")
     Q._require_cuda(tensor, "tensor")
     rows, cols = tensor.shape  # [out, in]
-    if tensor.dtype not in (torch.float32, torch.bfloat16):
-        raise ValueError("checkpoint linears are f32 or bf16")
+    if tensor.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError("checkpoint linears are f32, bf16 or f16")
     src = tensor.contiguous()
     if store == WeightStore.F32:  # linear_param (src/qwennet.rs:1396-1420): the transposed f32 weight
         w = torch.empty(cols, rows, dtype=torch.float32, device=src.device)
-        L.check(L.lib().unifur_nf4_transpose_checkpoint(src.data_ptr(), Q._dtype_code(src.dtype), rows, cols,
+        L.check(L.lib().unifur_nf4_transpose_checkpoint(src.data_ptr(), Q._src_dtype_code(src.dtype), rows, cols,
                                                         w.data_ptr(), Q._stream()))
         return QwenLinear(QwenLinear.F32, Q.DenseLinear(w)), 4 * tensor.numel()
     if rows % 64 == 0:
         lin = Q.quantize_checkpoint_linears([src])[0]
     else:
         flat = torch.empty(rows * cols, dtype=torch.float32, device=src.device)
-        L.check(L.lib().unifur_nf4_transpose_checkpoint(src.data_ptr(), Q._dtype_code(src.dtype), rows, cols,
+        L.check(L.lib().unifur_nf4_transpose_checkpoint(src.data_ptr(), Q._src_dtype_code(src.dtype), rows, cols,
                                                         flat.data_ptr(), Q._stream()))
         lin = Q.Nf4Linear.from_packed(Q.PackedNf4Tensor.quantize(flat).with_double_quantization(), cols, rows)
     return QwenLinear(QwenLinear.NF4, lin), lin.resident_bytes()
