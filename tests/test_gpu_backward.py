@@ -176,6 +176,32 @@ def test_fused_dx_with_the_minimum_workspace(device, oracle, case):
             ql.backward(xt, dyt_, dx_dtype=dxt, workspace=ws[:need - 256])
 
 
+@pytest.mark.parametrize("work", ["default", "least"])
+@pytest.mark.parametrize("r", [3, 16])
+def test_dx_adapter_term_alone_over_a_zero_weight(device, oracle, r, work):
+    """Over an all-zero base weight dx is the adapter's term
+    ((dy s) B^T) A^T alone, so its error is taken against that term (with a
+    normal base weight the term is a few per cent of dx).  Default
+    workspace: s A B merged into the expanded weight; least: the fused dX
+    kernel's epilogue."""
+    from test_gpu_gemm import zero_linear
+    M, K, N = 192, 512, 1024
+    lin = zero_linear(K, N, device, striped=True)
+    s = 16.0 / r
+    a, b, ad = lora_parts(oracle, K, N, r, 1781 + r, device, scaling=s, sigma=0.05)
+    x, xt = acts(oracle, M, K, 1782, torch.bfloat16, device)
+    dy, dyt_ = acts(oracle, M, N, 1783, torch.bfloat16, device)
+    ws = None
+    if work == "least":
+        need = L.lib().unifur_nf4_linear_backward_min_workspace_size(M, K, N, L.BF16, r, L.LAYOUT_STRIPED)
+        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=device)[:need]
+    dx, ga, gb = Q.QloraLinear(lin, ad).backward(xt, dyt_, dx_dtype=torch.float32, workspace=ws)
+    rdx, bdx, rga, bga, rgb, bgb = refs(x, dy, np.zeros((K, N)), a, b, s)
+    e = (normwise(dx.cpu(), rdx, bdx), normwise(ga.cpu(), rga, bga), normwise(gb.cpu(), rgb, bgb))
+    print(f"dx adapter alone r={r} {work}: dx {e[0]:.2e} grad_a {e[1]:.2e} grad_b {e[2]:.2e}", flush=True)
+    assert e[0] <= 1e-2 and e[1] <= 1e-5 and e[2] <= 1e-5
+
+
 def test_min_workspace_for_a_row_major_weight(device, oracle):
     """Only a striped weight takes the fused dX kernel: for a row-major one
     the least workspace is the default size, and a backward given exactly

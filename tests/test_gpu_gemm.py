@@ -92,6 +92,49 @@ def test_bias_and_lora_ranks(device, oracle, r, striped):
     assert torch.equal(Q.QloraLinear(lin, fresh).forward(xt), lin.forward(xt))
 
 
+def zero_linear(K, N, device, striped):
+    """An NF4 layer whose every block is zero (absmax 0): deq(W) = 0."""
+    p = Q.PackedNf4Tensor.quantize(torch.zeros(K * N, device=device)).with_double_quantization()
+    lin = Q.Nf4Linear.from_packed(p, K, N, striped=striped)
+    assert float(lin.dequantized_weight().abs().max()) == 0.0
+    return lin
+
+
+@pytest.mark.parametrize("striped", [True, False])
+@pytest.mark.parametrize("work", ["default", "least"])
+@pytest.mark.parametrize("r", [3, 16, 40])
+def test_adapter_term_alone_over_a_zero_weight(device, oracle, r, work, striped):
+    """Over an all-zero base weight y is the adapter term (x A) B s alone
+    (src/quantize.rs:619-624), so its error is taken against that term: with
+    a normal base weight the adapter is a few per cent of y, and a wrong
+    factor row or column could hide inside the bf16 bar.  The default
+    workspace merges s A B into the expanded weight (rank 16: factors staged
+    through LDS; other ranks: per-wave fragment loads); the least workspace
+    takes the fused kernel's epilogue."""
+    M, K, N = 256, 1024, 512
+    lin = zero_linear(K, N, device, striped)
+    s = 16.0 / r
+    x, xt = acts(oracle, M, K, 0x77, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 0x78 + r, device, scaling=s, sigma=0.05)
+    ref = oracle.lora_ref_f64(x, a, b, s)
+    lib = L.lib()
+    size = lib.unifur_nf4_linear_workspace_size if work == "default" else lib.unifur_nf4_linear_min_workspace_size
+    need = size(M, K, N, L.BF16, r)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)
+    w, lo = lin.weight_struct(), ad.struct()
+    y = torch.empty(M, N, device=device)
+    L.check(lib.unifur_nf4_linear_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w), None, ctypes.byref(lo),
+                                          y.data_ptr(), L.F32, ws.data_ptr(), need,
+                                          torch.cuda.current_stream().cuda_stream))
+    got = y.cpu().numpy().astype(np.float64)
+    # per element against the sum of |products| of the adapter term
+    bound = (np.abs(x) @ np.abs(a)) @ np.abs(b) * s
+    nw = float(np.max(np.abs(got - ref) / bound))
+    lit = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+    print(f"adapter alone r={r} {work} striped={striped}: normwise {nw:.3e} literal {lit:.3e}", flush=True)
+    assert nw <= TOL_BF16 and lit <= TOL_BF16
+
+
 def test_misaligned_activations_take_the_generic_path(device, oracle):
     # X not 16-byte aligned: the generic dequantize + f32 matmul serves it,
     # with the same result to the bf16 tolerance.
