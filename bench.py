@@ -105,14 +105,20 @@ def replay_event_ms(torch, graph, launches: int, reps: int = 20) -> float:
     return start.elapsed_time(end) / (reps * launches)
 
 
-def graph_ms(torch, graph, reps: int) -> float:
-    """Average wall time of one graph replay over reps back-to-back replays."""
-    torch.cuda.synchronize()
+def steady_ms(torch, graph, launches: int, reps: int = 10, runs: int = 5, warm_s: float = 0.05) -> float:
+    """Per-launch GPU time of a graph at steady state: the graph is replayed
+    for at least warm_s seconds first (a pass timed straight after capture
+    meets the clocks still ramping: config 3 read 79 us per call there against
+    70 us a few passes later on the same box), then the median of `runs`
+    event-timed passes of `reps` back-to-back replays (replay_event_ms)."""
     t0 = time.perf_counter()
-    for _ in range(reps):
+    while True:
         graph.replay()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / reps
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_s:
+            break
+    times = sorted(replay_event_ms(torch, graph, launches, reps) for _ in range(runs))
+    return times[len(times) // 2]
 
 
 def _i64(v: int) -> int:
@@ -464,7 +470,7 @@ def bench_gemm(torch, Q, L) -> dict:
     for i in range(3):
         launch(i)
     graph = capture(torch, launch, 8)
-    ms = graph_ms(torch, graph, 10) / 8 if graph is not None else event_ms(torch, launch, 16)
+    ms = steady_ms(torch, graph, 8) if graph is not None else event_ms(torch, launch, 16)
     # the base GEMM kernel alone (no LoRA: one launch)
     ybase = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
 
@@ -472,7 +478,7 @@ def bench_gemm(torch, Q, L) -> dict:
         L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), L.BF16, M, ctypes.byref(w), None, None, ybase.data_ptr(),
                                               L.BF16, None, 0, torch.cuda.current_stream().cuda_stream))
     gbase = capture(torch, base, 8)
-    base_ms = replay_event_ms(torch, gbase, 8, reps=10) if gbase is not None else event_ms(torch, base, 16)
+    base_ms = steady_ms(torch, gbase, 8) if gbase is not None else event_ms(torch, base, 16)
     base_flops = 2 * M * N * K
     # the fused kernel (NF4 tiles dequantized on chip, LoRA in the epilogue):
     # what the least workspace selects, with the adapter and without
@@ -494,7 +500,7 @@ def bench_gemm(torch, Q, L) -> dict:
             if not ferr < 1e-2:
                 raise RuntimeError(f"fused GEMM sanity check failed: {ferr:.3e}")
         gf = capture(torch, fused_launch, 8)
-        f_ms = graph_ms(torch, gf, 10) / 8 if gf is not None else event_ms(torch, fused_launch, 16)
+        f_ms = steady_ms(torch, gf, 8) if gf is not None else event_ms(torch, fused_launch, 16)
         f_flops = flops if name == "qlora" else base_flops
         fused[name] = {"ms": round(f_ms, 5), "tflops": round(f_flops / f_ms / 1e9, 1),
                        "frac": round(f_flops / f_ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
@@ -516,7 +522,7 @@ def bench_gemm(torch, Q, L) -> dict:
     if not e32 < 1e-3:
         raise RuntimeError(f"f32 GEMM sanity check failed: {e32:.3e}")
     g32 = capture(torch, f32_launch, 4)
-    ms32 = graph_ms(torch, g32, 5) / 4 if g32 is not None else event_ms(torch, f32_launch, 8)
+    ms32 = steady_ms(torch, g32, 4, reps=5) if g32 is not None else event_ms(torch, f32_launch, 8)
     dy32 = g.normal(M, N)
     dx32 = torch.empty(M, K, device=dev)
     wsb = lib.unifur_nf4_linear_backward_workspace_size(M, K, N, L.F32, 0)
@@ -528,7 +534,7 @@ def bench_gemm(torch, Q, L) -> dict:
                                                torch.cuda.current_stream().cuda_stream))
     dx_launch(0)
     gdx = capture(torch, dx_launch, 4)
-    msdx = graph_ms(torch, gdx, 5) / 4 if gdx is not None else event_ms(torch, dx_launch, 8)
+    msdx = steady_ms(torch, gdx, 4, reps=5) if gdx is not None else event_ms(torch, dx_launch, 8)
     f32 = {"path": "f32 MFMA (v_mfma_f32_32x32x2f32) over NF4 tiles dequantized exactly in LDS",
            "qlora_ms": round(ms32, 5), "qlora_tflops": round(flops / ms32 / 1e9, 1),
            "frac_of_f32_mfma_peak": round(flops / ms32 / 1e9 / F32_MFMA_PEAK_TFLOPS, 4),
@@ -563,7 +569,7 @@ def bench_swiglu(torch, Q, L, tokens) -> dict:
         for i in range(copies):
             run(i)
         graph = capture(torch, run, copies)
-        ms = graph_ms(torch, graph, 10) / copies if graph is not None else event_ms(torch, run, 2 * copies)
+        ms = steady_ms(torch, graph, copies) if graph is not None else event_ms(torch, run, 2 * copies)
         flops = T * 270_532_608
         out[f"T{T}"] = {"ms": round(ms, 5), "weight_gbs": round(wbytes / ms / 1e6, 1),
                         "tflops": round(flops / ms / 1e9, 2)}
@@ -649,7 +655,7 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
 
         step(0)
         graph = capture(torch, step, mcopies)
-        ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, step, 2 * mcopies)
+        ms = steady_ms(torch, graph, mcopies) if graph is not None else event_ms(torch, step, 2 * mcopies)
         out[f"decode_{tag}"] = {"ms_per_token_step": round(ms, 4), "weight_gbs": round(wbytes / ms / 1e6, 1),
                                 "tokens_per_s": round(b / ms * 1e3, 1)}
 
@@ -666,7 +672,7 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
 
         layer_step(0)
         graph = capture(torch, layer_step, mcopies)
-        ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, layer_step, 2 * mcopies)
+        ms = steady_ms(torch, graph, mcopies) if graph is not None else event_ms(torch, layer_step, 2 * mcopies)
         out[f"decode_{tag}_layer_launches"] = {"ms_per_token_step": round(ms, 4),
                                               "weight_gbs": round(wbytes / ms / 1e6, 1),
                                               "tokens_per_s": round(b / ms * 1e3, 1), "launches": 4 * layers}
@@ -691,7 +697,7 @@ def bench_qwen(torch, Q, L, layers: int = 24) -> dict:
 
         decoder_step(0)
         graph = capture(torch, decoder_step, mcopies)
-        ms = graph_ms(torch, graph, 10) / mcopies if graph is not None else event_ms(torch, decoder_step, 2 * mcopies)
+        ms = steady_ms(torch, graph, mcopies) if graph is not None else event_ms(torch, decoder_step, 2 * mcopies)
         out[f"decode_{tag}_decoder_stages"] = {"ms_per_token_step": round(ms, 4),
                                               "weight_gbs": round(wbytes / ms / 1e6, 1),
                                               "tokens_per_s": round(b / ms * 1e3, 1),
@@ -753,7 +759,7 @@ def bench_backward(torch, Q, L) -> dict:
         for i in range(3):
             fn(i)
         graph = capture(torch, fn, 4)
-        res[name] = graph_ms(torch, graph, 10) / 4 if graph is not None else event_ms(torch, fn, 8)
+        res[name] = steady_ms(torch, graph, 4) if graph is not None else event_ms(torch, fn, 8)
     ms = res["ms"]
     flops = 2 * M * N * K + 2 * K * r * N + 4 * M * r * (K + N)
     # the adapter gradients read x and dy twice each (bf16)
@@ -794,7 +800,7 @@ def bench_embedding(torch, Q, L) -> dict:
 
         gather(0)
         graph = capture(torch, gather, 16)
-        ms = graph_ms(torch, graph, 10) / 16 if graph is not None else event_ms(torch, gather, 16)
+        ms = steady_ms(torch, graph, 16) if graph is not None else event_ms(torch, gather, 16)
         moved = t * (d // 2 + d // 64 + 4 * d) + 8 * t
         out[f"gather_T{t}_us"] = round(ms * 1e3, 2)
         out[f"gather_T{t}_gbs"] = round(moved / ms / 1e6, 1)
