@@ -185,3 +185,64 @@ def test_grouped_quantize_sweep(device, oracle, seed):
           for i, (di, do) in enumerate(shapes)]
     for (v, di, do), g in zip(ws, Q.quantize_linears(ws)):
         same_bytes(g, per_weight(v, di, do))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_checkpoint_pass_sweep(device, oracle, seed):
+    """The grouped checkpoint pass over drawn [out, in] shapes and element
+    types: the oracle's transpose2d + quantize + double quantization in the
+    striped permutation (qwen_linear, src/qwennet.rs:1687-1726)."""
+    from test_gpu_layout import striped_codes_np, striped_scales_np
+    from test_gpu_quantize_linears import checkpoint_tensors
+    r = np.random.default_rng(0xC4E0 + seed)
+    dtype = [torch.float32, torch.bfloat16, torch.float16][int(r.integers(3))]
+    count = int(r.integers(1, 70))
+    shapes = [(int(r.choice([1, 3, 8, 9, 64, 100, 130, 896])), int(64 * r.integers(1, 16))) for _ in range(count)]
+    print(f"sweep checkpoint seed {seed}: {count} tensors of {dtype}", flush=True)
+    host, dev = checkpoint_tensors(oracle, shapes, 0xC4E1 + 131 * seed, dtype, device)
+    got = Q.quantize_checkpoint_linears(dev)
+    for i, ((di, do), v, g) in enumerate(zip(shapes, host, got)):
+        packed, absmax = oracle.quantize_packed(oracle.transpose(v.reshape(-1), do, di))
+        q, sos = oracle.double_quantize(absmax)
+        assert (g.d_input(), g.d_output()) == (di, do)
+        assert np.array_equal(g._codes.cpu().numpy(), striped_codes_np(packed, di, do)), f"tensor {i} {(di, do)}"
+        assert np.array_equal(g._scales.cpu().numpy(), striped_scales_np(q, di, do)), f"tensor {i} {(di, do)}"
+        assert g._sos.cpu().numpy().view(np.uint32)[0] == np.float32(sos).view(np.uint32), f"tensor {i}"
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_decoder_stages_sweep(device, oracle, seed):
+    """QwenDecoderLayer::step's NF4 stages (src/qwennet.rs:1112-1129) over
+    drawn layer shapes, rows and types: input norm + q/k/v, then o +
+    residual, post norm + SwiGLU + residual, against the float64 oracle."""
+    from unifur_amd import qwennet as N
+    from test_gpu_decoder import EPS, assert_close, out_mlp_bound
+    r = np.random.default_rng(0xDEC0 + seed)
+    hidden = int(r.choice([64, 128, 256, 448, 896]))
+    q_out, kv_out = int(r.choice([64, 128, 256, 896])), int(r.choice([64, 128]))
+    inter = int(r.choice([128, 256, 704, 1408]))
+    rows = int(r.choice([1, 2, 3, 4, 5, 9, 16, 32, 40, 64, 80]))
+    dt = torch.bfloat16 if r.integers(2) else torch.float32
+    dq, striped = bool(r.integers(2)), None if r.integers(2) else False
+    print(f"sweep decoder seed {seed}: hidden {hidden} q {q_out} kv {kv_out} inter {inter} rows {rows} {dt} "
+          f"dq {dq} striped {striped}", flush=True)
+    shapes = {"q": (hidden, q_out), "k": (hidden, kv_out), "v": (hidden, kv_out), "o": (q_out, hidden),
+              "gate": (hidden, inter), "up": (hidden, inter), "down": (inter, hidden)}
+    lins, w = {}, {}
+    for i, (name, (d_in, d_out)) in enumerate(shapes.items()):
+        lins[name], w[name] = make_linear(oracle, d_in, d_out, 0xDEC1 + 16 * seed + i, device, dq=dq, striped=striped)
+    g_in = oracle.fill_normal(0xDEC2 + seed, 0.1, hidden)
+    g_post = oracle.fill_normal(0xDEC3 + seed, 0.1, hidden)
+    lay = N.QwenDecoderLayer(lins["q"], lins["k"], lins["v"], lins["o"],
+                             Q.QwenMlp(lins["gate"], lins["up"], lins["down"]),
+                             torch.from_numpy(g_in).to(device), torch.from_numpy(g_post).to(device), EPS)
+    tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+    x, xt = acts(oracle, rows, hidden, 0xDEC4 + seed, dt, device)
+    refs = oracle.decoder_attn_in_ref_f64(x, g_in, EPS, w["q"], w["k"], w["v"])
+    n = np.abs(oracle.rms_norm_f64(x, g_in, EPS))
+    for name, got, ref in zip("qkv", lay.project(xt), refs):
+        assert_close(got.float().cpu().numpy(), ref, n @ np.abs(w[name]), tol, f"sweep attn_in {name}")
+    ctx, ct = acts(oracle, rows, q_out, 0xDEC5 + seed, dt, device)
+    y = lay.attn_out_mlp(xt, ct)
+    _, ref = oracle.decoder_attn_out_mlp_ref_f64(x, ctx, g_post, EPS, w["o"], w["gate"], w["up"], w["down"])
+    assert_close(y.float().cpu().numpy(), ref, out_mlp_bound(oracle, x, ctx, w, g_post), tol, "sweep attn_out_mlp")
