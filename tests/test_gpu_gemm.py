@@ -135,6 +135,24 @@ def test_adapter_term_alone_over_a_zero_weight(device, oracle, r, work, striped)
     assert nw <= TOL_BF16 and lit <= TOL_BF16
 
 
+@pytest.mark.parametrize("K", [64, 128, 192, 320])
+def test_rank16_adapter_expand_at_one_and_two_k_tiles_per_workgroup(device, oracle, K):
+    """Rank 16 stages the factors through LDS in the expand (96 rows take
+    the expanded path); d_in of 1, 2, 3 and 5 64-row tiles give workgroups
+    of one, two, one and one tile (four tiles: the tests at d_in 1024),
+    each against the adapter term alone."""
+    M, N, r = 96, 384, 16
+    lin = zero_linear(K, N, device, True)
+    x, xt = acts(oracle, M, K, 0x79 + K, torch.bfloat16, device)
+    a, b, ad = lora_parts(oracle, K, N, r, 0x7A + K, device, scaling=1.0, sigma=0.05)
+    ref = oracle.lora_ref_f64(x, a, b, 1.0)
+    y = Q.QloraLinear(lin, ad).forward(xt, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+    bound = (np.abs(x) @ np.abs(a)) @ np.abs(b)
+    nw = float(np.max(np.abs(y - ref) / bound))
+    print(f"rank-16 expand K={K}: normwise {nw:.3e}", flush=True)
+    assert nw <= TOL_BF16
+
+
 def test_misaligned_activations_take_the_generic_path(device, oracle):
     # X not 16-byte aligned: the generic dequantize + f32 matmul serves it,
     # with the same result to the bf16 tolerance.
