@@ -246,3 +246,27 @@ def test_decoder_stages_sweep(device, oracle, seed):
     y = lay.attn_out_mlp(xt, ct)
     _, ref = oracle.decoder_attn_out_mlp_ref_f64(x, ctx, g_post, EPS, w["o"], w["gate"], w["up"], w["down"])
     assert_close(y.float().cpu().numpy(), ref, out_mlp_bound(oracle, x, ctx, w, g_post), tol, "sweep attn_out_mlp")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_embedding_sweep(device, oracle, seed):
+    """Nf4Embedding::forward (src/qwennet.rs:244-291) over drawn table shapes,
+    scale kinds, id types and counts: every gathered row bit for bit the
+    oracle's dequantized row (f32), and its RNE rounding (bf16)."""
+    from unifur_amd import qwennet as QN
+    from test_gpu_embedding import bf16_rne, table
+    r = np.random.default_rng(0xE3B0 + seed)
+    n_emb, d = int(r.integers(1, 5000)), int(r.choice([1, 3, 8, 64, 100, 257, 896, 1000]))
+    dq, ids_dtype = bool(r.integers(2)), [torch.int32, torch.int64][int(r.integers(2))]
+    count = int(r.integers(1, 3000))
+    print(f"sweep embedding seed {seed}: table {n_emb} x {d} dq {dq} ids {count} {ids_dtype}", flush=True)
+    v, deq = table(oracle, n_emb, d, 0xE3B1 + seed, dq=dq)
+    p = Q.PackedNf4Tensor.quantize(torch.from_numpy(v).to(device))
+    if dq:
+        p = p.with_double_quantization()
+    emb = QN.Nf4Embedding(p, n_emb, d)
+    ids = r.integers(0, n_emb, size=count)
+    got = emb.forward(torch.from_numpy(ids).to(ids_dtype).to(device))
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), deq[ids].view(np.uint32))
+    gb = emb.forward(torch.from_numpy(ids).to(ids_dtype).to(device), dtype=torch.bfloat16)
+    assert np.array_equal(gb.cpu().view(torch.int16).numpy().view(np.uint16), bf16_rne(deq[ids]))

@@ -182,3 +182,41 @@ def test_noalloc_refuses_what_does_not_fit(device, oracle):
     # an empty batch does nothing
     assert lib.unifur_nf4_linear_forward_noalloc(None, L.F32, 0, ctypes.byref(w), None, None, None, L.F32,
                                                  None) == L.OK
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_noalloc_sweep(device, oracle, seed):
+    """Drawn shapes, types, ranks and layouts, two calls in a row (the second
+    smaller) on the shared scratch, each within its path's bar of the
+    float64 product (1e-5 for f32 activations and output, 1e-2 otherwise)."""
+    from test_gpu_linear import TOL_F32
+    r = np.random.default_rng(0xA110 + seed)
+    k = int(r.choice([64, 192, 512, 896, 1000, 2048]))
+    n = int(r.choice([64, 128, 384, 896, 1024, 2048]))
+    m1 = int(r.choice([1, 3, 4, 16, 33, 64, 65, 129, 300, 513]))
+    m2 = max(1, int(m1 * r.uniform(0.2, 0.9)))
+    xt = torch.bfloat16 if r.integers(2) else torch.float32
+    yt = torch.bfloat16 if r.integers(2) else torch.float32
+    rank = int(r.choice([0, 0, 1, 8, 16, 40]))
+    striped = None if r.integers(2) else False
+    print(f"noalloc sweep seed {seed}: rows {m1} then {m2}, {k} -> {n}, x {xt} y {yt} rank {rank} "
+          f"striped {striped}", flush=True)
+    lin, wdeq = make_linear(oracle, k, n, 0xA111 + seed, device, dq=bool(r.integers(2)), striped=striped)
+    lora, a, b, s = None, None, None, 0.0
+    if rank:
+        s = 16.0 / rank
+        a, b, ad = lora_parts(oracle, k, n, rank, 0xA112 + seed, device, scaling=s)
+        lora = ad.struct()
+    tol = TOL_F32 if (xt == torch.float32 and yt == torch.float32) else TOL_BF16
+    for m, xs in ((m1, 0xA113 + seed), (m2, 0xA114 + seed)):
+        x, xd = acts(oracle, m, k, xs, xt, device)
+        got = noalloc(lin, xd, lora, yt).float().cpu().numpy().astype(np.float64)
+        ref = oracle.linear_ref_f64(x, wdeq)
+        bound = np.abs(x.astype(np.float64)) @ np.abs(wdeq.astype(np.float64))
+        if rank:
+            ref = ref + oracle.lora_ref_f64(x, a, b, s)
+            bound = bound + (np.abs(x.astype(np.float64)) @ np.abs(a)) @ np.abs(b) * s
+        nw = float(np.max(np.abs(got - ref) / np.maximum(bound, 1e-30)))
+        lit = float(np.max(np.abs(got - ref)) / max(float(np.max(np.abs(ref))), 1e-30))
+        print(f"  rows {m}: normwise {nw:.2e} literal {lit:.2e} (tol {tol})", flush=True)
+        assert nw <= tol and lit <= tol
