@@ -251,8 +251,11 @@ uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t
  * scratch -- and multiply with a BLAS GEMM; given a workspace smaller than
  * unifur_nf4_linear_workspace_size but at least this size, they take the
  * fused MFMA kernel instead, which dequantizes W tiles on chip and needs no
- * weight-sized scratch.  Has no counterpart in the reference (which
- * allocates freely); it is for callers with bounded device memory. */
+ * weight-sized scratch.  A batch of more than 2 GiB of activations is past
+ * the fused kernel's reach and takes the generic path (the weight
+ * dequantized to f32 in the workspace) when given less than the default
+ * size.  Has no counterpart in the reference (which allocates freely); it
+ * is for callers with bounded device memory. */
 uint64_t unifur_nf4_linear_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
                                               uint32_t lora_rank);
 

@@ -433,3 +433,41 @@ def test_fused_swiglu_pair_few_k_steps(device, oracle, hidden):
                  L.lib().unifur_nf4_swiglu_min_workspace_size(T, hidden, inter, L.BF16)):
         y, _ = swiglu_call(g, u, d, xt, T, hidden, need, device)
         check(y, ref, h, wd, TOL_BF16, f"pair hidden={hidden} workspace {need}")
+
+
+def test_prefill_past_two_gib_of_activations(device, oracle):
+    """262,200 bf16 rows of 4096 (2.15 GB of activations): past the fused
+    kernel's 2^31-byte reach of X offsets.  The default workspace keeps the
+    expanded weight and the BLAS GEMM (64-bit offsets), the least workspace
+    takes the generic path; for the linear with an adapter and for the SwiGLU
+    block, rows sampled at the start, the middle, the 2^31-byte boundary and
+    the end against the float64 oracle within the bf16 bar."""
+    M, K, N, r = 262_200, 4096, 256, 8
+    assert (M + 256) * K * 2 >= 1 << 31
+    g = torch.Generator(device=device).manual_seed(0x2617)
+    xt = torch.randn(M, K, generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
+    idx = np.array([0, 1, 7, M // 2, (1 << 31) // (2 * K) - 1, (1 << 31) // (2 * K), M - 2, M - 1])
+    xs = xt[torch.from_numpy(idx).to(device)].float().cpu().numpy().astype(np.float64)
+    lin, wdeq = make_linear(oracle, K, N, 0x2618, device, striped=True)
+    a, b, ad = lora_parts(oracle, K, N, r, 0x2619, device, scaling=2.0)
+    ref = oracle.linear_ref_f64(xs, wdeq) + oracle.lora_ref_f64(xs, a, b, 2.0)
+    lib = L.lib()
+    w, lo = lin.weight_struct(), ad.struct()
+    for size in (lib.unifur_nf4_linear_workspace_size, lib.unifur_nf4_linear_min_workspace_size):
+        need = size(M, K, N, L.BF16, r)
+        print(f"{M} rows, workspace {need} B", flush=True)
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        y = torch.empty(M, N, device=device)
+        L.check(lib.unifur_nf4_linear_forward(xt.data_ptr(), L.BF16, M, ctypes.byref(w), None, ctypes.byref(lo),
+                                              y.data_ptr(), L.F32, ws.data_ptr(), need,
+                                              torch.cuda.current_stream().cuda_stream))
+        check(y[torch.from_numpy(idx).to(device)], ref, xs, wdeq, TOL_BF16, f"{M} rows, workspace {need}")
+        del ws, y
+    # the SwiGLU block over the same rows (gate/up 4096 -> 256, down 256 -> 4096)
+    gl, wg = make_linear(oracle, K, N, 0x261A, device, striped=True)
+    ul, wu = make_linear(oracle, K, N, 0x261B, device, striped=True)
+    dl, wd = make_linear(oracle, N, K, 0x261C, device, striped=True)
+    ref = oracle.swiglu_ref_f64(xs, wg, wu, wd)
+    h = oracle.silu_f64(xs @ wg) * (xs @ wu)
+    y = Q.QwenMlp(gl, ul, dl).forward(xt, out_dtype=torch.float32)
+    check(y[torch.from_numpy(idx).to(device)], ref, h, wd, TOL_BF16, f"swiglu {M} rows")

@@ -224,8 +224,14 @@ LinearLayout plan_linear(uint64_t rows, uint64_t d_in, uint64_t d_out, uint32_t 
   Carver c;
   const bool small = rows <= (uint64_t)kGemvMaxRows;
   const bool layout_ok = striped || gemv_layout_ok(d_in, d_out, packed);
-  const bool mfma = !small && x_dtype == UNIFUR_NF4_BF16 && layout_ok && rows <= 0x7fffffffu &&
-                    gemm_supported((int)rows, (int)d_in, (int)d_out, x);
+  // bf16 batches past the GEMVs and the skinny kernel: the fused MFMA kernel
+  // (X offsets under 2^31 bytes), or the expanded weight and the BLAS GEMM,
+  // which address X with 64-bit offsets and so also take a batch past the
+  // fused kernel's reach (more than 2 GiB of activations)
+  const bool mfma_rows = !small && x_dtype == UNIFUR_NF4_BF16 && layout_ok && rows <= 0x7fffffffu;
+  const bool mfma = mfma_rows && (gemm_supported((int)rows, (int)d_in, (int)d_out, x) ||
+                                  (expand && aligned_to(x, 16) &&
+                                   expand_supported((int)d_in, (int)d_out, (int)lora_rank)));
   // f32 activations: skinny launches of at most kSkinnyMaxRowsF32 rows each
   const bool xf32 = x_dtype == UNIFUR_NF4_F32;
   const uint64_t sk_rows = xf32 ? std::min<uint64_t>(rows, kSkinnyMaxRowsF32) : rows;
@@ -355,13 +361,19 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   if (L.path == LinearPath::kMfma && L.expand &&
       ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
     // a workspace too small for the expanded weight (or an output the BLAS
-    // kernels cannot take with 16-byte accesses): the fused kernel
+    // kernels cannot take with 16-byte accesses): the fused kernel, or past
+    // its reach the generic path
     LinearLayout lean =
         plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false);
     if (workspace && workspace_bytes < lean.total)  // without the split-K partials
       lean = plan_linear(rows, w->d_in, w->d_out, rank, w->packed, x_dtype, x, is_striped(w), w->scales.kind, false,
                          false);
-    if (!workspace || workspace_bytes >= lean.total) L = lean;
+    if (!workspace || workspace_bytes >= lean.total)
+      L = lean;
+    else if (!aligned_to(y, 16))
+      return fail(UNIFUR_NF4_ERR_WORKSPACE, "linear: an output that is not 16-byte aligned needs " +
+                                                std::to_string(lean.total) + " bytes of workspace here, got " +
+                                                std::to_string(workspace_bytes));
   }
   if (L.path == LinearPath::kMfma && !L.expand && (L.splits > 1 || L.tail > 1) &&
       ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16) || !aligned_to(bias, 16))) {
@@ -506,9 +518,16 @@ MlpLayout plan_mlp(uint64_t rows, uint64_t hidden, uint64_t inter, const unifur_
   const bool same_kind = g->scales.kind == u->scales.kind;
   const bool small = rows <= (uint64_t)kGemvMaxRows;
   const bool layouts_ok = all_striped || row_major_ok;
-  const bool mfma = !small && x_dtype == UNIFUR_NF4_BF16 && layouts_ok && rows <= 0x7fffffffu &&
-                    gemm_supported((int)rows, (int)hidden, (int)inter, x) &&
-                    gemm_supported((int)rows, (int)inter, (int)hidden, reinterpret_cast<const void*>(uintptr_t{256}));
+  // as for a single linear: the fused kernels within their X offsets' reach,
+  // the expanded weights and BLAS GEMMs (64-bit offsets) past it
+  const bool mfma_rows = !small && x_dtype == UNIFUR_NF4_BF16 && layouts_ok && rows <= 0x7fffffffu;
+  const bool fused_ok =
+      gemm_supported((int)rows, (int)hidden, (int)inter, x) &&
+      gemm_supported((int)rows, (int)inter, (int)hidden, reinterpret_cast<const void*>(uintptr_t{256}));
+  const bool mfma = mfma_rows && (fused_ok || (expand && rows > (uint64_t)kFusedMlpMaxRows && aligned_to(x, 16) &&
+                                               expand_supported((int)hidden, (int)inter, 0) &&
+                                               expand_supported((int)inter, (int)hidden, 0) &&
+                                               2 * inter <= 0x7fffffffu));
   const int gi[2] = {(int)inter, (int)inter};
   const int hd = (int)hidden;
   // the skinny kernel for up to 64 bf16 (32 f32) rows; h lives 256-byte
@@ -624,7 +643,12 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
     MlpLayout lean = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x, false);
     if (workspace && workspace_bytes < lean.total)  // without the split-K partials
       lean = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x, false, false);
-    if (workspace_bytes >= lean.total || !workspace) L = lean;
+    if (workspace_bytes >= lean.total || !workspace)
+      L = lean;
+    else if (!aligned_to(y, 16))
+      return fail(UNIFUR_NF4_ERR_WORKSPACE, "swiglu: an output that is not 16-byte aligned needs " +
+                                                std::to_string(lean.total) + " bytes of workspace here, got " +
+                                                std::to_string(workspace_bytes));
   }
   if (L.path == MlpPath::kMfma && !L.expand && L.gemm_partials &&
       ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16)))
