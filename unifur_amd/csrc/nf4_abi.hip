@@ -1017,7 +1017,9 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
   if (want_dx && rows > 0) {
     // dX = dY (W + scaling A B)^T = dY W^T + ((dY scaling) B^T) A^T
     if (L.blas) {
-      uint16_t* wt = at<uint16_t>(ws, L.wt);
+      // E = bf16(W + scaling A B) in W's own [d_in][d_out] orientation, so
+      // that dX = dY E^T is the forward's TN product
+      uint16_t* e_rows = at<uint16_t>(ws, L.wt);
       const Branch br = mfma_grads ? branch_for(stream) : Branch{};
       bool forked = false;
       const auto fork = [&]() -> hipError_t {
@@ -1029,16 +1031,16 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
         const hipError_t j = hipEventRecord(br.join, br.side);  // recorded even when the launch failed
         return e != hipSuccess ? e : j;
       };
-      hipError_t e = launch_expand_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w),
-                                        lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
-                                        lora ? lora->scaling : 0.0f, wt, stream);
+      hipError_t e = launch_expand_rows_bf16(w->packed, to_scales(w->scales), k, n, is_striped(w),
+                                             lora ? lora->a : nullptr, lora ? lora->b : nullptr, (int)rank,
+                                             lora ? lora->scaling : 0.0f, e_rows, stream);
       // the gradients beside the GEMM, not the memory-bound expand; on a
       // shape's first call the GEMM's kernel is chosen by timing candidates,
       // so the gradients wait and run after it instead of contending
-      if (e == hipSuccess && br.side && blas_gemm_dyw_tuned(m, n, k, dx_dtype == UNIFUR_NF4_BF16)) e = fork();
+      if (e == hipSuccess && br.side && blas_gemm_xwt_tuned(m, k, n, dx_dtype == UNIFUR_NF4_BF16)) e = fork();
       if (e == hipSuccess)
-        e = blas_gemm_dyw(static_cast<const uint16_t*>(dy), wt, m, n, k, dx, dx_dtype == UNIFUR_NF4_BF16,
-                          at<void>(ws, L.blas_ws), kBlasWorkspace, stream);
+        e = blas_gemm_xwt(static_cast<const uint16_t*>(dy), e_rows, nullptr, m, k, n, dx,
+                          dx_dtype == UNIFUR_NF4_BF16, at<void>(ws, L.blas_ws), kBlasWorkspace, stream);
       if (forked) {  // every exit after a fork joins it first
         const hipError_t jn = hipStreamWaitEvent(stream, br.join, 0);
         if (e == hipSuccess) e = jn;

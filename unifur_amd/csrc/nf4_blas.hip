@@ -1,19 +1,22 @@
 // nf4_blas.hip -- the plain bf16 GEMMs of the prefill and backward paths,
 // through hipBLASLt.
 //
-// Row-major products in hipBLASLt's column-major terms (a row-major [R][C]
-// array is the column-major C x R matrix with leading dimension C):
-//   forward   Y[M][N] = X[M][K] Wt[N][K]^T (+ bias): D (N x M, ld N) =
-//             op_T(Wt as K x N, ld K) * (X as K x M, ld K) -- the "TN" form;
-//   backward  dX[M][K] = dY[M][N] Wt[N][K]: D (K x M, ld K) =
-//             (Wt as K x N, ld K) * (dY as N x M, ld N) -- the "NN" form.
+// One row-major product in hipBLASLt's column-major terms (a row-major
+// [R][C] array is the column-major C x R matrix with leading dimension C):
+//   Y[M][N] = X[M][K] Wt[N][K]^T (+ bias): D (N x M, ld N) =
+//             op_T(Wt as K x N, ld K) * (X as K x M, ld K) -- the "TN" form.
+// The forward takes it with Wt the weight expanded transposed; the
+// backward's dX[M][K] = dY[M][N] E[K][N]^T takes it with E the weight
+// expanded in its own [K][N] orientation (as an "NN" product of dY and the
+// transposed expansion the same shape ran 62.5 us against 53-54 us for the
+// TN kernels, 2048 x 4096 x 4096, every candidate of both forms timed).
 // bf16 operands, f32 accumulation (HIPBLAS_COMPUTE_32F), alpha 1, beta 0,
 // the bias added by the library's epilogue.
 //
 // The library's heuristic ranks candidates without running them and its
 // first choice is often not the fastest on this part, so the first call of a
-// shape on a device times every candidate it returns (one warm-up and three
-// timed launches each, on the caller's stream) and keeps the fastest.
+// shape on a device times the candidates it returns (on the caller's
+// stream) and keeps the fastest.
 #include "nf4_expand.hpp"
 
 #include <hipblaslt/hipblaslt.h>
@@ -28,9 +31,9 @@ namespace {
 constexpr int kMaxDevices = 64;
 // The first call of a shape times this many heuristic candidates, each over
 // kTimedRuns launches after one warm-up, and keeps the fastest.  Eight
-// candidates timed over three runs left the backward's dY . W^T product
-// (2048 x 4096 x 4096) at 111 us; thirty-two over twelve find a 105 us
-// kernel.  The search costs about 25 ms once per shape.
+// candidates timed over three runs left the backward's dX product
+// (2048 x 4096 x 4096, then an NN product) at 111 us; thirty-two over twelve
+// found a 105 us kernel.  The search costs about 25 ms once per shape.
 constexpr int kCandidates = 32;
 constexpr int kTimedRuns = 12;
 
@@ -228,19 +231,13 @@ hipError_t blas_gemm_xwt_ld(const uint16_t* x, const uint16_t* wt, const float* 
   return gemm_cm(sh, wt, x, bias, y, y_bf16, ws, ws_bytes, stream);
 }
 
-bool blas_gemm_dyw_tuned(int M, int N, int K, bool dx_bf16) {
+bool blas_gemm_xwt_tuned(int M, int N, int K, bool y_bf16) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return false;
-  const Shape sh{false, false, K, M, N, K, N, K};
+  const Shape sh{true, false, N, M, K, K, K, N};
   State& st = state();
   std::lock_guard<std::mutex> lock(st.mu);
-  return st.tuned.count(Key{dev, sh, dx_bf16, false}) != 0;
-}
-
-hipError_t blas_gemm_dyw(const uint16_t* dy, const uint16_t* wt, int M, int N, int K, void* dx, bool dx_bf16,
-                         void* ws, size_t ws_bytes, hipStream_t stream) {
-  const Shape sh{false, false, K, M, N, K, N, K};
-  return gemm_cm(sh, wt, dy, nullptr, dx, dx_bf16, ws, ws_bytes, stream);
+  return st.tuned.count(Key{dev, sh, y_bf16, false}) != 0;
 }
 
 }  // namespace unifur

@@ -31,6 +31,8 @@ constexpr int kTile = 64;
 constexpr int kLdsLut = 0;                        // NF4_LEVELS, 16 x f32 per wave
 constexpr int kLdsBytes = 256;                        // LDS bytes: the four waves' LUTs
 constexpr int kMaxRank = 64;
+constexpr int kRowPitch = 144;                    // LDS bytes per row of a ROWS tile (64 bf16 + 16: two-way banks)
+constexpr int kRowTileBytes = 64 * kRowPitch;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct ExpandArgs {
@@ -133,7 +135,15 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 // there: the per-wave strided loads fetched each factor twice per workgroup
 // and more bytes of factors than the workgroup writes (config 3: 15.8 ->
 // 13.6 us per expand).
-template <bool DQ, bool STRIPED, int KT, int NFR, bool STAGE>
+//
+// ROWS writes the same values row-major instead, E[k][n] ([K][N], the
+// weight's own orientation: the backward's dX = dY E^T then runs as the same
+// TN product as the forward), each 64 x 64 tile passed through LDS so that
+// the stores are whole 128-byte row segments (8-byte stores straight from
+// the MFMA layout, 32 rows x 16 bytes per instruction, took the config-3
+// expand from 11.2 to 17.6 us).  With rank 0 (ROWS only) the adapter term
+// is skipped and E is the dequantized weight.
+template <bool DQ, bool STRIPED, int KT, int NFR, bool STAGE, bool ROWS>
 __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
@@ -191,7 +201,9 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
   // lane l carries adapter indices 16 f + 8 (l / 32) .. + 7
   bf16x8_t bfr[NFR];
   bf16x8_t afr[KT][NFR];
-  if constexpr (STAGE) {
+  const bool lora = a.rank > 0;  // uniform: false only for ROWS launches without an adapter
+  if (!lora) {
+  } else if constexpr (STAGE) {
     // bf16 A [64 KT][16] and B^T [64][16] in LDS after the wave LUTs; each
     // lane then reads its fragments as 16-byte rows
     uint32_t* sa = reinterpret_cast<uint32_t*>(smem + kLdsBytes);
@@ -260,7 +272,7 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
     f32x16 acc = {};
 #pragma unroll
     for (int f = 0; f < NFR; ++f) {
-      if (f >= nf) break;
+      if (!lora || f >= nf) break;
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[f], afr[t][f], acc, 0, 0, 0);
     }
     // v[4 q + e]: row k, column cb + 8 q + 4 h + e
@@ -270,8 +282,28 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float w = lut[(cw[t][q] >> (16 * h + 4 * e)) & 15u] * s[t];  // NF4_LEVELS[c] * scale
-        v[4 * q + e] = w + a.scaling * acc[4 * q + e];
+        v[4 * q + e] = lora ? w + a.scaling * acc[4 * q + e] : w;
       }
+    if constexpr (ROWS) {
+      // the 64 x 64 tile through LDS: each wave puts its 32 x 32 block in
+      // (row 32 bi + lr, columns 32 bj + 8 q + 4 h .. + 3, 8 bytes per q),
+      // then each thread stores 16 bytes of rows tid / 8 and tid / 8 + 32,
+      // so that every store instruction writes eight whole 128-byte rows
+      unsigned char* tile = smem + kLdsBytes + (STAGE ? KT * 64 * 32 + 64 * 32 : 0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<u32x2*>(tile + (32 * bi + lr) * kRowPitch + (32 * bj + 8 * q + 4 * h) * 2) =
+            u32x2{pack_bf16x2(v[4 * q], v[4 * q + 1]), pack_bf16x2(v[4 * q + 2], v[4 * q + 3])};
+      __syncthreads();
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int r = tid / 8 + 32 * half, c = 8 * (tid % 8);
+        *reinterpret_cast<u32x4*>(a.wt + (size_t)(k0 + kTile * t + r) * a.N + n0 + c) =
+            *reinterpret_cast<const u32x4*>(tile + r * kRowPitch + c * 2);
+      }
+      __syncthreads();  // the next tile reuses the LDS tile
+      continue;
+    }
     // the even lane keeps columns q = 0, 1 and receives row k + 1 of them;
     // the odd lane keeps q = 2, 3 and receives row k - 1 of them; each
     // (k, k + 1) pair goes straight to Wt (for one j, 16 lanes write 64
@@ -290,28 +322,37 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
   }
 }
 
-template <bool DQ, bool STRIPED, int KT>
+template <bool DQ, bool STRIPED, int KT, bool ROWS>
 hipError_t launch_kt(const ExpandArgs& a, int n_count, hipStream_t stream) {
   const unsigned grid = (unsigned)((long long)(n_count / kTile) * (a.tiles_k / KT));
-  if (a.rank == 0)
+  if (a.rank == 0 && !ROWS)
     expand_kernel<DQ, STRIPED, KT><<<grid, 256, kLdsBytes, stream>>>(a);
   else if (a.rank == 16 && a.stage)
-    expand_lora_kernel<DQ, STRIPED, KT, 1, true><<<grid, 256, kLdsBytes + KT * 64 * 32 + 64 * 32, stream>>>(a);
+    expand_lora_kernel<DQ, STRIPED, KT, 1, true, ROWS>
+        <<<grid, 256, kLdsBytes + KT * 64 * 32 + 64 * 32 + (ROWS ? kRowTileBytes : 0), stream>>>(a);
   else if (a.rp == 16)
-    expand_lora_kernel<DQ, STRIPED, KT, 1, false><<<grid, 256, kLdsBytes, stream>>>(a);
+    expand_lora_kernel<DQ, STRIPED, KT, 1, false, ROWS>
+        <<<grid, 256, kLdsBytes + (ROWS ? kRowTileBytes : 0), stream>>>(a);
   else
-    expand_lora_kernel<DQ, STRIPED, 1, kMaxRank / 16, false><<<grid, 256, kLdsBytes, stream>>>(a);
+    expand_lora_kernel<DQ, STRIPED, 1, kMaxRank / 16, false, ROWS>
+        <<<grid, 256, kLdsBytes + (ROWS ? kRowTileBytes : 0), stream>>>(a);
   return hipGetLastError();
 }
 
-template <bool DQ, bool STRIPED>
+template <bool DQ, bool STRIPED, bool ROWS>
 hipError_t launch_t(const ExpandArgs& a, int n_count, hipStream_t stream) {
   // four (or two) tiles per workgroup where K allows: more loads in flight
   // (with an adapter of rank <= 16, whose fragments then fit the registers)
-  if (a.rank > 0 && a.rp > 16) return launch_kt<DQ, STRIPED, 1>(a, n_count, stream);
-  if (a.tiles_k % 4 == 0) return launch_kt<DQ, STRIPED, 4>(a, n_count, stream);
-  if (a.tiles_k % 2 == 0) return launch_kt<DQ, STRIPED, 2>(a, n_count, stream);
-  return launch_kt<DQ, STRIPED, 1>(a, n_count, stream);
+  if (a.rank > 0 && a.rp > 16) return launch_kt<DQ, STRIPED, 1, ROWS>(a, n_count, stream);
+  if (a.tiles_k % 4 == 0) return launch_kt<DQ, STRIPED, 4, ROWS>(a, n_count, stream);
+  if (a.tiles_k % 2 == 0) return launch_kt<DQ, STRIPED, 2, ROWS>(a, n_count, stream);
+  return launch_kt<DQ, STRIPED, 1, ROWS>(a, n_count, stream);
+}
+
+template <bool ROWS>
+hipError_t launch_layout(const ExpandArgs& a, bool dq, bool striped, int n_count, hipStream_t stream) {
+  if (dq) return striped ? launch_t<true, true, ROWS>(a, n_count, stream) : launch_t<true, false, ROWS>(a, n_count, stream);
+  return striped ? launch_t<false, true, ROWS>(a, n_count, stream) : launch_t<false, false, ROWS>(a, n_count, stream);
 }
 
 }  // namespace
@@ -327,35 +368,51 @@ hipError_t launch_expand_bf16(const uint8_t* packed, const ScalesArg& scales, in
   return launch_expand_cols(packed, scales, K, N, striped, lora_a, lora_b, rank, scaling, 0, N, wt, stream);
 }
 
+namespace {
+
+// The arguments of one expand launch over columns [n_begin, n_end).
+bool expand_args(const uint8_t* packed, const ScalesArg& scales, int K, int N, const float* lora_a,
+                 const float* lora_b, int rank, float scaling, int n_begin, int n_end, uint16_t* out, ExpandArgs* a) {
+  if (!expand_supported(K, N, rank) || (rank > 0 && (!lora_a || !lora_b)) || n_begin < 0 || n_end > N ||
+      n_begin % kTile != 0 || n_end % kTile != 0 || n_begin >= n_end)
+    return false;
+  if ((long long)(K / kTile) * ((n_end - n_begin) / kTile) > 0x7fffffffLL) return false;
+  *a = ExpandArgs{};
+  a->packed = packed;
+  a->scales = scales;
+  a->K = K;
+  a->N = N;
+  a->la = lora_a;
+  a->lb = lora_b;
+  a->la_vec = rank % 8 == 0 && (reinterpret_cast<uintptr_t>(lora_a) & 15u) == 0;
+  a->stage = rank == 16 && (reinterpret_cast<uintptr_t>(lora_a) & 15u) == 0 &&
+             (reinterpret_cast<uintptr_t>(lora_b) & 15u) == 0;
+  a->rank = rank;
+  a->rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
+  a->scaling = scaling;
+  a->wt = out;
+  a->tiles_k = K / kTile;
+  a->n_base = n_begin;
+  return true;
+}
+
+}  // namespace
+
 hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
                               const float* lora_a, const float* lora_b, int rank, float scaling, int n_begin, int n_end,
                               uint16_t* wt, hipStream_t stream) {
-  if (!expand_supported(K, N, rank) || (rank > 0 && (!lora_a || !lora_b)) || n_begin < 0 || n_end > N ||
-      n_begin % kTile != 0 || n_end % kTile != 0 || n_begin >= n_end)
+  ExpandArgs a;
+  if (!expand_args(packed, scales, K, N, lora_a, lora_b, rank, scaling, n_begin, n_end, wt, &a))
     return hipErrorInvalidValue;
-  const int rp = rank <= 16 ? 16 : rank <= 32 ? 32 : 64;
-  ExpandArgs a{};
-  a.packed = packed;
-  a.scales = scales;
-  a.K = K;
-  a.N = N;
-  a.la = lora_a;
-  a.lb = lora_b;
-  a.la_vec = rank % 8 == 0 && (reinterpret_cast<uintptr_t>(lora_a) & 15u) == 0;
-  a.stage = rank == 16 && (reinterpret_cast<uintptr_t>(lora_a) & 15u) == 0 &&
-            (reinterpret_cast<uintptr_t>(lora_b) & 15u) == 0;
-  a.rank = rank;
-  a.rp = rp;
-  a.scaling = scaling;
-  a.wt = wt;
-  a.tiles_k = K / kTile;
-  a.n_base = n_begin;
-  const int nc = n_end - n_begin;
-  const long long tiles = (long long)(K / kTile) * (nc / kTile);
-  if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-  const bool dq = scales.kind == kScalesDQ;
-  if (dq) return striped ? launch_t<true, true>(a, nc, stream) : launch_t<true, false>(a, nc, stream);
-  return striped ? launch_t<false, true>(a, nc, stream) : launch_t<false, false>(a, nc, stream);
+  return launch_layout<false>(a, scales.kind == kScalesDQ, striped, n_end - n_begin, stream);
+}
+
+hipError_t launch_expand_rows_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
+                                   const float* lora_a, const float* lora_b, int rank, float scaling, uint16_t* e,
+                                   hipStream_t stream) {
+  ExpandArgs a;
+  if (!expand_args(packed, scales, K, N, lora_a, lora_b, rank, scaling, 0, N, e, &a)) return hipErrorInvalidValue;
+  return launch_layout<true>(a, scales.kind == kScalesDQ, striped, N, stream);
 }
 
 }  // namespace unifur

@@ -20,6 +20,13 @@ hipError_t launch_expand_cols(const uint8_t* packed, const ScalesArg& scales, in
                               const float* lora_a, const float* lora_b, int rank, float scaling, int n_begin, int n_end,
                               uint16_t* wt, hipStream_t stream);
 
+// E[K][N] bf16 row-major (the weight's own orientation): the same values as
+// launch_expand_bf16 writes transposed, rank 0 included.  The backward's
+// dX = dY E^T then runs as blas_gemm_xwt, the forward's TN product.
+hipError_t launch_expand_rows_bf16(const uint8_t* packed, const ScalesArg& scales, int K, int N, bool striped,
+                                   const float* lora_a, const float* lora_b, int rank, float scaling, uint16_t* e,
+                                   hipStream_t stream);
+
 // Scratch the BLAS GEMM may use (its kernels' split-K partials and the like).
 constexpr size_t kBlasWorkspace = 32u << 20;
 
@@ -34,12 +41,9 @@ hipError_t blas_gemm_xwt(const uint16_t* x, const uint16_t* wt, const float* bia
 hipError_t blas_gemm_xwt_ld(const uint16_t* x, const uint16_t* wt, const float* bias, int M, int N, int K, void* y,
                             int ldy, bool y_bf16, void* ws, size_t ws_bytes, hipStream_t stream);
 
-// dX[M][K] = dY[M][N] Wt[N][K] (the backward of the product above with
-// respect to X), bf16 operands, dX f32 or bf16; same kernel choice rule.
-hipError_t blas_gemm_dyw(const uint16_t* dy, const uint16_t* wt, int M, int N, int K, void* dx, bool dx_bf16,
-                         void* ws, size_t ws_bytes, hipStream_t stream);
-// Whether this device has chosen its blas_gemm_dyw kernel for the shape (a
-// call before that times the candidates, which wants the GPU to itself).
-bool blas_gemm_dyw_tuned(int M, int N, int K, bool dx_bf16);
+// Whether this device has chosen its blas_gemm_xwt kernel for the shape
+// (without bias; a call before that times the candidates, which wants the
+// GPU to itself).
+bool blas_gemm_xwt_tuned(int M, int N, int K, bool y_bf16);
 
 }  // namespace unifur
