@@ -104,3 +104,34 @@ def test_double_quantized_infinite_block_poisons_every_output(device, oracle, ro
     assert np.isnan(wdeq).all()
     x, xt = acts(oracle, rows, d_in, 0x1AF9 + rows, xdt, device)
     assert np.isnan(run_linear(lin, xt, rows, d_in, d_out, xdt, work, device)).all()
+
+
+@pytest.mark.parametrize("rows,xdt,work", PATHS)
+def test_non_finite_activations_propagate(device, oracle, rows, xdt, work):
+    """x with an infinity and a NaN in two of its rows and finite weights
+    (double-quantized): inf * w is +-inf, inf * 0 (a weight of level 0) NaN,
+    and a NaN reaches its row's every output -- the pattern the float64
+    product gives, whatever the order of the sum; the untouched rows keep
+    their bar."""
+    from test_gpu_linear import make_linear
+    d_in, d_out = 256, 192
+    print(f"non-finite x: rows {rows} {xdt} {work}", flush=True)
+    lin, wdeq = make_linear(oracle, d_in, d_out, 0x1B00 + rows, device, striped=True)
+    x, _ = acts(oracle, rows, d_in, 0x1B01 + rows, xdt, device)
+    x = x.copy()
+    x[0, 5] = np.inf
+    x[rows - 1, 77] = np.nan
+    if rows > 2:
+        x[1, 200] = -np.inf
+    xt = torch.from_numpy(x).to(device).to(xdt)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = x.astype(np.float64) @ wdeq.astype(np.float64)
+        bound = np.abs(x.astype(np.float64)) @ np.abs(wdeq.astype(np.float64))
+    got = run_linear(lin, xt, rows, d_in, d_out, xdt, work, device)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN outputs differ"
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)) and np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert not fin.all()
+    if fin.any():
+        tol = TOL_F32 if xdt == torch.float32 else TOL_BF16
+        assert float(np.max(np.abs(got[fin] - ref[fin]) / bound[fin])) <= tol
