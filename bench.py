@@ -278,6 +278,29 @@ def bench_gemv(torch, Q, L, args) -> dict:
     gb = capture(torch, launch_b, copies)
     out["kernel_cold_ms_bf16x"] = replay_event_ms(torch, gb, copies) if gb is not None else event_ms(
         torch, launch_b, 4 * copies)
+    del gb
+    # plain f32 block scales (PackedScales::F32, the variant without double
+    # quantization): 25,422,848 bytes per launch, rotated cold likewise
+    gp = Rng(torch, 0x4E463459)
+    base_p = rand_weights(torch, Q, d_in, d_out, gp, dq=False)
+    nbytes_p = gemv_bytes(d_in, d_out, dq=False)
+    copies_p = max(2, -(-(2 * MALL_BYTES) // nbytes_p))
+    layers_p = [base_p] + [Q.Nf4Linear.from_packed(base_p.packed(), d_in, d_out) for _ in range(copies_p - 1)]
+    structs_p = [lay.weight_struct() for lay in layers_p]
+
+    def launch_p(i: int) -> None:
+        L.check(lib.unifur_nf4_linear_forward(x.data_ptr(), L.F32, 1, ctypes.byref(structs_p[i % copies_p]), None,
+                                              None, y.data_ptr(), L.F32, None, 0,
+                                              torch.cuda.current_stream().cuda_stream))
+    launch_p(0)
+    ref_p = x @ layers_p[0].dequantized_weight()
+    torch.cuda.synchronize()
+    if not float((y - ref_p).abs().max() / ref_p.abs().max()) < 1e-4:
+        raise RuntimeError("plain-scale GEMV sanity check failed")
+    gpl = capture(torch, launch_p, copies_p)
+    plain_ms = replay_event_ms(torch, gpl, copies_p) if gpl is not None else event_ms(torch, launch_p, 4 * copies_p)
+    out["plain_scales"] = {"kernel_ms": plain_ms, "bytes": nbytes_p, "copies": copies_p}
+    del gpl, layers_p, structs_p
     return out
 
 
@@ -435,8 +458,43 @@ def bench_codec(torch, Q, L) -> dict:
     q_ms = replay_event_ms(torch, gq, copies) if gq is not None else event_ms(torch, quant, 4 * copies)
     d_ms = replay_event_ms(torch, gd, copies) if gd is not None else event_ms(torch, deq, 4 * copies)
     codec_bytes = 4 * n + n // 2 + 4 * (n // 64)  # f32 values + packed codes + f32 absmax
-    return {"quantize_ms": q_ms, "dequant_ms": d_ms, "bytes": codec_bytes,
-            "quantize_gbs": codec_bytes / q_ms / 1e6, "dequant_gbs": codec_bytes / d_ms / 1e6}
+    out = {"quantize_ms": q_ms, "dequant_ms": d_ms, "bytes": codec_bytes,
+           "quantize_gbs": codec_bytes / q_ms / 1e6, "dequant_gbs": codec_bytes / d_ms / 1e6}
+    del gq, gd
+    # the variants: dequantize to bf16 (codes + f32 absmax in, 2 B out per
+    # value: 42,991,616 B), double quantization of the block scales, and the
+    # dequantize from double-quantized scales (u8 codes + scale of scales)
+    outs_b = [torch.empty(n, dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+
+    def deq_b(i: int) -> None:
+        p = packs[i % copies]
+        L.check(lib.unifur_nf4_dequantize(p.codes.data_ptr(), ctypes.byref(structs[i % copies]), n,
+                                          outs_b[i % copies].data_ptr(), L.BF16,
+                                          torch.cuda.current_stream().cuda_stream))
+    nb = n // 64
+    qs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(copies)]
+    sos = [torch.empty(1, device=dev) for _ in range(copies)]
+
+    def dq(i: int) -> None:
+        L.check(lib.unifur_nf4_double_quantize(packs[i % copies].absmax.data_ptr(), nb, qs[i % copies].data_ptr(),
+                                               sos[i % copies].data_ptr(), torch.cuda.current_stream().cuda_stream))
+    for i in range(copies):
+        dq(i)
+    dq_structs = [L.Scales(L.SCALES_DOUBLE_QUANTIZED, None, qs[i].data_ptr(), sos[i].data_ptr()) for i in range(copies)]
+
+    def deq_dq(i: int) -> None:
+        p = packs[i % copies]
+        L.check(lib.unifur_nf4_dequantize(p.codes.data_ptr(), ctypes.byref(dq_structs[i % copies]), n,
+                                          outs[i % copies].data_ptr(), L.F32,
+                                          torch.cuda.current_stream().cuda_stream))
+    gdb, gdq, gdd = capture(torch, deq_b, copies), capture(torch, dq, copies), capture(torch, deq_dq, copies)
+    out["dequant_bf16_ms"] = replay_event_ms(torch, gdb, copies) if gdb is not None else event_ms(torch, deq_b, 4 * copies)
+    out["dequant_bf16_bytes"] = n // 2 + 4 * nb + 2 * n
+    out["double_quantize_ms"] = replay_event_ms(torch, gdq, copies) if gdq is not None else event_ms(torch, dq, 4 * copies)
+    out["double_quantize_bytes"] = 4 * nb + nb + 4
+    out["dequant_dq_ms"] = replay_event_ms(torch, gdd, copies) if gdd is not None else event_ms(torch, deq_dq, 4 * copies)
+    out["dequant_dq_bytes"] = n // 2 + nb + 4 + 4 * n
+    return out
 
 
 # --------------------------------------------------------------- config 3 --
@@ -1017,6 +1075,18 @@ def main() -> int:
         "gemv_bf16_activations_cold": {
             "kernel_ms": round(gemv["kernel_cold_ms_bf16x"], 5),
             "gbs": round(gemv_bytes(4096, 11008, True, 2, 4) / gemv["kernel_cold_ms_bf16x"] / 1e6, 1)},
+        "gemv_plain_scales_cold": {
+            "kernel_ms": round(gemv["plain_scales"]["kernel_ms"], 5), "bytes": gemv["plain_scales"]["bytes"],
+            "gbs": round(gemv["plain_scales"]["bytes"] / gemv["plain_scales"]["kernel_ms"] / 1e6, 1),
+            "frac": round(gemv["plain_scales"]["bytes"] / gemv["plain_scales"]["kernel_ms"] / 1e6 / HBM_PEAK_GBS, 4)},
+        "dequantize_bf16_config1": {
+            "kernel_ms": round(codec["dequant_bf16_ms"], 5), "bytes": codec["dequant_bf16_bytes"],
+            "gbs": round(codec["dequant_bf16_bytes"] / codec["dequant_bf16_ms"] / 1e6, 1)},
+        "dequantize_f32_double_quantized_config1": {
+            "kernel_ms": round(codec["dequant_dq_ms"], 5), "bytes": codec["dequant_dq_bytes"],
+            "gbs": round(codec["dequant_dq_bytes"] / codec["dequant_dq_ms"] / 1e6, 1)},
+        "double_quantize_config1": {"kernel_ms": round(codec["double_quantize_ms"], 5),
+                                    "bytes": codec["double_quantize_bytes"]},
         "dequantize_f32_config1": {"kernel_ms": round(codec["dequant_ms"], 5), "gbs": round(codec["dequant_gbs"], 1),
                                    "frac": round(codec["dequant_gbs"] / HBM_PEAK_GBS, 4),
                                    "frac_of_write_dominated_ceiling":

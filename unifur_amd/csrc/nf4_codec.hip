@@ -184,7 +184,14 @@ __global__ void quantize_tail_kernel(const float* __restrict__ values, uint8_t* 
 // Pass 1: max over the f32 absmax values.  All are >= 0 and never NaN (they
 // come out of a NaN-ignoring max from 0), so their bit patterns order like
 // the values and an integer atomic max is exact.  Pass 2 encodes.
-__global__ void dq_max_kernel(const float* __restrict__ absmax, size_t nb, uint32_t* __restrict__ max_bits) {
+// The global max of the block scales: a grid-stride max per thread, the
+// workgroup's max through LDS, then one atomic max per workgroup.  The grid
+// is capped at kDqMaxBlocks: the atomics on the one address serialise (one
+// per wave over a 1024-workgroup grid took config 1's 262,144 scales 48 us).
+constexpr int kDqMaxBlocks = 64;
+__global__ __launch_bounds__(256) void dq_max_kernel(const float* __restrict__ absmax, size_t nb,
+                                                     uint32_t* __restrict__ max_bits) {
+  __shared__ float wave_max[4];
   float m = 0.0f;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nb; i += (size_t)gridDim.x * blockDim.x)
     m = fmaxf(m, absmax[i]);
@@ -194,7 +201,12 @@ __global__ void dq_max_kernel(const float* __restrict__ absmax, size_t nb, uint3
   m = fmaxf(m, __shfl_xor(m, 8));
   m = fmaxf(m, __shfl_xor(m, 16));
   m = fmaxf(m, __shfl_xor(m, 32));
-  if ((threadIdx.x & 63) == 0) atomicMax(max_bits, __float_as_uint(m));
+  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+    atomicMax(max_bits, __float_as_uint(m));
+  }
 }
 
 __global__ void zero_u32_kernel(uint32_t* p) { *p = 0u; }
@@ -700,7 +712,7 @@ hipError_t launch_double_quantize(const float* absmax, size_t nb, uint8_t* q, fl
   uint32_t* max_bits = reinterpret_cast<uint32_t*>(scale_of_scales);
   zero_u32_kernel<<<1, 1, 0, stream>>>(max_bits);
   if (nb == 0) return hipGetLastError();
-  dq_max_kernel<<<grid_for(nb, 256, 1024), 256, 0, stream>>>(absmax, nb, max_bits);
+  dq_max_kernel<<<grid_for(nb, 256, kDqMaxBlocks), 256, 0, stream>>>(absmax, nb, max_bits);
   dq_encode_kernel<<<grid_for(nb, 256, 4096), 256, 0, stream>>>(absmax, nb, max_bits, q);
   return hipGetLastError();
 }
