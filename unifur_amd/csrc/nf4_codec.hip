@@ -85,7 +85,7 @@ constexpr int kQuantThreads = kQuantWaves * 64;
 // values and the steps are integer maxes (no canonicalisation).
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
-  return __builtin_amdgcn_update_dpp(0u, v, CTRL, 0xF, 0xF, false);
+  return dpp_mov<CTRL>(v);
 }
 __device__ __forceinline__ float max16(float f) {
   uint32_t v = __float_as_uint(f);

@@ -87,6 +87,20 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t a, uint32_t b, uint32_t se
   return __builtin_amdgcn_perm(a, b, sel);
 }
 
+// DPP move with every lane written: CTRL is a pattern whose source lane is
+// always in the wave (quad_perm, row_mirror 0x140, row_half_mirror 0x141,
+// row_newbcast 0x150 + j) and all rows and banks are enabled.  bound_ctrl
+// (a lane with no source lane reads 0 -- there is none here) tells the
+// compiler that no lane keeps the old value, so a move whose result is not
+// folded into its user (v_max_u32_dpp, v_add_f32_dpp) needs no initialising
+// v_mov_b32 of the destination, which the form without it costs per use.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  static_assert(CTRL <= 0xFF || CTRL == 0x140 || CTRL == 0x141 || (CTRL >= 0x150 && CTRL <= 0x15F),
+                "a DPP pattern with out-of-range source lanes");
+  return __builtin_amdgcn_update_dpp(0u, v, CTRL, 0xF, 0xF, true);
+}
+
 // Split-K hand-off between workgroups.  Partial sums are written with
 // agent-scope atomic stores (coherent across the XCDs' L2s) and the writer
 // waits for them to complete before it counts itself in; the last arrival

@@ -314,7 +314,7 @@ __global__ __launch_bounds__(256) void expand_lora_kernel(ExpandArgs a) {
       const float send = odd ? v[j] : v[8 + j];
       const float keep = odd ? v[8 + j] : v[j];
       const float got = __uint_as_float(
-          __builtin_amdgcn_update_dpp(0u, __float_as_uint(send), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+          dpp_mov<0xB1>(__float_as_uint(send)));  // quad_perm [1,0,3,2]
       const int q = (odd ? 2 : 0) + (j >> 2), e = j & 3;
       const int col = 32 * bj + 8 * q + 4 * h + e;
       dst[(size_t)col * (a.K / 2)] = odd ? pack_bf16x2(got, keep) : pack_bf16x2(keep, got);

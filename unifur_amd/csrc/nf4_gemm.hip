@@ -254,7 +254,7 @@ __device__ __forceinline__ void store_b_at(const BStep& B, unsigned char* smem, 
 #define UNIFUR_GEMM_STORE64 2
 #endif
 __device__ __forceinline__ uint32_t swap_lane_pair(uint32_t v) {
-  return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  return dpp_mov<0xB1>(v);  // quad_perm [1,0,3,2]
 }
 
 template <bool DQ, bool STRIPED>
@@ -292,12 +292,12 @@ __device__ __forceinline__ void store_b64(const BStep& B, unsigned char* smem, i
     const uint32_t ks = (2u * e) | ((2u * e + 1u) << 8) | ((4u + 2u * e) << 16) | ((5u + 2u * e) << 24);
     const uint32_t ss = ks ^ 0x02020202u;  // the other half
     const uint32_t k01 = __builtin_amdgcn_perm(w[1], w[0], ks), k23 = __builtin_amdgcn_perm(w[3], w[2], ks);
-    const uint32_t r01 = __builtin_amdgcn_update_dpp(0u, __builtin_amdgcn_perm(w[1], w[0], ss), 0x4E, 0xF, 0xF, false);
-    const uint32_t r23 = __builtin_amdgcn_update_dpp(0u, __builtin_amdgcn_perm(w[3], w[2], ss), 0x4E, 0xF, 0xF, false);
+    const uint32_t r01 = dpp_mov<0x4E>(__builtin_amdgcn_perm(w[1], w[0], ss));
+    const uint32_t r23 = dpp_mov<0x4E>(__builtin_amdgcn_perm(w[3], w[2], ss));
     float so[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      so[q] = __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(sc[q]), 0x4E, 0xF, 0xF, false));
+      so[q] = __uint_as_float(dpp_mov<0x4E>(__float_as_uint(sc[q])));
     // rows 8g + 2p, 8g + 2p + 1 in dword p (low, high u16)
     const uint32_t D[4] = {e ? r01 : k01, e ? r23 : k23, e ? k01 : r01, e ? k23 : r23};
     float s8[8];

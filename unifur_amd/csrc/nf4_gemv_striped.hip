@@ -220,7 +220,7 @@ __device__ __forceinline__ float wave_column_sum(const float (&acc)[16], int lan
     for (int i = 0; i < 2; ++i) {
       const float send = hi ? v[i] : v[i + 2];
       const float keep = hi ? v[i + 2] : v[i];
-      v[i] = keep + as_f(__builtin_amdgcn_update_dpp(0u, as_u(send), 0x140, 0xF, 0xF, false));
+      v[i] = keep + as_f(dpp_mov<0x140>(as_u(send)));
     }
   }
   float col;
@@ -228,11 +228,11 @@ __device__ __forceinline__ float wave_column_sum(const float (&acc)[16], int lan
     const bool hi = (lane & 4) != 0;
     const float send = hi ? v[0] : v[1];
     const float keep = hi ? v[1] : v[0];
-    col = keep + as_f(__builtin_amdgcn_update_dpp(0u, as_u(send), 0x141, 0xF, 0xF, false));
+    col = keep + as_f(dpp_mov<0x141>(as_u(send)));
   }
   // the four lanes of a quad now hold the same column: add them
-  col += as_f(__builtin_amdgcn_update_dpp(0u, as_u(col), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
-  col += as_f(__builtin_amdgcn_update_dpp(0u, as_u(col), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  col += as_f(dpp_mov<0x4E>(as_u(col)));  // quad_perm [2,3,0,1]
+  col += as_f(dpp_mov<0xB1>(as_u(col)));  // quad_perm [1,0,3,2]
   return col;
 }
 
@@ -575,7 +575,7 @@ constexpr int kSkStageOffset = kStripedSmem;  // after the level and DQ LUTs
 // the value of lane 16 (l / 16) + J, in every lane l
 template <int J>
 __device__ __forceinline__ float row_bcast(float v) {
-  return as_f(__builtin_amdgcn_update_dpp(0u, as_u(v), 0x150 + J, 0xF, 0xF, false));
+  return as_f(dpp_mov<0x150 + J>(as_u(v)));
 }
 template <int J>
 __device__ __forceinline__ void row_bcast_all(float v, float (&o)[16]) {
