@@ -1085,18 +1085,23 @@ StripedPlan plan_skinny(int rows, int d_in, const int* d_out, int nweights, bool
   const int g = (pair && tiles > 1) ? 2 : 4;
   int group = 1, splits = 1;
   if (tiles == 1 && chunks >= 64) {
-    // one token tile over a long d_in: two stripes per wave and d_in slabs
-    // up to ~512 four-wave workgroups (measured on the 7B-shaped MLP at 16
+    // one token tile over a long d_in: two stripes per wave and d_in slabs,
+    // the pair in up to ~512 four-wave workgroups, a single weight in up to
+    // ~256 eight-wave ones -- the same rows per wave, one LUT build per CU
+    // and half the slabs to hand off (measured on the 7B-shaped MLP at 16
     // tokens: the gate/up pair 21.4 us against 24.1 us as 172 eight-wave
-    // workgroups of four stripes; the down projection 13.6 us either way)
+    // workgroups of four stripes; the block 34.7 us with down as 256
+    // eight-wave workgroups over two slabs against 35.2-35.3 us as 512
+    // four-wave ones over four)
     group = 2;
-    while ((stripes / group) * splits < 512 && chunks / (splits * 2) >= 32) splits *= 2;
+    const int waves = pair ? 4 : 8;
+    while ((stripes / group) * splits < (pair ? 512 : 256) && chunks / (splits * 2) >= 32) splits *= 2;
     p.group = group;
-    p.waves = 4;
+    p.waves = waves;
     p.splits = splits;
     const int cps = (chunks + splits - 1) / splits;
-    p.rows_per_wave = (cps + 3) / 4 * 64;
-    p.rows_per_split = p.rows_per_wave * 4;
+    p.rows_per_wave = (cps + waves - 1) / waves * 64;
+    p.rows_per_split = p.rows_per_wave * waves;
     p.stripes = stripes;
     return p;
   }
