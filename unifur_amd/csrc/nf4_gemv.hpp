@@ -66,6 +66,9 @@ struct StripedArgs {
   int rows_per_wave;
   int rows_per_split;  // skinny kernel: d_in rows per workgroup along gridDim.y
   int nweights;
+  // XCD-aware order: gridDim.x / 8 when that divides evenly, else 0 (set by
+  // the launcher, so that the kernels need not read the grid size first)
+  int xcd_run;
   GemvWeight w[kMaxGemvWeights];
   int stripe_begin[kMaxGemvWeights + 1];  // prefix sums of stripes per weight
   // QwenRmsNorm folded into the launch, x -> x * rsqrt(mean(x^2) +

@@ -57,7 +57,6 @@ constexpr int kStripedSmem = kDqLutOffset + 2 * 256 * 4;
 constexpr int kGemvRedOffset = kStripedSmem;
 constexpr int kGemvSmem = kGemvRedOffset + (512 + 64) * 4;
 
-typedef const __attribute__((address_space(4))) float const_f32;
 typedef __attribute__((address_space(3))) const f32x2 lds_f32x2;
 
 __device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
@@ -74,6 +73,26 @@ __device__ __forceinline__ float silu_f32(float z) { return z * (1.0f / (1.0f + 
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Workgroup index in XCD-aware order: blockIdx.x % 8 is the XCD it runs on,
+// and with run = gridDim.x / 8 (0 when 8 does not divide the grid) XCD x
+// takes the run of indices from x * run.  A select, not a branch, so that
+// the argument loads after it are not held behind the load of run.
+__device__ __forceinline__ int xcd_order(int run) {
+  const uint32_t bid = blockIdx.x;
+  const uint32_t r = (bid & 7u) * (uint32_t)run + (bid >> 3);
+  return (int)__builtin_amdgcn_readfirstlane(run != 0 ? r : bid);
+}
+
+// The scale of scales of a double-quantized weight as a vector load (every
+// lane reads the one float), issued ahead of a launch's first chunk loads:
+// vector loads return in order, so the first chunk's wait covers it.  Read
+// through the scalar cache instead it held the LUT barrier, which waits on
+// the LDS stores with the one counter that scalar loads share, until the
+// value arrived behind every workgroup's first chunks.
+__device__ __forceinline__ float load_scale_of_scales(const float* p) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(p, 4u), 0, 0, 0));
 }
 
 // One chunk of one weight in flight: this lane's code bytes (8 per row) and
@@ -284,9 +303,10 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 
   // XCD-aware order: workgroup b runs on XCD b % 8, so each XCD takes a
   // contiguous run of stripes and the four stripes of a 64-column block
-  // (which share their scale codes) meet in one L2.
-  const int nb = gridDim.x;
-  const int b = (nb % 8 == 0) ? ((int)blockIdx.x % 8) * (nb / 8) + (int)blockIdx.x / 8 : (int)blockIdx.x;
+  // (which share their scale codes) meet in one L2.  The run length comes
+  // with the arguments: derived from gridDim here, it put a load of the grid
+  // size and a branch ahead of every other argument load.
+  const int b = xcd_order(a.xcd_run);
   // which weight (several weights of one x can share a launch) and stripe
   int wi = 0;
   if constexpr (!PAIR) {
@@ -334,17 +354,19 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   // loop head wait for the newest loads), before the LUT build, so that
   // their memory latency overlaps the build and its barrier (config 2:
   // 8.85 -> 8.65 us per launch).  The DQ table holds q / 255 and the scale
-  // of scales (read through the scalar cache) is applied per row, so the
-  // table does not wait for that load.
+  // of scales, loaded ahead of the chunks, is applied per row, so the table
+  // does not wait for that load.
+  float sos[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+    sos[w] = DQ ? load_scale_of_scales(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
+  __builtin_amdgcn_sched_barrier(0);
   Chunk<T, NW, XBF16, DQ, RPL> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     issue_chunk<T, NW, XBF16, DQ, NORM, RPL>(ring[j], ww, xr, gr, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
-  float sos[NW];
-#pragma unroll
-  for (int w = 0; w < NW; ++w) sos[w] = DQ ? *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
   if (tid < 256) {
     const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
     const f32x4 v = {lo, hi, lo, hi};
@@ -496,7 +518,9 @@ hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
     done.fetch_or(bit, std::memory_order_acq_rel);
   }
   static_assert(NWof<PAIR>() * T * W * 16 + T * W <= 512 + 64, "GEMV reduction space");
-  fn<<<grid, W * 64, kGemvSmem, stream>>>(a);
+  StripedArgs args = a;
+  args.xcd_run = grid % 8 == 0 ? grid / 8 : 0;
+  fn<<<grid, W * 64, kGemvSmem, stream>>>(args);
   return hipGetLastError();
 }
 
@@ -656,8 +680,7 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int nb = gridDim.x;
-  const int b = (nb % 8 == 0) ? ((int)blockIdx.x % 8) * (nb / 8) + (int)blockIdx.x / 8 : (int)blockIdx.x;
+  const int b = xcd_order(a.xcd_run);  // as in the GEMV
   const int gs = b * S;  // first stripe of this workgroup over the launch
   int wi = 0;
   if constexpr (!PAIR) {
@@ -689,17 +712,20 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   // scaled by 1 / sqrt(mean(x_t^2) + eps) before the epilogue
   const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM ? a.norm_w + kw : a.x, NORM ? (uint32_t)nrows * 4u : 0u);
 
-  // as in the GEMV: the first chunks in flight before the LUT build, and the
-  // scale of scales applied per row (the DQ table holds q / 255)
+  // as in the GEMV: the scale of scales and then the first chunks in flight
+  // before the LUT build, the scale of scales applied per row (the DQ table
+  // holds q / 255)
+  float sos[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+    sos[w] = DQ ? load_scale_of_scales(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
+  __builtin_amdgcn_sched_barrier(0);
   SkChunk<NT, NW, S, DQ, XF32> ring[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {  // in chunk order, as in the GEMV
     sk_issue<NT, NW, S, DQ, XF32, NORM>(ring[j], ww, xr, gr, K, kw, kw + nrows, j, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
-  float sos[NW];
-#pragma unroll
-  for (int w = 0; w < NW; ++w) sos[w] = DQ ? *(const_f32*)(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
   if (tid < 256) {  // level-pair LUT and DQ scale table, as in the GEMV
     const float lo = level_select(tid & 15), hi = level_select(tid >> 4);
     const f32x4 v = {lo, hi, lo, hi};
@@ -956,7 +982,9 @@ hipError_t sk_launch_t(const StripedArgs& a, int grid, int splits, hipStream_t s
   static_assert(smem <= 65536, "skinny LDS");
   static_assert(W * NW * 1024 <= 16384, "the reduction reuses the LUT space below the norm's sums");
   static_assert(16384 + (NT * W * 16 + NT * 16) * 4 <= kLutBytes, "the norm's sums fit the LUT space");
-  skinny_kernel<NT, W, D, S, DQ, PAIR, XF32, NORM><<<dim3(grid, splits), W * 64, smem, stream>>>(a);
+  StripedArgs args = a;
+  args.xcd_run = grid % 8 == 0 ? grid / 8 : 0;
+  skinny_kernel<NT, W, D, S, DQ, PAIR, XF32, NORM><<<dim3(grid, splits), W * 64, smem, stream>>>(args);
   return hipGetLastError();
 }
 
