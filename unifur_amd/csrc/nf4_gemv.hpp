@@ -59,6 +59,16 @@ struct StripedPlan {
   int rows_per_split; // skinny kernel: waves * rows_per_wave
 };
 
+// What the first loads of a striped launch need of weight slot i.  With the
+// shape fields and stripe_begin these lie in the first two 64-byte lines of
+// the arguments, so that the prologue's argument loads miss the scalar cache
+// at most once; the full GemvWeight records, which the epilogue reads, follow.
+struct StripedSlot {
+  const uint8_t* packed;
+  const void* scales;  // u8 DQ codes or f32 absmax, as the weight's scale kind
+  const float* scale_of_scales;
+};
+
 struct StripedArgs {
   const void* x;  // [rows, d_in] f32 or bf16
   int rows;
@@ -69,8 +79,9 @@ struct StripedArgs {
   // XCD-aware order: gridDim.x / 8 when that divides evenly, else 0 (set by
   // the launcher, so that the kernels need not read the grid size first)
   int xcd_run;
-  GemvWeight w[kMaxGemvWeights];
+  StripedSlot slot[kMaxGemvWeights];
   int stripe_begin[kMaxGemvWeights + 1];  // prefix sums of stripes per weight
+  GemvWeight w[kMaxGemvWeights];
   // QwenRmsNorm folded into the launch, x -> x * rsqrt(mean(x^2) +
   // norm_eps) * (norm_w + 1) per row
   const float* norm_w;  // [d_in] or null

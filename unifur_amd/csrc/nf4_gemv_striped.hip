@@ -85,6 +85,44 @@ __device__ __forceinline__ int xcd_order(int run) {
   return (int)__builtin_amdgcn_readfirstlane(run != 0 ? r : bid);
 }
 
+// What the first loads of weight slot wi need -- its first stripe, codes,
+// block scales and scale of scales -- read from every slot at fixed offsets
+// and picked by wi: indexed by wi, these argument loads waited for the ones
+// wi is found from, a second round trip before any weight byte is requested.
+struct SlotHead {
+  int stripe_begin;
+  const uint8_t* packed;
+  const void* scales;  // u8 DQ codes or f32 absmax
+  const float* scale_of_scales;
+};
+__device__ __forceinline__ SlotHead slot_read(const StripedArgs& a, int i) {
+  SlotHead c{a.stripe_begin[i], a.slot[i].packed, a.slot[i].scales, a.slot[i].scale_of_scales};
+  // an empty operand barrier (no instruction): the values are loaded here,
+  // so the selection below cannot become a load through a selected address
+  asm volatile("" : "+s"(c.stripe_begin), "+s"(c.packed), "+s"(c.scales), "+s"(c.scale_of_scales));
+  return c;
+}
+__device__ __forceinline__ SlotHead slot_head(const StripedArgs& a, int wi) {
+  SlotHead h = slot_read(a, 0);
+#pragma unroll
+  for (int i = 1; i < kMaxGemvWeights; ++i) {
+    const SlotHead c = slot_read(a, i);
+    if (wi == i) h = c;
+  }
+  return h;
+}
+
+// The slot records of a launch's weights (the rest stay zero).
+void set_slots(StripedArgs& a, const GemvWeight* weights, int nweights) {
+  for (int i = 0; i < nweights; ++i) {
+    const ScalesArg& sc = weights[i].scales;
+    a.slot[i] = StripedSlot{weights[i].packed,
+                            sc.kind == kScalesDQ ? static_cast<const void*>(sc.dq_codes)
+                                                 : static_cast<const void*>(sc.absmax),
+                            sc.scale_of_scales};
+  }
+}
+
 // The scale of scales of a double-quantized weight as a vector load (every
 // lane reads the one float), issued ahead of a launch's first chunk loads:
 // vector loads return in order, so the first chunk's wait covers it.  Read
@@ -314,7 +352,10 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
     for (int i = 1; i < kMaxGemvWeights; ++i)
       if (i < a.nweights && b >= a.stripe_begin[i]) wi = i;
   }
-  const int s = b - a.stripe_begin[wi];
+  SlotHead head[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) head[w] = slot_head(a, PAIR ? w : wi);
+  const int s = b - head[0].stripe_begin;
   const int K = a.d_in;
   const int kw = wave * a.rows_per_wave;
   const int nrows = max(0, min(a.rows_per_wave, K - kw));
@@ -323,11 +364,10 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   WaveW ww[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    const GemvWeight& G = a.w[PAIR ? w : wi];
-    ww[w].codes = make_rsrc(G.packed + ((size_t)s * K + kw) * 8, (uint32_t)nrows * 8u);
+    ww[w].codes = make_rsrc(head[w].packed + ((size_t)s * K + kw) * 8, (uint32_t)nrows * 8u);
     const size_t srow = (size_t)(s / 4) * K + kw;
-    ww[w].scales = DQ ? make_rsrc(G.scales.dq_codes + srow, (uint32_t)nrows)
-                      : make_rsrc(G.scales.absmax + srow, (uint32_t)nrows * 4u);
+    ww[w].scales = DQ ? make_rsrc(static_cast<const uint8_t*>(head[w].scales) + srow, (uint32_t)nrows)
+                      : make_rsrc(static_cast<const float*>(head[w].scales) + srow, (uint32_t)nrows * 4u);
   }
   __amdgpu_buffer_rsrc_t xr[T];
 #pragma unroll
@@ -359,7 +399,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   float sos[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w)
-    sos[w] = DQ ? load_scale_of_scales(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
+    sos[w] = DQ ? load_scale_of_scales(head[w].scale_of_scales) : 1.0f;
   __builtin_amdgcn_sched_barrier(0);
   Chunk<T, NW, XBF16, DQ, RPL> ring[D];
 #pragma unroll
@@ -688,7 +728,10 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
     for (int i = 1; i < kMaxGemvWeights; ++i)
       if (i < a.nweights && gs >= a.stripe_begin[i]) wi = i;
   }
-  const int s0 = gs - a.stripe_begin[wi];
+  SlotHead head[NW];  // as in the GEMV
+#pragma unroll
+  for (int w = 0; w < NW; ++w) head[w] = slot_head(a, PAIR ? w : wi);
+  const int s0 = gs - head[0].stripe_begin;
   const int K = a.d_in;
   const int P = gridDim.y, p = blockIdx.y;  // d_in slabs
   const int kw = p * a.rows_per_split + wave * a.rows_per_wave;
@@ -698,11 +741,10 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   WaveW ww[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    const GemvWeight& G = a.w[PAIR ? w : wi];
-    ww[w].codes = make_rsrc(G.packed + ((size_t)s0 * K + kw) * 8, (uint32_t)((S - 1) * K + nrows) * 8u);
+    ww[w].codes = make_rsrc(head[w].packed + ((size_t)s0 * K + kw) * 8, (uint32_t)((S - 1) * K + nrows) * 8u);
     const size_t srow = (size_t)(s0 / 4) * K + kw;
-    ww[w].scales = DQ ? make_rsrc(G.scales.dq_codes + srow, (uint32_t)nrows)
-                      : make_rsrc(G.scales.absmax + srow, (uint32_t)nrows * 4u);
+    ww[w].scales = DQ ? make_rsrc(static_cast<const uint8_t*>(head[w].scales) + srow, (uint32_t)nrows)
+                      : make_rsrc(static_cast<const float*>(head[w].scales) + srow, (uint32_t)nrows * 4u);
   }
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.rows * (uint32_t)K * (XF32 ? 4u : 2u));
   // NORM: QwenRmsNorm over x folded in (src/qwennet.rs:104-109), over the
@@ -718,7 +760,7 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   float sos[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w)
-    sos[w] = DQ ? load_scale_of_scales(a.w[PAIR ? w : wi].scales.scale_of_scales) : 1.0f;
+    sos[w] = DQ ? load_scale_of_scales(head[w].scale_of_scales) : 1.0f;
   __builtin_amdgcn_sched_barrier(0);
   SkChunk<NT, NW, S, DQ, XF32> ring[D];
 #pragma unroll
@@ -1077,6 +1119,7 @@ hipError_t launch_gemv_striped(const StripedPlan& p, const void* x, bool x_bf16,
     if (!pair || i == 0) s += weights[i].d_out / kStripeCols;
   }
   for (int i = nweights; i <= kMaxGemvWeights; ++i) a.stripe_begin[i] = s;
+  set_slots(a, weights, nweights);
   const bool dq = weights[0].scales.kind == kScalesDQ;
   if (pair) {
     if (rows == 1) return dispatch_w<1, true>(a, s, p.waves, x_bf16, dq, stream);
@@ -1180,6 +1223,7 @@ hipError_t launch_skinny(const StripedPlan& p, const void* x, bool x_f32, int ro
     if (!pair || i == 0) s += weights[i].d_out / kStripeCols;  // a multiple of 4: groups never straddle weights
   }
   for (int i = nweights; i <= kMaxGemvWeights; ++i) a.stripe_begin[i] = s;
+  set_slots(a, weights, nweights);
   const bool dq = weights[0].scales.kind == kScalesDQ;
   const int grid = s / p.group;
   if (x_f32)
