@@ -35,6 +35,10 @@
  *     d_out.  On the device it may also be held in the column-striped
  *     layout (UNIFUR_NF4_LAYOUT_STRIPED), a byte permutation of the same
  *     codes and scales that the decode kernels stream contiguously.
+ *   - Shapes past any device -- rows, d_in or d_out above 2^31-1, or an
+ *     element count rows x width or d_in x d_out above 2^48 -- are refused:
+ *     the workspace-size queries return UINT64_MAX for them (never a byte
+ *     count that wrapped) and the calls fail with UNIFUR_NF4_ERR_INVALID.
  */
 #ifndef UNIFUR_NF4_H
 #define UNIFUR_NF4_H

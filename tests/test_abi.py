@@ -78,6 +78,35 @@ def test_invalid_arguments_fail_before_any_device_work(lib):
                                         None) == _lib.ERR_INVALID
 
 
+def test_shapes_past_any_device_are_refused(lib):
+    """An element count over 2^48 (rows x a width, or a weight's d_in x
+    d_out) is past any device: the size queries answer UINT64_MAX instead
+    of a byte count that wrapped 64 bits, and the calls refuse the shape
+    before any device work."""
+    from unifur_amd import _lib
+    top = (1 << 64) - 1
+    big = (1 << 31) - 1  # each dimension within its own 2^31 bound
+    assert lib.unifur_nf4_linear_workspace_size(big, big, big, 0, 0) == top
+    assert lib.unifur_nf4_linear_min_workspace_size(big, 4096, big, 1, 16) == top
+    assert lib.unifur_nf4_linear_backward_workspace_size(big, big, 4096, 1, 0) == top
+    assert lib.unifur_nf4_linear_backward_min_workspace_size(big, big, 4096, 1, 0, 1) == top
+    assert lib.unifur_nf4_swiglu_workspace_size(big, 4096, big, 1) == top
+    assert lib.unifur_nf4_swiglu_min_workspace_size(big, big, 11008, 1) == top
+    d_out = (ctypes.c_uint64 * 1)(big)
+    assert lib.unifur_nf4_linear_multi_workspace_size(big, big, d_out, 1, 0) == top
+    assert lib.unifur_nf4_quantize_linears_workspace_size((ctypes.c_uint64 * 1)(big), d_out, 1) == top
+    # at the bound a weight of exactly 2^48 values still gets its byte count
+    # (one row: the GEMV's counter region), one block more does not
+    assert 0 < lib.unifur_nf4_linear_workspace_size(1, 1 << 24, 1 << 24, 0, 0) < top
+    assert lib.unifur_nf4_linear_workspace_size(1, (1 << 24) + 64, 1 << 24, 0, 0) == top
+    # a call with such a shape fails on the host (the pointers are never read)
+    fake = 1 << 20
+    w = _lib.Weight(fake, _lib.Scales(_lib.SCALES_F32, fake, None, None), big, 1 << 20, 0)
+    assert lib.unifur_nf4_linear_forward(fake, _lib.F32, big, ctypes.byref(w), None, None, fake, _lib.F32, None, 0,
+                                         None) == _lib.ERR_INVALID
+    assert b"2^48" in lib.unifur_nf4_last_error()
+
+
 def test_workspace_sizes_are_consistent(lib):
     # GEMV path: counters + split-K partials; generic path: an f32 weight copy
     small = lib.unifur_nf4_linear_workspace_size(1, 4096, 11008, 0, 0)

@@ -179,6 +179,20 @@ constexpr size_t kCounterRegion = 64 << 10;
 constexpr int kMaxCounters = (int)(kCounterRegion / sizeof(unsigned));
 
 // Carves consecutive 256-byte-aligned regions out of one workspace.
+// Shapes past any device: every element count a plan forms -- rows times a
+// width, a weight's d_in x d_out, an MLP's middle -- stays at or below 2^48,
+// so that no byte count derived from one (times an element size, a slab
+// count, a rank of at most 64) wraps 64 bits.  Size queries answer
+// UINT64_MAX for a shape past it and the calls refuse it.
+constexpr uint64_t kMaxElements = 1ull << 48;
+bool fits_elements(uint64_t a, uint64_t b) {
+  uint64_t p = 0;
+  return !__builtin_mul_overflow(a, b, &p) && p <= kMaxElements;
+}
+bool shape_fits(uint64_t rows, uint64_t d_in, uint64_t d_out) {
+  return fits_elements(rows, d_in) && fits_elements(rows, d_out) && fits_elements(d_in, d_out);
+}
+
 struct Carver {
   size_t off = kCounterRegion;
   size_t take(size_t bytes) {
@@ -351,6 +365,7 @@ int run_linear(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr && y != nullptr, "x or y is NULL");
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  UNIFUR_ARG(shape_fits(rows, w->d_in, w->d_out), "linear: shape too large (an element count over 2^48)");
   const uint32_t rank = lora ? lora->rank : 0;
   if (lora) {
     UNIFUR_ARG(lora->a != nullptr && lora->b != nullptr, "lora factors are NULL");
@@ -636,6 +651,7 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr && y != nullptr, "x or y is NULL");
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  UNIFUR_ARG(shape_fits(rows, hidden, inter), "swiglu: shape too large (an element count over 2^48)");
   MlpLayout L = plan_mlp(rows, hidden, inter, gate, up, down, x_dtype, x);
   if (L.path == MlpPath::kMfma && L.expand && ((workspace && workspace_bytes < L.total) || !aligned_to(y, 16))) {
     // a workspace too small for an expanded weight, or an output the BLAS
@@ -823,6 +839,7 @@ int run_swiglu(const void* x, int x_dtype, uint64_t rows, const unifur_nf4_weigh
 uint64_t swiglu_workspace(uint64_t rows, uint64_t hidden, uint64_t intermediate, int x_dtype, bool expand,
                           bool split = true) {
   if (rows == 0 || hidden == 0 || intermediate == 0) return 0;
+  if (rows > 0x7fffffffu || !shape_fits(rows, hidden, intermediate)) return UINT64_MAX;
   const uint8_t* p = reinterpret_cast<const uint8_t*>(uintptr_t{256});
   uint64_t need = 0;
   for (int striped = 0; striped < 2; ++striped) {
@@ -988,6 +1005,7 @@ int run_backward(const void* dy, int dy_dtype, uint64_t rows, const unifur_nf4_w
   UNIFUR_ARG(!want_grads || rows == 0 || x != nullptr, "adapter gradients need x");
   const uint64_t K = w->d_in, N = w->d_out;
   UNIFUR_ARG(K <= 0x7fffffffu && N <= 0x7fffffffu, "weight too large");
+  UNIFUR_ARG(shape_fits(rows, K, N), "linear_backward: shape too large (an element count over 2^48)");
   const bool aligned = aligned_to(dy, 16) && aligned_to(dx, 16);
   BackwardLayout L = plan_backward(rows, K, N, rank, dy_dtype, want_dx && rows > 0, want_grads, is_striped(w),
                                    w->scales.kind, aligned, true, true, aligned_to(w->packed, 8));
@@ -1181,6 +1199,9 @@ int run_linear_multi(const void* x, int x_dtype, uint64_t rows, const unifur_nf4
   }
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr, "x is NULL");
+  UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  for (uint32_t i = 0; i < n; ++i)
+    UNIFUR_ARG(shape_fits(rows, w[i].d_in, w[i].d_out), "linear_forward_multi: shape too large (an element count over 2^48)");
   uint64_t d_out[kMaxGemvWeights] = {};
   for (uint32_t i = 0; i < n; ++i) d_out[i] = w[i].d_out;
   const MultiLayout L = plan_multi(rows, w[0].d_in, d_out, w, n, x_dtype, x);
@@ -1279,6 +1300,7 @@ int run_attn_in(const void* x, int dtype, uint64_t rows, const unifur_nf4_decode
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr && q != nullptr && k != nullptr && v != nullptr, "x, q, k or v is NULL");
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  UNIFUR_ARG(shape_fits(rows, l->q.d_in, l->gate.d_out), "decoder layer: shape too large (an element count over 2^48)");
   const bool bf = dtype == UNIFUR_NF4_BF16;
   const unifur_nf4_weight w[3] = {l->q, l->k, l->v};
   void* const outs[3] = {q, k, v};
@@ -1396,6 +1418,7 @@ int run_attn_out_mlp(const void* x, const void* ctx, int dtype, uint64_t rows, c
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr && ctx != nullptr && y != nullptr, "x, ctx or y is NULL");
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  UNIFUR_ARG(shape_fits(rows, l->q.d_in, l->gate.d_out), "decoder layer: shape too large (an element count over 2^48)");
   const bool bf = dtype == UNIFUR_NF4_BF16;
   const uint64_t hid = l->o.d_out, inter = l->gate.d_out;
   const AttnOutLayout L = plan_attn_out(rows, l, dtype, ctx, reinterpret_cast<const void*>(uintptr_t{256}));
@@ -1527,6 +1550,7 @@ int run_linear_noalloc(const void* x, int x_dtype, uint64_t rows, const unifur_n
   if (rows == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(x != nullptr && y != nullptr, "x or y is NULL");
   UNIFUR_ARG(rows <= 0x7fffffffu, "rows exceeds 2^31-1");
+  UNIFUR_ARG(shape_fits(rows, w->d_in, w->d_out), "linear: shape too large (an element count over 2^48)");
   const uint32_t rank = lora ? lora->rank : 0;
   if (lora) UNIFUR_ARG(rank >= 1 && rank <= 64, "lora rank must be in [1, 64]");
   LinearLayout L =
@@ -1654,6 +1678,7 @@ int unifur_nf4_pack_codes(const uint8_t* codes, uint64_t len, uint8_t* packed, v
 
 uint64_t unifur_nf4_decoder_attn_in_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer* layer, int dtype) {
   if (rows == 0 || check_layer(layer) != UNIFUR_NF4_OK || !valid_dtype(dtype)) return 0;
+  if (rows > 0x7fffffffu || !shape_fits(rows, layer->q.d_in, layer->gate.d_out)) return UINT64_MAX;
   if (attn_in_fused(rows, layer)) return 0;
   return plan_attn_in(rows, layer, dtype).total;
 }
@@ -1666,6 +1691,7 @@ int unifur_nf4_decoder_attn_in(const void* x, int dtype, uint64_t rows, const un
 uint64_t unifur_nf4_decoder_attn_out_mlp_workspace_size(uint64_t rows, const unifur_nf4_decoder_layer* layer,
                                                         int dtype) {
   if (rows == 0 || check_layer(layer) != UNIFUR_NF4_OK || !valid_dtype(dtype)) return 0;
+  if (rows > 0x7fffffffu || !shape_fits(rows, layer->q.d_in, layer->gate.d_out)) return UINT64_MAX;
   // a ctx off the 16-byte alignment can move the o projection to the
   // general path, whose workspace differs: the larger of both plans
   const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
@@ -1683,6 +1709,8 @@ int unifur_nf4_decoder_attn_out_mlp(const void* x, const void* ctx, int dtype, u
 uint64_t unifur_nf4_linear_multi_workspace_size(uint64_t rows, uint64_t d_in, const uint64_t* d_out, uint32_t n,
                                                 int x_dtype) {
   if (rows == 0 || d_in == 0 || !d_out || n == 0 || n > (uint32_t)kMaxGemvWeights) return 0;
+  for (uint32_t i = 0; i < n; ++i)
+    if (rows > 0x7fffffffu || !shape_fits(rows, d_in, d_out[i])) return UINT64_MAX;
   const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
   const MultiLayout L = plan_multi(rows, d_in, d_out, nullptr, n, x_dtype, aligned);
   uint64_t need = L.total;
@@ -1701,6 +1729,7 @@ int unifur_nf4_linear_forward_multi(const void* x, int x_dtype, uint64_t rows, c
 uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
                                                    uint32_t lora_rank) {
   if (d_in == 0 || d_out == 0) return 0;
+  if (rows > 0x7fffffffu || !shape_fits(rows, d_in, d_out)) return UINT64_MAX;
   uint64_t need = 0;
   for (int striped = 0; striped < 2; ++striped)
     for (int kind = 0; kind < 2; ++kind)
@@ -1713,6 +1742,7 @@ uint64_t unifur_nf4_linear_backward_workspace_size(uint64_t rows, uint64_t d_in,
 uint64_t unifur_nf4_linear_backward_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int dy_dtype,
                                                        uint32_t lora_rank, int layout) {
   if (d_in == 0 || d_out == 0) return 0;
+  if (rows > 0x7fffffffu || !shape_fits(rows, d_in, d_out)) return UINT64_MAX;
   // only a striped weight can take the fused dX kernel; any other layout
   // (or an unknown value) gets the default size
   if (layout != UNIFUR_NF4_LAYOUT_STRIPED || d_out % 64 != 0)
@@ -1759,6 +1789,7 @@ int unifur_nf4_embedding_forward(const uint8_t* packed, const unifur_nf4_scales*
 uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
                                           uint32_t lora_rank) {
   if (rows == 0 || d_in == 0 || d_out == 0) return 0;
+  if (rows > 0x7fffffffu || !shape_fits(rows, d_in, d_out)) return UINT64_MAX;
   // sized for 16-byte-aligned buffers, as hipMalloc returns them; a call
   // with misaligned buffers may take the generic path, which needs more and
   // reports UNIFUR_NF4_ERR_WORKSPACE with the size when given less
@@ -1774,6 +1805,7 @@ uint64_t unifur_nf4_linear_workspace_size(uint64_t rows, uint64_t d_in, uint64_t
 uint64_t unifur_nf4_linear_min_workspace_size(uint64_t rows, uint64_t d_in, uint64_t d_out, int x_dtype,
                                               uint32_t lora_rank) {
   if (rows == 0 || d_in == 0 || d_out == 0) return 0;
+  if (rows > 0x7fffffffu || !shape_fits(rows, d_in, d_out)) return UINT64_MAX;
   const void* aligned = reinterpret_cast<const void*>(uintptr_t{256});
   uint64_t need = 0;
   for (int striped = 0; striped < 2; ++striped)
@@ -1827,6 +1859,8 @@ int unifur_nf4_quantize_transposed(const void* src, int src_dtype, uint64_t out_
 
 uint64_t unifur_nf4_quantize_linears_workspace_size(const uint64_t* d_in, const uint64_t* d_out, uint32_t n) {
   if (n == 0 || !d_in || !d_out) return 0;
+  for (uint32_t i = 0; i < n; ++i)
+    if (!fits_elements(d_in[i], d_out[i])) return UINT64_MAX;
   Carver c;
   c.take(quantize_linears_scratch_bytes(d_in, d_out, n));
   return c.off;
@@ -1842,7 +1876,8 @@ int run_quantize_linears(const void* const* values, int src_kind, const uint64_t
   const uintptr_t align = src_kind == kQuantSrcF32 ? 16 : src_kind == kQuantSrcF32T ? 4 : 2;
   for (uint32_t i = 0; i < n; ++i) {
     UNIFUR_ARG(d_in[i] > 0 && d_out[i] > 0 && d_out[i] % 64 == 0, "quantize_linears needs d_out % 64 == 0");
-    UNIFUR_ARG(d_in[i] <= 0x7fffffffu && d_out[i] <= 0x7fffffffu, "quantize_linears: weight too large");
+    UNIFUR_ARG(d_in[i] <= 0x7fffffffu && d_out[i] <= 0x7fffffffu && fits_elements(d_in[i], d_out[i]),
+               "quantize_linears: weight too large");
     UNIFUR_ARG(values[i] && packed[i] && dq_codes[i] && scale_of_scales[i], "a tensor pointer is NULL");
     UNIFUR_ARG(aligned_to(values[i], align) && aligned_to(packed[i], 8) && aligned_to(scale_of_scales[i], 4),
                src_kind == kQuantSrcF32 ? "values must be 16-byte, packed 8-byte aligned"
@@ -1894,6 +1929,7 @@ int unifur_nf4_quantize_checkpoint_linears(const void* const* values, int src_dt
 
 uint64_t unifur_nf4_dense_linear_workspace_size(uint64_t rows, uint32_t lora_rank) {
   if (rows == 0 || lora_rank == 0) return 0;
+  if (!fits_elements(rows, lora_rank)) return UINT64_MAX;
   Carver c;
   c.take((size_t)rows * lora_rank * sizeof(float));
   return c.off;
