@@ -105,6 +105,9 @@ def test_shapes_past_any_device_are_refused(lib):
     assert lib.unifur_nf4_linear_forward(fake, _lib.F32, big, ctypes.byref(w), None, None, fake, _lib.F32, None, 0,
                                          None) == _lib.ERR_INVALID
     assert b"2^48" in lib.unifur_nf4_last_error()
+    assert lib.unifur_nf4_embedding_forward(fake, None, 1 << 30, 1 << 20, fake, 0, 1, fake, _lib.F32,
+                                            None) == _lib.ERR_INVALID
+    assert b"2^48" in lib.unifur_nf4_last_error()
 
 
 def test_workspace_sizes_are_consistent(lib):

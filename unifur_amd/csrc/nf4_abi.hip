@@ -1773,7 +1773,8 @@ int unifur_nf4_embedding_forward(const uint8_t* packed, const unifur_nf4_scales*
              "ids_dtype must be UNIFUR_NF4_IDS_I32 or UNIFUR_NF4_IDS_I64");
   if (n_ids == 0 || d_model == 0) return UNIFUR_NF4_OK;
   UNIFUR_ARG(ids && out, "ids or out is NULL");
-  UNIFUR_ARG(n_embedding == 0 || d_model <= ~0ull / n_embedding, "table size overflows");
+  UNIFUR_ARG(fits_elements(n_ids, d_model) && fits_elements(n_embedding, d_model),
+             "embedding: shape too large (an element count over 2^48)");
   if (n_embedding > 0) {
     if (int r = check_scales(scales)) return r;
     UNIFUR_ARG(packed != nullptr, "packed is NULL");
