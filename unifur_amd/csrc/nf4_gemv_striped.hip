@@ -905,33 +905,62 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   }
 
   // acc[w][i][tt][e] = C[token 16 tt + 4 (lane / 16) + e][column lane % 16 of
-  // stripe s0 + i]; waves added through LDS (LUT space), one (tile, stripe)
-  // at a time, both weights of a pair together.  Thread tid < 256 owns
-  // token 16 tt + tid / 16, column tid % 16 of every (tile, stripe).
+  // stripe s0 + i]; waves added through LDS (LUT space, below the norm's
+  // sums at 16 KiB), both weights of a pair together, in wave order.  When
+  // every (tile, stripe) fits there at once, one write phase and one read
+  // phase (two barriers); else one (tile, stripe) at a time (two barriers
+  // each).  Thread tid < 256 owns token 16 tt + tid / 16, column tid % 16 of
+  // every (tile, stripe).
   float* red = reinterpret_cast<float*>(smem);
   const GemvWeight& G = a.w[wi];
   const int t_l = tid >> 4, cc = tid & 15;
   const int src = ((t_l >> 2) * 16 + cc) * 4 + (t_l & 3);
   float sums[NW][S][NT];
+  constexpr bool kOnePass = NT * S * NW * W * 1024 <= 16384;
+  if constexpr (kOnePass) {
+    __syncthreads();  // every wave is past its LUT lookups
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt)
+    for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-    for (int i = 0; i < S; ++i) {
-      __syncthreads();
+      for (int i = 0; i < S; ++i)
 #pragma unroll
-      for (int w = 0; w < NW; ++w)
-        *reinterpret_cast<f32x4*>(red + ((w * W + wave) * 64 + lane) * 4) = acc[w][i][tt];
-      __syncthreads();
+        for (int w = 0; w < NW; ++w)
+          *reinterpret_cast<f32x4*>(red + ((((tt * S + i) * NW + w) * W + wave) * 64 + lane) * 4) = acc[w][i][tt];
+    __syncthreads();
 #pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        float v = 0.0f;
-        if (tid < 256) {
+    for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-          for (int qq = 0; qq < W; ++qq) v += red[(w * W + qq) * 256 + src];
+      for (int i = 0; i < S; ++i)
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          float v = 0.0f;
+          if (tid < 256) {
+#pragma unroll
+            for (int qq = 0; qq < W; ++qq) v += red[(((tt * S + i) * NW + w) * W + qq) * 256 + src];
+          }
+          sums[w][i][tt] = v;
         }
-        sums[w][i][tt] = v;
+  } else {
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+          *reinterpret_cast<f32x4*>(red + ((w * W + wave) * 64 + lane) * 4) = acc[w][i][tt];
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          float v = 0.0f;
+          if (tid < 256) {
+#pragma unroll
+            for (int qq = 0; qq < W; ++qq) v += red[(w * W + qq) * 256 + src];
+          }
+          sums[w][i][tt] = v;
+        }
       }
-    }
+  }
   const bool mine = tid < 256;
   if (P > 1) {
     // slab p's sums to the partials, then the last slab to arrive adds all
