@@ -31,6 +31,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions.  The striped GEMV passes what its prologue reads as
+# leading scalar kernel parameters, which this preloads into SGPRs before a
+# wave starts (with the loads as a fallback the code object carries for
+# firmware without preloading).
+EXTRA_FLAGS = {
+    "nf4_gemv_striped.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+}
+
 # hipBLASLt: the plain bf16 GEMM of the prefill path (nf4_blas.hip).
 LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 
@@ -44,7 +52,7 @@ def hipcc() -> str:
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")

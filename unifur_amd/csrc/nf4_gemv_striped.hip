@@ -329,8 +329,17 @@ __device__ __forceinline__ void store_y(const GemvWeight& W, size_t idx, float y
     reinterpret_cast<float*>(W.y)[idx] = y;
 }
 
+// What the prologue of a one-weight launch reads comes first, as scalar
+// parameters: the build preloads the leading kernel arguments into SGPRs
+// (amdgpu-kernarg-preload-count), so those need no load through the scalar
+// cache before the first weight byte is requested.  x_arg, slot0, d_in,
+// rows_per_wave, xcd_run and nweights repeat the fields of a; a launch with
+// several weights (or the SwiGLU pair) reads the other slots from a.
 template <int T, int W, int D, bool XBF16, bool DQ, bool PAIR, bool NORM, int RPL>
-__global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
+__global__ __launch_bounds__(W * 64) void gemv_striped_kernel(const void* x_arg, const uint8_t* packed0,
+                                                              const void* scales0, const float* sos0, int d_in_arg,
+                                                              int rows_per_wave_arg, int xcd_run_arg,
+                                                              int nweights_arg, StripedArgs a) {
   constexpr int NW = PAIR ? 2 : 1;
   static_assert(RPL == 1 || RPL == 2, "one or two rows per lane and chunk");
   static_assert(D % 2 == 0, "the lookup double buffer is indexed by chunk parity");
@@ -344,21 +353,23 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   // (which share their scale codes) meet in one L2.  The run length comes
   // with the arguments: derived from gridDim here, it put a load of the grid
   // size and a branch ahead of every other argument load.
-  const int b = xcd_order(a.xcd_run);
+  const int b = xcd_order(xcd_run_arg);
   // which weight (several weights of one x can share a launch) and stripe
   int wi = 0;
-  if constexpr (!PAIR) {
+  SlotHead head[NW];
+  head[0] = SlotHead{0, packed0, scales0, sos0};  // slot 0 starts at stripe 0
+  if constexpr (PAIR) {
+    head[1] = slot_read(a, 1);
+  } else if (nweights_arg > 1) {
 #pragma unroll
     for (int i = 1; i < kMaxGemvWeights; ++i)
-      if (i < a.nweights && b >= a.stripe_begin[i]) wi = i;
+      if (i < nweights_arg && b >= a.stripe_begin[i]) wi = i;
+    head[0] = slot_head(a, wi);
   }
-  SlotHead head[NW];
-#pragma unroll
-  for (int w = 0; w < NW; ++w) head[w] = slot_head(a, PAIR ? w : wi);
   const int s = b - head[0].stripe_begin;
-  const int K = a.d_in;
-  const int kw = wave * a.rows_per_wave;
-  const int nrows = max(0, min(a.rows_per_wave, K - kw));
+  const int K = d_in_arg;
+  const int kw = wave * rows_per_wave_arg;
+  const int nrows = max(0, min(rows_per_wave_arg, K - kw));
   const int nchunks = (nrows + 64 * RPL - 1) / (64 * RPL);
 
   WaveW ww[NW];
@@ -373,8 +384,8 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const size_t off = (size_t)t * K + kw;
-    xr[t] = XBF16 ? make_rsrc(static_cast<const uint16_t*>(a.x) + off, (uint32_t)nrows * 2u)
-                  : make_rsrc(static_cast<const float*>(a.x) + off, (uint32_t)nrows * 4u);
+    xr[t] = XBF16 ? make_rsrc(static_cast<const uint16_t*>(x_arg) + off, (uint32_t)nrows * 2u)
+                  : make_rsrc(static_cast<const float*>(x_arg) + off, (uint32_t)nrows * 4u);
   }
   // folded QwenRmsNorm (src/qwennet.rs:104-109): the products take
   // x * (w + 1), each lane sums x^2 over its rows, and the column sums are
@@ -387,7 +398,7 @@ __global__ __launch_bounds__(W * 64) void gemv_striped_kernel(StripedArgs a) {
   // quarter of a chunk's loads: config 2 9.0 -> 8.5 us without it); the
   // SwiGLU pair keeps one, which measured faster with the loads than without.
   const bool norm = NORM && a.norm_w != nullptr;
-  const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : a.x, norm ? (uint32_t)nrows * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? a.norm_w + kw : x_arg, norm ? (uint32_t)nrows * 4u : 0u);
 
   // The prologue issues the first D chunks, in chunk order like the steady
   // state (a load of chunk 0 issued last would make every pass through the
@@ -560,7 +571,9 @@ hipError_t launch_t(const StripedArgs& a, int grid, hipStream_t stream) {
   static_assert(NWof<PAIR>() * T * W * 16 + T * W <= 512 + 64, "GEMV reduction space");
   StripedArgs args = a;
   args.xcd_run = grid % 8 == 0 ? grid / 8 : 0;
-  fn<<<grid, W * 64, kGemvSmem, stream>>>(args);
+  fn<<<grid, W * 64, kGemvSmem, stream>>>(args.x, args.slot[0].packed, args.slot[0].scales,
+                                          args.slot[0].scale_of_scales, args.d_in, args.rows_per_wave, args.xcd_run,
+                                          args.nweights, args);
   return hipGetLastError();
 }
 
