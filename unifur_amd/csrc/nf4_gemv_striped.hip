@@ -723,7 +723,12 @@ __device__ __forceinline__ void sk_lookup(f32x2 (&lv)[8], u32x2 code, uint32_t s
 }
 
 template <int NT, int W, int D, int S, bool DQ, bool PAIR, bool XF32, bool NORM>
-__global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
+__global__ __launch_bounds__(W * 64) void skinny_kernel(const void* x_arg, const uint8_t* packed0,
+                                                        const void* scales0, const float* sos0, int d_in_arg,
+                                                        int rows_per_wave_arg, int rows_per_split_arg, int rows_arg,
+                                                        int xcd_run_arg, int nweights_arg, int splits_arg,
+                                                        const float* norm_w_arg,
+                                                        StripedArgs a) {  // leading parameters as in the GEMV
   constexpr int NW = PAIR ? 2 : 1;
   constexpr int U = NW * S;  // units per chunk
   static_assert(D % 2 == 0, "the scale double buffer is indexed by chunk parity");
@@ -733,22 +738,24 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int b = xcd_order(a.xcd_run);  // as in the GEMV
+  const int b = xcd_order(xcd_run_arg);  // as in the GEMV
   const int gs = b * S;  // first stripe of this workgroup over the launch
   int wi = 0;
-  if constexpr (!PAIR) {
+  SlotHead head[NW];  // as in the GEMV
+  head[0] = SlotHead{0, packed0, scales0, sos0};
+  if constexpr (PAIR) {
+    head[1] = slot_read(a, 1);
+  } else if (nweights_arg > 1) {
 #pragma unroll
     for (int i = 1; i < kMaxGemvWeights; ++i)
-      if (i < a.nweights && gs >= a.stripe_begin[i]) wi = i;
+      if (i < nweights_arg && gs >= a.stripe_begin[i]) wi = i;
+    head[0] = slot_head(a, wi);
   }
-  SlotHead head[NW];  // as in the GEMV
-#pragma unroll
-  for (int w = 0; w < NW; ++w) head[w] = slot_head(a, PAIR ? w : wi);
   const int s0 = gs - head[0].stripe_begin;
-  const int K = a.d_in;
-  const int P = gridDim.y, p = blockIdx.y;  // d_in slabs
-  const int kw = p * a.rows_per_split + wave * a.rows_per_wave;
-  const int nrows = max(0, min(a.rows_per_wave, K - kw));
+  const int K = d_in_arg;
+  const int P = splits_arg, p = blockIdx.y;  // d_in slabs (gridDim.y)
+  const int kw = p * rows_per_split_arg + wave * rows_per_wave_arg;
+  const int nrows = max(0, min(rows_per_wave_arg, K - kw));
   const int nchunks = (nrows + 63) / 64;
 
   WaveW ww[NW];
@@ -759,13 +766,13 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
     ww[w].scales = DQ ? make_rsrc(static_cast<const uint8_t*>(head[w].scales) + srow, (uint32_t)nrows)
                       : make_rsrc(static_cast<const float*>(head[w].scales) + srow, (uint32_t)nrows * 4u);
   }
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.rows * (uint32_t)K * (XF32 ? 4u : 2u));
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x_arg, (uint32_t)rows_arg * (uint32_t)K * (XF32 ? 4u : 2u));
   // NORM: QwenRmsNorm over x folded in (src/qwennet.rs:104-109), over the
   // whole of d_in in one workgroup (no d_in slabs): each row's (w + 1) rides
   // on its block scale -- B = level * (scale * (w + 1)) -- each lane sums x^2
   // of the activations it feeds the MFMAs, and the outputs of token t are
   // scaled by 1 / sqrt(mean(x_t^2) + eps) before the epilogue
-  const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM ? a.norm_w + kw : a.x, NORM ? (uint32_t)nrows * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM ? norm_w_arg + kw : x_arg, NORM ? (uint32_t)nrows * 4u : 0u);
 
   // as in the GEMV: the scale of scales and then the first chunks in flight
   // before the LUT build, the scale of scales applied per row (the DQ table
@@ -982,10 +989,10 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt) {
         const int t = 16 * tt + t_l;
-        if (t >= a.rows) continue;
+        if (t >= rows_arg) continue;
 #pragma unroll
         for (int i = 0; i < S; ++i) {
-          const size_t idx = ((size_t)p * a.rows + t) * G.d_out + (s0 + i) * kStripeCols + cc;
+          const size_t idx = ((size_t)p * rows_arg + t) * G.d_out + (s0 + i) * kStripeCols + cc;
 #pragma unroll
           for (int w = 0; w < NW; ++w) store_coherent(&a.w[PAIR ? w : wi].partials[idx], sums[w][i][tt]);
         }
@@ -1006,7 +1013,7 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
       // per U slabs rather than one per slab
       constexpr int kVals = NT * S * NW;
       constexpr int U = kVals <= 8 ? 4 : kVals <= 16 ? 2 : 1;
-      const size_t stride = (size_t)a.rows * G.d_out;
+      const size_t stride = (size_t)rows_arg * G.d_out;
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -1025,7 +1032,7 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
               for (int w = 0; w < NW; ++w) {
                 const int t = 16 * tt + t_l;
                 const size_t idx = (size_t)t * G.d_out + (s0 + i) * kStripeCols + cc;
-                pv[dq][tt][i][w] = (q0 + dq < P && t < a.rows)
+                pv[dq][tt][i][w] = (q0 + dq < P && t < rows_arg)
                                        ? load_coherent(a.w[PAIR ? w : wi].partials + idx + (q0 + dq) * stride)
                                        : 0.0f;
               }
@@ -1046,7 +1053,7 @@ __global__ __launch_bounds__(W * 64) void skinny_kernel(StripedArgs a) {
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
     const int t = 16 * tt + t_l;
-    if (t >= a.rows) continue;
+    if (t >= rows_arg) continue;
     const float nrm = NORM ? inv_tok[tt * 16 + t_l] : 1.0f;
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -1068,7 +1075,9 @@ hipError_t sk_launch_t(const StripedArgs& a, int grid, int splits, hipStream_t s
   static_assert(16384 + (NT * W * 16 + NT * 16) * 4 <= kLutBytes, "the norm's sums fit the LUT space");
   StripedArgs args = a;
   args.xcd_run = grid % 8 == 0 ? grid / 8 : 0;
-  skinny_kernel<NT, W, D, S, DQ, PAIR, XF32, NORM><<<dim3(grid, splits), W * 64, smem, stream>>>(args);
+  skinny_kernel<NT, W, D, S, DQ, PAIR, XF32, NORM><<<dim3(grid, splits), W * 64, smem, stream>>>(
+      args.x, args.slot[0].packed, args.slot[0].scales, args.slot[0].scale_of_scales, args.d_in, args.rows_per_wave,
+      args.rows_per_split, args.rows, args.xcd_run, args.nweights, splits, args.norm_w, args);
   return hipGetLastError();
 }
 
