@@ -31,13 +31,13 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-source additions.  The striped GEMV passes what its prologue reads as
-# leading scalar kernel parameters, which this preloads into SGPRs before a
-# wave starts (with the loads as a fallback the code object carries for
-# firmware without preloading).
-EXTRA_FLAGS = {
-    "nf4_gemv_striped.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
-}
+# -amdgpu-kernarg-preload-count: a kernel's leading scalar parameters are
+# preloaded into SGPRs before a wave starts, so the prologue needs no load
+# through the scalar cache for them (the code object keeps the loads as a
+# fallback for firmware without preloading).  The striped GEMV and skinny
+# kernels pass what their prologues read that way.
+HIPCC_FLAGS += ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+EXTRA_FLAGS: dict = {}
 
 # hipBLASLt: the plain bf16 GEMM of the prefill path (nf4_blas.hip).
 LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
