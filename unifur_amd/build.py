@@ -37,7 +37,6 @@ HIPCC_FLAGS = [
 # fallback for firmware without preloading).  The striped GEMV and skinny
 # kernels pass what their prologues read that way.
 HIPCC_FLAGS += ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
-EXTRA_FLAGS: dict = {}
 
 # hipBLASLt: the plain bf16 GEMM of the prefill path (nf4_blas.hip).
 LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
@@ -52,7 +51,7 @@ def hipcc() -> str:
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
