@@ -41,6 +41,21 @@ def test_qkv_shared_input(device, oracle, rows, dt):
         check(y, oracle.linear_ref_f64(x, wdeq, b), x, wdeq, tol, f"qkv rows={rows} d_out={lin.d_output()}")
 
 
+@pytest.mark.parametrize("rows,dt", [(1, torch.float32), (3, torch.float32), (16, torch.bfloat16),
+                                     (40, torch.bfloat16)])
+def test_qkv_shared_input_grid_off_the_xcds(device, oracle, rows, dt):
+    """hidden 960 and kv 64: 60 + 4 + 4 = 68 stripes, so the launch's
+    workgroups (68, or 68 / stripes per wave) are not a multiple of the 8
+    XCDs and keep their plain order, while the workgroups of k and v take
+    their weight slots (1 and 2) by the selects over the argument block."""
+    layers = qkv(oracle, device, hidden=960, kv=64, seed=1900)
+    x, xt = acts(oracle, rows, 960, 1950 + rows, dt, device)
+    ys = Q.forward_shared_input(xt, [l for l, _, _ in layers], out_dtype=torch.float32)
+    tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+    for (lin, wdeq, b), y in zip(layers, ys):
+        check(y, oracle.linear_ref_f64(x, wdeq, b), x, wdeq, tol, f"qkv 960/64 rows={rows} d_out={lin.d_output()}")
+
+
 @pytest.mark.parametrize("variant", ["mixed_kinds", "row_major", "two", "one"])
 def test_fallbacks_and_counts(device, oracle, variant):
     kinds, striped, n = (True, True, True), (True, True, True), 3
